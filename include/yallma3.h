@@ -1,0 +1,253 @@
+/*
+ * yallma3.h -- C ABI of the MI355X-native quantized LLaMA forward path.
+ *
+ * Library: libyallma3_amd.so (HIP for gfx950 + C++ host).  Every entry
+ * point is `extern "C"`, takes plain pointers and sizes, and reports errors
+ * through a status code plus yl_last_error() instead of panicking.
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   load_transformer_ffi   src_llm/lib.rs:135-152
+ *   infer_ffi, free_string README.md:81-92, PoC_Bun_load.js:12-38 (documented,
+ *                          not implemented by the reference)
+ *   yl_load                lib.rs:107-133 load_transformer (".gguf" branch) ->
+ *                          transformer_llama_gguf.rs:179-655
+ *   yl_forward_x           Transformer::forward_x, transformer.rs:53 ->
+ *                          forward.rs:282-297 llama_forward_x
+ *   yl_create_session      Transformer::create_session, transformer.rs:56;
+ *                          InferenceSession::new, base_transformer.rs:89-98
+ *   yl_session_reset       InferenceSession::reset, base_transformer.rs:100-104
+ *   yl_get_embeddings      Transformer::get_embeddings_batch, transformer.rs:42;
+ *                          base_transformer.rs:143-161
+ *   yl_quantize            weight_type::quantize, weight_type.rs:76-90
+ *                          (quantization.rs:29-52 / weight_type.rs:52-74)
+ *   yl_matmul              weight_type::matmul, weight_type.rs:92-106 ->
+ *                          matmul_q8_slices, weight_type.rs:122-226
+ *   yl_rmsnorm_quantize    util::rmsnorm, util.rs:389-426 (+ quantize)
+ *   yl_rope_gguf           util::rope_gguf, util.rs:653-718
+ *   yl_attention           forward.rs fused_attention, forward.rs:299-400
+ *   yl_swiglu_quantize     forward.rs:220-237 (+ quantize)
+ *   yl_logits_argmax       forward.rs:261-279 + Sampler::sample_argmax,
+ *                          sampler.rs:67-79
+ *
+ * Memory: functions documented "device" take pointers from yl_malloc (or
+ * any HIP device allocation on the current device); "host" pointers are
+ * ordinary process memory.  `stream` is a hipStream_t or NULL (the null
+ * stream).  Not thread-safe per model/session; distinct models may be used
+ * from distinct threads.
+ */
+#ifndef YALLMA3_H
+#define YALLMA3_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+typedef int32_t yl_status;
+#define YL_OK               0
+#define YL_ERR_ARG         -1  /* bad argument / shape */
+#define YL_ERR_FORMAT      -2  /* format/variant mismatch (weight_type.rs:88,104) */
+#define YL_ERR_IO          -3  /* file cannot be opened or read */
+#define YL_ERR_GGUF        -4  /* malformed or unsupported GGUF (gguf.rs:189-267 asserts) */
+#define YL_ERR_HIP         -5  /* HIP runtime error / no GPU */
+#define YL_ERR_UNSUPPORTED -6  /* valid for the reference, not built here (see yl_last_error) */
+#define YL_ERR_NOMEM       -7
+#define YL_ERR_RANGE       -8  /* position beyond ctx_len */
+
+/* Message of the last failure on this thread ("" if none). */
+const char *yl_last_error(void);
+
+/* WeightFormat, weight_type.rs:17-22 */
+typedef enum { YL_Q8_0 = 0, YL_Q4_0 = 1, YL_F16 = 2 } yl_format;
+
+/* ------------------------------------------------ product ABI (unchanged) */
+/* lib.rs:135-152: loads a model (".gguf") into the process-wide current
+ * transformer, replacing the previous one.  false on NULL, unknown
+ * extension or any load error. */
+bool load_transformer_ffi(const char *model_path);
+/* README.md:81-92: generate a reply to `prompt` with the current model.
+ * Returns a library-owned NUL-terminated string (release with free_string)
+ * or NULL on error / no model. */
+char *infer_ffi(const char *prompt);
+/* Releases a string returned by infer_ffi; NULL is ignored. */
+void free_string(char *s);
+
+/* ------------------------------------------------------- device helpers */
+yl_status yl_device_count(int *count);
+void *yl_malloc(size_t bytes);                      /* device memory, 256-B aligned */
+void yl_free(void *p);
+yl_status yl_memcpy_h2d(void *dst_dev, const void *src_host, size_t bytes);
+yl_status yl_memcpy_d2h(void *dst_host, const void *src_dev, size_t bytes);
+yl_status yl_memset_d(void *dst_dev, int value, size_t bytes);
+yl_status yl_synchronize(void);
+
+/* -------------------------------------------------------------- L1 ops */
+/* quantization::quantize (Q8_0) / weight_type::q4_0_quantize (Q4_0) of n
+ * device floats in groups of gs (gs must be 32; n a multiple of 32).
+ * q: n int8 (device), scale: n/32 f32 (device). */
+yl_status yl_quantize(yl_format fmt, int8_t *q, float *scale, const float *x, size_t n,
+                      uint32_t gs, void *stream);
+
+/* A quantized weight matrix [o][n] resident on the device
+ * (QuantizedTensor::{Q8,Q4_0}, weight_type.rs:30-50). */
+typedef struct yl_weight yl_weight;
+/* From the reference's in-memory form (host): quant_vals o*n int8 (Q4_0:
+ * unsigned nibble values 0..15 per element, as load_q4_0_tensor produces,
+ * transformer_llama_gguf.rs:394-405) and scale_factor o*n/32 f32.  Scales
+ * must be exactly representable in binary16 (every GGUF scale is). */
+yl_weight *yl_weight_upload(yl_format fmt, const int8_t *quant_vals, const float *scale_factor,
+                            size_t o, size_t n);
+/* From raw GGUF blocks (host): Q8_0 34-byte / Q4_0 18-byte blocks of a
+ * row-major [o][n] tensor (transformer_llama_gguf.rs:345-410). */
+yl_weight *yl_weight_upload_gguf(yl_format fmt, const void *blocks, size_t o, size_t n);
+void yl_weight_free(yl_weight *w);
+/* Bytes the matrix occupies on the device (quantized values + f16 scales). */
+size_t yl_weight_bytes(const yl_weight *w);
+
+/* weight_type::matmul for quantized formats.  x: batch*n int8 + batch*n/32
+ * f32 scales (device), out: batch*o f32 (device).  Columns c < 4*floor(o/4)
+ * accumulate into out (`+=`, weight_type.rs:190-201), the rest are assigned
+ * (:207-224); each column sums its block terms ((float)isum*w_scale)*x_scale
+ * in block order.  gs must be 32.  YL_ERR_FORMAT if fmt differs from w's. */
+yl_status yl_matmul(float *out, yl_format fmt, const int8_t *xq, const float *xs, size_t batch,
+                    const yl_weight *w, size_t n, size_t o, uint32_t gs, void *stream);
+
+/* util::rmsnorm per row (batch rows of size floats, device), optionally
+ * followed by quantization of the normalized row.  qfmt: YL_Q8_0 / YL_Q4_0
+ * to quantize into q/scale, or -1 for none.  xn (nullable) receives the f32
+ * normalized rows. */
+yl_status yl_rmsnorm_quantize(const float *x, const float *weight, size_t size, float eps,
+                              size_t batch, float *xn, int32_t qfmt, int8_t *q, float *scale,
+                              void *stream);
+
+/* RoPE parameters (TransformerShape fields read by rope_gguf). */
+typedef struct {
+    uint32_t head_size, n_heads, n_kv_heads;
+    float rope_theta, freq_scale, ext_factor, attn_factor;
+    uint32_t original_ctx_len;
+} yl_rope_params;
+
+/* util::rope_gguf in place on q [batch][n_heads*head_size] and k
+ * [batch][n_kv_heads*head_size] (device) at positions start_pos+t. */
+yl_status yl_rope_gguf(const yl_rope_params *p, float *q, float *k, size_t batch,
+                       uint32_t start_pos, void *stream);
+
+/* fused_attention over a cache [seq][kv_dim] (device): out [batch][n_heads*
+ * head_size] f32 for query rows q [batch][n_heads*head_size], positions
+ * start_pos..start_pos+batch-1, seq_len = start_pos+batch. */
+yl_status yl_attention(float *out, const float *q, const float *key_cache, const float *value_cache,
+                       size_t batch, uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads,
+                       uint32_t head_size, float attn_scale, void *stream);
+
+/* SwiGLU (forward.rs:220-237) of gate/up [batch][hidden] (device) into h
+ * (nullable, f32), optionally quantized (qfmt -1 = none). */
+yl_status yl_swiglu_quantize(const float *gate, const float *up, size_t hidden, size_t batch,
+                             float *h, int32_t qfmt, int8_t *q, float *scale, void *stream);
+
+/* --------------------------------------------------- model and session */
+typedef struct yl_model yl_model;
+typedef struct yl_session yl_session;
+
+typedef struct {                 /* TransformerShape, base_transformer.rs:25-44 */
+    uint32_t dimension, hidden_dimension, n_heads, head_size, n_kv_heads, vocab_size;
+    uint32_t n_layers, ctx_len;
+    float rms_norm_eps, rope_theta;
+    uint32_t group_size;
+    float rope_freq_scale, rope_ext_factor, rope_attn_factor;
+    uint32_t rope_original_ctx_len;
+    float attention_scale;
+    int32_t weight_format;       /* yl_format the file declares (general.file_type) */
+} yl_shape;
+
+/* Load a GGUF v3 llama model onto the current device.  max_ctx_len caps
+ * llama.context_length (gguf.rs:233); fmt_override -1 = none.  Tensors keep
+ * their own stored format (a Q4_0 FFN beside Q8_0 attention works). */
+yl_model *yl_load(const char *path, uint32_t max_ctx_len, int32_t fmt_override);
+void yl_model_free(yl_model *m);
+const char *yl_model_name(const yl_model *m);
+yl_status yl_model_shape(const yl_model *m, yl_shape *out);
+size_t yl_vocab_size(const yl_model *m);
+uint32_t yl_max_ctx_len(const yl_model *m);
+uint32_t yl_bos_token(const yl_model *m);
+uint32_t yl_eos_token(const yl_model *m);
+/* Bytes of quantized layer weights read per decoded token (all seven
+ * projections of every layer) and of the logits embedding pass. */
+size_t yl_model_weight_bytes(const yl_model *m);
+size_t yl_model_embedding_bytes(const yl_model *m);
+
+/* get_embeddings_batch: n rows of dimension floats (host); out-of-range ids
+ * give zero rows. */
+yl_status yl_get_embeddings(const yl_model *m, const uint32_t *tokens, size_t n, float *out);
+
+yl_session *yl_create_session(const yl_model *m);
+void yl_session_free(yl_session *s);
+yl_status yl_session_reset(yl_session *s);
+/* InferenceSession.pos: kept for the caller, as in the reference (the
+ * forward pass itself only reads start_pos). */
+uint32_t yl_session_pos(const yl_session *s);
+void yl_session_set_pos(yl_session *s, uint32_t pos);
+/* Device pointers of the KV cache [n_layers][ctx_len][kv_dim] (f32). */
+yl_status yl_session_kv(yl_session *s, float **key_cache, float **value_cache, size_t *floats);
+
+/* Transformer::forward_x: tokens (host) at start_pos..start_pos+n-1; writes
+ * the last token's logits (host, vocab floats) when logits != NULL and its
+ * greedy argmax when argmax != NULL.  K/V accumulate into the session's
+ * cache as in the reference (forward.rs:166-169). */
+yl_status yl_forward_x(const yl_model *m, const uint32_t *tokens, size_t n, uint32_t start_pos,
+                       yl_session *s, float *logits, uint32_t *argmax);
+
+/* Greedy decode: n_steps forward_x calls of one token each, the first on
+ * `token` at start_pos, each next one on the previous step's argmax, without
+ * host round trips (tokens stay on the device; each step is one HIP graph
+ * launch).  out_tokens (host, n_steps) receives the argmax of every step. */
+yl_status yl_generate_greedy(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
+                             uint32_t n_steps, uint32_t *out_tokens);
+
+/* ------------------------------------------------------------ profiling */
+/* Per-kernel-class timing of greedy decode steps with HIP events recorded
+ * around every launch of the class on the session's stream (steps run
+ * eagerly, not as a graph).  kernel_class: 0 = quantized GEMV (all seven
+ * projections), 1 = attention, 2 = logits.  Returns the summed event time
+ * (ms), the launch count and the algorithmic bytes those launches read or
+ * wrote.  Also advances the session like yl_generate_greedy. */
+yl_status yl_profile_decode(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
+                            uint32_t n_steps, int32_t kernel_class, double *ms, uint64_t *launches,
+                            uint64_t *bytes);
+
+/* Elementwise probe of the device arithmetic the path relies on (device
+ * pointers, n floats): exp, sqrt(|x|), 1/x and f16 widening of (i & 0xffff). */
+yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt_out,
+                           float *recip_out, float *f16_out);
+
+/* ----------------------------------------------------- synthetic models */
+typedef struct {
+    uint32_t dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx_len;
+    float rope_theta, rms_eps, weight_std;
+    int32_t attn_format;   /* yl_format of attn_q/k/v/output */
+    int32_t ffn_format;    /* yl_format of ffn_gate/up/down */
+    int32_t embd_format;   /* yl_format of token_embd (Q8_0 or Q4_0) */
+    int32_t file_type;     /* general.file_type written (1, 2 or 7) */
+    uint64_t seed;
+} yl_synth_config;
+
+/* Writes a deterministic GGUF v3 llama model: every weight ~N(0, weight_std)
+ * from splitmix64 + Box-Muller (element index -> value, thread-count
+ * independent), quantized GGML-style (Q8_0: d = absmax/127, q = round(x/d);
+ * Q4_0: d = max/-8, q = min(15, (int)(x/d + 8.5)), element j in the low
+ * nibble of byte j and j+16 in the high nibble), norms = 1.0, and a vocabulary
+ * of placeholder token strings.  Host only (no GPU needed). */
+yl_status yl_write_synthetic_gguf(const char *path, const yl_synth_config *cfg);
+
+/* Fills `out` (host, count floats) with the generator's N(0, std) stream
+ * `stream` starting at element `first` (same values the writer uses). */
+yl_status yl_synthetic_normal(uint64_t seed, uint64_t stream, uint64_t first, size_t count,
+                              float std_dev, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

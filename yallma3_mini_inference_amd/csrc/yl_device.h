@@ -1,0 +1,111 @@
+// yl_device.h -- device-side arithmetic shared by every kernel.
+//
+// Bit-exactness contract: the forward path reproduces the reference's f32
+// operation order (products and sums rounded one at a time, no fused
+// multiply-add).  All HIP sources are compiled with -ffp-contract=off;
+// the helpers below spell each rounding step out so the order is visible.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "yl_internal.h"
+
+namespace yl {
+
+constexpr int kGroup = 32;        // block size of Q8_0/Q4_0 (transformer_llama_gguf.rs:281)
+
+__device__ __forceinline__ float fadd(float a, float b) { return a + b; }
+__device__ __forceinline__ float fmul(float a, float b) { return a * b; }
+
+// IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16 keeps f16 subnormals).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+// wide::f32x8::reduce_add as built without AVX (forward.rs:340,391,273;
+// util.rs:406): each f32x4 half summed left to right, then the halves added.
+__device__ __forceinline__ float reduce_add8(const float l[8]) {
+    float a = fadd(fadd(fadd(l[0], l[1]), l[2]), l[3]);
+    float b = fadd(fadd(fadd(l[4], l[5]), l[6]), l[7]);
+    return fadd(a, b);
+}
+
+// exp evaluated in binary64, rounded once to binary32: x*log2(e) -> k
+// (nearest), r = (x - k*ln2_hi) - k*ln2_lo with the fdlibm split of ln2,
+// e^r by the degree-13 Taylor polynomial (Horner), scaled by 2^k.  It is the
+// correctly rounded expf except with probability ~1e-9 per input; it stands
+// in for f32::exp in the softmax (forward.rs:358) and wide::f32x8::exp in
+// SwiGLU (forward.rs:230).
+__device__ __forceinline__ float expf_rn(float xf) {
+    if (xf != xf) return xf;
+    if (xf > 88.8f) return __builtin_inff();
+    if (xf < -104.0f) return 0.0f;
+    const double x = (double)xf;
+    const double log2e = 0x1.71547652b82fep+0;
+    const double ln2_hi = 0x1.62e42fee00000p-1;
+    const double ln2_lo = 0x1.a39ef35793c76p-33;
+    const double kd = __builtin_rint(x * log2e);
+    const double r = (x - kd * ln2_hi) - kd * ln2_lo;
+    double p = 0x1.6124613a86d09p-33;
+    p = p * r + 0x1.1eed8eff8d898p-29;
+    p = p * r + 0x1.ae64567f544e4p-26;
+    p = p * r + 0x1.27e4fb7789f5cp-22;
+    p = p * r + 0x1.71de3a556c734p-19;
+    p = p * r + 0x1.a01a01a01a01ap-16;
+    p = p * r + 0x1.a01a01a01a01ap-13;
+    p = p * r + 0x1.6c16c16c16c17p-10;
+    p = p * r + 0x1.1111111111111p-7;
+    p = p * r + 0x1.5555555555555p-5;
+    p = p * r + 0x1.5555555555555p-3;
+    p = p * r + 0x1.0000000000000p-1;
+    p = p * r + 1.0;
+    p = p * r + 1.0;
+    return (float)__builtin_amdgcn_ldexp(p, (int)kd);
+}
+
+// Rust `(v).round() as i8`: half away from zero, saturating, NaN -> 0.
+__device__ __forceinline__ int round_to_i8(float v) {
+    if (v != v) return 0;
+    float r = __builtin_roundf(v);
+    if (r >= 127.0f) return 127;
+    if (r <= -128.0f) return -128;
+    return (int)r;
+}
+
+// One group of 32 activations -> quantized values and scale.
+//   Q8_0: quantization.rs:29-52  (scale = absmax/127, q = round(x/scale))
+//   Q4_0: weight_type.rs:52-74   (scale = absmax/7,  then clamp to +-7)
+// `absmax` follows the reference's `if val > wmax` scan from 0 (NaN never
+// wins), which equals fmaxf over |x| and 0.
+template <int FMT>
+__device__ __forceinline__ float group_scale(float absmax) {
+    return FMT == kQ4 ? absmax / 7.0f : absmax / 127.0f;
+}
+template <int FMT>
+__device__ __forceinline__ int quant_one(float x, float scale) {
+    int q = round_to_i8(x / scale);
+    if (FMT == kQ4) q = q < -7 ? -7 : (q > 7 ? 7 : q);
+    return q;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Orderable 64-bit argmax key: larger key = larger value, ties broken toward
+// the smaller index (Sampler::sample_argmax keeps the first maximum,
+// sampler.rs:67-79).  NaN maps to the smallest key so it never wins.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    if (v != v) return 0ull;
+    if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+}  // namespace yl

@@ -1,0 +1,109 @@
+// yl_internal.h -- host-side declarations shared by the library's sources.
+//
+// Device data layout (HBM), all allocations 256-byte aligned:
+//   Quantized matrix [o][n] (a reference QuantizedTensor after GGUF decode):
+//     qs : Q8_0 -> int8  [o][n]            (one byte per weight)
+//          Q4_0 -> uint8 [o][n/2]          (16 B per 32-block, the reference's
+//                                           nibble order: byte j of a block holds
+//                                           element 2j in its low nibble and 2j+1
+//                                           in its high nibble, values 0..15)
+//     d  : f16 bits [o][n/32]              (the GGUF block scale, widened exactly
+//                                           in registers)
+//   Token embedding for the logits pass and the embedding lookup, Q8_0,
+//   interleaved so a wavefront reading 64 consecutive vocabulary rows issues
+//   one contiguous 1 KiB load per 16-element chunk:
+//     eq : int8 [vocab/64][dim/16][64][16]
+//     ed : f16  [vocab/64][dim/32][64]
+//   KV cache: f32 [n_layers][ctx_len][kv_dim] for keys and for values
+//   (InferenceSession, base_transformer.rs:81-98).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace yl {
+
+enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs:17-22
+
+struct QMat {          // device-resident quantized matrix
+    int fmt = 0;       // kQ8 / kQ4
+    int o = 0, n = 0, nb = 0;
+    uint8_t* qs = nullptr;
+    uint16_t* d = nullptr;
+    size_t bytes() const { return (size_t)o * (fmt == 1 ? n / 2 : n) + (size_t)o * nb * 2; }
+};
+
+struct EmbQ8 {         // interleaved Q8_0 token embedding
+    int vocab = 0, dim = 0, tiles = 0;
+    int8_t* q = nullptr;
+    uint16_t* d = nullptr;
+};
+
+// Per-session step state on the device: read by every kernel of a decode
+// step, advanced by the final kernel so greedy steps chain without the host.
+struct StepState {
+    int32_t pos;               // position of the first token of this call
+    uint32_t token;            // decode input token (next greedy token after a step)
+    uint32_t n_out;            // tokens written to the output ring so far
+    uint32_t pad;
+    unsigned long long argmax; // packed argmax key of the current step
+};
+
+// Epilogue kinds of the quantized GEMV kernel.
+enum Epi : int {
+    kEpiStore = 0,    // out[r] = (accumulate ? out[r] : 0) + sum of block terms
+    kEpiQkvRope = 1,  // rows [q | k | v]: q stored, k/v accumulate into the cache, RoPE on q,k
+    kEpiResid = 2,    // x[r] += sum; the last workgroup then runs RMSNorm (+quantize)
+    kEpiSwiglu = 3,   // 64-row groups [32 gate | 32 up] -> SwiGLU -> quantize one 32-block
+};
+
+struct GemvArgs {
+    // weights and activations
+    const uint8_t* qs; const uint16_t* d; int n, o, nb;
+    const int8_t* xq; const float* xs;        // [batch][n], [batch][nb]
+    // kEpiStore
+    float* out; int accumulate_cols;           // columns < accumulate_cols start from out[]
+    // kEpiQkvRope
+    float* q_out; float* k_cache; float* v_cache;
+    int att_dim, kv_dim, head_size;
+    const float* rope_cos; const float* rope_sin;  // [ctx][head_size/2]
+    const StepState* state;
+    // kEpiResid
+    float* x; const float* norm_w; float eps; int dim;
+    int norm_fmt;                              // -1: f32 normalized output only
+    int8_t* nq; float* ns; float* xn;          // quantized / f32 normalized outputs
+    unsigned int* counters;                    // one per batch row, zero between uses
+    // kEpiSwiglu
+    int8_t* hq; float* hs; float* h_f32; int hidden; int h_fmt;
+};
+
+// kernel launchers (yl_kernels.hip); all return hipError_t of the launch
+hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
+hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s);
+hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, float eps, int batch,
+                          float* xn, int8_t* xq, float* xs, hipStream_t s);
+hipError_t launch_embed_norm(const EmbQ8& e, const uint32_t* tokens, int batch, float* x,
+                             const float* w, float eps, int qfmt, float* xn, int8_t* xq, float* xs,
+                             hipStream_t s);
+hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st,
+                            int batch, int max_seq, int n_heads, int n_kv_heads, int head_size,
+                            float scale, int qfmt, int8_t* aq, float* as, float* att_f32,
+                            hipStream_t s);
+hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,
+                       float* q, float* k, int n_heads, int n_kv_heads, int head_size, hipStream_t s);
+hipError_t launch_swiglu_quant(int qfmt, const float* gate, const float* up, int hidden, int batch,
+                               float* h_f32, int8_t* hq, float* hs, hipStream_t s);
+hipError_t launch_logits(const EmbQ8& e, const float* xn, float* logits, unsigned long long* key,
+                         hipStream_t s);
+hipError_t launch_finalize(StepState* st, uint32_t* out_tokens, uint32_t out_cap, int advance,
+                           hipStream_t s);
+hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
+                                float* div_out, float* f16_out, hipStream_t s);
+
+// error reporting shared by the C ABI
+void set_error(const std::string& msg);
+
+}  // namespace yl

@@ -1,0 +1,1082 @@
+// yl_model.hip -- model loading, device repack, sessions, the forward driver
+// (eager for prompts, one HIP graph per decode step) and the C ABI.
+//
+// Mirrors the reference's Transformer trait (transformer.rs:19-69) and
+// llama_forward_x (forward.rs:120-297): per layer
+//   RMSNorm -> quantize -> Q,K,V matmuls (K/V += into the cache) -> RoPE ->
+//   attention -> quantize -> WO -> residual -> RMSNorm -> quantize ->
+//   W1,W3 -> SwiGLU -> quantize -> W2 -> residual,
+// then the final RMSNorm and the tied-embedding logits of the last token.
+// Kernel fusion (same arithmetic, fewer launches):
+//   embed + RMSNorm + quantize                      k_embed_norm
+//   Q/K/V matmul + K/V cache accumulate + RoPE      k_gemv<..., kEpiQkvRope>
+//   attention + quantize                            k_attention
+//   WO matmul + residual + RMSNorm + quantize       k_gemv<..., kEpiResid>
+//   W1/W3 matmul + SwiGLU + quantize                k_gemv<..., kEpiSwiglu>
+//   W2 matmul + residual + next RMSNorm + quantize  k_gemv<..., kEpiResid>
+//   logits + argmax                                 k_logits
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/yallma3.h"
+#include "yl_gguf.h"
+#include "yl_internal.h"
+
+namespace yl {
+
+thread_local std::string g_err;
+void set_error(const std::string& msg) { g_err = msg; }
+
+constexpr uint32_t kGgmlF32 = 0, kGgmlF16 = 1, kGgmlQ4_0 = 2, kGgmlQ8_0 = 8;
+
+static float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { man <<= 1; e++; } while ((man & 0x400u) == 0);
+            bits = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// binary32 -> binary16 when exact; false otherwise.
+static bool float_to_half_exact(float f, uint16_t* out) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    uint16_t h;
+    if (ax == 0) {
+        h = (uint16_t)sign;
+    } else if (ax >= 0x7f800000u) {
+        h = (uint16_t)(sign | 0x7c00u | ((ax & 0x7fffffu) ? 0x200u : 0u));
+    } else if (ax >= 0x38800000u && ax < 0x47800000u) {
+        if (ax & 0x1fffu) return false;
+        h = (uint16_t)(sign | ((ax >> 13) - (112u << 10)));
+    } else if (ax < 0x38800000u) {
+        const int e = (int)(ax >> 23);
+        const uint32_t m = (ax & 0x7fffffu) | (e ? 0x800000u : 0u);
+        const int shift = 126 - e;
+        if (e == 0 || shift > 24 || (m & ((1u << shift) - 1u))) return false;
+        h = (uint16_t)(sign | (m >> shift));
+    } else {
+        return false;
+    }
+    *out = h;
+    return half_to_float(h) == f || (f != f);
+}
+
+// Host staging of one device matrix in the repacked layout.
+struct HostQMat {
+    int fmt = kQ8;
+    size_t o = 0, n = 0, nb = 0;
+    std::vector<uint8_t> qs;
+    std::vector<uint16_t> d;
+    size_t row_bytes() const { return fmt == kQ4 ? n / 2 : n; }
+};
+
+// GGUF blocks -> repacked planes (transformer_llama_gguf.rs:345-410).
+static bool host_from_gguf(uint32_t type, const uint8_t* src, uint64_t avail, size_t o, size_t n,
+                           HostQMat* h, std::string* err) {
+    if (n % 32) { *err = "row length must be a multiple of 32"; return false; }
+    h->o = o; h->n = n; h->nb = n / 32;
+    const size_t blocks = o * h->nb;
+    if (type == kGgmlQ8_0) {
+        if (blocks * 34 > avail) { *err = "Q8_0 tensor exceeds the file"; return false; }
+        h->fmt = kQ8;
+        h->qs.resize(o * n);
+        h->d.resize(blocks);
+        for (size_t b = 0; b < blocks; b++) {
+            const uint8_t* blk = src + b * 34;
+            h->d[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+            memcpy(&h->qs[b * 32], blk + 2, 32);
+        }
+        return true;
+    }
+    if (type == kGgmlQ4_0) {
+        if (blocks * 18 > avail) { *err = "Q4_0 tensor exceeds the file"; return false; }
+        h->fmt = kQ4;
+        h->qs.resize(o * n / 2);
+        h->d.resize(blocks);
+        for (size_t b = 0; b < blocks; b++) {
+            const uint8_t* blk = src + b * 18;
+            h->d[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+            memcpy(&h->qs[b * 16], blk + 2, 16);
+        }
+        return true;
+    }
+    *err = "unsupported tensor type " + std::to_string(type) +
+           " for a quantized matmul (Q8_0 and Q4_0 are built; F16 is not)";
+    return false;
+}
+
+static bool host_concat_rows(const std::vector<const HostQMat*>& parts, HostQMat* out, std::string* err) {
+    out->fmt = parts[0]->fmt; out->n = parts[0]->n; out->nb = parts[0]->nb; out->o = 0;
+    for (auto p : parts) {
+        if (p->fmt != out->fmt || p->n != out->n) {
+            *err = "attn_q/attn_k/attn_v must share one format and row length";
+            return false;
+        }
+        out->o += p->o;
+    }
+    for (auto p : parts) {
+        out->qs.insert(out->qs.end(), p->qs.begin(), p->qs.end());
+        out->d.insert(out->d.end(), p->d.begin(), p->d.end());
+    }
+    return true;
+}
+
+// [w1 rows 32g..32g+31 | w3 rows 32g..32g+31] for every 32-row group g, so
+// one workgroup of the fused kernel sees gate and up of the same outputs.
+static bool host_interleave_gate_up(const HostQMat& w1, const HostQMat& w3, HostQMat* out, std::string* err) {
+    if (w1.fmt != w3.fmt || w1.n != w3.n || w1.o != w3.o || w1.o % 32) {
+        *err = "ffn_gate/ffn_up must share format and shape (rows a multiple of 32)";
+        return false;
+    }
+    out->fmt = w1.fmt; out->n = w1.n; out->nb = w1.nb; out->o = 2 * w1.o;
+    const size_t rb = w1.row_bytes();
+    out->qs.resize(out->o * rb);
+    out->d.resize(out->o * out->nb);
+    for (size_t g = 0; g < w1.o / 32; g++) {
+        for (int half = 0; half < 2; half++) {
+            const HostQMat& src = half ? w3 : w1;
+            const size_t dst_row = g * 64 + half * 32;
+            memcpy(&out->qs[dst_row * rb], &src.qs[g * 32 * rb], 32 * rb);
+            memcpy(&out->d[dst_row * out->nb], &src.d[g * 32 * src.nb], 32 * src.nb * 2);
+        }
+    }
+    return true;
+}
+
+static bool upload_qmat(const HostQMat& h, QMat* m, std::string* err) {
+    m->fmt = h.fmt; m->o = (int)h.o; m->n = (int)h.n; m->nb = (int)h.nb;
+    if (hipMalloc(&m->qs, h.qs.size() + 256) != hipSuccess || hipMalloc(&m->d, h.d.size() * 2 + 256) != hipSuccess) {
+        *err = "hipMalloc failed for a weight matrix";
+        return false;
+    }
+    if (hipMemcpy(m->qs, h.qs.data(), h.qs.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->d, h.d.data(), h.d.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "hipMemcpy failed for a weight matrix";
+        return false;
+    }
+    return true;
+}
+
+static void free_qmat(QMat* m) {
+    if (m->qs) hipFree(m->qs);
+    if (m->d) hipFree(m->d);
+    m->qs = nullptr; m->d = nullptr;
+}
+
+static float* upload_f32(const float* src, size_t n, std::string* err) {
+    float* p = nullptr;
+    if (hipMalloc(&p, n * 4 + 256) != hipSuccess || hipMemcpy(p, src, n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "upload of f32 vector failed";
+        return nullptr;
+    }
+    return p;
+}
+
+// The (cos, sin) per pair and position of rope_gguf (util.rs:653-718), with
+// the C library's powf/cosf/sinf/logf as Rust's std calls them.
+static void rope_table(const yl_rope_params& p, uint32_t pos_begin, uint32_t count, float* cos_t, float* sin_t) {
+    const float beta_fast = 32.0f, beta_slow = 1.0f;
+    const float two_pi = 2.0f * 3.14159265358979323846f;
+    const uint32_t n_pairs = p.head_size / 2;
+    const float theta_scale = powf(p.rope_theta, -2.0f / (float)p.head_size);
+    const float n_ctx_orig = (float)p.original_ctx_len;
+    float corr_start = fmaf(logf(n_ctx_orig / (beta_fast * two_pi)), (float)p.head_size, 0.0f) /
+                       (2.0f * logf(p.rope_theta));
+    corr_start = floorf(corr_start);
+    if (corr_start < 0.0f) corr_start = 0.0f;
+    const float corr_end = fmaf(logf(n_ctx_orig / (beta_slow * two_pi)), (float)p.head_size, 0.0f) /
+                           (2.0f * logf(p.rope_theta));
+    const float corr_dims_1 =
+        fminf(corr_start, corr_end) + fminf(corr_end, (float)n_pairs) - fmaxf(corr_start, 0.0f);
+    for (uint32_t r = 0; r < count; r++) {
+        float theta = (float)(pos_begin + r);
+        for (uint32_t k = 0; k < n_pairs; k++) {
+            const float theta_interp = p.freq_scale * theta / 1.0f;
+            float t = theta_interp;
+            if (p.ext_factor != 0.0f) {
+                float dd = corr_dims_1 - corr_start;
+                if (dd < 0.001f) dd = 0.001f;
+                float y = ((float)(k * 2) * 0.5f - corr_start) / dd;
+                y = y < 0.0f ? 0.0f : (y > 1.0f ? 1.0f : y);
+                const float ramp_mix = (1.0f - y) * p.ext_factor;
+                t = theta_interp * (1.0f - ramp_mix) + theta / 1.0f * ramp_mix;
+            }
+            cos_t[(size_t)r * n_pairs + k] = cosf(t) * p.attn_factor;
+            sin_t[(size_t)r * n_pairs + k] = sinf(t) * p.attn_factor;
+            theta = theta * theta_scale;
+        }
+    }
+}
+
+}  // namespace yl
+
+using namespace yl;
+
+struct yl_weight {
+    QMat m;
+};
+
+struct Layer {
+    QMat qkv, wo, w13, w2;
+    float* rms_att = nullptr;
+    float* rms_ffn = nullptr;
+};
+
+struct yl_model {
+    yl_shape shape{};
+    int dim = 0, hidden = 0, n_layers = 0, n_heads = 0, n_kv = 0, hd = 0, vocab = 0, ctx = 0;
+    int att = 0, kv = 0;
+    float eps = 0.0f, attn_scale = 0.0f;
+    yl_rope_params rope{};
+    std::vector<Layer> layers;
+    float* rms_final = nullptr;
+    EmbQ8 emb;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    uint32_t bos = 128000, eos = 128009;
+    std::string name = "TransformerLlamaGguf";
+    std::vector<std::string> vocab_str;
+    size_t weight_bytes = 0, emb_bytes = 0;
+    int device = 0;
+};
+
+struct yl_session {
+    const yl_model* m = nullptr;
+    hipStream_t stream = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    size_t kv_floats = 0;
+    StepState* st = nullptr;        // device
+    StepState* st_host = nullptr;   // pinned
+    int cap_b = 0;
+    float *x = nullptr, *xn = nullptr, *sq = nullptr, *logits = nullptr;
+    int8_t *xq = nullptr, *aq = nullptr, *hq = nullptr;
+    float *xs = nullptr, *as_ = nullptr, *hs = nullptr;
+    unsigned* counters = nullptr;
+    uint32_t* tokens = nullptr;
+    uint32_t* ring = nullptr;
+    uint32_t ring_cap = 0;
+    hipGraphExec_t graph = nullptr;
+    uint32_t pos = 0;
+};
+
+namespace {
+
+void model_release(yl_model* m) {
+    if (!m) return;
+    for (auto& L : m->layers) {
+        free_qmat(&L.qkv); free_qmat(&L.wo); free_qmat(&L.w13); free_qmat(&L.w2);
+        if (L.rms_att) hipFree(L.rms_att);
+        if (L.rms_ffn) hipFree(L.rms_ffn);
+    }
+    if (m->rms_final) hipFree(m->rms_final);
+    if (m->emb.q) hipFree(m->emb.q);
+    if (m->emb.d) hipFree(m->emb.d);
+    if (m->rope_cos) hipFree(m->rope_cos);
+    if (m->rope_sin) hipFree(m->rope_sin);
+    delete m;
+}
+
+// token_embd (Q8_0 or Q4_0 blocks) -> interleaved Q8_0 planes.  A Q4_0 row
+// element is the unsigned nibble times the f16 scale (gguf.rs:394-405,474-486),
+// which the Q8_0 plane holds exactly as q = nibble.
+bool upload_embedding(const GgufTensor* t, int dim, int vocab, EmbQ8* e, std::string* err) {
+    if ((uint64_t)dim * vocab > t->n_elements) { *err = "token_embd.weight smaller than vocab*dim"; return false; }
+    if (dim % 32) { *err = "embedding length must be a multiple of 32"; return false; }
+    const int tiles = (vocab + 63) / 64;
+    const int k16n = dim / 16, nbE = dim / 32;
+    std::vector<int8_t> q((size_t)tiles * 64 * dim, 0);
+    std::vector<uint16_t> d((size_t)tiles * 64 * nbE, 0);
+    const size_t blocks = (size_t)vocab * nbE;
+    if (t->type == kGgmlQ8_0) {
+        if (blocks * 34 > t->avail) { *err = "token_embd exceeds the file"; return false; }
+    } else if (t->type == kGgmlQ4_0) {
+        if (blocks * 18 > t->avail) { *err = "token_embd exceeds the file"; return false; }
+    } else {
+        *err = "token_embd.weight type " + std::to_string(t->type) + " is not built (Q8_0 and Q4_0 are)";
+        return false;
+    }
+    for (int v = 0; v < vocab; v++) {
+        const size_t tile = v / 64, lane = v % 64;
+        for (int b = 0; b < nbE; b++) {
+            int8_t vals[32];
+            uint16_t sc;
+            if (t->type == kGgmlQ8_0) {
+                const uint8_t* blk = t->data + ((size_t)v * nbE + b) * 34;
+                sc = (uint16_t)(blk[0] | (blk[1] << 8));
+                memcpy(vals, blk + 2, 32);
+            } else {
+                const uint8_t* blk = t->data + ((size_t)v * nbE + b) * 18;
+                sc = (uint16_t)(blk[0] | (blk[1] << 8));
+                for (int j = 0; j < 16; j++) {
+                    vals[2 * j] = (int8_t)(blk[2 + j] & 0x0f);
+                    vals[2 * j + 1] = (int8_t)((blk[2 + j] >> 4) & 0x0f);
+                }
+            }
+            d[(tile * nbE + b) * 64 + lane] = sc;
+            for (int h = 0; h < 2; h++) {
+                const size_t k16 = (size_t)2 * b + h;
+                memcpy(&q[((tile * k16n + k16) * 64 + lane) * 16], vals + 16 * h, 16);
+            }
+        }
+    }
+    e->vocab = vocab; e->dim = dim; e->tiles = tiles;
+    if (hipMalloc(&e->q, q.size() + 256) != hipSuccess || hipMalloc(&e->d, d.size() * 2 + 256) != hipSuccess ||
+        hipMemcpy(e->q, q.data(), q.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(e->d, d.data(), d.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "upload of the token embedding failed";
+        return false;
+    }
+    return true;
+}
+
+yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_override, yl_status* st) {
+    std::string err;
+    *st = YL_ERR_GGUF;
+    GgufFile g;
+    if (!g.open(path, &err)) {
+        set_error(err);
+        *st = (err.rfind("cannot", 0) == 0) ? YL_ERR_IO : YL_ERR_GGUF;
+        return nullptr;
+    }
+    const GgufValue* arch = g.get("general.architecture");
+    if (!arch || arch->type != 8) { set_error("Missing or wrong type for metadata key: general.architecture"); return nullptr; }
+    if (arch->s != "llama") { set_error("Unsupported GGUF architecture: " + arch->s); return nullptr; }
+    std::unique_ptr<yl_model, void (*)(yl_model*)> m(new yl_model(), model_release);
+    uint64_t u = 0;
+    float f = 0.0f;
+    auto req_u = [&](const char* k, int* dst) {
+        if (!meta_u64(g, k, &u)) { set_error(std::string("Missing or wrong type for metadata key: ") + k); return false; }
+        *dst = (int)u;
+        return true;
+    };
+    if (!req_u("llama.embedding_length", &m->dim) || !req_u("llama.feed_forward_length", &m->hidden) ||
+        !req_u("llama.block_count", &m->n_layers) || !req_u("llama.attention.head_count", &m->n_heads))
+        return nullptr;
+    m->n_kv = meta_u64(g, "llama.attention.head_count_kv", &u) ? (int)u : m->n_heads;
+    if (!meta_f32(g, "llama.attention.layer_norm_rms_epsilon", &m->eps)) {
+        set_error("Missing or wrong type for metadata key: llama.attention.layer_norm_rms_epsilon");
+        return nullptr;
+    }
+    const uint64_t file_type = meta_u64(g, "general.file_type", &u) ? u : 7;
+    const float rope_theta = meta_f32(g, "llama.rope.freq_base", &f) ? f : 10000.0f;
+    int seq_len = 0;
+    if (!req_u("llama.context_length", &seq_len)) return nullptr;
+    if (m->n_heads <= 0 || m->dim % m->n_heads) { set_error("dim must be divisible by n_heads"); return nullptr; }
+    m->hd = m->dim / m->n_heads;
+    m->ctx = (int)((uint32_t)seq_len < max_ctx_len ? (uint32_t)seq_len : max_ctx_len);
+    const GgufValue* toks = g.get("tokenizer.ggml.tokens");
+    if (!toks) { set_error("tokenizer.ggml.tokens metadata key not found"); return nullptr; }
+    if (toks->type != 9) { set_error("tokenizer.ggml.tokens must be an array of strings"); return nullptr; }
+    m->vocab = (int)toks->arr_len;
+    m->vocab_str = toks->arr_str;
+    const float raw = meta_f32(g, "llama.rope.scaling.factor", &f) ? f : 1.0f;
+    m->rope.freq_scale = raw != 0.0f ? 1.0f / raw : 1.0f;
+    m->rope.ext_factor = meta_f32(g, "llama.rope.scaling.ext_factor", &f) ? f : 0.0f;
+    m->rope.attn_factor = meta_f32(g, "llama.rope.scaling.attn_factor", &f) ? f : 1.0f;
+    m->rope.original_ctx_len = meta_u64(g, "llama.rope.scaling.original_context_length", &u) ? (uint32_t)u : (uint32_t)seq_len;
+    const float att_scale_meta = meta_f32(g, "llama.attention.scale", &f) ? f : 0.0f;
+    m->rope.rope_theta = rope_theta;
+    m->rope.head_size = (uint32_t)m->hd;
+    m->rope.n_heads = (uint32_t)m->n_heads;
+    m->rope.n_kv_heads = (uint32_t)m->n_kv;
+    int wfmt;
+    if (fmt_override >= 0) {
+        if (fmt_override > 2) { set_error("invalid format override"); *st = YL_ERR_ARG; return nullptr; }
+        wfmt = fmt_override;
+    } else if (file_type == 1) wfmt = YL_F16;
+    else if (file_type == 2) wfmt = YL_Q4_0;
+    else if (file_type == 7) wfmt = YL_Q8_0;
+    else { set_error("Unsupported GGUF file_type: " + std::to_string(file_type) + " -- supported: F16=1, Q4_0=2, Q8_0=7"); return nullptr; }
+    if (const GgufValue* b = g.get("tokenizer.ggml.bos_token_id")) m->bos = (uint32_t)(b->type == 5 || b->type == 11 ? (uint64_t)b->i : b->u);
+    if (const GgufValue* e = g.get("tokenizer.ggml.eos_token_id")) m->eos = (uint32_t)(e->type == 5 || e->type == 11 ? (uint64_t)e->i : e->u);
+
+    m->att = m->n_heads * m->hd;
+    m->kv = m->n_kv * m->hd;
+    m->attn_scale = att_scale_meta != 0.0f ? att_scale_meta : 1.0f / sqrtf((float)m->hd);
+    if (m->n_kv <= 0 || m->n_heads % m->n_kv) { set_error("n_heads must be a multiple of n_kv_heads"); return nullptr; }
+    if (m->dim % 32 || m->hidden % 32 || m->kv % 32 || m->hd % 32 || m->dim > 16384 || m->ctx <= 0) {
+        set_error("unsupported shape: dim, hidden, kv_dim and head_size must be multiples of 32, dim <= 16384");
+        *st = YL_ERR_UNSUPPORTED;
+        return nullptr;
+    }
+    if ((size_t)m->ctx * 4 + (size_t)m->hd * 40 > 60 * 1024) {
+        set_error("context too long for the single-pass attention kernel (ctx_len <= ~15000)");
+        *st = YL_ERR_UNSUPPORTED;
+        return nullptr;
+    }
+    hipGetDevice(&m->device);
+
+    const GgufTensor* te = g.tensor("token_embd.weight");
+    if (!te) { set_error("token_embd.weight not found"); return nullptr; }
+    if (!upload_embedding(te, m->dim, m->vocab, &m->emb, &err)) { set_error(err); *st = YL_ERR_UNSUPPORTED; return nullptr; }
+    m->emb_bytes = (size_t)m->vocab * m->dim + (size_t)m->vocab * (m->dim / 32) * 2;
+
+    auto load_f32 = [&](const std::string& nm, size_t n, float** dst) {
+        const GgufTensor* t = g.tensor(nm);
+        if (!t) { set_error("Missing tensor: " + nm); return false; }
+        if (t->type != kGgmlF32) { set_error("Expected F32 tensor: " + nm); return false; }
+        if (t->n_elements < n || t->avail < n * 4) { set_error("tensor too small: " + nm); return false; }
+        std::vector<float> v(n);
+        memcpy(v.data(), t->data, n * 4);
+        *dst = upload_f32(v.data(), n, &err);
+        if (!*dst) { set_error(err); return false; }
+        return true;
+    };
+    if (!load_f32("output_norm.weight", m->dim, &m->rms_final)) return nullptr;
+    m->layers.resize(m->n_layers);
+    for (int l = 0; l < m->n_layers; l++) {
+        Layer& L = m->layers[l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        if (!load_f32(p + "attn_norm.weight", m->dim, &L.rms_att) || !load_f32(p + "ffn_norm.weight", m->dim, &L.rms_ffn))
+            return nullptr;
+        const char* names[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_down", "ffn_up"};
+        const size_t rows[7] = {(size_t)m->att, (size_t)m->kv, (size_t)m->kv, (size_t)m->dim,
+                                (size_t)m->hidden, (size_t)m->dim, (size_t)m->hidden};
+        const size_t cols[7] = {(size_t)m->dim, (size_t)m->dim, (size_t)m->dim, (size_t)m->att,
+                                (size_t)m->dim, (size_t)m->hidden, (size_t)m->dim};
+        HostQMat h[7];
+        for (int k = 0; k < 7; k++) {
+            const GgufTensor* t = g.tensor(p + names[k] + ".weight");
+            if (!t) { set_error("Missing tensor: " + p + names[k] + ".weight"); return nullptr; }
+            if (t->n_elements != rows[k] * cols[k]) { set_error("unexpected element count for " + t->name); return nullptr; }
+            if (!host_from_gguf(t->type, t->data, t->avail, rows[k], cols[k], &h[k], &err)) {
+                set_error(t->name + ": " + err);
+                *st = YL_ERR_UNSUPPORTED;
+                return nullptr;
+            }
+        }
+        HostQMat qkv, w13;
+        if (!host_concat_rows({&h[0], &h[1], &h[2]}, &qkv, &err) || !host_interleave_gate_up(h[4], h[6], &w13, &err) ||
+            !upload_qmat(qkv, &L.qkv, &err) || !upload_qmat(h[3], &L.wo, &err) || !upload_qmat(w13, &L.w13, &err) ||
+            !upload_qmat(h[5], &L.w2, &err)) {
+            set_error(p + err);
+            return nullptr;
+        }
+        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w13.bytes() + L.w2.bytes();
+    }
+    // RoPE angle table for every position of the context
+    {
+        const size_t half = m->hd / 2;
+        std::vector<float> c((size_t)m->ctx * half), s((size_t)m->ctx * half);
+        rope_table(m->rope, 0, (uint32_t)m->ctx, c.data(), s.data());
+        m->rope_cos = upload_f32(c.data(), c.size(), &err);
+        m->rope_sin = upload_f32(s.data(), s.size(), &err);
+        if (!m->rope_cos || !m->rope_sin) { set_error(err); return nullptr; }
+    }
+    yl_shape& S = m->shape;
+    S.dimension = m->dim; S.hidden_dimension = m->hidden; S.n_heads = m->n_heads; S.head_size = m->hd;
+    S.n_kv_heads = m->n_kv; S.vocab_size = m->vocab; S.n_layers = m->n_layers; S.ctx_len = m->ctx;
+    S.rms_norm_eps = m->eps; S.rope_theta = rope_theta; S.group_size = 32;
+    S.rope_freq_scale = m->rope.freq_scale; S.rope_ext_factor = m->rope.ext_factor;
+    S.rope_attn_factor = m->rope.attn_factor; S.rope_original_ctx_len = m->rope.original_ctx_len;
+    S.attention_scale = att_scale_meta; S.weight_format = wfmt;
+    *st = YL_OK;
+    return m.release();
+}
+
+bool session_grow(yl_session* s, int batch) {
+    if (batch <= s->cap_b) return true;
+    const yl_model* m = s->m;
+    // the decode graph holds the old buffer addresses: drop it, it is
+    // captured again on the next decode step
+    hipStreamSynchronize(s->stream);
+    if (s->graph) { hipGraphExecDestroy(s->graph); s->graph = nullptr; }
+    auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
+    rel(s->x); rel(s->xn); rel(s->sq); rel(s->xq); rel(s->aq); rel(s->hq); rel(s->xs); rel(s->as_); rel(s->hs);
+    rel(s->counters); rel(s->tokens);
+    const size_t B = (size_t)batch;
+    bool ok = hipMalloc(&s->x, B * m->dim * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->xn, B * m->dim * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->sq, B * m->att * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->xq, B * m->dim + 256) == hipSuccess &&
+              hipMalloc(&s->aq, B * m->att + 256) == hipSuccess &&
+              hipMalloc(&s->hq, B * m->hidden + 256) == hipSuccess &&
+              hipMalloc(&s->xs, B * m->dim / 8 + 256) == hipSuccess &&
+              hipMalloc(&s->as_, B * m->att / 8 + 256) == hipSuccess &&
+              hipMalloc(&s->hs, B * m->hidden / 8 + 256) == hipSuccess &&
+              hipMalloc(&s->counters, B * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->tokens, B * 4 + 256) == hipSuccess;
+    if (!ok) { set_error("hipMalloc failed for session buffers"); s->cap_b = 0; return false; }
+    if (hipMemset(s->counters, 0, B * 4 + 256) != hipSuccess) { set_error("hipMemset failed"); return false; }
+    s->cap_b = batch;
+    return true;
+}
+
+// Event timing of one kernel class inside eager steps.
+struct Prof {
+    int cls = -1;
+    std::vector<hipEvent_t> ev;
+    int used = 0;
+    double ms = 0.0;
+    uint64_t launches = 0, bytes = 0;
+    hipStream_t stream = nullptr;
+    void begin(int c) {
+        if (c != cls) return;
+        if ((size_t)used + 2 > ev.size()) {
+            hipEvent_t a, b;
+            hipEventCreate(&a); hipEventCreate(&b);
+            ev.push_back(a); ev.push_back(b);
+        }
+        hipEventRecord(ev[used], stream);
+    }
+    void end(int c, uint64_t nbytes) {
+        if (c != cls) return;
+        hipEventRecord(ev[used + 1], stream);
+        used += 2;
+        launches += 1;
+        bytes += nbytes;
+    }
+    void collect() {
+        if (used) hipEventSynchronize(ev[used - 1]);
+        for (int i = 0; i < used; i += 2) {
+            float t = 0.0f;
+            hipEventElapsedTime(&t, ev[i], ev[i + 1]);
+            ms += t;
+        }
+        used = 0;
+    }
+    ~Prof() { for (auto e : ev) hipEventDestroy(e); }
+};
+
+uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
+    return (uint64_t)w.bytes() + (uint64_t)batch * ((uint64_t)w.n + (uint64_t)w.nb * 4 + (uint64_t)out_elems * 4);
+}
+
+// One forward pass over `batch` tokens whose ids are at `tok` (device) and
+// whose first position is st->pos (device).  Enqueued on s->stream only.
+hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance,
+                           Prof* prof) {
+    hipStream_t st = s->stream;
+    hipError_t e;
+#define YL_TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
+    const Layer& L0 = m->layers[0];
+    YL_TRY(launch_embed_norm(m->emb, tok, batch, s->x, L0.rms_att, m->eps, L0.qkv.fmt, nullptr, s->xq, s->xs, st));
+    const size_t lay_kv = (size_t)m->ctx * m->kv;
+    for (int l = 0; l < m->n_layers; l++) {
+        const Layer& L = m->layers[l];
+        const bool last = l + 1 == m->n_layers;
+        float* kc = s->kc + (size_t)l * lay_kv;
+        float* vc = s->vc + (size_t)l * lay_kv;
+        GemvArgs a{};
+        a.qs = L.qkv.qs; a.d = L.qkv.d; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
+        a.xq = s->xq; a.xs = s->xs;
+        a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
+        a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd;
+        a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
+        if (prof) prof->begin(0);
+        YL_TRY(launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st));
+        if (prof) prof->end(0, gemv_bytes(L.qkv, L.qkv.o, batch));
+
+        if (prof) prof->begin(1);
+        YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->n_heads, m->n_kv, m->hd, m->attn_scale,
+                                L.wo.fmt, s->aq, s->as_, nullptr, st));
+        if (prof) prof->end(1, 0);
+
+        GemvArgs b{};
+        b.qs = L.wo.qs; b.d = L.wo.d; b.n = L.wo.n; b.o = L.wo.o; b.nb = L.wo.nb;
+        b.xq = s->aq; b.xs = s->as_;
+        b.x = s->x; b.norm_w = L.rms_ffn; b.eps = m->eps; b.dim = m->dim; b.norm_fmt = L.w13.fmt;
+        b.nq = s->xq; b.ns = s->xs; b.xn = nullptr; b.counters = s->counters;
+        if (prof) prof->begin(0);
+        YL_TRY(launch_gemv(b, L.wo.fmt, kEpiResid, batch, st));
+        if (prof) prof->end(0, gemv_bytes(L.wo, L.wo.o, batch));
+
+        GemvArgs c{};
+        c.qs = L.w13.qs; c.d = L.w13.d; c.n = L.w13.n; c.o = L.w13.o; c.nb = L.w13.nb;
+        c.xq = s->xq; c.xs = s->xs;
+        c.hq = s->hq; c.hs = s->hs; c.h_f32 = nullptr; c.hidden = m->hidden; c.h_fmt = L.w2.fmt;
+        if (prof) prof->begin(0);
+        YL_TRY(launch_gemv(c, L.w13.fmt, kEpiSwiglu, batch, st));
+        if (prof) prof->end(0, gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch));
+
+        GemvArgs d{};
+        d.qs = L.w2.qs; d.d = L.w2.d; d.n = L.w2.n; d.o = L.w2.o; d.nb = L.w2.nb;
+        d.xq = s->hq; d.xs = s->hs;
+        d.x = s->x; d.eps = m->eps; d.dim = m->dim; d.counters = s->counters;
+        if (!last) {
+            d.norm_w = m->layers[l + 1].rms_att; d.norm_fmt = m->layers[l + 1].qkv.fmt;
+            d.nq = s->xq; d.ns = s->xs; d.xn = nullptr;
+        } else {
+            d.norm_w = m->rms_final; d.norm_fmt = -1; d.xn = s->xn;
+        }
+        if (prof) prof->begin(0);
+        YL_TRY(launch_gemv(d, L.w2.fmt, kEpiResid, batch, st));
+        if (prof) prof->end(0, gemv_bytes(L.w2, L.w2.o, batch));
+    }
+    if (prof) prof->begin(2);
+    YL_TRY(launch_logits(m->emb, s->xn + (size_t)(batch - 1) * m->dim, s->logits, &s->st->argmax, st));
+    if (prof) prof->end(2, (uint64_t)m->emb_bytes + (uint64_t)m->dim * 4 + (uint64_t)m->vocab * 4);
+    YL_TRY(launch_finalize(s->st, s->ring, s->ring_cap, advance, st));
+#undef YL_TRY
+    return hipSuccess;
+}
+
+bool ensure_graph(const yl_model* m, yl_session* s) {
+    if (s->graph) return true;
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        set_error("hipStreamBeginCapture failed");
+        return false;
+    }
+    const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1, nullptr);
+    const hipError_t e2 = hipStreamEndCapture(s->stream, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+        set_error(std::string("decode graph capture failed: ") + hipGetErrorString(e != hipSuccess ? e : e2));
+        if (g) hipGraphDestroy(g);
+        return false;
+    }
+    const hipError_t e3 = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e3 != hipSuccess) {
+        set_error(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(e3));
+        s->graph = nullptr;
+        return false;
+    }
+    return true;
+}
+
+yl_status hip_fail(hipError_t e, const char* what) {
+    set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return YL_ERR_HIP;
+}
+
+yl_status put_state(yl_session* s, int32_t pos, uint32_t token) {
+    s->st_host->pos = pos;
+    s->st_host->token = token;
+    s->st_host->n_out = 0;
+    s->st_host->pad = 0;
+    s->st_host->argmax = 0ull;
+    const hipError_t e = hipMemcpyAsync(s->st, s->st_host, sizeof(StepState), hipMemcpyHostToDevice, s->stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "state upload");
+}
+
+}  // namespace
+
+// ============================================================== C ABI ====
+
+extern "C" {
+
+const char* yl_last_error(void) { return g_err.c_str(); }
+
+yl_status yl_device_count(int* count) {
+    if (!count) return YL_ERR_ARG;
+    const hipError_t e = hipGetDeviceCount(count);
+    if (e != hipSuccess) { *count = 0; return hip_fail(e, "hipGetDeviceCount"); }
+    return YL_OK;
+}
+
+void* yl_malloc(size_t bytes) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) { hip_fail(e, "hipMalloc"); return nullptr; }
+    return p;
+}
+void yl_free(void* p) { if (p) hipFree(p); }
+yl_status yl_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "hipMemcpy H2D");
+}
+yl_status yl_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "hipMemcpy D2H");
+}
+yl_status yl_memset_d(void* dst, int value, size_t bytes) {
+    const hipError_t e = hipMemset(dst, value, bytes);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "hipMemset");
+}
+yl_status yl_synchronize(void) {
+    const hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? YL_OK : hip_fail(e, "hipDeviceSynchronize");
+}
+
+yl_status yl_quantize(yl_format fmt, int8_t* q, float* scale, const float* x, size_t n, uint32_t gs, void* stream) {
+    if (gs != 32) { set_error("group size must be 32 (GGUF blocks)"); return YL_ERR_UNSUPPORTED; }
+    if (fmt != YL_Q8_0 && fmt != YL_Q4_0) { set_error("quantize: F16 has no quantized form"); return YL_ERR_FORMAT; }
+    if (n % 32 || (n && (!q || !scale || !x))) { set_error("quantize: n must be a multiple of 32"); return YL_ERR_ARG; }
+    const hipError_t e = launch_quantize(fmt, q, scale, x, n, (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "quantize launch");
+}
+
+yl_weight* yl_weight_upload(yl_format fmt, const int8_t* qv, const float* sf, size_t o, size_t n) {
+    if ((fmt != YL_Q8_0 && fmt != YL_Q4_0) || !qv || !sf || !o || n % 32) {
+        set_error("yl_weight_upload: Q8_0/Q4_0 [o][n] with n a multiple of 32");
+        return nullptr;
+    }
+    HostQMat h;
+    h.fmt = fmt == YL_Q4_0 ? kQ4 : kQ8;
+    h.o = o; h.n = n; h.nb = n / 32;
+    h.d.resize(o * h.nb);
+    for (size_t i = 0; i < h.d.size(); i++) {
+        if (!float_to_half_exact(sf[i], &h.d[i])) {
+            set_error("yl_weight_upload: scale " + std::to_string(i) + " is not exactly representable in binary16");
+            return nullptr;
+        }
+    }
+    if (h.fmt == kQ8) {
+        h.qs.assign((const uint8_t*)qv, (const uint8_t*)qv + o * n);
+    } else {
+        h.qs.resize(o * n / 2);
+        for (size_t i = 0; i < o * n / 2; i++) {
+            const int lo = qv[2 * i], hi = qv[2 * i + 1];
+            if (lo < 0 || lo > 15 || hi < 0 || hi > 15) {
+                set_error("yl_weight_upload: Q4_0 values must be nibbles 0..15");
+                return nullptr;
+            }
+            h.qs[i] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+    auto* w = new yl_weight();
+    std::string err;
+    if (!upload_qmat(h, &w->m, &err)) { set_error(err); free_qmat(&w->m); delete w; return nullptr; }
+    return w;
+}
+
+yl_weight* yl_weight_upload_gguf(yl_format fmt, const void* blocks, size_t o, size_t n) {
+    if ((fmt != YL_Q8_0 && fmt != YL_Q4_0) || !blocks || !o || n % 32) {
+        set_error("yl_weight_upload_gguf: Q8_0/Q4_0 [o][n] with n a multiple of 32");
+        return nullptr;
+    }
+    HostQMat h;
+    std::string err;
+    const uint32_t type = fmt == YL_Q4_0 ? kGgmlQ4_0 : kGgmlQ8_0;
+    if (!host_from_gguf(type, (const uint8_t*)blocks, ~0ull, o, n, &h, &err)) { set_error(err); return nullptr; }
+    auto* w = new yl_weight();
+    if (!upload_qmat(h, &w->m, &err)) { set_error(err); free_qmat(&w->m); delete w; return nullptr; }
+    return w;
+}
+
+void yl_weight_free(yl_weight* w) {
+    if (!w) return;
+    free_qmat(&w->m);
+    delete w;
+}
+
+size_t yl_weight_bytes(const yl_weight* w) { return w ? w->m.bytes() : 0; }
+
+yl_status yl_matmul(float* out, yl_format fmt, const int8_t* xq, const float* xs, size_t batch, const yl_weight* w,
+                    size_t n, size_t o, uint32_t gs, void* stream) {
+    if (!w || !out || !xq || !xs) { set_error("yl_matmul: null argument"); return YL_ERR_ARG; }
+    if ((fmt == YL_Q4_0 ? kQ4 : (fmt == YL_Q8_0 ? kQ8 : -1)) != w->m.fmt) {
+        set_error("matmul: format/variant mismatch or mixed formats");
+        return YL_ERR_FORMAT;
+    }
+    if (gs != 32) { set_error("group size must be 32 (GGUF blocks)"); return YL_ERR_UNSUPPORTED; }
+    if ((int)n != w->m.n || (int)o != w->m.o) { set_error("yl_matmul: n/o do not match the weight"); return YL_ERR_ARG; }
+    if (batch == 0) return YL_OK;
+    if (batch > 65535) { set_error("yl_matmul: batch > 65535"); return YL_ERR_ARG; }
+    GemvArgs a{};
+    a.qs = w->m.qs; a.d = w->m.d; a.n = w->m.n; a.o = w->m.o; a.nb = w->m.nb;
+    a.xq = xq; a.xs = xs; a.out = out; a.accumulate_cols = (int)(o / 4 * 4);
+    const hipError_t e = launch_gemv(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "matmul launch");
+}
+
+yl_status yl_rmsnorm_quantize(const float* x, const float* weight, size_t size, float eps, size_t batch, float* xn,
+                              int32_t qfmt, int8_t* q, float* scale, void* stream) {
+    if (!x || !weight || !size || size > 16384) { set_error("rmsnorm: bad arguments (size <= 16384)"); return YL_ERR_ARG; }
+    if (qfmt >= 0 && (size % 32 || !q || !scale || qfmt > 1)) { set_error("rmsnorm: quantized output needs size % 32 == 0"); return YL_ERR_ARG; }
+    if (batch == 0) return YL_OK;
+    const hipError_t e = launch_rmsnorm(qfmt, x, weight, (int)size, eps, (int)batch, xn, q, scale, (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "rmsnorm launch");
+}
+
+yl_status yl_rope_gguf(const yl_rope_params* p, float* q, float* k, size_t batch, uint32_t start_pos, void* stream) {
+    if (!p || !q || !k || p->head_size % 2 || !p->head_size) { set_error("rope: bad arguments"); return YL_ERR_ARG; }
+    if (batch == 0) return YL_OK;
+    const size_t half = p->head_size / 2;
+    std::vector<float> c(batch * half), s(batch * half);
+    rope_table(*p, start_pos, (uint32_t)batch, c.data(), s.data());
+    float *dc = nullptr, *ds = nullptr;
+    StepState* dst = nullptr;
+    StepState hst{};
+    hst.pos = 0;
+    hipStream_t strm = (hipStream_t)stream;
+    hipError_t e = hipMalloc(&dc, c.size() * 4);
+    if (e == hipSuccess) e = hipMalloc(&ds, s.size() * 4);
+    if (e == hipSuccess) e = hipMalloc(&dst, sizeof(StepState));
+    if (e == hipSuccess) e = hipMemcpy(dc, c.data(), c.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(ds, s.data(), s.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_rope(dc, ds, dst, (int)batch, q, k, p->n_heads, p->n_kv_heads, p->head_size, strm);
+    if (e == hipSuccess) e = hipStreamSynchronize(strm);
+    if (dc) hipFree(dc);
+    if (ds) hipFree(ds);
+    if (dst) hipFree(dst);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "rope");
+}
+
+yl_status yl_attention(float* out, const float* q, const float* kc, const float* vc, size_t batch, uint32_t start_pos,
+                       uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, float attn_scale, void* stream) {
+    if (!out || !q || !kc || !vc || !n_heads || !n_kv_heads || n_heads % n_kv_heads || hd % 8 || !hd) {
+        set_error("attention: bad arguments");
+        return YL_ERR_ARG;
+    }
+    if (batch == 0) return YL_OK;
+    const size_t seq = start_pos + batch;
+    if (seq * 4 + (size_t)hd * 40 > 60 * 1024) { set_error("attention: seq_len too long for one workgroup"); return YL_ERR_UNSUPPORTED; }
+    StepState* dst = nullptr;
+    StepState hst{};
+    hst.pos = (int32_t)start_pos;
+    hipStream_t strm = (hipStream_t)stream;
+    hipError_t e = hipMalloc(&dst, sizeof(StepState));
+    if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_attention(q, kc, vc, dst, (int)batch, (int)seq, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale,
+                             -1, nullptr, nullptr, out, strm);
+    if (e == hipSuccess) e = hipStreamSynchronize(strm);
+    if (dst) hipFree(dst);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "attention");
+}
+
+yl_status yl_swiglu_quantize(const float* gate, const float* up, size_t hidden, size_t batch, float* h, int32_t qfmt,
+                             int8_t* q, float* scale, void* stream) {
+    if (!gate || !up || !hidden) { set_error("swiglu: bad arguments"); return YL_ERR_ARG; }
+    if (qfmt >= 0 && (hidden % 32 || !q || !scale || qfmt > 1)) { set_error("swiglu: quantized output needs hidden % 32 == 0"); return YL_ERR_ARG; }
+    if (batch == 0) return YL_OK;
+    const hipError_t e = launch_swiglu_quant(qfmt, gate, up, (int)hidden, (int)batch, h, q, scale, (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "swiglu launch");
+}
+
+yl_status yl_math_selftest(const float* x, size_t n, float* exp_out, float* sqrt_out, float* recip_out, float* f16_out) {
+    if (!n) return YL_OK;
+    hipError_t e = launch_math_selftest(x, (int)n, exp_out, sqrt_out, recip_out, f16_out, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    return e == hipSuccess ? YL_OK : hip_fail(e, "math selftest");
+}
+
+// ---------------------------------------------------------------- model
+
+yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) {
+    if (!path) { set_error("null path"); return nullptr; }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) { set_error("no HIP device"); return nullptr; }
+    yl_status st;
+    return load_model(path, max_ctx_len, fmt_override, &st);
+}
+
+void yl_model_free(yl_model* m) { model_release(m); }
+const char* yl_model_name(const yl_model* m) { return m ? m->name.c_str() : ""; }
+yl_status yl_model_shape(const yl_model* m, yl_shape* out) {
+    if (!m || !out) return YL_ERR_ARG;
+    *out = m->shape;
+    return YL_OK;
+}
+size_t yl_vocab_size(const yl_model* m) { return m ? (size_t)m->vocab : 0; }
+uint32_t yl_max_ctx_len(const yl_model* m) { return m ? (uint32_t)m->ctx : 2048; }
+uint32_t yl_bos_token(const yl_model* m) { return m ? m->bos : 0; }
+uint32_t yl_eos_token(const yl_model* m) { return m ? m->eos : 0; }
+size_t yl_model_weight_bytes(const yl_model* m) { return m ? m->weight_bytes : 0; }
+size_t yl_model_embedding_bytes(const yl_model* m) { return m ? m->emb_bytes : 0; }
+
+yl_status yl_get_embeddings(const yl_model* m, const uint32_t* tokens, size_t n, float* out) {
+    if (!m || (!tokens && n) || (!out && n)) return YL_ERR_ARG;
+    if (!n) return YL_OK;
+    float *x = nullptr;
+    int8_t* q = nullptr;
+    float* s = nullptr;
+    uint32_t* t = nullptr;
+    hipError_t e = hipMalloc(&x, n * m->dim * 4);
+    if (e == hipSuccess) e = hipMalloc(&q, n * m->dim);
+    if (e == hipSuccess) e = hipMalloc(&s, n * m->dim / 8 + 4);
+    if (e == hipSuccess) e = hipMalloc(&t, n * 4);
+    if (e == hipSuccess) e = hipMemcpy(t, tokens, n * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_embed_norm(m->emb, t, (int)n, x, m->layers[0].rms_att, m->eps, kQ8, nullptr, q, s, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, x, n * m->dim * 4, hipMemcpyDeviceToHost);
+    if (x) hipFree(x);
+    if (q) hipFree(q);
+    if (s) hipFree(s);
+    if (t) hipFree(t);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "get_embeddings");
+}
+
+yl_session* yl_create_session(const yl_model* m) {
+    if (!m) { set_error("null model"); return nullptr; }
+    auto* s = new yl_session();
+    s->m = m;
+    s->kv_floats = (size_t)m->n_layers * m->ctx * m->kv;
+    s->ring_cap = (uint32_t)m->ctx;
+    bool ok = hipStreamCreate(&s->stream) == hipSuccess &&
+              hipMalloc(&s->kc, s->kv_floats * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->vc, s->kv_floats * 4 + 256) == hipSuccess &&
+              hipMemset(s->kc, 0, s->kv_floats * 4) == hipSuccess &&
+              hipMemset(s->vc, 0, s->kv_floats * 4) == hipSuccess &&
+              hipMalloc(&s->st, sizeof(StepState)) == hipSuccess &&
+              hipMemset(s->st, 0, sizeof(StepState)) == hipSuccess &&
+              hipHostMalloc(&s->st_host, sizeof(StepState), 0) == hipSuccess &&
+              hipMalloc(&s->logits, (size_t)m->vocab * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess && session_grow(s, 1);
+    if (!ok) {
+        if (yl_last_error()[0] == 0) set_error("session allocation failed");
+        yl_session_free(s);
+        return nullptr;
+    }
+    return s;
+}
+
+void yl_session_free(yl_session* s) {
+    if (!s) return;
+    if (s->stream) hipStreamSynchronize(s->stream);
+    if (s->graph) hipGraphExecDestroy(s->graph);
+    void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->xn, s->sq, s->xq, s->aq, s->hq,
+                   s->xs, s->as_, s->hs, s->counters, s->tokens};
+    for (void* p : dev) if (p) hipFree(p);
+    if (s->st_host) hipHostFree(s->st_host);
+    if (s->stream) hipStreamDestroy(s->stream);
+    delete s;
+}
+
+yl_status yl_session_reset(yl_session* s) {
+    if (!s) return YL_ERR_ARG;
+    hipError_t e = hipMemsetAsync(s->kc, 0, s->kv_floats * 4, s->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, s->kv_floats * 4, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    s->pos = 0;
+    return e == hipSuccess ? YL_OK : hip_fail(e, "session reset");
+}
+
+uint32_t yl_session_pos(const yl_session* s) { return s ? s->pos : 0; }
+void yl_session_set_pos(yl_session* s, uint32_t pos) { if (s) s->pos = pos; }
+
+yl_status yl_session_kv(yl_session* s, float** k, float** v, size_t* floats) {
+    if (!s) return YL_ERR_ARG;
+    if (k) *k = s->kc;
+    if (v) *v = s->vc;
+    if (floats) *floats = s->kv_floats;
+    return YL_OK;
+}
+
+yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint32_t start_pos, yl_session* s,
+                       float* logits, uint32_t* argmax) {
+    if (!m || !s || s->m != m || !tokens) { set_error("forward_x: null model/session/tokens"); return YL_ERR_ARG; }
+    if (n == 0) { set_error("forward_x: empty token batch"); return YL_ERR_ARG; }
+    if ((uint64_t)start_pos + n > (uint64_t)m->ctx) {
+        set_error("forward_x: positions beyond ctx_len " + std::to_string(m->ctx));
+        return YL_ERR_RANGE;
+    }
+    if (n > 65535) { set_error("forward_x: more than 65535 tokens in one call"); return YL_ERR_ARG; }
+    yl_status rs = put_state(s, (int32_t)start_pos, tokens[0]);
+    if (rs != YL_OK) return rs;
+    hipError_t e;
+    if (n == 1) {
+        if (!ensure_graph(m, s)) return YL_ERR_HIP;
+        e = hipGraphLaunch(s->graph, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    } else {
+        if (!session_grow(s, (int)n)) return YL_ERR_NOMEM;
+        e = hipMemcpyAsync(s->tokens, tokens, n * 4, hipMemcpyHostToDevice, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "token upload");
+        e = enqueue_forward(m, s, (int)n, s->tokens, 0, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "forward launch");
+    }
+    if (logits) {
+        e = hipMemcpyAsync(logits, s->logits, (size_t)m->vocab * 4, hipMemcpyDeviceToHost, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "logits download");
+    }
+    e = hipMemcpyAsync(s->st_host, s->st, sizeof(StepState), hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "forward_x");
+    if (argmax) *argmax = s->st_host->token;
+    return YL_OK;
+}
+
+yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, uint32_t n_steps,
+                             uint32_t* out_tokens) {
+    if (!m || !s || s->m != m) { set_error("generate: null model/session"); return YL_ERR_ARG; }
+    if (n_steps == 0) return YL_OK;
+    if ((uint64_t)start_pos + n_steps > (uint64_t)m->ctx) {
+        set_error("generate: positions beyond ctx_len " + std::to_string(m->ctx));
+        return YL_ERR_RANGE;
+    }
+    yl_status rs = put_state(s, (int32_t)start_pos, token);
+    if (rs != YL_OK) return rs;
+    if (!ensure_graph(m, s)) return YL_ERR_HIP;
+    for (uint32_t i = 0; i < n_steps; i++) {
+        const hipError_t e = hipGraphLaunch(s->graph, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    }
+    hipError_t e = hipSuccess;
+    if (out_tokens) e = hipMemcpyAsync(out_tokens, s->ring, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "generate");
+}
+
+yl_status yl_profile_decode(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, uint32_t n_steps,
+                            int32_t kernel_class, double* ms, uint64_t* launches, uint64_t* bytes) {
+    if (!m || !s || s->m != m || kernel_class < 0 || kernel_class > 2) { set_error("profile: bad arguments"); return YL_ERR_ARG; }
+    if ((uint64_t)start_pos + n_steps > (uint64_t)m->ctx) { set_error("profile: positions beyond ctx_len"); return YL_ERR_RANGE; }
+    yl_status rs = put_state(s, (int32_t)start_pos, token);
+    if (rs != YL_OK) return rs;
+    Prof prof;
+    prof.cls = kernel_class;
+    prof.stream = s->stream;
+    for (uint32_t i = 0; i < n_steps; i++) {
+        const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1, &prof);
+        if (e != hipSuccess) return hip_fail(e, "profile step");
+        prof.collect();
+    }
+    const hipError_t e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "profile");
+    if (ms) *ms = prof.ms;
+    if (launches) *launches = prof.launches;
+    if (bytes) *bytes = prof.bytes;
+    return YL_OK;
+}
+
+// ------------------------------------------------------- product FFI
+
+static std::mutex g_ffi_mu;
+static yl_model* g_current = nullptr;
+
+bool load_transformer_ffi(const char* model_path) {
+    if (!model_path) return false;
+    const std::string p(model_path);
+    const size_t dot = p.rfind('.');
+    const std::string ext = dot == std::string::npos ? "" : p.substr(dot + 1);
+    if (ext != "gguf") {
+        set_error(ext == "lmrs" || ext == "safetensors"
+                      ? "Unsupported model extension here: ." + ext + " loaders are not built (GGUF is)"
+                      : "Unsupported model extension for path: " + p);
+        return false;
+    }
+    yl_model* m = yl_load(model_path, 0xFFFFFFFFu, -1);
+    if (!m) return false;
+    std::lock_guard<std::mutex> lk(g_ffi_mu);
+    if (g_current) model_release(g_current);
+    g_current = m;
+    return true;
+}
+
+char* infer_ffi(const char* prompt) {
+    std::lock_guard<std::mutex> lk(g_ffi_mu);
+    if (!prompt || !g_current) { set_error("infer_ffi: no prompt or no model loaded"); return nullptr; }
+    set_error("infer_ffi: text generation needs the tokenizer, which is not built yet");
+    return nullptr;
+}
+
+void free_string(char* s) { free(s); }
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+"""Seeded synthetic GGUF llama models of the benchmark shapes.
+
+    python -m yallma3_mini_inference_amd.synth llama32_1b /tmp/l1.gguf
+
+Weights ~N(0, 0.02), RMSNorm weights 1.0, placeholder vocabulary strings;
+written by the library's host-side generator (yl_write_synthetic_gguf), so
+the same (config, seed) gives the same bytes on every machine.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+import sys
+
+from ._lib import SynthConfig, check, lib
+from .weight_type import WeightFormat
+
+Q8, Q4 = WeightFormat.Q8_0, WeightFormat.Q4_0
+
+
+@dataclasses.dataclass(frozen=True)
+class ModelConfig:
+    dim: int
+    hidden: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    vocab: int
+    ctx_len: int
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-5
+    weight_std: float = 0.02
+    attn_format: int = Q8
+    ffn_format: int = Q8
+    embd_format: int = Q8
+    file_type: int = 7
+    seed: int = 0
+
+    def to_c(self) -> SynthConfig:
+        return SynthConfig(self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.vocab,
+                           self.ctx_len, self.rope_theta, self.rms_eps, self.weight_std, int(self.attn_format),
+                           int(self.ffn_format), int(self.embd_format), self.file_type, self.seed)
+
+
+CONFIGS = {
+    # small shapes the CPU oracle finishes in seconds
+    "tiny": ModelConfig(128, 256, 2, 4, 2, 512, 256),
+    "tiny_q4": ModelConfig(128, 256, 2, 4, 2, 512, 256, attn_format=Q4, ffn_format=Q4, file_type=2),
+    "tiny_mixed": ModelConfig(128, 384, 3, 4, 1, 1000, 300, rope_theta=500000.0, ffn_format=Q4),
+    # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
+    "smollm2_135m": ModelConfig(576, 1536, 30, 9, 3, 49152, 2048),
+    # Llama-3.2-1B shape: dim 2048, FFN 8192, 16 layers, 32/8 heads, vocab 128256
+    "llama32_1b": ModelConfig(2048, 8192, 16, 32, 8, 128256, 4096, rope_theta=500000.0),
+    "llama32_1b_q4": ModelConfig(2048, 8192, 16, 32, 8, 128256, 4096, rope_theta=500000.0, attn_format=Q4,
+                                 ffn_format=Q4, file_type=2),
+    # Llama-3-8B shape, Q4_0 FFN beside Q8_0 attention, context for 8192 + 256 tokens
+    "llama3_8b_mixed": ModelConfig(4096, 14336, 32, 32, 8, 128256, 8448, rope_theta=500000.0, ffn_format=Q4),
+}
+
+
+def write(path: str, cfg: ModelConfig) -> str:
+    c = cfg.to_c()
+    check(lib().yl_write_synthetic_gguf(os.fsencode(path), C.byref(c)))
+    return path
+
+
+def model_dir() -> str:
+    d = os.environ.get("YL_MODEL_DIR", os.path.join(os.environ.get("TMPDIR", "/tmp"), "yallma3_models"))
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def ensure(name: str, directory: str | None = None) -> str:
+    """Path of the named synthetic model, written on first use."""
+    cfg = CONFIGS[name]
+    path = os.path.join(directory or model_dir(), f"{name}_seed{cfg.seed}.gguf")
+    if not os.path.exists(path):
+        tmp = path + f".tmp{os.getpid()}"
+        write(tmp, cfg)
+        os.replace(tmp, path)
+    return path
+
+
+if __name__ == "__main__":
+    if len(sys.argv) != 3 or sys.argv[1] not in CONFIGS:
+        print(f"usage: python -m yallma3_mini_inference_amd.synth <{'|'.join(CONFIGS)}> <out.gguf>")
+        sys.exit(2)
+    write(sys.argv[2], CONFIGS[sys.argv[1]])

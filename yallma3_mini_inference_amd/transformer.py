@@ -1,0 +1,197 @@
+"""The Transformer trait and InferenceSession over the HIP forward path.
+
+Python mirror of the reference's model API:
+  load_transformer(path, ...)     lib.rs:107-133 (".gguf" models)
+  Transformer                     trait Transformer, transformer.rs:19-69,
+                                  implemented as TransformerLlamaGguf
+                                  (transformer_llama_gguf.rs:658-729)
+  InferenceSession                base_transformer.rs:81-105 (KV cache on
+                                  the device; `pos` kept for the caller)
+  load_transformer_ffi / infer_ffi
+                                  lib.rs:135-152, README.md:81-92
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from ._lib import Shape, YlError, check, last_error, lib
+from .weight_type import WeightFormat
+
+
+class InferenceSession:
+    """Per-conversation state: device KV cache [n_layers][ctx_len][kv_dim] and `pos`."""
+
+    def __init__(self, model: "Transformer"):
+        self.model = model
+        self._h = lib().yl_create_session(model._h)
+        if not self._h:
+            raise YlError(-5, last_error())
+
+    @property
+    def pos(self) -> int:
+        return int(lib().yl_session_pos(self._h))
+
+    @pos.setter
+    def pos(self, value: int) -> None:
+        lib().yl_session_set_pos(self._h, int(value))
+
+    def reset(self) -> None:
+        """InferenceSession::reset (base_transformer.rs:100-104)."""
+        check(lib().yl_session_reset(self._h))
+
+    def _kv(self):
+        k, v, n = C.c_void_p(), C.c_void_p(), C.c_size_t()
+        check(lib().yl_session_kv(self._h, C.byref(k), C.byref(v), C.byref(n)))
+        return k.value, v.value, n.value
+
+    def key_cache(self) -> np.ndarray:
+        return self._download(self._kv()[0])
+
+    def value_cache(self) -> np.ndarray:
+        return self._download(self._kv()[1])
+
+    def _download(self, ptr) -> np.ndarray:
+        m = self.model
+        shp = (m.shape.n_layers, m.shape.ctx_len, m.shape.n_kv_heads * m.shape.head_size)
+        out = np.empty(shp, np.float32)
+        check(lib().yl_memcpy_d2h(out.ctypes.data, ptr, out.nbytes))
+        return out
+
+    def upload_kv(self, key: np.ndarray, value: np.ndarray) -> None:
+        """Overwrite the device KV cache (tests and benchmarks pre-fill it)."""
+        kp, vp, n = self._kv()
+        for ptr, a in ((kp, key), (vp, value)):
+            a = np.ascontiguousarray(a, np.float32)
+            if a.size != n:
+                raise ValueError("cache shape mismatch")
+            check(lib().yl_memcpy_h2d(ptr, a.ctypes.data, a.nbytes))
+
+    def close(self) -> None:
+        if self._h:
+            lib().yl_session_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Transformer:
+    """TransformerLlamaGguf on one MI355X."""
+
+    def __init__(self, path: str, max_ctx_len: int = 0xFFFFFFFF, fmt_override: WeightFormat | None = None):
+        ov = -1 if fmt_override is None else int(fmt_override)
+        self._h = lib().yl_load(os.fsencode(path), max_ctx_len, ov)
+        if not self._h:
+            raise YlError(-4, last_error())
+        self.shape = Shape()
+        check(lib().yl_model_shape(self._h, C.byref(self.shape)))
+
+    # trait Transformer, transformer.rs:19-69
+    @classmethod
+    def load_model(cls, model_path: str, max_ctx_len: int) -> "Transformer":
+        return cls(model_path, max_ctx_len)
+
+    def name(self) -> str:
+        return lib().yl_model_name(self._h).decode()
+
+    def vocab_size(self) -> int:
+        return int(lib().yl_vocab_size(self._h))
+
+    def get_embeddings(self, token: int) -> np.ndarray:
+        return self.get_embeddings_batch([token])[0]
+
+    def get_embeddings_batch(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.zeros((t.size, self.shape.dimension), np.float32)
+        check(lib().yl_get_embeddings(self._h, t.ctypes.data, t.size, out.ctypes.data))
+        return out
+
+    def forward_x(self, tokens, start_pos: int, session: InferenceSession) -> np.ndarray:
+        """Logits (vocab f32) of the last token; K/V accumulate into the session cache."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.vocab_size(), np.float32)
+        check(lib().yl_forward_x(self._h, t.ctypes.data, t.size, int(start_pos), session._h, logits.ctypes.data,
+                                 None))
+        return logits
+
+    def forward_argmax(self, tokens, start_pos: int, session: InferenceSession) -> int:
+        """forward_x followed by greedy sampling on the device (no logits copy)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = C.c_uint32(0)
+        check(lib().yl_forward_x(self._h, t.ctypes.data, t.size, int(start_pos), session._h, None, C.byref(out)))
+        return int(out.value)
+
+    def generate_greedy(self, session: InferenceSession, token: int, start_pos: int, n_steps: int) -> np.ndarray:
+        """n_steps single-token forward_x calls chained on the device by argmax."""
+        out = np.zeros(n_steps, np.uint32)
+        check(lib().yl_generate_greedy(self._h, session._h, int(token), int(start_pos), int(n_steps),
+                                       out.ctypes.data))
+        return out
+
+    def profile_decode(self, session: InferenceSession, token: int, start_pos: int, n_steps: int,
+                       kernel_class: int):
+        ms, launches, nbytes = C.c_double(), C.c_uint64(), C.c_uint64()
+        check(lib().yl_profile_decode(self._h, session._h, int(token), int(start_pos), int(n_steps),
+                                      int(kernel_class), C.byref(ms), C.byref(launches), C.byref(nbytes)))
+        return ms.value, launches.value, nbytes.value
+
+    def create_session(self) -> InferenceSession:
+        return InferenceSession(self)
+
+    def max_ctx_len(self) -> int:
+        return int(lib().yl_max_ctx_len(self._h))
+
+    def eos_token(self) -> int:
+        return int(lib().yl_eos_token(self._h))
+
+    def bos_token(self) -> int:
+        return int(lib().yl_bos_token(self._h))
+
+    def weight_bytes(self) -> int:
+        return int(lib().yl_model_weight_bytes(self._h))
+
+    def embedding_bytes(self) -> int:
+        return int(lib().yl_model_embedding_bytes(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib().yl_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+TransformerLlamaGguf = Transformer
+
+
+def load_transformer(model_path: str, sequential: bool = False, max_ctx_len: int = 0xFFFFFFFF,
+                     fmt_override: WeightFormat | None = None) -> Transformer:
+    """lib.rs:107-133.  Only the ".gguf" branch is built; others raise."""
+    ext = os.path.splitext(model_path)[1].lstrip(".")
+    if ext != "gguf":
+        raise YlError(-6, f"Unsupported model extension for path: {model_path} (GGUF is built)")
+    return Transformer(model_path, max_ctx_len, fmt_override)
+
+
+def load_transformer_ffi(model_path: str | None) -> bool:
+    return bool(lib().load_transformer_ffi(None if model_path is None else os.fsencode(model_path)))
+
+
+def infer_ffi(prompt: str) -> str | None:
+    p = lib().infer_ffi(prompt.encode())
+    if not p:
+        return None
+    try:
+        return C.string_at(p).decode(errors="replace")
+    finally:
+        lib().free_string(p)
