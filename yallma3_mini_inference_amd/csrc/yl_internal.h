@@ -12,8 +12,9 @@
 //   Token embedding for the logits pass and the embedding lookup, Q8_0,
 //   interleaved so a wavefront reading 64 consecutive vocabulary rows issues
 //   one contiguous 1 KiB load per 16-element chunk:
-//     eq : int8 [vocab/64][dim/16][64][16]
-//     ed : f16  [vocab/64][dim/32][64]
+//     eq : uint8 [vocab/64][dim/16][64][16], holding u = q + 128 (so the
+//          logits pass widens it with one unsigned-byte conversion)
+//     ed : f16   [vocab/64][dim/32][64]
 //   KV cache: f32 [n_layers][ctx_len][kv_dim] for keys and for values
 //   (InferenceSession, base_transformer.rs:81-98).
 #pragma once
@@ -56,14 +57,18 @@ struct StepState {
 enum Epi : int {
     kEpiStore = 0,    // out[r] = (accumulate ? out[r] : 0) + sum of block terms
     kEpiQkvRope = 1,  // rows [q | k | v]: q stored, k/v accumulate into the cache, RoPE on q,k
-    kEpiResid = 2,    // x[r] += sum; the last workgroup then runs RMSNorm (+quantize)
+                      // (prologue: RMSNorm + quantize of the residual stream)
+    kEpiResid = 2,    // x[r] += sum (residual add)
     kEpiSwiglu = 3,   // 64-row groups [32 gate | 32 up] -> SwiGLU -> quantize one 32-block
 };
 
 struct GemvArgs {
     // weights and activations
     const uint8_t* qs; const uint16_t* d; int n, o, nb;
-    const int8_t* xq; const float* xs;        // [batch][n], [batch][nb]
+    const int8_t* xq; const float* xs;        // [batch][n], [batch][nb] (staged prologue)
+    // kEpiQkvRope / kEpiSwiglu prologue: RMSNorm + quantize of x [batch][n]
+    float* x; const float* norm_w; float eps;
+    EmbQ8 emb; const uint32_t* tokens;         // emb.q set: x starts as the tokens' embedding rows
     // kEpiStore
     float* out; int accumulate_cols;           // columns < accumulate_cols start from out[]
     // kEpiQkvRope
@@ -71,35 +76,36 @@ struct GemvArgs {
     int att_dim, kv_dim, head_size;
     const float* rope_cos; const float* rope_sin;  // [ctx][head_size/2]
     const StepState* state;
-    // kEpiResid
-    float* x; const float* norm_w; float eps; int dim;
-    int norm_fmt;                              // -1: f32 normalized output only
-    int8_t* nq; float* ns; float* xn;          // quantized / f32 normalized outputs
-    unsigned int* counters;                    // one per batch row, zero between uses
     // kEpiSwiglu
     int8_t* hq; float* hs; float* h_f32; int hidden; int h_fmt;
 };
 
-// kernel launchers (yl_kernels.hip); all return hipError_t of the launch
+// kernel launchers; all return the hipError_t of the launch
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s);
 hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, float eps, int batch,
                           float* xn, int8_t* xq, float* xs, hipStream_t s);
-hipError_t launch_embed_norm(const EmbQ8& e, const uint32_t* tokens, int batch, float* x,
-                             const float* w, float eps, int qfmt, float* xn, int8_t* xq, float* xs,
-                             hipStream_t s);
+hipError_t launch_embed(const EmbQ8& e, const uint32_t* tokens, int batch, float* x, hipStream_t s);
 hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st,
                             int batch, int max_seq, int n_heads, int n_kv_heads, int head_size,
                             float scale, int qfmt, int8_t* aq, float* as, float* att_f32,
                             hipStream_t s);
+int attn_decode_splits(int max_seq);
+size_t attn_decode_lds_bytes(int max_seq, int hd);
+hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st,
+                              int max_seq, int n_heads, int n_kv_heads, int head_size, float scale,
+                              int qfmt, float* scores, unsigned* counters, int8_t* aq, float* as,
+                              float* att_f32, hipStream_t s);
 hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,
                        float* q, float* k, int n_heads, int n_kv_heads, int head_size, hipStream_t s);
 hipError_t launch_swiglu_quant(int qfmt, const float* gate, const float* up, int hidden, int batch,
                                float* h_f32, int8_t* hq, float* hs, hipStream_t s);
-hipError_t launch_logits(const EmbQ8& e, const float* xn, float* logits, unsigned long long* key,
+size_t logits_lds_bytes(int dim);
+int logits_blocks(const EmbQ8& e);
+// logits pass (keys: logits_blocks() per-workgroup argmax keys) + finalize
+hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, float eps, float* logits,
+                         unsigned long long* keys, StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
                          hipStream_t s);
-hipError_t launch_finalize(StepState* st, uint32_t* out_tokens, uint32_t out_cap, int advance,
-                           hipStream_t s);
 hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
                                 float* div_out, float* f16_out, hipStream_t s);
 

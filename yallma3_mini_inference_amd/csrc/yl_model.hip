@@ -271,10 +271,12 @@ struct yl_session {
     StepState* st = nullptr;        // device
     StepState* st_host = nullptr;   // pinned
     int cap_b = 0;
-    float *x = nullptr, *xn = nullptr, *sq = nullptr, *logits = nullptr;
-    int8_t *xq = nullptr, *aq = nullptr, *hq = nullptr;
-    float *xs = nullptr, *as_ = nullptr, *hs = nullptr;
-    unsigned* counters = nullptr;
+    float *x = nullptr, *sq = nullptr, *logits = nullptr;
+    int8_t *aq = nullptr, *hq = nullptr;
+    float *as_ = nullptr, *hs = nullptr;
+    float* scores = nullptr;        // [n_heads][ctx] attention score rows (decode)
+    unsigned* counters = nullptr;   // [n_heads] finished attention splits per head
+    unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
     uint32_t ring_cap = 0;
@@ -338,7 +340,8 @@ bool upload_embedding(const GgufTensor* t, int dim, int vocab, EmbQ8* e, std::st
             d[(tile * nbE + b) * 64 + lane] = sc;
             for (int h = 0; h < 2; h++) {
                 const size_t k16 = (size_t)2 * b + h;
-                memcpy(&q[((tile * k16n + k16) * 64 + lane) * 16], vals + 16 * h, 16);
+                int8_t* dst = &q[((tile * k16n + k16) * 64 + lane) * 16];
+                for (int j = 0; j < 16; j++) dst[j] = (int8_t)((uint8_t)vals[16 * h + j] ^ 0x80u);  // u = q + 128
             }
         }
     }
@@ -417,8 +420,10 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     m->kv = m->n_kv * m->hd;
     m->attn_scale = att_scale_meta != 0.0f ? att_scale_meta : 1.0f / sqrtf((float)m->hd);
     if (m->n_kv <= 0 || m->n_heads % m->n_kv) { set_error("n_heads must be a multiple of n_kv_heads"); return nullptr; }
-    if (m->dim % 32 || m->hidden % 32 || m->kv % 32 || m->hd % 32 || m->dim > 16384 || m->ctx <= 0) {
-        set_error("unsupported shape: dim, hidden, kv_dim and head_size must be multiples of 32, dim <= 16384");
+    if (m->dim % 32 || m->hidden % 32 || m->kv % 32 || (m->hd != 32 && m->hd != 64 && m->hd != 128) ||
+        m->dim > 8192 || m->ctx <= 0) {
+        set_error("unsupported shape: dim, hidden and kv_dim must be multiples of 32, head_size 32/64/128, "
+                  "dim <= 8192");
         *st = YL_ERR_UNSUPPORTED;
         return nullptr;
     }
@@ -505,22 +510,16 @@ bool session_grow(yl_session* s, int batch) {
     hipStreamSynchronize(s->stream);
     if (s->graph) { hipGraphExecDestroy(s->graph); s->graph = nullptr; }
     auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
-    rel(s->x); rel(s->xn); rel(s->sq); rel(s->xq); rel(s->aq); rel(s->hq); rel(s->xs); rel(s->as_); rel(s->hs);
-    rel(s->counters); rel(s->tokens);
+    rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens);
     const size_t B = (size_t)batch;
     bool ok = hipMalloc(&s->x, B * m->dim * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->xn, B * m->dim * 4 + 256) == hipSuccess &&
               hipMalloc(&s->sq, B * m->att * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->xq, B * m->dim + 256) == hipSuccess &&
               hipMalloc(&s->aq, B * m->att + 256) == hipSuccess &&
               hipMalloc(&s->hq, B * m->hidden + 256) == hipSuccess &&
-              hipMalloc(&s->xs, B * m->dim / 8 + 256) == hipSuccess &&
               hipMalloc(&s->as_, B * m->att / 8 + 256) == hipSuccess &&
               hipMalloc(&s->hs, B * m->hidden / 8 + 256) == hipSuccess &&
-              hipMalloc(&s->counters, B * 4 + 256) == hipSuccess &&
               hipMalloc(&s->tokens, B * 4 + 256) == hipSuccess;
     if (!ok) { set_error("hipMalloc failed for session buffers"); s->cap_b = 0; return false; }
-    if (hipMemset(s->counters, 0, B * 4 + 256) != hipSuccess) { set_error("hipMemset failed"); return false; }
     s->cap_b = batch;
     return true;
 }
@@ -572,17 +571,16 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
     hipStream_t st = s->stream;
     hipError_t e;
 #define YL_TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
-    const Layer& L0 = m->layers[0];
-    YL_TRY(launch_embed_norm(m->emb, tok, batch, s->x, L0.rms_att, m->eps, L0.qkv.fmt, nullptr, s->xq, s->xs, st));
     const size_t lay_kv = (size_t)m->ctx * m->kv;
     for (int l = 0; l < m->n_layers; l++) {
         const Layer& L = m->layers[l];
-        const bool last = l + 1 == m->n_layers;
         float* kc = s->kc + (size_t)l * lay_kv;
         float* vc = s->vc + (size_t)l * lay_kv;
+        // RMSNorm + quantize (prologue) -> Q,K,V -> K/V += into the cache -> RoPE
         GemvArgs a{};
         a.qs = L.qkv.qs; a.d = L.qkv.d; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
-        a.xq = s->xq; a.xs = s->xs;
+        a.x = s->x; a.norm_w = L.rms_att; a.eps = m->eps;
+        if (l == 0) { a.emb = m->emb; a.tokens = tok; }
         a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
         a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd;
         a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
@@ -590,46 +588,46 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
         YL_TRY(launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st));
         if (prof) prof->end(0, gemv_bytes(L.qkv, L.qkv.o, batch));
 
+        // attention (+ quantize of its output)
         if (prof) prof->begin(1);
-        YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->n_heads, m->n_kv, m->hd, m->attn_scale,
-                                L.wo.fmt, s->aq, s->as_, nullptr, st));
+        if (batch == 1)
+            YL_TRY(launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->n_heads, m->n_kv, m->hd, m->attn_scale,
+                                      L.wo.fmt, s->scores, s->counters, s->aq, s->as_, nullptr, st));
+        else
+            YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->n_heads, m->n_kv, m->hd,
+                                    m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st));
         if (prof) prof->end(1, 0);
 
+        // WO -> residual add
         GemvArgs b{};
         b.qs = L.wo.qs; b.d = L.wo.d; b.n = L.wo.n; b.o = L.wo.o; b.nb = L.wo.nb;
-        b.xq = s->aq; b.xs = s->as_;
-        b.x = s->x; b.norm_w = L.rms_ffn; b.eps = m->eps; b.dim = m->dim; b.norm_fmt = L.w13.fmt;
-        b.nq = s->xq; b.ns = s->xs; b.xn = nullptr; b.counters = s->counters;
+        b.xq = s->aq; b.xs = s->as_; b.x = s->x;
         if (prof) prof->begin(0);
         YL_TRY(launch_gemv(b, L.wo.fmt, kEpiResid, batch, st));
         if (prof) prof->end(0, gemv_bytes(L.wo, L.wo.o, batch));
 
+        // RMSNorm + quantize (prologue) -> W1, W3 -> SwiGLU -> quantize
         GemvArgs c{};
         c.qs = L.w13.qs; c.d = L.w13.d; c.n = L.w13.n; c.o = L.w13.o; c.nb = L.w13.nb;
-        c.xq = s->xq; c.xs = s->xs;
+        c.x = s->x; c.norm_w = L.rms_ffn; c.eps = m->eps;
         c.hq = s->hq; c.hs = s->hs; c.h_f32 = nullptr; c.hidden = m->hidden; c.h_fmt = L.w2.fmt;
         if (prof) prof->begin(0);
         YL_TRY(launch_gemv(c, L.w13.fmt, kEpiSwiglu, batch, st));
         if (prof) prof->end(0, gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch));
 
+        // W2 -> residual add
         GemvArgs d{};
         d.qs = L.w2.qs; d.d = L.w2.d; d.n = L.w2.n; d.o = L.w2.o; d.nb = L.w2.nb;
-        d.xq = s->hq; d.xs = s->hs;
-        d.x = s->x; d.eps = m->eps; d.dim = m->dim; d.counters = s->counters;
-        if (!last) {
-            d.norm_w = m->layers[l + 1].rms_att; d.norm_fmt = m->layers[l + 1].qkv.fmt;
-            d.nq = s->xq; d.ns = s->xs; d.xn = nullptr;
-        } else {
-            d.norm_w = m->rms_final; d.norm_fmt = -1; d.xn = s->xn;
-        }
+        d.xq = s->hq; d.xs = s->hs; d.x = s->x;
         if (prof) prof->begin(0);
         YL_TRY(launch_gemv(d, L.w2.fmt, kEpiResid, batch, st));
         if (prof) prof->end(0, gemv_bytes(L.w2, L.w2.o, batch));
     }
+    // final RMSNorm + logits of the last token + argmax + step bookkeeping
     if (prof) prof->begin(2);
-    YL_TRY(launch_logits(m->emb, s->xn + (size_t)(batch - 1) * m->dim, s->logits, &s->st->argmax, st));
-    if (prof) prof->end(2, (uint64_t)m->emb_bytes + (uint64_t)m->dim * 4 + (uint64_t)m->vocab * 4);
-    YL_TRY(launch_finalize(s->st, s->ring, s->ring_cap, advance, st));
+    YL_TRY(launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->keys,
+                         s->st, s->ring, s->ring_cap, advance, st));
+    if (prof) prof->end(2, (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4);
 #undef YL_TRY
     return hipSuccess;
 }
@@ -796,7 +794,7 @@ yl_status yl_matmul(float* out, yl_format fmt, const int8_t* xq, const float* xs
 
 yl_status yl_rmsnorm_quantize(const float* x, const float* weight, size_t size, float eps, size_t batch, float* xn,
                               int32_t qfmt, int8_t* q, float* scale, void* stream) {
-    if (!x || !weight || !size || size > 16384) { set_error("rmsnorm: bad arguments (size <= 16384)"); return YL_ERR_ARG; }
+    if (!x || !weight || !size || size > 8192) { set_error("rmsnorm: bad arguments (size <= 8192)"); return YL_ERR_ARG; }
     if (qfmt >= 0 && (size % 32 || !q || !scale || qfmt > 1)) { set_error("rmsnorm: quantized output needs size % 32 == 0"); return YL_ERR_ARG; }
     if (batch == 0) return YL_OK;
     const hipError_t e = launch_rmsnorm(qfmt, x, weight, (int)size, eps, (int)batch, xn, q, scale, (hipStream_t)stream);
@@ -894,21 +892,14 @@ size_t yl_model_embedding_bytes(const yl_model* m) { return m ? m->emb_bytes : 0
 yl_status yl_get_embeddings(const yl_model* m, const uint32_t* tokens, size_t n, float* out) {
     if (!m || (!tokens && n) || (!out && n)) return YL_ERR_ARG;
     if (!n) return YL_OK;
-    float *x = nullptr;
-    int8_t* q = nullptr;
-    float* s = nullptr;
+    float* x = nullptr;
     uint32_t* t = nullptr;
     hipError_t e = hipMalloc(&x, n * m->dim * 4);
-    if (e == hipSuccess) e = hipMalloc(&q, n * m->dim);
-    if (e == hipSuccess) e = hipMalloc(&s, n * m->dim / 8 + 4);
     if (e == hipSuccess) e = hipMalloc(&t, n * 4);
     if (e == hipSuccess) e = hipMemcpy(t, tokens, n * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = launch_embed_norm(m->emb, t, (int)n, x, m->layers[0].rms_att, m->eps, kQ8, nullptr, q, s, nullptr);
+    if (e == hipSuccess) e = launch_embed(m->emb, t, (int)n, x, nullptr);
     if (e == hipSuccess) e = hipMemcpy(out, x, n * m->dim * 4, hipMemcpyDeviceToHost);
     if (x) hipFree(x);
-    if (q) hipFree(q);
-    if (s) hipFree(s);
     if (t) hipFree(t);
     return e == hipSuccess ? YL_OK : hip_fail(e, "get_embeddings");
 }
@@ -928,7 +919,11 @@ yl_session* yl_create_session(const yl_model* m) {
               hipMemset(s->st, 0, sizeof(StepState)) == hipSuccess &&
               hipHostMalloc(&s->st_host, sizeof(StepState), 0) == hipSuccess &&
               hipMalloc(&s->logits, (size_t)m->vocab * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess && session_grow(s, 1);
+              hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->scores, (size_t)m->n_heads * m->ctx * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->counters, (size_t)m->n_heads * 4 + 256) == hipSuccess &&
+              hipMemset(s->counters, 0, (size_t)m->n_heads * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->keys, (size_t)logits_blocks(m->emb) * 8 + 256) == hipSuccess && session_grow(s, 1);
     if (!ok) {
         if (yl_last_error()[0] == 0) set_error("session allocation failed");
         yl_session_free(s);
@@ -941,8 +936,8 @@ void yl_session_free(yl_session* s) {
     if (!s) return;
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->graph) hipGraphExecDestroy(s->graph);
-    void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->xn, s->sq, s->xq, s->aq, s->hq,
-                   s->xs, s->as_, s->hs, s->counters, s->tokens};
+    void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
+                   s->as_, s->hs, s->scores, s->counters, s->keys, s->tokens};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
