@@ -49,6 +49,53 @@ def test_quantize(gpu, oracle, fmt):
     assert_bits(s, os_)
 
 
+def _near_tie_groups(rng, n_groups, qmax):
+    """Groups whose values sit on or within a few ulps of x/scale = k + 1/2.
+
+    Each group holds its absmax (fixing scale = absmax/qmax) and 31 values
+    built from (k + 0.5) * scale, nudged by -3..3 ulps, so both rounding
+    directions of the reference's quotient are exercised."""
+    out = []
+    for _ in range(n_groups):
+        am = np.float32(rng.uniform(0.05, 900.0))
+        sc = np.float32(am / np.float32(qmax))
+        k = rng.integers(-qmax, qmax, 31)
+        v = ((k + 0.5) * np.float64(sc)).astype(np.float32)
+        for i, u in enumerate(rng.integers(-3, 4, 31)):
+            for _ in range(abs(int(u))):
+                v[i] = np.nextafter(v[i], np.float32(np.inf if u > 0 else -np.inf))
+        v = np.clip(v, -am, am)
+        out.append(np.concatenate([[am if rng.random() < 0.5 else -am], v]).astype(np.float32))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_quantize_ties(gpu, oracle, fmt):
+    # The GPU quantizer divides only near half-integer quotients; this
+    # drives many values onto and around those boundaries, plus power-of-two
+    # scales (exact ties), subnormal scales, NaN and infinities.
+    from yallma3_mini_inference_amd import WeightFormat, quantize
+    qmax = 127 if fmt == 0 else 7
+    rng = np.random.default_rng(11 + fmt)
+    parts = [_near_tie_groups(rng, 400, qmax)]
+    exact = np.concatenate([[float(qmax)], (np.arange(31) % (2 * qmax) - qmax) + 0.5]).astype(np.float32)
+    parts.append(exact)                                   # scale 1: every quotient an exact tie
+    parts.append(exact * np.float32(2.0 ** -20))          # power-of-two scale
+    parts.append((rng.normal(0, 1, 32) * 1e-41).astype(np.float32))   # subnormal scale
+    nan = rng.normal(0, 1, 32).astype(np.float32)
+    nan[5] = np.nan
+    parts.append(nan)
+    inf = rng.normal(0, 1, 32).astype(np.float32)
+    inf[9] = np.inf
+    parts.append(inf)
+    x = np.concatenate(parts)
+    with np.errstate(invalid="ignore", over="ignore"):
+        q, s = quantize(WeightFormat(fmt), x)
+        oq, os_ = oracle.quantize(fmt, x)
+    np.testing.assert_array_equal(q, oq)
+    assert_bits(s, os_)
+
+
 def test_matmul_reference_kat(gpu):
     # tests/matmul_q8_tests.rs:30-53 through the HIP GEMV
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul

@@ -5,14 +5,6 @@
 
 namespace yl {
 
-// Row stride (floats) of the transposed RMSNorm layout: lane chain j of the
-// f32x8 accumulator reads its elements x[8i+j] contiguously at xt[j*S + i].
-// S is a multiple of 4 (float4 reads) and S % 32 == 4 or 12 or 20 ... so the
-// 8 chain lanes hit distinct LDS banks.
-__host__ __device__ inline int norm_stride(int dim) { return (((dim / 8) + 3) & ~3) + 4; }
-// transposed row 8*S | reduction 16 | norm weights dim
-__host__ __device__ inline size_t norm_lds_floats(int dim) { return (size_t)8 * norm_stride(dim) + 16 + dim; }
-
 // Position of element i inside the activation staging buffer of a Q4_0
 // matmul: each 8-group is stored as its 4 even elements then its 4 odd ones,
 // matching the low/high nibbles of one weight dword.
@@ -21,16 +13,24 @@ __device__ __forceinline__ int q4_pos(int i) {
     return (i & ~7) | ((k & 1) ? 4 + (k >> 1) : (k >> 1));
 }
 
-// RMSNorm of one row (util.rs:389-426) followed by group quantization.
-//   xt  : LDS, norm_lds_floats(dim); the row and the norm weights must
-//         already be stored there by store_norm_input() (transposed row, so
-//         the serial lane chains read float4s without waiting on HBM).
-//   QF  : kQ8 / kQ4 -> q_lds/s_lds receive the quantized row (Q4 reordered
-//         when PERM); QF < 0 -> no quantization.
-//   xn  : optional f32 output of the normalized row (global or LDS).
-// The 8 lane sums run as 8 serial chains (one lane each) over float4 reads;
-// normalization and quantization use every thread, one element per thread,
-// a 32-group per half-wave (absmax by shuffles: order-free max).
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// ---------------------------------------------------------------------------
+// General RMSNorm (+ quantize) of one row of any length, for the standalone
+// rmsnorm entry point (util.rs:389-426: elements past the last whole 8-group
+// are neither summed nor written).
+//
+// Row stride (floats) of the transposed layout: lane chain j of the f32x8
+// accumulator reads its elements x[8i+j] contiguously at xt[j*S + i].  S is a
+// multiple of 4 (float4 reads) and S % 32 == 4, 12, 20 or 28, so the 8 chain
+// lanes hit distinct LDS banks.
+__host__ __device__ inline int norm_stride(int dim) { return (((dim / 8) + 3) & ~3) + 4; }
+// transposed row 8*S | reduction 16 | norm weights dim
+__host__ __device__ inline size_t norm_lds_floats(int dim) { return (size_t)8 * norm_stride(dim) + 16 + dim; }
+
 // Stores element i of the row (v) and of the norm weight (w) for the block.
 __device__ __forceinline__ void store_norm_input(float* xt, int dim, int i, float v, float w) {
     const int n8 = (dim / 8) * 8;
@@ -39,6 +39,13 @@ __device__ __forceinline__ void store_norm_input(float* xt, int dim, int i, floa
     xt[8 * S + 16 + i] = w;
 }
 
+//   xt  : LDS, norm_lds_floats(dim), filled by store_norm_input()
+//   QF  : kQ8 / kQ4 -> q_lds/s_lds receive the quantized row (Q4 reordered
+//         when PERM); QF < 0 -> no quantization.
+//   xn  : optional f32 output of the normalized row (global or LDS).
+// The 8 lane sums run as 8 serial chains (one lane each) over float4 reads;
+// normalization and quantization use one element per thread, a 32-group per
+// half-wave (absmax by shuffles: order-free max).
 template <int QF, bool PERM>
 __device__ void rmsnorm_quant_block(float* xt, int dim, float eps, int8_t* q_lds, float* s_lds, float* xn) {
     const int tid = threadIdx.x, nthr = blockDim.x;
@@ -90,6 +97,289 @@ __device__ void rmsnorm_quant_block(float* xt, int dim, float eps, int8_t* q_lds
             }
         }
     }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm + quantize of one row inside a fused kernel (dim % 32 == 0).
+//
+// A team of threads -- the whole workgroup, or one wavefront -- walks the row
+// in passes; in pass p team member i holds the 8 elements from
+// e = (p * team_size + i) * 8, so each 32-group belongs to an aligned quad of
+// lanes and its absmax takes two DPP steps.  Members past the row load a
+// clamped copy of the last slice and write nothing; they form whole quads.
+//
+// Sum of squares: the reference's f32x8 accumulator is 8 serial chains (lane
+// j adds x[8i+j]^2 for i = 0, 1, ...; util.rs:398-405).  The squares go to LDS
+// transposed (row j holds chain j), and lanes 0-7 of every wavefront of the
+// team run the 8 chains over float4 reads kept in flight a block ahead; each
+// wavefront reads the 8 results by readlane.
+//
+// The chains need no workgroup barrier when one wavefront staged the row
+// (the LDS operations of one wavefront complete in issue order), so in a
+// GEMV that wavefront runs them while the others issue weight loads: a
+// workgroup barrier completes only once every wavefront has issued all its
+// loads, which under full HBM load is most of the kernel's duration.
+//
+// Use: rowq_load_* issue the global loads into registers; rowq_stage moves
+// the row, the norm weights and the squares to LDS (freeing the registers for
+// the chain loop); rowq_chain yields the reciprocal RMS; rowq_quant
+// normalizes and quantizes.
+struct RowTeam {
+    int idx, size;   // member index, member count (a multiple of 64)
+};
+__device__ __forceinline__ RowTeam team_workgroup() { return RowTeam{(int)threadIdx.x, (int)blockDim.x}; }
+__device__ __forceinline__ RowTeam team_wave() { return RowTeam{(int)(threadIdx.x & 63), 64}; }
+
+__host__ __device__ inline int rowq_passes(int dim, int team) { return (dim + 8 * team - 1) / (8 * team); }
+// Chain row length: dim/8 squares padded with zeros to a multiple of 64
+// (pairs of 8-vf4 read blocks; adding +0 to a sum of squares is exact), and
+// a stride of that + 4 floats so the 8 chain lanes read distinct banks.
+__host__ __device__ inline int rowq_chain_len(int dim) { return ((dim / 8) + 63) & ~63; }
+__host__ __device__ inline int rowq_stride(int dim) { return rowq_chain_len(dim) + 4; }
+// Row and norm-weight regions: dim floats rounded up to whole 1 KiB DMA rows.
+__host__ __device__ inline int rowq_row_len(int dim) { return (dim + 255) & ~255; }
+// LDS floats used: transposed squares | row | norm weights
+__host__ __device__ inline size_t rowq_lds_floats(int dim) {
+    return (size_t)8 * rowq_stride(dim) + 2 * (size_t)rowq_row_len(dim);
+}
+
+// first element of the member's slice in pass p (clamped past the row)
+__device__ __forceinline__ int rowq_elem(RowTeam tm, int p, int dim) {
+    const int e = (p * tm.size + tm.idx) * 8;
+    return e < dim ? e : dim - 8;
+}
+__device__ __forceinline__ bool rowq_live(RowTeam tm, int p, int dim) { return (p * tm.size + tm.idx) * 8 < dim; }
+
+// f32 slices of src -> registers, two vf4 per pass (issue only)
+template <int MP>
+__device__ __forceinline__ void rowq_load_f32(RowTeam tm, vf4 (&dst)[2 * MP], const float* __restrict__ src,
+                                              int dim, int passes) {
+#pragma unroll
+    for (int p = 0; p < MP; p++)
+        if (p < passes) {
+            const vf4* s4 = reinterpret_cast<const vf4*>(src + rowq_elem(tm, p, dim));
+            dst[2 * p] = s4[0];
+            dst[2 * p + 1] = s4[1];
+        }
+}
+
+// Raw bytes + scale of one token's row slices in the interleaved Q8_0
+// embedding (bytes q+128 at [vocab/64][dim/16][64][16], f16 scales at
+// [vocab/64][dim/32][64]).  Ids outside the vocabulary read row 0; their
+// values are zeroed by rowq_embed_values.
+template <int MP>
+struct EmbRegs {
+    uint2 q[MP];
+    uint16_t d[MP];
+};
+template <int MP>
+__device__ __forceinline__ void rowq_load_emb(RowTeam tm, EmbRegs<MP>& r, const EmbQ8& e, uint32_t tok,
+                                              int passes) {
+    const bool in_vocab = tok < (uint32_t)e.vocab;
+    const size_t tile = in_vocab ? tok >> 6 : 0;
+    const int lane = (int)(tok & 63u);
+    const int k16n = e.dim / 16, nbE = e.dim / 32;
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(e.q);
+#pragma unroll
+    for (int p = 0; p < MP; p++)
+        if (p < passes) {
+            const int el = rowq_elem(tm, p, e.dim);
+            r.q[p] = *reinterpret_cast<const uint2*>(q + ((tile * k16n + (el >> 4)) * 64 + lane) * 16 + (el & 15));
+            r.d[p] = e.d[(tile * nbE + (el >> 5)) * 64 + lane];
+        }
+}
+// Embedding values q*scale (transformer_llama_gguf.rs:459-473), zero for ids
+// outside the vocabulary (base_transformer.rs:143-161)
+template <int MP>
+__device__ __forceinline__ void rowq_embed_values(vf4 (&dst)[2 * MP], const EmbRegs<MP>& r, bool in_vocab,
+                                                  int passes) {
+#pragma unroll
+    for (int p = 0; p < MP; p++)
+        if (p < passes) {
+            const float sc = f16_to_f32(r.d[p]);
+            float v[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint32_t w = b < 4 ? r.q[p].x : r.q[p].y;
+                const int u = (int)((w >> (8 * (b & 3))) & 0xffu);
+                v[b] = in_vocab ? fmul((float)(u - 128), sc) : 0.0f;
+            }
+            dst[2 * p] = vf4{v[0], v[1], v[2], v[3]};
+            dst[2 * p + 1] = vf4{v[4], v[5], v[6], v[7]};
+        }
+}
+
+// Row, norm weights and squares -> LDS (sq: rowq_lds_floats(dim) floats).
+template <int MP>
+__device__ __forceinline__ void rowq_stage(RowTeam tm, const vf4 (&x)[2 * MP], const vf4 (&w)[2 * MP],
+                                           int dim, int passes, float* sq) {
+    const int S = rowq_stride(dim);
+    float* xl = sq + 8 * S;
+    float* wl = xl + rowq_row_len(dim);
+#pragma unroll
+    for (int p = 0; p < MP; p++)
+        if (p < passes && rowq_live(tm, p, dim)) {
+            const int e = rowq_elem(tm, p, dim);
+            const int i = e >> 3;
+            const vf4 a = x[2 * p], b = x[2 * p + 1];
+            sq[0 * S + i] = fmul(a.x, a.x);
+            sq[1 * S + i] = fmul(a.y, a.y);
+            sq[2 * S + i] = fmul(a.z, a.z);
+            sq[3 * S + i] = fmul(a.w, a.w);
+            sq[4 * S + i] = fmul(b.x, b.x);
+            sq[5 * S + i] = fmul(b.y, b.y);
+            sq[6 * S + i] = fmul(b.z, b.z);
+            sq[7 * S + i] = fmul(b.w, b.w);
+            *reinterpret_cast<vf4*>(xl + e) = a;
+            *reinterpret_cast<vf4*>(xl + e + 4) = b;
+            *reinterpret_cast<vf4*>(wl + e) = w[2 * p];
+            *reinterpret_cast<vf4*>(wl + e + 4) = w[2 * p + 1];
+        }
+    const int n8 = dim / 8, pad = rowq_chain_len(dim) - n8;
+    for (int i = tm.idx; i < 8 * pad; i += tm.size) sq[(i / pad) * S + n8 + i % pad] = 0.0f;
+}
+
+// Staging by one wavefront through LDS DMA (global_load_lds_dwordx4: 16
+// bytes per lane straight into LDS, no registers).  Lanes past the row
+// re-read its last 16 bytes into the padding of the 1 KiB-rounded region.
+// The caller waits for the copies (wait_vm_all) before reading them.
+__device__ __forceinline__ void rowq_dma_f32(float* dst, const float* __restrict__ src, int dim) {
+    const int lane = threadIdx.x & 63;
+    for (int j = 0; j * 256 < dim; j++) {
+        const int e = min(j * 256 + lane * 4, dim - 4);
+        __builtin_amdgcn_global_load_lds(src + e, dst + j * 256, 16, 0, 0);
+    }
+}
+// Waits for every vector-memory load of the calling wavefront, LDS DMA
+// included (the compiler does not order LDS reads after DMA writes itself).
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Squares of a row already in LDS (row region of sq) -> transposed chain rows,
+// plus the zero padding of the chain rows; one wavefront.
+__device__ __forceinline__ void rowq_squares_wave(int dim, float* sq) {
+    const RowTeam tm = team_wave();
+    const int S = rowq_stride(dim);
+    const float* xl = sq + 8 * S;
+    const int passes = rowq_passes(dim, 64);
+    for (int p = 0; p < passes; p++) {
+        if (!rowq_live(tm, p, dim)) break;
+        const int e = rowq_elem(tm, p, dim);
+        const int i = e >> 3;
+        const vf4 a = *reinterpret_cast<const vf4*>(xl + e), b = *reinterpret_cast<const vf4*>(xl + e + 4);
+        sq[0 * S + i] = fmul(a.x, a.x);
+        sq[1 * S + i] = fmul(a.y, a.y);
+        sq[2 * S + i] = fmul(a.z, a.z);
+        sq[3 * S + i] = fmul(a.w, a.w);
+        sq[4 * S + i] = fmul(b.x, b.x);
+        sq[5 * S + i] = fmul(b.y, b.y);
+        sq[6 * S + i] = fmul(b.z, b.z);
+        sq[7 * S + i] = fmul(b.w, b.w);
+    }
+    const int n8 = dim / 8, pad = rowq_chain_len(dim) - n8;
+    for (int i = tm.idx; i < 8 * pad; i += 64) sq[(i / pad) * S + n8 + i % pad] = 0.0f;
+}
+
+// RMSNorm (util.rs:389-426) of a staged row, in two parts.
+//
+// rowq_chain: the sum of squares (the 8 serial chains, run by lanes 0-7 of
+// each calling wavefront) -> the reciprocal RMS `ss`, returned to every lane.
+// A single wavefront may call it without any workgroup barrier (its own LDS
+// writes are complete in issue order).
+__device__ __forceinline__ float rowq_chain(int dim, float eps, const float* sq) {
+    const int S = rowq_stride(dim);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    float l = 0.0f;
+    if ((threadIdx.x & 63) < 8) {
+        // blocks of 8 vf4s; the next block's reads are issued before the
+        // current block's adds (the read after the last block is a re-read)
+        const vf4* r4 = reinterpret_cast<const vf4*>(sq + (threadIdx.x & 7) * S);
+        const int nblk = rowq_chain_len(dim) / 32;
+        vf4 va[8], vb[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) va[k] = r4[k];
+        for (int b = 0; b < nblk; b += 2) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) vb[k] = r4[(b + 1) * 8 + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                l = fadd(l, va[k].x);
+                l = fadd(l, va[k].y);
+                l = fadd(l, va[k].z);
+                l = fadd(l, va[k].w);
+            }
+            const int nb2 = b + 2 < nblk ? b + 2 : b;
+#pragma unroll
+            for (int k = 0; k < 8; k++) va[k] = r4[nb2 * 8 + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                l = fadd(l, vb[k].x);
+                l = fadd(l, vb[k].y);
+                l = fadd(l, vb[k].z);
+                l = fadd(l, vb[k].w);
+            }
+        }
+    }
+    float part[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) part[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), j));
+    float ss = reduce_add8(part);
+    ss = ss / (float)dim;
+    ss = fadd(ss, eps);
+    return 1.0f / sqrtf(ss);
+}
+
+// rowq_quant: o = w * (ss * x) over the team's slices, then group
+// quantization (quantization.rs:29-52 / weight_type.rs:52-74).
+//   QF : kQ8 / kQ4 -> q_lds/s_lds (LDS) receive the quantized row, each
+//        8-group reordered to (even, odd) elements when PERM; QF < 0 -> none
+//   xn : optional f32 output of the normalized row (LDS or global)
+template <int QF, bool PERM>
+__device__ __forceinline__ void rowq_quant(RowTeam tm, int dim, float ss, const float* sq, int8_t* q_lds,
+                                           float* s_lds, float* xn) {
+    const int S = rowq_stride(dim);
+    const float* xl = sq + 8 * S;
+    const float* wl = xl + rowq_row_len(dim);
+    const int passes = rowq_passes(dim, tm.size);
+    for (int p = 0; p < passes; p++) {
+        if (!rowq_live(tm, p, dim)) break;
+        const int e = rowq_elem(tm, p, dim);
+        const vf4 x0 = *reinterpret_cast<const vf4*>(xl + e), x1 = *reinterpret_cast<const vf4*>(xl + e + 4);
+        const vf4 w0 = *reinterpret_cast<const vf4*>(wl + e), w1 = *reinterpret_cast<const vf4*>(wl + e + 4);
+        float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float am = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            v[k] = fmul(w[k], fmul(ss, v[k]));
+            am = fmaxf(am, fabsf(v[k]));
+        }
+        if constexpr (QF >= 0) {
+            // the quad of this 32-group is live as a whole
+            am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
+            am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
+            const float sc = group_scale<QF>(am);
+            int q[8];
+            quant8<QF>(v, sc, q);
+            *reinterpret_cast<uint2*>(q_lds + e) =
+                PERM ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
+                     : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
+            if ((tm.idx & 3) == 0) s_lds[e >> 5] = sc;
+        }
+        if (xn) {
+            *reinterpret_cast<vf4*>(xn + e) = vf4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<vf4*>(xn + e + 4) = vf4{v[4], v[5], v[6], v[7]};
+        }
+    }
+}
+
+// Both parts by the whole workgroup (every wavefront runs the chains);
+// starts and ends with a workgroup barrier.
+template <int QF, bool PERM>
+__device__ void rowq_norm_quant(int dim, float eps, float* sq, int8_t* q_lds, float* s_lds, float* xn) {
+    __syncthreads();
+    const float ss = rowq_chain(dim, eps, sq);
+    rowq_quant<QF, PERM>(team_workgroup(), dim, ss, sq, q_lds, s_lds, xn);
     __syncthreads();
 }
 

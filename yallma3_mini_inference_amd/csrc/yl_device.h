@@ -15,6 +15,10 @@ namespace yl {
 
 constexpr int kGroup = 32;        // block size of Q8_0/Q4_0 (transformer_llama_gguf.rs:281)
 
+// Native 4-float vector for register arrays: copies of HIP's float4 (a
+// struct) lower to memcpy, which can keep an array out of registers.
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float fadd(float a, float b) { return a + b; }
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
 
@@ -66,13 +70,12 @@ __device__ __forceinline__ float expf_rn(float xf) {
     return (float)__builtin_amdgcn_ldexp(p, (int)kd);
 }
 
-// Rust `(v).round() as i8`: half away from zero, saturating, NaN -> 0.
+// Rust `(v).round() as i8`: half away from zero, saturating, NaN -> 0
+// (written with selects only, no branches).
 __device__ __forceinline__ int round_to_i8(float v) {
-    if (v != v) return 0;
     float r = __builtin_roundf(v);
-    if (r >= 127.0f) return 127;
-    if (r <= -128.0f) return -128;
-    return (int)r;
+    r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+    return v != v ? 0 : (int)r;
 }
 
 // One group of 32 activations -> quantized values and scale.
@@ -89,6 +92,53 @@ __device__ __forceinline__ int quant_one(float x, float scale) {
     int q = round_to_i8(x / scale);
     if (FMT == kQ4) q = q < -7 ? -7 : (q > 7 ? 7 : q);
     return q;
+}
+
+// quant_one over 8 values of one group, without a division per value.
+// y = x * fl(1/scale) is within |x/scale| * 2^-23 <= 2^-16 of x/scale (the
+// quotient never exceeds 127 * (1 + 2^-23) in magnitude), and so is the
+// reference's fl(x/scale).  When y lies more than 2^-14 from every
+// half-integer, both round to rint(y); otherwise (and for NaN, an infinite
+// or zero reciprocal, or a scale below 2^-100) the lane takes quant_one's
+// exact division.  Ties therefore always go through the exact path.
+template <int FMT>
+__device__ __forceinline__ void quant8(const float v[8], float scale, int q[8]) {
+    const float rinv = 1.0f / scale;
+    bool slow = !(rinv <= 0x1p100f);
+    constexpr float lo = FMT == kQ4 ? -7.0f : -128.0f, hi = FMT == kQ4 ? 7.0f : 127.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float y = v[k] * rinv;
+        const float r = __builtin_rintf(y);
+        slow = slow || !(__builtin_fabsf(y - r) <= 0.5f - 0x1p-14f);
+        q[k] = (int)__builtin_fminf(__builtin_fmaxf(r, lo), hi);
+    }
+    if (slow) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) q[k] = quant_one<FMT>(v[k], scale);
+    }
+}
+
+// Lane permutation by DPP (a VALU operand modifier, no LDS round trip).
+// Lanes whose source is out of range keep their own value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, 0xF, 0xF, false));
+}
+
+// Maximum over aligned groups of P consecutive lanes (P = 1, 2, ..., 32,
+// uniform across the wavefront).  Every lane of the wavefront must be active.
+// After the quad steps each quad holds its maximum, so mirroring within
+// half-rows (8 lanes) and rows (16 lanes) pairs each lane with the other
+// half; the last step crosses rows.
+__device__ __forceinline__ float group_max(float v, int P) {
+    if (P >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));    // quad_perm [1,0,3,2]
+    if (P >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));    // quad_perm [2,3,0,1]
+    if (P >= 8) v = fmaxf(v, dpp_mov<0x141>(v));   // row_half_mirror
+    if (P >= 16) v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+    if (P >= 32) v = fmaxf(v, __shfl_xor(v, 16, 32));
+    return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -86,12 +86,15 @@ static size_t gemv_smem(int n, int nb, int R, int epi, int dim) {
     size_t s = (size_t)n + (size_t)nb * 4;
     s = (s + 15) & ~(size_t)15;
     s += (size_t)R * terms_stride(nb) * 4 + 64 * 4;
-    if (epi == kEpiQkvRope || epi == kEpiSwiglu) s += norm_lds_floats(dim) * 4;
+    if (epi == kEpiQkvRope || epi == kEpiSwiglu) s += rowq_lds_floats(dim) * 4;
     return s;
 }
 
+// Few wavefronts per SIMD (2, or 3 for 9-wavefront workgroups): a decode
+// launch has 1-2 workgroups per CU, so registers go to loads in flight
+// rather than to occupancy.
 template <int WF, int R, int TPB, int PMAX, int EPI, bool EMB>
-__global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 512 ? 3 : 2))) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int n = a.n, nb = a.nb, o = a.o;
     const int tid = threadIdx.x;
@@ -105,81 +108,53 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
     float* xt = accs + 64;
     constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
 
-    // Global loads are issued in the order they are needed: first the
-    // activation inputs (recently written, cache-hot), then every weight block
-    // of this thread.  Vector-memory loads retire in order, so waiting for the
-    // activations then leaves the weights in flight while the prologue runs.
+    // Global loads are issued in the order they are needed: activation
+    // inputs (recently written, cache-hot) before weights, weights before
+    // what only the epilogue reads.  Vector-memory loads retire in order, so
+    // waiting for the activations leaves the weights in flight.
+    // With an RMSNorm prologue, wavefront 0 loads the row and runs the serial
+    // sum of squares while the other wavefronts issue weight loads: a
+    // workgroup barrier completes only once every wavefront has issued all
+    // its loads, so only the short, parallel quantization waits for one.
     // All loads are unconditional (out-of-range indices are clamped and their
     // data ignored): a load under a divergent branch makes the compiler wait
     // for it at the branch join, which would serialize the HBM round trips.
     const int dim = n;
-    constexpr int kMaxPer = 8192 / TPB;          // normalized rows: dim <= 8192
-    constexpr int kMaxStage = 16384 / 8 / TPB;   // staged int8 rows: n <= 16384
-    constexpr int kMaxScale = (512 + TPB - 1) / TPB;
-    float xv[kNorm ? kMaxPer : 1], wn[kNorm ? kMaxPer : 1];
-    uint2 qv[kNorm ? 1 : kMaxStage];
-    float sv[kNorm ? 1 : kMaxScale];
-
-    // 1a. activation inputs -> registers (the decode position first: the
-    // epilogue's cache addresses depend on it)
-    const int pos = (EPI == kEpiQkvRope) ? a.state->pos + t : 0;
-    int eqv[EMB ? kMaxPer : 1];
-    uint16_t edv[EMB ? kMaxPer : 1];
-    bool in_vocab = true;
-    if constexpr (kNorm) {
-        const float* __restrict__ nw = a.norm_w;
-        if constexpr (EMB) {
-            // layer 0: the residual stream starts as the token's embedding row
-            // (base_transformer.rs:143-161, zero for ids >= vocab)
-            const uint32_t tok = a.tokens[t];
-            in_vocab = tok < (uint32_t)a.emb.vocab;
-            const size_t tile = in_vocab ? tok >> 6 : 0;
-            const int lane = (int)(tok & 63u);
-            const int8_t* __restrict__ eq = a.emb.q;
-            const uint16_t* __restrict__ ed = a.emb.d;
-#pragma unroll
-            for (int k = 0; k < kMaxPer; k++) {
-                const int i = tid + k * TPB;
-                if (k * TPB < dim) {
-                    const int ic = i < dim ? i : 0;
-                    eqv[k] = eq[((tile * (dim / 16) + (ic >> 4)) * 64 + lane) * 16 + (ic & 15)];
-                    edv[k] = ed[(tile * (dim / 32) + (ic >> 5)) * 64 + lane];
-                    wn[k] = nw[ic];
-                }
-            }
-        } else {
-            const float* __restrict__ xin = a.x + (size_t)t * dim;
-#pragma unroll
-            for (int k = 0; k < kMaxPer; k++) {
-                const int i = tid + k * TPB;
-                if (k * TPB < dim) {
-                    const int ic = i < dim ? i : 0;
-                    xv[k] = xin[ic];
-                    wn[k] = nw[ic];
-                }
-            }
-        }
-    } else {
-        const uint2* __restrict__ xg = reinterpret_cast<const uint2*>(a.xq + (size_t)t * n);
-        const float* __restrict__ xsg = a.xs + (size_t)t * nb;
-#pragma unroll
-        for (int k = 0; k < kMaxStage; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < n / 8) qv[k] = xg[i < n / 8 ? i : 0];
-        }
-#pragma unroll
-        for (int k = 0; k < kMaxScale; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < nb) sv[k] = xsg[i < nb ? i : 0];
-        }
-    }
-
-    // 1a'. values the epilogue reads (cache initial values and RoPE angles,
-    // the residual row, the accumulate-into output), fetched now
+    constexpr int WT = kNorm ? TPB - 64 : TPB;   // threads that load weights
+    // the gate/up matmul issues many loads per thread, so its wavefront 0
+    // also quantizes (a barrier would wait for all those loads to issue)
+    constexpr bool kWaveQuant = EPI == kEpiSwiglu;
+    const int tw = kNorm ? tid - 64 : tid;       // weight-thread index
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int total = R * nb;
+    WBlock<WF> wv[PMAX];
+    uint16_t dv[PMAX];
     float ep0 = 0.0f, ep1 = 1.0f, ep2 = 0.0f;
     bool ep_acc = false;
-    {
-        const int er = min(row0 + (tid < R ? tid : 0), o - 1);
+    int pos = 0;
+
+    auto load_weights = [&]() {
+        const size_t row_bytes = WF == kQ8 ? (size_t)n : (size_t)n / 2;
+        const int dr = WT / nb, db = WT % nb;
+        int r = tw / nb, b = tw - (tw / nb) * nb;
+#pragma unroll
+        for (int k = 0; k < PMAX; k++) {
+            const bool ok = tw + k * WT < total && row0 + r < o;
+            const size_t row = ok ? (size_t)(row0 + r) : 0;
+            load_block<WF>(wv[k], a.qs + row * row_bytes + (size_t)b * (WF == kQ8 ? 32 : 16));
+            dv[k] = a.d[row * nb + b];
+            r += dr;
+            b += db;
+            if (b >= nb) { b -= nb; r += 1; }
+        }
+    };
+    // values the epilogue reads (cache initial values and RoPE angles at the
+    // decode position, the residual row, the accumulate-into output); row r
+    // of the workgroup is finished by weight thread r (R <= 64: one
+    // wavefront), which issues these loads right after its weight loads
+    auto load_epilogue = [&]() {
+        pos = (EPI == kEpiQkvRope) ? a.state->pos + t : 0;
+        const int er = min(row0 + (tw >= 0 && tw < R ? tw : 0), o - 1);
         if constexpr (EPI == kEpiQkvRope) {
             // K/V rows accumulate into the cache (forward.rs:166-169)
             const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
@@ -197,45 +172,83 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
             ep_acc = er < a.accumulate_cols;
             ep0 = a.out[(size_t)t * o + er];
         }
-    }
+    };
 
-    // 1b. weights of every pair of this thread -> registers
-    const size_t row_bytes = WF == kQ8 ? (size_t)n : (size_t)n / 2;
-    const int total = R * nb;
-    WBlock<WF> wv[PMAX];
-    uint16_t dv[PMAX];
-    {
-        const int dr = TPB / nb, db = TPB % nb;
-        int r = tid / nb, b = tid - (tid / nb) * nb;
-#pragma unroll
-        for (int k = 0; k < PMAX; k++) {
-            const bool ok = tid + k * TPB < total && row0 + r < o;
-            const size_t row = ok ? (size_t)(row0 + r) : 0;
-            load_block<WF>(wv[k], a.qs + row * row_bytes + (size_t)b * (WF == kQ8 ? 32 : 16));
-            dv[k] = a.d[row * nb + b];
-            r += dr;
-            b += db;
-            if (b >= nb) { b -= nb; r += 1; }
-        }
-    }
-
-    // 2. activation row -> LDS (int8 values + f32 group scales)
     if constexpr (kNorm) {
-#pragma unroll
-        for (int k = 0; k < kMaxPer; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < dim && i < dim) {
-                float v;
-                if constexpr (EMB)
-                    v = in_vocab ? fmul((float)((int)(uint8_t)eqv[k] - 128), f16_to_f32(edv[k])) : 0.0f;
-                else v = xv[k];
-                store_norm_input(xt, dim, i, v, wn[k]);
-                if (EMB && blockIdx.x == 0) a.x[(size_t)t * dim + i] = v;
+        if (wave == 0) {
+            // 1 (wavefront 0). residual row (or, in layer 0, the token's
+            // embedding row) + norm weights -> LDS; the serial sum of squares
+            constexpr int MP = 8;   // dim <= 4096
+            const RowTeam tm = team_wave();
+            const int passes = rowq_passes(dim, 64);
+            float* xrow = xt + 8 * rowq_stride(dim);
+            float* wrow = xrow + rowq_row_len(dim);
+            EmbRegs<EMB ? MP : 1> er_;
+            bool in_vocab = true;
+            if constexpr (EMB) {
+                const uint32_t tok = a.tokens[t];
+                in_vocab = tok < (uint32_t)a.emb.vocab;
+                rowq_load_emb<MP>(tm, er_, a.emb, tok, passes);
+            } else {
+                rowq_dma_f32(xrow, a.x + (size_t)t * dim, dim);
             }
+            rowq_dma_f32(wrow, a.norm_w, dim);
+            wait_vm_all();
+            if constexpr (EMB) {
+                // the residual stream starts as the embedding row
+                vf4 xv[2 * MP];
+                rowq_embed_values<MP>(xv, er_, in_vocab, passes);
+#pragma unroll
+                for (int p = 0; p < MP; p++)
+                    if (p < passes && rowq_live(tm, p, dim)) {
+                        const int e = rowq_elem(tm, p, dim);
+                        *reinterpret_cast<vf4*>(xrow + e) = xv[2 * p];
+                        *reinterpret_cast<vf4*>(xrow + e + 4) = xv[2 * p + 1];
+                        if (blockIdx.x == 0) {
+                            vf4* xo = reinterpret_cast<vf4*>(a.x + (size_t)t * dim + e);
+                            xo[0] = xv[2 * p];
+                            xo[1] = xv[2 * p + 1];
+                        }
+                    }
+            }
+            rowq_squares_wave(dim, xt);
+            const float ss = rowq_chain(dim, a.eps, xt);
+            if constexpr (kWaveQuant) rowq_quant<WF, WF == kQ4>(tm, dim, ss, xt, xl, xsl, nullptr);
+            else if (tid == 0) accs[0] = ss;
+        } else {
+            // 1 (other wavefronts). weights -> registers
+            load_weights();
+            if (wave == 1) load_epilogue();
         }
         __syncthreads();
-        rmsnorm_quant_block<WF, WF == kQ4>(xt, dim, a.eps, xl, xsl, nullptr);
+        if constexpr (!kWaveQuant) {
+            // 2. the whole workgroup quantizes the normalized row (the
+            // barrier costs little when every thread issues few weight loads)
+            rowq_quant<WF, WF == kQ4>(team_workgroup(), dim, accs[0], xt, xl, xsl, nullptr);
+            __syncthreads();
+        }
     } else {
+        // 1a. quantized activation row -> registers
+        constexpr int kMaxStage = 16384 / 8 / TPB;   // staged int8 rows: n <= 16384
+        constexpr int kMaxScale = (512 + TPB - 1) / TPB;
+        uint2 qv[kMaxStage];
+        float sv[kMaxScale];
+        const uint2* __restrict__ xg = reinterpret_cast<const uint2*>(a.xq + (size_t)t * n);
+        const float* __restrict__ xsg = a.xs + (size_t)t * nb;
+#pragma unroll
+        for (int k = 0; k < kMaxStage; k++) {
+            const int i = tid + k * TPB;
+            if (k * TPB < n / 8) qv[k] = xg[i < n / 8 ? i : 0];
+        }
+#pragma unroll
+        for (int k = 0; k < kMaxScale; k++) {
+            const int i = tid + k * TPB;
+            if (k * TPB < nb) sv[k] = xsg[i < nb ? i : 0];
+        }
+        // 1b. weights, 1c. epilogue values
+        load_weights();
+        load_epilogue();
+        // 2. activation row -> LDS (int8 values + f32 group scales)
         uint2* xd = reinterpret_cast<uint2*>(xl);
 #pragma unroll
         for (int k = 0; k < kMaxStage; k++) {
@@ -255,32 +268,49 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
     }
 
     // 3. exact block dots -> f32 terms in LDS
-    {
-        const int dr = TPB / nb, db = TPB % nb;
-        int r = tid / nb, b = tid - (tid / nb) * nb;
+    if (!kNorm || wave != 0) {
+        const int dr = WT / nb, db = WT % nb;
+        int r = tw / nb, b = tw - (tw / nb) * nb;
+        if (db == 0) {
+            // every pair of this thread uses the same activation block
+            int32_t xw[8];
 #pragma unroll
-        for (int k = 0; k < PMAX; k++) {
-            if (tid + k * TPB < total) {
-                float term = 0.0f;
-                if (row0 + r < o) {
-                    const int isum = block_dot<WF>(wv[k], reinterpret_cast<const int32_t*>(xl + b * 32));
-                    term = fmul(fmul((float)isum, f16_to_f32(dv[k])), xsl[b]);
+            for (int j = 0; j < 8; j++) xw[j] = reinterpret_cast<const int32_t*>(xl + b * 32)[j];
+            const float xs_b = xsl[b];
+#pragma unroll
+            for (int k = 0; k < PMAX; k++) {
+                if (tw + k * WT < total) {
+                    float term = 0.0f;
+                    if (row0 + r < o) term = fmul(fmul((float)block_dot<WF>(wv[k], xw), f16_to_f32(dv[k])), xs_b);
+                    terms[r * TS + b] = term;
                 }
-                terms[r * TS + b] = term;
+                r += dr;
             }
-            r += dr;
-            b += db;
-            if (b >= nb) { b -= nb; r += 1; }
+        } else {
+#pragma unroll
+            for (int k = 0; k < PMAX; k++) {
+                if (tw + k * WT < total) {
+                    float term = 0.0f;
+                    if (row0 + r < o) {
+                        const int isum = block_dot<WF>(wv[k], reinterpret_cast<const int32_t*>(xl + b * 32));
+                        term = fmul(fmul((float)isum, f16_to_f32(dv[k])), xsl[b]);
+                    }
+                    terms[r * TS + b] = term;
+                }
+                r += dr;
+                b += db;
+                if (b >= nb) { b -= nb; r += 1; }
+            }
         }
     }
     __syncthreads();
 
     // 4. ordered per-row sums
-    if (tid < R) {
-        const int row = row0 + tid;
+    if (tw >= 0 && tw < R) {
+        const int row = row0 + tw;
         if (row < o) {
             float acc = ep_acc ? ep0 : 0.0f;
-            const float* tr = terms + tid * TS;
+            const float* tr = terms + tw * TS;
             const float4* t4 = reinterpret_cast<const float4*>(tr);
             int b = 0;
 #pragma unroll 4
@@ -292,7 +322,7 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
                 acc = fadd(acc, v.w);
             }
             for (int bb = b * 4; bb < nb; bb++) acc = fadd(acc, tr[bb]);
-            accs[tid] = acc;
+            accs[tw] = acc;
             if constexpr (EPI == kEpiStore) a.out[(size_t)t * o + row] = acc;
             if constexpr (EPI == kEpiResid) {
                 // residual add (forward.rs:196-204 / 245-253)
@@ -307,18 +337,18 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
     if constexpr (EPI == kEpiQkvRope) {
         // rope_gguf (util.rs:653-718): pair (2i, 2i+1) of a head rotated by the
         // angle table row `pos`; v rows are stored as summed.
-        if (tid < R) {
-            const int row = row0 + tid;
+        if (tw >= 0 && tw < R) {
+            const int row = row0 + tw;
             if (row < o) {
                 const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
-                const float v = accs[tid];
+                const float v = accs[tw];
                 if (row >= att + kv) {
                     a.v_cache[(size_t)pos * kv + (row - att - kv)] = v;
                 } else {
                     const int col = row < att ? row : row - att;
                     const float c = ep1, s = ep2;
-                    const float v0 = accs[tid & ~1], v1 = accs[tid | 1];
-                    const float r = (tid & 1) ? fadd(fmul(v0, s), fmul(v1, c)) : fmul(v0, c) - fmul(v1, s);
+                    const float v0 = accs[tw & ~1], v1 = accs[tw | 1];
+                    const float r = (tw & 1) ? fadd(fmul(v0, s), fmul(v1, c)) : fmul(v0, c) - fmul(v1, s);
                     if (row < att) a.q_out[(size_t)t * att + col] = r;
                     else a.k_cache[(size_t)pos * kv + col] = r;
                 }
@@ -327,22 +357,22 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
     } else if constexpr (EPI == kEpiSwiglu) {
         // SwiGLU (forward.rs:220-237): h = (g / (1 + exp(-g))) * u, then this
         // 32-group of h is quantized for the down projection.
-        if (tid < 32) {
-            const float g = accs[tid];
-            const float u = accs[32 + tid];
+        if (tw >= 0 && tw < 32) {
+            const float g = accs[tw];
+            const float u = accs[32 + tw];
             const float den = fadd(1.0f, expf_rn(-g));
             const float h = fmul(g / den, u);
             const int grp = blockIdx.x;
             const size_t base = (size_t)t * a.hidden + (size_t)grp * kGroup;
-            if (a.h_f32) a.h_f32[base + tid] = h;
+            if (a.h_f32) a.h_f32[base + tw] = h;
             float am = fabsf(h);
 #pragma unroll
             for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
             am = fmaxf(am, 0.0f);
             const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
             const int q = a.h_fmt == kQ4 ? quant_one<kQ4>(h, sc) : quant_one<kQ8>(h, sc);
-            a.hq[base + tid] = (int8_t)q;
-            if (tid == 0) a.hs[(size_t)t * (a.hidden / kGroup) + grp] = sc;
+            a.hq[base + tw] = (int8_t)q;
+            if (tw == 0) a.hs[(size_t)t * (a.hidden / kGroup) + grp] = sc;
         }
     }
 }
@@ -350,30 +380,35 @@ __global__ __launch_bounds__(TPB) void k_gemv(GemvArgs a) {
 // ------------------------------------------------------------ dispatch ----
 
 struct GemvShape {
-    int R, TPB, PMAX;
+    int R, WT, PMAX;   // rows per workgroup, weight-loading threads, pairs per thread
 };
 
 // Rows per workgroup and threads: enough workgroups to cover the 256 CUs,
 // 32-128 KiB of weights in flight per CU, and every pair of a thread loaded
-// before its first use.
+// before its first use.  Kernels with an RMSNorm prologue launch one more
+// wavefront (the normalizing one) than WT.
 static GemvShape pick_shape(int o, int nb, int epi) {
     GemvShape s;
-    if (epi == kEpiSwiglu) {
-        s.R = 64;
-        s.TPB = 512;
-    } else if (nb >= 192) {
-        s.R = 4;
-        s.TPB = 256;
-    } else if (o >= 8192) {
-        s.R = 16;
-        s.TPB = 256;
-    } else {
-        s.R = 8;
-        s.TPB = 256;
-    }
-    const int p = (s.R * nb + s.TPB - 1) / s.TPB;
+    s.WT = epi == kEpiSwiglu ? 512 : 256;
+    if (epi == kEpiSwiglu) s.R = 64;
+    else if (nb >= 192) s.R = 4;
+    else if (o >= 8192) s.R = 16;
+    else s.R = 8;
+    const int p = (s.R * nb + s.WT - 1) / s.WT;
     s.PMAX = p <= 1 ? 1 : p <= 2 ? 2 : p <= 4 ? 4 : p <= 8 ? 8 : p <= 16 ? 16 : 0;
     return s;
+}
+
+template <int WF, int R, int TPB, int PMAX, int EPI, bool EMB>
+static hipError_t launch_k(const GemvArgs& a, dim3 grid, size_t smem, hipStream_t st) {
+    if (smem > 65536) {
+        // rows longer than 4096 need more than the default 64 KiB of LDS
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<WF, R, TPB, PMAX, EPI, EMB>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_gemv<WF, R, TPB, PMAX, EPI, EMB>), grid, dim3(TPB), smem, st, a);
+    return hipGetLastError();
 }
 
 template <int WF, int R, int TPB, int EPI, bool EMB>
@@ -381,14 +416,13 @@ static hipError_t launch_r2(const GemvArgs& a, int pmax, int batch, hipStream_t 
     const size_t smem = gemv_smem(a.n, a.nb, R, EPI, a.n);
     const dim3 grid((a.o + R - 1) / R, batch);
     switch (pmax) {
-    case 1: hipLaunchKernelGGL((k_gemv<WF, R, TPB, 1, EPI, EMB>), grid, dim3(TPB), smem, st, a); break;
-    case 2: hipLaunchKernelGGL((k_gemv<WF, R, TPB, 2, EPI, EMB>), grid, dim3(TPB), smem, st, a); break;
-    case 4: hipLaunchKernelGGL((k_gemv<WF, R, TPB, 4, EPI, EMB>), grid, dim3(TPB), smem, st, a); break;
-    case 8: hipLaunchKernelGGL((k_gemv<WF, R, TPB, 8, EPI, EMB>), grid, dim3(TPB), smem, st, a); break;
-    case 16: hipLaunchKernelGGL((k_gemv<WF, R, TPB, 16, EPI, EMB>), grid, dim3(TPB), smem, st, a); break;
+    case 1: return launch_k<WF, R, TPB, 1, EPI, EMB>(a, grid, smem, st);
+    case 2: return launch_k<WF, R, TPB, 2, EPI, EMB>(a, grid, smem, st);
+    case 4: return launch_k<WF, R, TPB, 4, EPI, EMB>(a, grid, smem, st);
+    case 8: return launch_k<WF, R, TPB, 8, EPI, EMB>(a, grid, smem, st);
+    case 16: return launch_k<WF, R, TPB, 16, EPI, EMB>(a, grid, smem, st);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 template <int WF, int R, int TPB, int EPI>
@@ -404,11 +438,12 @@ static hipError_t launch_epi(const GemvArgs& a, int batch, hipStream_t st) {
     const GemvShape s = pick_shape(a.o, a.nb, EPI);
     if (s.PMAX == 0) return hipErrorInvalidValue;
     if constexpr (EPI == kEpiSwiglu) {
-        return launch_r<WF, 64, 512, EPI>(a, s.PMAX, batch, st);
+        return launch_r<WF, 64, 512 + 64, EPI>(a, s.PMAX, batch, st);
     } else {
-        if (s.R == 4) return launch_r<WF, 4, 256, EPI>(a, s.PMAX, batch, st);
-        if (s.R == 16) return launch_r<WF, 16, 256, EPI>(a, s.PMAX, batch, st);
-        return launch_r<WF, 8, 256, EPI>(a, s.PMAX, batch, st);
+        constexpr int T = EPI == kEpiQkvRope ? 256 + 64 : 256;
+        if (s.R == 4) return launch_r<WF, 4, T, EPI>(a, s.PMAX, batch, st);
+        if (s.R == 16) return launch_r<WF, 16, T, EPI>(a, s.PMAX, batch, st);
+        return launch_r<WF, 8, T, EPI>(a, s.PMAX, batch, st);
     }
 }
 
@@ -424,7 +459,7 @@ static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t s
 }
 
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s) {
-    if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (a.n % 32 || a.n > 8192)) return hipErrorInvalidValue;
+    if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (a.n % 32 || a.n > 4096)) return hipErrorInvalidValue;
     if (a.n % 32 || a.n > 16384) return hipErrorInvalidValue;
     if (wfmt == kQ8) return launch_wf<kQ8>(a, epi, batch, s);
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);

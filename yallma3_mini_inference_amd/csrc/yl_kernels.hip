@@ -67,7 +67,15 @@ __global__ void k_quantize(int8_t* __restrict__ q, float* __restrict__ s, const 
     for (int k = 0; k < kGroup; k++) amax = fmaxf(amax, fabsf(xg[k]));
     const float sc = group_scale<QF>(amax);
     s[g] = sc;
-    for (int k = 0; k < kGroup; k++) q[g * kGroup + k] = (int8_t)quant_one<QF>(xg[k], sc);
+    for (int k8 = 0; k8 < kGroup; k8 += 8) {
+        float v[8];
+        int qv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = xg[k8 + k];
+        quant8<QF>(v, sc, qv);
+#pragma unroll
+        for (int k = 0; k < 8; k++) q[g * kGroup + k8 + k] = (int8_t)qv[k];
+    }
 }
 
 // RoPE on q [batch][n_heads*hd] and k [batch][n_kv_heads*hd] at positions

@@ -29,9 +29,10 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                                                           unsigned long long* __restrict__ keys) {
     extern __shared__ __align__(16) float lds[];
     __shared__ unsigned long long wkey[kLogitThreads / 64];
+    constexpr int MP = 8192 / 8 / kLogitThreads;   // dim <= 8192
     const int dim = e.dim, tid = threadIdx.x;
     float* xn = lds;
-    float* xt = lds + dim;
+    float* sq = lds + dim;
     const int wave = tid >> 6, lane = tid & 63;
     const int tile = blockIdx.x * (kLogitThreads / 64) + wave;
     const bool live = tile < e.tiles;
@@ -39,15 +40,21 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * k16n * 64 + lane;
     const uint16_t* dp = e.d + (size_t)(live ? tile : 0) * nbE * 64 + lane;
 
-    int4 qv[kLogitChunks];
-    if (live) {
-#pragma unroll
-        for (int k = 0; k < kLogitChunks; k++)
-            if (k < k16n) qv[k] = qp[(size_t)k * 64];
-    }
-    for (int i = tid; i < dim; i += kLogitThreads) store_norm_input(xt, dim, i, x[i], norm_w[i]);
+    // the residual row and norm weights first (every wavefront's loads issued
+    // before the barrier), then the first embedding chunks, which stay in
+    // flight while the row is normalized (loads retire in issue order)
+    const RowTeam tm = team_workgroup();
+    const int passes = rowq_passes(dim, kLogitThreads);
+    vf4 xv[2 * MP], wv[2 * MP];
+    rowq_load_f32<MP>(tm, xv, x, dim, passes);
+    rowq_load_f32<MP>(tm, wv, norm_w, dim, passes);
     __syncthreads();
-    rmsnorm_quant_block<-1, false>(xt, dim, eps, nullptr, nullptr, xn);
+    int4 qv[kLogitChunks];
+#pragma unroll
+    for (int k = 0; k < kLogitChunks; k++)
+        if (k < k16n) qv[k] = qp[(size_t)k * 64];
+    rowq_stage<MP>(tm, xv, wv, dim, passes, sq);
+    rowq_norm_quant<-1, false>(dim, eps, sq, nullptr, nullptr, xn);
 
     unsigned long long kk = 0ull;
     if (live) {
@@ -124,13 +131,20 @@ __global__ __launch_bounds__(512) void k_finalize(const unsigned long long* __re
     st->pos += advance;
 }
 
-size_t logits_lds_bytes(int dim) { return ((size_t)dim + norm_lds_floats(dim)) * sizeof(float); }
+size_t logits_lds_bytes(int dim) { return ((size_t)dim + rowq_lds_floats(dim)) * sizeof(float); }
 int logits_blocks(const EmbQ8& e) { return (e.tiles + kLogitThreads / 64 - 1) / (kLogitThreads / 64); }
 
 hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, float eps, float* logits,
                          unsigned long long* keys, StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
                          hipStream_t s) {
     const int nblk = logits_blocks(e);
+    if (e.dim % 32 || e.dim > 8192) return hipErrorInvalidValue;
+    if (logits_lds_bytes(e.dim) > 65536) {
+        const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(k_logits),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)logits_lds_bytes(e.dim));
+        if (err != hipSuccess) return err;
+    }
     hipLaunchKernelGGL(k_logits, dim3(nblk), dim3(kLogitThreads), logits_lds_bytes(e.dim), s, e, x, norm_w, eps,
                        logits, keys);
     hipError_t err = hipGetLastError();

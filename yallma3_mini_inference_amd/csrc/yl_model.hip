@@ -421,9 +421,11 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     m->attn_scale = att_scale_meta != 0.0f ? att_scale_meta : 1.0f / sqrtf((float)m->hd);
     if (m->n_kv <= 0 || m->n_heads % m->n_kv) { set_error("n_heads must be a multiple of n_kv_heads"); return nullptr; }
     if (m->dim % 32 || m->hidden % 32 || m->kv % 32 || (m->hd != 32 && m->hd != 64 && m->hd != 128) ||
-        m->dim > 8192 || m->ctx <= 0) {
+        m->dim > 4096 || m->ctx <= 0) {
+        // dim <= 4096: one wavefront normalizes the residual row inside the
+        // QKV and gate/up matmuls
         set_error("unsupported shape: dim, hidden and kv_dim must be multiples of 32, head_size 32/64/128, "
-                  "dim <= 8192");
+                  "dim <= 4096");
         *st = YL_ERR_UNSUPPORTED;
         return nullptr;
     }
