@@ -6,12 +6,9 @@
 //   p = e * (1/sum_exp);  out[d] = reduce_add(lane j sums p*v over t2 = 8c+j
 //   in c order) + the seq_len % 8 tail in t2 order.
 //
-// k_attn_decode (one token): grid (n_heads, C).  Workgroup (h, c) computes
-// the scores of positions [c*chunk, (c+1)*chunk) for head h into a scratch
-// row; the last of the C workgroups of head h to finish (atomic counter, the
-// pattern of a split reduction) runs the softmax and P.V for the head from
-// the complete row and quantizes its output groups for the output
-// projection.  k_attention (prompt batches) keeps one workgroup per
+// k_attn_decode (one token): grid (n_heads, head_size/32), one workgroup
+// per 32 output dimensions of a head, independent of every other
+// workgroup.  k_attention (prompt batches) keeps one workgroup per
 // (head, token) with the causal mask of the whole call's span.
 #include <hip/hip_runtime.h>
 
@@ -21,7 +18,6 @@
 namespace yl {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnTile = 64;   // positions per LDS K tile
 
 template <int QF>
 __device__ void quantize_head_output(const float* outl, int hd, int8_t* aq, float* as, size_t group0) {
@@ -36,151 +32,154 @@ __device__ void quantize_head_output(const float* outl, int hd, int8_t* aq, floa
     }
 }
 
-// LDS (floats): q hd | K tile kAttnTile*(hd+4) in phase 1, reused for the
-// scores max_seq(+pad) in phase 2 | transposed p 8*PCS | partials 8*hd |
-// out hd | reduction 16
-__host__ __device__ inline size_t attn_decode_region(int max_seq, int hd) {
-    const size_t a = (size_t)kAttnTile * (hd + 4), b = ((size_t)max_seq + 3) & ~(size_t)3;
-    return a > b ? a : b;
-}
-__host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq / 8 + 1 + 3) & ~3) + 4; }
-__host__ __device__ inline size_t attn_decode_lds_floats(int max_seq, int hd) {
-    return (size_t)hd + attn_decode_region(max_seq, hd) + 8 * (size_t)attn_pt_stride(max_seq) + 9 * (size_t)hd + 16;
-}
-
-// Decode kernel: 512 threads.  Phase 2 keeps each thread's P.V chains'
-// V values for up to kVChunk chain steps (and the seq_len % 8 tail rows) in
-// registers, loaded before the softmax so their HBM latency overlaps the
-// max / exp / serial sum.
+// ---------------------------------------------------------------------------
+// Decode (one token).  Workgroup (h, ds) owns query head h and the 32
+// output dimensions [32*ds, 32*ds + 32) of it -- exactly one quantization
+// group of the attention output -- and needs no other workgroup:
+//   1. scores of all seq positions, one position per thread per round, the K
+//      row loaded straight into registers and q read as uniform (scalar)
+//      values; every workgroup of the head recomputes them (K is read from
+//      L2 after the first);
+//   2. max, exp, and the serial sum (one lane, LDS reads kept in flight);
+//   3. the P.V chains of its 32 dimensions, V prefetched into registers
+//      while the softmax runs;
+//   4. the 8-lane reduction + tail, and the quantized group.
+// LDS (floats): e/p row kDecScLen | transposed p 8*PCS | partials 8*32 |
+// out 32 | reduction 16
+// ---------------------------------------------------------------------------
 constexpr int kDecThreads = 512;
+constexpr int kDecDims = 32;                   // output dims per workgroup
+constexpr int kDecChains = 8 * kDecDims;       // P.V chains per workgroup
+constexpr int kDecVSteps = 64;                 // chain steps of V held in registers
+
+__host__ __device__ inline int attn_sc_len(int max_seq) { return (max_seq + 63) & ~63; }
+__host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq / 8 + 1 + 3) & ~3) + 4; }
+__host__ __device__ inline size_t attn_decode_lds_floats(int max_seq) {
+    return (size_t)attn_sc_len(max_seq) + 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16;
+}
 
 template <int QF, int HD>
-__global__ __launch_bounds__(kDecThreads) void k_attn_decode(const float* __restrict__ sq,
-                                                             const float* __restrict__ kc,
-                                                             const float* __restrict__ vc,
-                                                             const StepState* __restrict__ st, int n_heads,
-                                                             int n_kv_heads, float attn_scale, int max_seq,
-                                                             float* __restrict__ scores,
-                                                             unsigned* __restrict__ counters,
-                                                             int8_t* __restrict__ aq, float* __restrict__ as,
-                                                             float* __restrict__ att_f32) {
-    constexpr int hd = HD;
-    constexpr int CPT = (8 * HD + kDecThreads - 1) / kDecThreads;   // P.V chains per thread
-    constexpr int kVChunk = 128 / CPT;                               // chain steps held in registers
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_decode(
+    const float* __restrict__ sq, const float* __restrict__ kc, const float* __restrict__ vc,
+    const StepState* __restrict__ st, int n_heads, int n_kv_heads, float attn_scale, int max_seq,
+    int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32) {
+    constexpr int RB = HD == 128 ? 1 : (HD == 64 ? 2 : 4);   // score rounds per load batch
     extern __shared__ __align__(16) float lds[];
-    __shared__ int is_last;
-    const int h = blockIdx.x, c = blockIdx.y, C = gridDim.y, tid = threadIdx.x;
+    const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x;
     const int kvh = h / (n_heads / n_kv_heads);
-    const int kv_dim = n_kv_heads * hd;
+    const int kv_dim = n_kv_heads * HD;
     const int seq = st->pos + 1;
-    const int chunk = (seq + C - 1) / C;
-    const int p0 = c * chunk;
-    const int p1 = min(seq, p0 + chunk);
-    constexpr int KS = hd + 4;
-    float* ql = lds;
-    float* kt = ql + hd;
-    float* sc = kt;
-    float* pt = kt + attn_decode_region(max_seq, hd);
-    float* part = pt + 8 * attn_pt_stride(max_seq);
-    float* outl = part + 8 * hd;
-    float* red = outl + hd;
-    float* srow = scores + (size_t)h * max_seq;
+    const int n_chunks = seq / 8;
+    const int PCS = attn_pt_stride(max_seq);
+    float* sc = lds;
+    float* pt = sc + attn_sc_len(max_seq);
+    float* part = pt + 8 * PCS;
+    float* outl = part + kDecChains;
+    float* red = outl + kDecDims;
+    const float* __restrict__ qh = sq + (size_t)h * HD;
+    const float* kbase = kc + (size_t)kvh * HD;
+    // chain (j, d) of this thread (tid < kDecChains): lane j of position
+    // group c, output dimension d of this workgroup's slice
+    const int cj = (tid >> 5) & 7, cd = tid & 31;
+    const float* vcol = vc + (size_t)kvh * HD + ds * kDecDims + cd;
 
-    for (int i = tid; i < hd; i += kDecThreads) ql[i] = sq[(size_t)h * hd + i];
-    // phase 1: scores of this workgroup's positions
-    for (int base = p0; base < p1; base += kAttnTile) {
-        const int cnt = min(kAttnTile, p1 - base);
-        __syncthreads();
-        constexpr int h4 = hd / 4;
-        for (int e = tid; e < cnt * h4; e += kDecThreads) {
-            const int r = e / h4, q4 = e - r * h4;
-            const float4 v = *reinterpret_cast<const float4*>(kc + (size_t)(base + r) * kv_dim + (size_t)kvh * hd + q4 * 4);
-            *reinterpret_cast<float4*>(kt + r * KS + q4 * 4) = v;
+    // 1. scores; the V values of the first kDecVSteps chain steps are issued
+    // after the first K batch (loads retire in order: waiting for K does
+    // not wait for V)
+    float vbuf[kDecVSteps];
+    float vtail[7];
+    float lmax = -1e10f;
+    for (int r0 = 0; r0 * kDecThreads < seq; r0 += RB) {
+        vf4 kr[RB][HD / 4];
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            const int p = min((r0 + r) * kDecThreads + tid, seq - 1);
+            const vf4* k4 = reinterpret_cast<const vf4*>(kbase + (size_t)p * kv_dim);
+#pragma unroll
+            for (int i = 0; i < HD / 4; i++) kr[r][i] = k4[i];
         }
-        __syncthreads();
-        if (tid < cnt) {
-            const float* kr = kt + tid * KS;
+        if (r0 == 0) {
+#pragma unroll
+            for (int i = 0; i < kDecVSteps; i++) vbuf[i] = vcol[(size_t)min(8 * i + cj, seq - 1) * kv_dim];
+#pragma unroll
+            for (int i = 0; i < 7; i++) vtail[i] = vcol[(size_t)min(n_chunks * 8 + i, seq - 1) * kv_dim];
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            const int p = (r0 + r) * kDecThreads + tid;
             float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-            for (int s = 0; s < hd / 8; s++) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) l[j] = fadd(l[j], fmul(ql[s * 8 + j], kr[s * 8 + j]));
+            for (int s = 0; s < HD / 8; s++) {
+                const vf4 a = kr[r][2 * s], b = kr[r][2 * s + 1];
+                l[0] = fadd(l[0], fmul(qh[8 * s + 0], a.x));
+                l[1] = fadd(l[1], fmul(qh[8 * s + 1], a.y));
+                l[2] = fadd(l[2], fmul(qh[8 * s + 2], a.z));
+                l[3] = fadd(l[3], fmul(qh[8 * s + 3], a.w));
+                l[4] = fadd(l[4], fmul(qh[8 * s + 4], b.x));
+                l[5] = fadd(l[5], fmul(qh[8 * s + 5], b.y));
+                l[6] = fadd(l[6], fmul(qh[8 * s + 6], b.z));
+                l[7] = fadd(l[7], fmul(qh[8 * s + 7], b.w));
             }
-            srow[base + tid] = fmul(reduce_add8(l), attn_scale);
+            const float sv = fmul(reduce_add8(l), attn_scale);
+            // unconditional store (positions past seq go to a spare slot):
+            // a conditional one would let the compiler sink the K loads
+            // into a divergent branch and wait for them at its end
+            const bool live = p < seq;
+            *(live ? sc + p : red + 15) = sv;
+            lmax = fmaxf(lmax, live ? sv : -1e10f);
         }
-    }
-    // last arriver of this head runs phase 2 (the barrier orders every
-    // thread's score stores before thread 0's release fence and count)
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        const unsigned prev = atomicAdd(counters + h, 1u);
-        is_last = prev == (unsigned)(C - 1) ? 1 : 0;
-        if (is_last) {
-            __threadfence();
-            counters[h] = 0u;
-        }
-    }
-    __syncthreads();
-    if (!is_last) return;
-
-    // softmax: max from -1e10, exp, serial sum, p = e * (1/sum)
-    float lmax = -1e10f;
-    for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
-        const float v = __hip_atomic_load(srow + t2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sc[t2] = v;
-        lmax = fmaxf(lmax, v);
     }
 
-    // V values of this thread's chains (d, j) for the first kVChunk steps,
-    // issued now so they arrive during the softmax (clamped, unconditional
-    // loads: a divergent branch would make the compiler wait at its join)
-    const int n_chunks = seq / 8;
-    const float* vbase = vc + (size_t)kvh * hd;
-    float vtail[7];
-    {
-        const int d = tid < hd ? tid : 0;
-#pragma unroll
-        for (int i = 0; i < 7; i++) vtail[i] = vbase[(size_t)min(n_chunks * 8 + i, seq - 1) * kv_dim + d];
-    }
-    float vbuf[CPT][kVChunk];
-#pragma unroll
-    for (int k = 0; k < CPT; k++) {
-        const int ch = min(tid + k * kDecThreads, 8 * hd - 1);
-        const int j = (ch / hd) & 7, d = ch % hd;
-#pragma unroll
-        for (int i = 0; i < kVChunk; i++) {
-            const int row = min(8 * i + j, seq - 1);
-            vbuf[k][i] = vbase[(size_t)row * kv_dim + d];
-        }
-    }
+    // 2. softmax: max from -1e10 (forward.rs:351-356), e = exp(s - max),
+    // sum_exp serial in position order, p = e * (1 / sum_exp)
     lmax = wave_max(lmax);
     if ((tid & 63) == 0) red[tid >> 6] = lmax;
     __syncthreads();
     float mx = red[0];
+#pragma unroll
     for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
-    for (int t2 = tid; t2 < seq; t2 += kDecThreads) sc[t2] = expf_rn(sc[t2] - mx);
+    const int sc_pad = (seq + 63) & ~63;
+    for (int t2 = tid; t2 < sc_pad; t2 += kDecThreads) sc[t2] = t2 < seq ? expf_rn(sc[t2] - mx) : 0.0f;
     __syncthreads();
     if (tid == 0) {
+        // blocks of 8 vf4s, the next block read before the current one is
+        // added; the zero padding past seq adds nothing
+        const vf4* s4 = reinterpret_cast<const vf4*>(sc);
+        const int nblk = sc_pad / 32;
         float sum = 0.0f;
-        int t2 = 0;
-        const float4* s4 = reinterpret_cast<const float4*>(sc);
-#pragma unroll 8
-        for (; t2 + 4 <= seq; t2 += 4) {
-            const float4 e4 = s4[t2 >> 2];
-            sum = fadd(sum, e4.x);
-            sum = fadd(sum, e4.y);
-            sum = fadd(sum, e4.z);
-            sum = fadd(sum, e4.w);
+        vf4 va[8], vb[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) va[k] = s4[k];
+        for (int b = 0; b < nblk; b += 2) {
+            const int b1 = b + 1 < nblk ? b + 1 : b;
+#pragma unroll
+            for (int k = 0; k < 8; k++) vb[k] = s4[b1 * 8 + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                sum = fadd(sum, va[k].x);
+                sum = fadd(sum, va[k].y);
+                sum = fadd(sum, va[k].z);
+                sum = fadd(sum, va[k].w);
+            }
+            const int b2 = b + 2 < nblk ? b + 2 : b;
+#pragma unroll
+            for (int k = 0; k < 8; k++) va[k] = s4[b2 * 8 + k];
+            if (b + 1 < nblk) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    sum = fadd(sum, vb[k].x);
+                    sum = fadd(sum, vb[k].y);
+                    sum = fadd(sum, vb[k].z);
+                    sum = fadd(sum, vb[k].w);
+                }
+            }
         }
-        for (; t2 < seq; t2++) sum = fadd(sum, sc[t2]);
         red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
     const float inv = red[8];
-    // p = e * inv, kept in sc and also transposed into pt[j][c] = p[8c+j] so
-    // a chain reads its probabilities as consecutive floats
-    const int PCS = attn_pt_stride(max_seq);
+    // p kept in sc (for the tail) and transposed, pt[j][c] = p[8c + j], so a
+    // chain reads its probabilities as consecutive floats
     for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
         const float p = fmul(sc[t2], inv);
         sc[t2] = p;
@@ -188,54 +187,52 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_decode(const float* __rest
     }
     __syncthreads();
 
-    // P.V chains: lane j of position group c, in c order
-    float l[CPT];
+    // 3. P.V chains (forward.rs:372-395): lane j adds p*v over c in order
+    if (tid < kDecChains) {
+        float acc = 0.0f;
+        const float* pj = pt + cj * PCS;
+        for (int c0 = 0; c0 < n_chunks; c0 += kDecVSteps) {
+            if (c0 > 0) {
 #pragma unroll
-    for (int k = 0; k < CPT; k++) l[k] = 0.0f;
-    for (int r0 = 0; r0 < n_chunks; r0 += kVChunk) {
-        if (r0 > 0) {
+                for (int i = 0; i < kDecVSteps; i++)
+                    vbuf[i] = vcol[(size_t)min(8 * (c0 + i) + cj, seq - 1) * kv_dim];
+            }
+            const int steps = min(kDecVSteps, n_chunks - c0);
 #pragma unroll
-            for (int k = 0; k < CPT; k++) {
-                const int ch = min(tid + k * kDecThreads, 8 * hd - 1);
-                const int j = (ch / hd) & 7, d = ch % hd;
-#pragma unroll
-                for (int i = 0; i < kVChunk; i++) {
-                    const int row = min(8 * (r0 + i) + j, seq - 1);
-                    vbuf[k][i] = vbase[(size_t)row * kv_dim + d];
-                }
+            for (int i = 0; i < kDecVSteps; i += 4) {
+                const vf4 p4 = *reinterpret_cast<const vf4*>(pj + c0 + i);
+                if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vbuf[i + 0]));
+                if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vbuf[i + 1]));
+                if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vbuf[i + 2]));
+                if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vbuf[i + 3]));
             }
         }
-        const int steps = min(kVChunk, n_chunks - r0);
-#pragma unroll
-        for (int k = 0; k < CPT; k++) {
-            const int ch = tid + k * kDecThreads;
-            const float* pj = pt + ((ch / hd) & 7) * PCS + r0;
-            float acc = l[k];
-#pragma unroll
-            for (int i = 0; i < kVChunk; i++)
-                if (i < steps) acc = fadd(acc, fmul(pj[i], vbuf[k][i]));
-            if (ch < 8 * hd) l[k] = acc;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < CPT; k++) {
-        const int ch = tid + k * kDecThreads;
-        if (ch < 8 * hd) part[(ch / hd) * hd + (ch % hd)] = l[k];
+        part[cj * kDecDims + cd] = acc;
     }
     __syncthreads();
-    for (int d = tid; d < hd; d += kDecThreads) {
+
+    // 4. out[d] = reduce_add(8 lane chains) + the seq % 8 tail in order,
+    // then the 32-group quantization of the output projection's input
+    if (tid < kDecDims) {
         float lj[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) lj[j] = part[j * hd + d];
-        float sum = reduce_add8(lj);
+        for (int j = 0; j < 8; j++) lj[j] = part[j * kDecDims + tid];
+        float out = reduce_add8(lj);
 #pragma unroll
         for (int i = 0; i < 7; i++)
-            if (n_chunks * 8 + i < seq) sum = fadd(sum, fmul(sc[n_chunks * 8 + i], vtail[i]));
-        outl[d] = sum;
-        if (att_f32) att_f32[(size_t)h * hd + d] = sum;
+            if (n_chunks * 8 + i < seq) out = fadd(out, fmul(sc[n_chunks * 8 + i], vtail[i]));
+        const size_t col = (size_t)h * HD + (size_t)ds * kDecDims + tid;
+        if (att_f32) att_f32[col] = out;
+        if constexpr (QF >= 0) {
+            float am = fabsf(out);
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+            am = fmaxf(am, 0.0f);
+            const float s = group_scale<QF>(am);
+            aq[col] = (int8_t)quant_one<QF>(out, s);
+            if (tid == 0) as[col / kGroup] = s;
+        }
     }
-    __syncthreads();
-    if constexpr (QF >= 0) quantize_head_output<QF>(outl, hd, aq, as, ((size_t)h * hd) / kGroup);
 }
 
 // ---------------------------------------------------------------------------
@@ -358,59 +355,47 @@ hipError_t launch_attention(const float* sq, const float* kc, const float* vc, c
     return hipGetLastError();
 }
 
-int attn_decode_splits(int max_seq) {
-    // enough workgroups per head to spread the K reads, few enough that the
-    // per-head counter sees little contention
-    int c = (max_seq + 255) / 256;
-    return c < 4 ? 4 : (c > 16 ? 16 : c);
-}
+size_t attn_decode_lds_bytes(int max_seq) { return attn_decode_lds_floats(max_seq) * sizeof(float); }
 
-size_t attn_decode_lds_bytes(int max_seq, int hd) { return attn_decode_lds_floats(max_seq, hd) * sizeof(float); }
-
-template <int QF>
-static hipError_t launch_attn_decode_q(const float* sq, const float* kc, const float* vc, const StepState* st,
-                                       int max_seq, int n_heads, int n_kv_heads, int hd, float scale, float* scores,
-                                       unsigned* counters, int8_t* aq, float* as, float* att_f32, hipStream_t s) {
-    const size_t smem = attn_decode_lds_bytes(max_seq, hd);
-    const dim3 grid(n_heads, attn_decode_splits(max_seq));
+template <int QF, int HD>
+static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const float* vc, const StepState* st,
+                                       int max_seq, int n_heads, int n_kv_heads, float scale, int8_t* aq, float* as,
+                                       float* att_f32, hipStream_t s) {
+    const size_t smem = attn_decode_lds_bytes(max_seq);
     if (smem > 65536) {
         // long contexts: opt in to more than the default 64 KiB of LDS
-        hipError_t e = hipSuccess;
-        if (hd == 32) e = hipFuncSetAttribute((const void*)&k_attn_decode<QF, 32>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (hd == 64) e = hipFuncSetAttribute((const void*)&k_attn_decode<QF, 64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (hd == 128) e = hipFuncSetAttribute((const void*)&k_attn_decode<QF, 128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<QF, HD>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return e;
     }
-    switch (hd) {
-    case 32:
-        hipLaunchKernelGGL((k_attn_decode<QF, 32>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
-                           n_kv_heads, scale, max_seq, scores, counters, aq, as, att_f32);
-        break;
-    case 64:
-        hipLaunchKernelGGL((k_attn_decode<QF, 64>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
-                           n_kv_heads, scale, max_seq, scores, counters, aq, as, att_f32);
-        break;
-    case 128:
-        hipLaunchKernelGGL((k_attn_decode<QF, 128>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
-                           n_kv_heads, scale, max_seq, scores, counters, aq, as, att_f32);
-        break;
-    default:
-        return hipErrorInvalidValue;
-    }
+    hipLaunchKernelGGL((k_attn_decode<QF, HD>), dim3(n_heads, HD / kDecDims), dim3(kDecThreads), smem, s, sq, kc, vc,
+                       st, n_heads, n_kv_heads, scale, max_seq, aq, as, att_f32);
     return hipGetLastError();
 }
 
+template <int QF>
+static hipError_t launch_attn_decode_q(const float* sq, const float* kc, const float* vc, const StepState* st,
+                                       int max_seq, int n_heads, int n_kv_heads, int hd, float scale, int8_t* aq,
+                                       float* as, float* att_f32, hipStream_t s) {
+    switch (hd) {
+    case 32: return launch_attn_decode_k<QF, 32>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 64: return launch_attn_decode_k<QF, 64>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 128: return launch_attn_decode_k<QF, 128>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st, int max_seq,
-                              int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, float* scores,
-                              unsigned* counters, int8_t* aq, float* as, float* att_f32, hipStream_t s) {
+                              int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, int8_t* aq, float* as,
+                              float* att_f32, hipStream_t s) {
     if (qfmt == kQ8)
-        return launch_attn_decode_q<kQ8>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, scores,
-                                         counters, aq, as, att_f32, s);
+        return launch_attn_decode_q<kQ8>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as,
+                                         att_f32, s);
     if (qfmt == kQ4)
-        return launch_attn_decode_q<kQ4>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, scores,
-                                         counters, aq, as, att_f32, s);
-    return launch_attn_decode_q<-1>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, scores, counters,
-                                    aq, as, att_f32, s);
+        return launch_attn_decode_q<kQ4>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as,
+                                         att_f32, s);
+    return launch_attn_decode_q<-1>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as, att_f32,
+                                    s);
 }
 
 }  // namespace yl

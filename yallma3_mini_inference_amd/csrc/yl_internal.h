@@ -90,12 +90,10 @@ hipError_t launch_attention(const float* sq, const float* kc, const float* vc, c
                             int batch, int max_seq, int n_heads, int n_kv_heads, int head_size,
                             float scale, int qfmt, int8_t* aq, float* as, float* att_f32,
                             hipStream_t s);
-int attn_decode_splits(int max_seq);
-size_t attn_decode_lds_bytes(int max_seq, int hd);
+size_t attn_decode_lds_bytes(int max_seq);
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st,
                               int max_seq, int n_heads, int n_kv_heads, int head_size, float scale,
-                              int qfmt, float* scores, unsigned* counters, int8_t* aq, float* as,
-                              float* att_f32, hipStream_t s);
+                              int qfmt, int8_t* aq, float* as, float* att_f32, hipStream_t s);
 hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,
                        float* q, float* k, int n_heads, int n_kv_heads, int head_size, hipStream_t s);
 hipError_t launch_swiglu_quant(int qfmt, const float* gate, const float* up, int hidden, int batch,

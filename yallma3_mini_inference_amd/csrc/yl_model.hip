@@ -274,8 +274,6 @@ struct yl_session {
     float *x = nullptr, *sq = nullptr, *logits = nullptr;
     int8_t *aq = nullptr, *hq = nullptr;
     float *as_ = nullptr, *hs = nullptr;
-    float* scores = nullptr;        // [n_heads][ctx] attention score rows (decode)
-    unsigned* counters = nullptr;   // [n_heads] finished attention splits per head
     unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
@@ -594,7 +592,7 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
         if (prof) prof->begin(1);
         if (batch == 1)
             YL_TRY(launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->n_heads, m->n_kv, m->hd, m->attn_scale,
-                                      L.wo.fmt, s->scores, s->counters, s->aq, s->as_, nullptr, st));
+                                      L.wo.fmt, s->aq, s->as_, nullptr, st));
         else
             YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->n_heads, m->n_kv, m->hd,
                                     m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st));
@@ -836,14 +834,26 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     }
     if (batch == 0) return YL_OK;
     const size_t seq = start_pos + batch;
-    if (seq * 4 + (size_t)hd * 40 > 60 * 1024) { set_error("attention: seq_len too long for one workgroup"); return YL_ERR_UNSUPPORTED; }
+    // one token: the decode kernel (as in a decode step); several: the
+    // prompt kernel, whose workgroup holds a whole score row
+    if (batch > 1 && seq * 4 + (size_t)hd * 40 > 60 * 1024) {
+        set_error("attention: seq_len too long for one workgroup");
+        return YL_ERR_UNSUPPORTED;
+    }
+    if (batch == 1 && (hd % 32 || attn_decode_lds_bytes((int)seq) > 160 * 1024)) {
+        set_error("attention: unsupported head size or seq_len for the decode kernel");
+        return YL_ERR_UNSUPPORTED;
+    }
     StepState* dst = nullptr;
     StepState hst{};
     hst.pos = (int32_t)start_pos;
     hipStream_t strm = (hipStream_t)stream;
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
     if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
+    if (e == hipSuccess && batch == 1)
+        e = launch_attn_decode(q, kc, vc, dst, (int)seq, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
+                               nullptr, nullptr, out, strm);
+    else if (e == hipSuccess)
         e = launch_attention(q, kc, vc, dst, (int)batch, (int)seq, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale,
                              -1, nullptr, nullptr, out, strm);
     if (e == hipSuccess) e = hipStreamSynchronize(strm);
@@ -922,9 +932,6 @@ yl_session* yl_create_session(const yl_model* m) {
               hipHostMalloc(&s->st_host, sizeof(StepState), 0) == hipSuccess &&
               hipMalloc(&s->logits, (size_t)m->vocab * 4 + 256) == hipSuccess &&
               hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->scores, (size_t)m->n_heads * m->ctx * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->counters, (size_t)m->n_heads * 4 + 256) == hipSuccess &&
-              hipMemset(s->counters, 0, (size_t)m->n_heads * 4 + 256) == hipSuccess &&
               hipMalloc(&s->keys, (size_t)logits_blocks(m->emb) * 8 + 256) == hipSuccess && session_grow(s, 1);
     if (!ok) {
         if (yl_last_error()[0] == 0) set_error("session allocation failed");
@@ -939,7 +946,7 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->graph) hipGraphExecDestroy(s->graph);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->scores, s->counters, s->keys, s->tokens};
+                   s->as_, s->hs, s->keys, s->tokens};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
