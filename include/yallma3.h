@@ -190,7 +190,10 @@ yl_status yl_session_reset(yl_session *s);
  * forward pass itself only reads start_pos). */
 uint32_t yl_session_pos(const yl_session *s);
 void yl_session_set_pos(yl_session *s, uint32_t pos);
-/* Device pointers of the KV cache [n_layers][ctx_len][kv_dim] (f32). */
+/* Device pointers of the KV cache (f32), each `floats` = n_layers * kv_ld *
+ * kv_dim long, kv_ld = ctx_len rounded up to a multiple of 4: values
+ * [n_layers][kv_ld][kv_dim] as in the reference (rows past ctx_len unused),
+ * keys transposed per layer, [n_layers][kv_dim][kv_ld]. */
 yl_status yl_session_kv(yl_session *s, float **key_cache, float **value_cache, size_t *floats);
 
 /* Transformer::forward_x: tokens (host) at start_pos..start_pos+n-1; writes

@@ -12,6 +12,7 @@
 // (head, token) with the causal mask of the whole call's span.
 #include <hip/hip_runtime.h>
 
+#include "yl_blocks.h"
 #include "yl_device.h"
 #include "yl_internal.h"
 
@@ -36,99 +37,189 @@ __device__ void quantize_head_output(const float* outl, int hd, int8_t* aq, floa
 // Decode (one token).  Workgroup (h, ds) owns query head h and the 32
 // output dimensions [32*ds, 32*ds + 32) of it -- exactly one quantization
 // group of the attention output -- and needs no other workgroup:
-//   1. scores of all seq positions, one position per thread per round, the K
-//      row loaded straight into registers and q read as uniform (scalar)
-//      values; every workgroup of the head recomputes them (K is read from
-//      L2 after the first);
+//   1. scores: thread t scores positions 4t..4t+3 (+ 4*512 per round); the
+//      key cache is transposed ([kv_dim][kv_ld]), so one 16-byte load per
+//      lane brings a key dimension of 4 positions, and the dimensions are
+//      consumed in groups of 8 (the reference's lane partials) with the next
+//      group's loads in flight; q is read as uniform (scalar) values;
 //   2. max, exp, and the serial sum (one lane, LDS reads kept in flight);
-//   3. the P.V chains of its 32 dimensions, V prefetched into registers
-//      while the softmax runs;
+//   3. the P.V chains of its 32 dimensions, reading V from LDS tiles of 256
+//      positions that LDS DMA (16 bytes per lane) fills up to 4 tiles ahead;
 //   4. the 8-lane reduction + tail, and the quantized group.
-// LDS (floats): e/p row kDecScLen | transposed p 8*PCS | partials 8*32 |
-// out 32 | reduction 16
+// Only 16-byte loads per lane keep the CU's memory pipeline at full width
+// (a 4-byte load per lane moves a quarter of the bytes per address cycle).
+// Scores, exponentials and probabilities live in one transposed array,
+// pt[j][c] = x[8c + j], the layout the chains read.
+// LDS (floats): pt 8*PCS | V tiles n_vt*256*32 | partials 8*32 | out 32 |
+// reduction 16
 // ---------------------------------------------------------------------------
 constexpr int kDecThreads = 512;
 constexpr int kDecDims = 32;                   // output dims per workgroup
 constexpr int kDecChains = 8 * kDecDims;       // P.V chains per workgroup
-constexpr int kDecVSteps = 64;                 // chain steps of V held in registers
+constexpr int kVTileRows = 256;                // V rows (positions) per LDS tile
+constexpr int kVTileFloats = kVTileRows * kDecDims;
+constexpr int kMaxVTiles = 4;                  // V tiles in flight
+constexpr int kDecLdsBudget = 156 * 1024;      // LDS bytes one workgroup may use
+constexpr int kBufFlags = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
 
-__host__ __device__ inline int attn_sc_len(int max_seq) { return (max_seq + 63) & ~63; }
-__host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq / 8 + 1 + 3) & ~3) + 4; }
+// pt row stride: positions up to max_seq rounded to 64 (the serial sum
+// reads zero padding to that length), + 4 floats to spread banks
+__host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq + 63) & ~63) / 8 + 4; }
+__host__ __device__ inline size_t attn_fixed_lds_floats(int max_seq) {
+    return 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16;
+}
+// V tile buffers that fit beside the fixed part (0: fewer than 2 fit)
+__host__ __device__ inline int attn_v_tiles(int max_seq) {
+    const long long free_b = kDecLdsBudget - (long long)attn_fixed_lds_floats(max_seq) * 4;
+    const int n = free_b > 0 ? (int)(free_b / (kVTileFloats * 4)) : 0;
+    return n >= 2 ? (n > kMaxVTiles ? kMaxVTiles : n) : 0;
+}
 __host__ __device__ inline size_t attn_decode_lds_floats(int max_seq) {
-    return (size_t)attn_sc_len(max_seq) + 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16;
+    return attn_fixed_lds_floats(max_seq) + (size_t)attn_v_tiles(max_seq) * kVTileFloats;
+}
+
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ vf4 buf_load_f32x4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// LDS DMA of V rows [r0, r0 + kVTileRows) of 32 columns from col0 into an
+// LDS tile [kVTileRows][32]: one instruction moves 8 rows (64 lanes x 16
+// bytes); each wavefront issues exactly kVTileDmaPerWave of them.  Rows
+// past `rows` re-read the last one (never used).
+constexpr int kVTileDmaPerWave = kVTileRows / 8 / (kDecThreads / 64);
+__device__ __forceinline__ void v_tile_dma(float* tile, const float* __restrict__ vc, int kv_dim, int col0, int r0,
+                                           int rows) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < kVTileDmaPerWave; k++) {
+        const int g = wave + k * (kDecThreads / 64);
+        const int row = min(r0 + g * 8 + (lane >> 3), rows - 1);
+        __builtin_amdgcn_global_load_lds(vc + (size_t)row * kv_dim + col0 + (lane & 7) * 4, tile + g * 8 * kDecDims,
+                                         16, 0, 0);
+    }
+}
+// Waits until at most `later` tiles' DMA of this wavefront is in flight.
+__device__ __forceinline__ void wait_v_tiles(int later) {
+    static_assert(kVTileDmaPerWave == 4, "wait counts below assume 4 DMA instructions per tile");
+    switch (later) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    }
 }
 
 template <int QF, int HD>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_decode(
     const float* __restrict__ sq, const float* __restrict__ kc, const float* __restrict__ vc,
-    const StepState* __restrict__ st, int n_heads, int n_kv_heads, float attn_scale, int max_seq,
-    int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32) {
-    constexpr int RB = HD == 128 ? 1 : (HD == 64 ? 2 : 4);   // score rounds per load batch
+    const StepState* __restrict__ st, int n_heads, int n_kv_heads, float attn_scale, int max_seq, int kv_ld,
+    int n_vt, int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = h / (n_heads / n_kv_heads);
     const int kv_dim = n_kv_heads * HD;
     const int seq = st->pos + 1;
     const int n_chunks = seq / 8;
     const int PCS = attn_pt_stride(max_seq);
-    float* sc = lds;
-    float* pt = sc + attn_sc_len(max_seq);
-    float* part = pt + 8 * PCS;
+    float* pt = lds;
+    float* vt = pt + 8 * PCS;
+    float* part = vt + n_vt * kVTileFloats;
     float* outl = part + kDecChains;
     float* red = outl + kDecDims;
     const float* __restrict__ qh = sq + (size_t)h * HD;
-    const float* kbase = kc + (size_t)kvh * HD;
-    // chain (j, d) of this thread (tid < kDecChains): lane j of position
-    // group c, output dimension d of this workgroup's slice
-    const int cj = (tid >> 5) & 7, cd = tid & 31;
-    const float* vcol = vc + (size_t)kvh * HD + ds * kDecDims + cd;
+    const int col0 = kvh * HD + ds * kDecDims;
+    // keys of this kv head through a buffer descriptor: a per-lane 32-bit
+    // offset (4 positions) and a uniform offset per key dimension, so no
+    // load needs a 64-bit address register; quads start at most at the last
+    // position, and rows are kv_ld >= seq (a multiple of 4) long, so every
+    // 16-byte read stays inside its row
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(kc + (size_t)kvh * HD * kv_ld), (short)0, HD * kv_ld * 4, kBufFlags);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(vc), (short)0, max_seq * kv_dim * 4, kBufFlags);
 
-    // 1. scores; the V values of the first kDecVSteps chain steps are issued
-    // after the first K batch (loads retire in order: waiting for K does
-    // not wait for V)
-    float vbuf[kDecVSteps];
+    // the seq % 8 tail rows of V, for the output threads (tid < 32)
     float vtail[7];
+#pragma unroll
+    for (int i = 0; i < 7; i++)
+        vtail[i] = buf_load_f32(vrs, (col0 + (tid & 31)) * 4, min(n_chunks * 8 + i, seq - 1) * kv_dim * 4);
+
+    // 1. scores -> pt (transposed)
+    const int n_quads = (seq + 3) / 4;
     float lmax = -1e10f;
-    for (int r0 = 0; r0 * kDecThreads < seq; r0 += RB) {
-        vf4 kr[RB][HD / 4];
+    // each wavefront walks its own 64-quad slices (wavefronts past the last
+    // quad do not enter)
+    const int lane = tid & 63;
+    for (int q0 = wave * 64; q0 < n_quads; q0 += kDecThreads) {
+        const int quad = min(q0 + lane, n_quads - 1);
+        const int voff = quad * 16;
+        float l[4][8];
 #pragma unroll
-        for (int r = 0; r < RB; r++) {
-            const int p = min((r0 + r) * kDecThreads + tid, seq - 1);
-            const vf4* k4 = reinterpret_cast<const vf4*>(kbase + (size_t)p * kv_dim);
+        for (int pp = 0; pp < 4; pp++)
 #pragma unroll
-            for (int i = 0; i < HD / 4; i++) kr[r][i] = k4[i];
+            for (int j = 0; j < 8; j++) l[pp][j] = 0.0f;
+        // the query pointer and the row offset are made opaque per slice, so
+        // the per-dimension query values and row offsets are not hoisted
+        // out of the slice loop (they would need a scalar register each)
+        // (readfirstlane: asm results count as divergent, and a divergent
+        // index would turn the scalar query loads into vector ones)
+        int row_off = 0, q_off = 0;
+        asm volatile("" : "+s"(row_off), "+s"(q_off));
+        row_off = __builtin_amdgcn_readfirstlane(row_off);
+        const float* qp = qh + __builtin_amdgcn_readfirstlane(q_off);
+        const int row_step = kv_ld * 4;
+        vf4 kq[2][8];
+        float qg[2][8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            kq[0][j] = buf_load_f32x4(krs, voff, row_off + j * row_step);
+            qg[0][j] = qp[j];
         }
-        if (r0 == 0) {
 #pragma unroll
-            for (int i = 0; i < kDecVSteps; i++) vbuf[i] = vcol[(size_t)min(8 * i + cj, seq - 1) * kv_dim];
+        for (int s = 0; s < HD / 8; s++) {
+            if (s + 1 < HD / 8) {
 #pragma unroll
-            for (int i = 0; i < 7; i++) vtail[i] = vcol[(size_t)min(n_chunks * 8 + i, seq - 1) * kv_dim];
-        }
-#pragma unroll
-        for (int r = 0; r < RB; r++) {
-            const int p = (r0 + r) * kDecThreads + tid;
-            float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-            for (int s = 0; s < HD / 8; s++) {
-                const vf4 a = kr[r][2 * s], b = kr[r][2 * s + 1];
-                l[0] = fadd(l[0], fmul(qh[8 * s + 0], a.x));
-                l[1] = fadd(l[1], fmul(qh[8 * s + 1], a.y));
-                l[2] = fadd(l[2], fmul(qh[8 * s + 2], a.z));
-                l[3] = fadd(l[3], fmul(qh[8 * s + 3], a.w));
-                l[4] = fadd(l[4], fmul(qh[8 * s + 4], b.x));
-                l[5] = fadd(l[5], fmul(qh[8 * s + 5], b.y));
-                l[6] = fadd(l[6], fmul(qh[8 * s + 6], b.z));
-                l[7] = fadd(l[7], fmul(qh[8 * s + 7], b.w));
+                for (int j = 0; j < 8; j++) {
+                    kq[(s + 1) & 1][j] = buf_load_f32x4(krs, voff, row_off + (8 * (s + 1) + j) * row_step);
+                    qg[(s + 1) & 1][j] = qp[8 * (s + 1) + j];
+                }
             }
-            const float sv = fmul(reduce_add8(l), attn_scale);
+            // one group ahead only
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float qv = qg[s & 1][j];
+                const vf4 k4 = kq[s & 1][j];
+                l[0][j] = fadd(l[0][j], fmul(qv, k4.x));
+                l[1][j] = fadd(l[1][j], fmul(qv, k4.y));
+                l[2][j] = fadd(l[2][j], fmul(qv, k4.z));
+                l[3][j] = fadd(l[3][j], fmul(qv, k4.w));
+            }
+            // the group's products are complete here: left free, the
+            // compiler defers the .y/.z/.w lanes and keeps every key vector
+            // of every group alive
+#pragma unroll
+            for (int j = 0; j < 8; j++) asm volatile("" : "+v"(l[0][j]), "+v"(l[1][j]), "+v"(l[2][j]), "+v"(l[3][j]));
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) {
+            const int p = (q0 + lane) * 4 + pp;
+            const float sv = fmul(reduce_add8(l[pp]), attn_scale);
             // unconditional store (positions past seq go to a spare slot):
             // a conditional one would let the compiler sink the K loads
             // into a divergent branch and wait for them at its end
             const bool live = p < seq;
-            *(live ? sc + p : red + 15) = sv;
+            *(live ? pt + (p & 7) * PCS + (p >> 3) : red + 15) = sv;
             lmax = fmaxf(lmax, live ? sv : -1e10f);
         }
     }
+    // the first V tiles start now; their latency overlaps the softmax
+    const int n_tiles = (8 * n_chunks + kVTileRows - 1) / kVTileRows;
+    for (int t = 0; t < n_tiles && t < n_vt; t++) v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
 
     // 2. softmax: max from -1e10 (forward.rs:351-356), e = exp(s - max),
     // sum_exp serial in position order, p = e * (1 / sum_exp)
@@ -138,77 +229,80 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     float mx = red[0];
 #pragma unroll
     for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
-    const int sc_pad = (seq + 63) & ~63;
-    for (int t2 = tid; t2 < sc_pad; t2 += kDecThreads) sc[t2] = t2 < seq ? expf_rn(sc[t2] - mx) : 0.0f;
+    const int pad = (seq + 63) & ~63;
+    for (int t2 = tid; t2 < pad; t2 += kDecThreads) {
+        float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
+        *e = t2 < seq ? expf_rn(*e - mx) : 0.0f;
+    }
     __syncthreads();
     if (tid == 0) {
-        // blocks of 8 vf4s, the next block read before the current one is
-        // added; the zero padding past seq adds nothing
-        const vf4* s4 = reinterpret_cast<const vf4*>(sc);
-        const int nblk = sc_pad / 32;
+        // blocks of 32 positions = 4 columns of the 8 rows, read as 8 vf4s;
+        // each block's reads are issued before the previous block is added
+        // (the scheduling barriers keep that order); the number of blocks
+        // is even and the zero padding adds nothing
+        const int nblk = pad / 32;
         float sum = 0.0f;
         vf4 va[8], vb[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) va[k] = s4[k];
+        for (int j = 0; j < 8; j++) va[j] = *reinterpret_cast<const vf4*>(pt + j * PCS);
         for (int b = 0; b < nblk; b += 2) {
-            const int b1 = b + 1 < nblk ? b + 1 : b;
 #pragma unroll
-            for (int k = 0; k < 8; k++) vb[k] = s4[b1 * 8 + k];
+            for (int j = 0; j < 8; j++) vb[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * (b + 1));
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                sum = fadd(sum, va[k].x);
-                sum = fadd(sum, va[k].y);
-                sum = fadd(sum, va[k].z);
-                sum = fadd(sum, va[k].w);
-            }
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) sum = fadd(sum, va[j][c]);
             const int b2 = b + 2 < nblk ? b + 2 : b;
 #pragma unroll
-            for (int k = 0; k < 8; k++) va[k] = s4[b2 * 8 + k];
-            if (b + 1 < nblk) {
+            for (int j = 0; j < 8; j++) va[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * b2);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    sum = fadd(sum, vb[k].x);
-                    sum = fadd(sum, vb[k].y);
-                    sum = fadd(sum, vb[k].z);
-                    sum = fadd(sum, vb[k].w);
-                }
-            }
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) sum = fadd(sum, vb[j][c]);
         }
         red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
     const float inv = red[8];
-    // p kept in sc (for the tail) and transposed, pt[j][c] = p[8c + j], so a
-    // chain reads its probabilities as consecutive floats
     for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
-        const float p = fmul(sc[t2], inv);
-        sc[t2] = p;
-        pt[(t2 & 7) * PCS + (t2 >> 3)] = p;
+        float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
+        *e = fmul(*e, inv);
     }
-    __syncthreads();
 
-    // 3. P.V chains (forward.rs:372-395): lane j adds p*v over c in order
-    if (tid < kDecChains) {
-        float acc = 0.0f;
-        const float* pj = pt + cj * PCS;
-        for (int c0 = 0; c0 < n_chunks; c0 += kDecVSteps) {
-            if (c0 > 0) {
+    // 3. P.V chains (forward.rs:372-395): lane j adds p*v over c in order.
+    // Chain (j, d) of thread tid < kDecChains: j = tid / 32, d = tid % 32.
+    const int cj = (tid >> 5) & 7, cd = tid & 31;
+    float acc = 0.0f;
+    for (int t = 0; t < n_tiles; t++) {
+        // this wavefront's DMA into tile t; the later tiles already issued
+        // may stay in flight
+        wait_v_tiles(min(n_vt - 1, n_tiles - 1 - t));
+        __syncthreads();    // everyone's DMA (and, for t = 0, the p row)
+        const float* tile = vt + (t % n_vt) * kVTileFloats;
+        if (tid < kDecChains) {
+            const int c0 = t * (kVTileRows / 8);
+            const int steps = min(kVTileRows / 8, n_chunks - c0);
+            const float* pj = pt + cj * PCS + c0;
+            float vv[kVTileRows / 8];
 #pragma unroll
-                for (int i = 0; i < kDecVSteps; i++)
-                    vbuf[i] = vcol[(size_t)min(8 * (c0 + i) + cj, seq - 1) * kv_dim];
-            }
-            const int steps = min(kDecVSteps, n_chunks - c0);
+            for (int i = 0; i < kVTileRows / 8; i++) vv[i] = tile[(8 * i + cj) * kDecDims + cd];
 #pragma unroll
-            for (int i = 0; i < kDecVSteps; i += 4) {
-                const vf4 p4 = *reinterpret_cast<const vf4*>(pj + c0 + i);
-                if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vbuf[i + 0]));
-                if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vbuf[i + 1]));
-                if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vbuf[i + 2]));
-                if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vbuf[i + 3]));
+            for (int i = 0; i < kVTileRows / 8; i += 4) {
+                const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
+                if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vv[i + 0]));
+                if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vv[i + 1]));
+                if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vv[i + 2]));
+                if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vv[i + 3]));
             }
         }
-        part[cj * kDecDims + cd] = acc;
+        if (t + n_vt < n_tiles) {
+            __syncthreads();    // tile t consumed before it is refilled
+            v_tile_dma(vt + (t % n_vt) * kVTileFloats, vc, kv_dim, col0, (t + n_vt) * kVTileRows, seq);
+        }
     }
+    if (tid < kDecChains) part[cj * kDecDims + cd] = acc;
     __syncthreads();
 
     // 4. out[d] = reduce_add(8 lane chains) + the seq % 8 tail in order,
@@ -220,7 +314,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         float out = reduce_add8(lj);
 #pragma unroll
         for (int i = 0; i < 7; i++)
-            if (n_chunks * 8 + i < seq) out = fadd(out, fmul(sc[n_chunks * 8 + i], vtail[i]));
+            if (n_chunks * 8 + i < seq) out = fadd(out, fmul(pt[i * PCS + n_chunks], vtail[i]));
         const size_t col = (size_t)h * HD + (size_t)ds * kDecDims + tid;
         if (att_f32) att_f32[col] = out;
         if constexpr (QF >= 0) {
@@ -245,7 +339,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc,
                                                             const StepState* __restrict__ st, int batch,
-                                                            int n_heads, int n_kv_heads, int hd,
+                                                            int kv_ld, int n_heads, int n_kv_heads, int hd,
                                                             float attn_scale, int8_t* __restrict__ aq,
                                                             float* __restrict__ as,
                                                             float* __restrict__ att_f32) {
@@ -269,19 +363,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     float lmax = -1e10f;
     const int n_simd = hd / 8;
     for (int t2 = tid; t2 <= max_t2; t2 += kAttnThreads) {
-        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)t2 * kv_dim + (size_t)kvh * hd);
+        // keys transposed: dimension i of position t2 at kt[i * kv_ld]
+        const float* kt = kc + (size_t)kvh * hd * kv_ld + t2;
         float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (int s = 0; s < n_simd; s++) {
-            const float4 k0 = kr[2 * s], k1 = kr[2 * s + 1];
             const float* q = ql + s * 8;
-            l[0] = fadd(l[0], fmul(q[0], k0.x));
-            l[1] = fadd(l[1], fmul(q[1], k0.y));
-            l[2] = fadd(l[2], fmul(q[2], k0.z));
-            l[3] = fadd(l[3], fmul(q[3], k0.w));
-            l[4] = fadd(l[4], fmul(q[4], k1.x));
-            l[5] = fadd(l[5], fmul(q[5], k1.y));
-            l[6] = fadd(l[6], fmul(q[6], k1.z));
-            l[7] = fadd(l[7], fmul(q[7], k1.w));
+#pragma unroll
+            for (int j = 0; j < 8; j++) l[j] = fadd(l[j], fmul(q[j], kt[(size_t)(8 * s + j) * kv_ld]));
         }
         const float sv = fmul(reduce_add8(l), attn_scale);
         sc[t2] = sv;
@@ -339,63 +427,67 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
 }
 
 hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
-                            int max_seq, int n_heads, int n_kv_heads, int head_size, float scale, int qfmt,
+                            int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale, int qfmt,
                             int8_t* aq, float* as, float* att_f32, hipStream_t s) {
     const size_t smem = ((size_t)((max_seq + 3) & ~3) + 10 * (size_t)head_size) * sizeof(float);
     const dim3 grid(n_heads, batch);
     if (qfmt == kQ8)
-        hipLaunchKernelGGL((k_attention<kQ8>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, n_heads,
-                           n_kv_heads, head_size, scale, aq, as, att_f32);
+        hipLaunchKernelGGL((k_attention<kQ8>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, kv_ld,
+                           n_heads, n_kv_heads, head_size, scale, aq, as, att_f32);
     else if (qfmt == kQ4)
-        hipLaunchKernelGGL((k_attention<kQ4>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, n_heads,
-                           n_kv_heads, head_size, scale, aq, as, att_f32);
+        hipLaunchKernelGGL((k_attention<kQ4>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, kv_ld,
+                           n_heads, n_kv_heads, head_size, scale, aq, as, att_f32);
     else
-        hipLaunchKernelGGL((k_attention<-1>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, n_heads,
-                           n_kv_heads, head_size, scale, aq, as, att_f32);
+        hipLaunchKernelGGL((k_attention<-1>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, kv_ld,
+                           n_heads, n_kv_heads, head_size, scale, aq, as, att_f32);
     return hipGetLastError();
 }
 
 size_t attn_decode_lds_bytes(int max_seq) { return attn_decode_lds_floats(max_seq) * sizeof(float); }
+bool attn_decode_fits(int max_seq) { return attn_v_tiles(max_seq) >= 2; }
 
 template <int QF, int HD>
 static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const float* vc, const StepState* st,
-                                       int max_seq, int n_heads, int n_kv_heads, float scale, int8_t* aq, float* as,
-                                       float* att_f32, hipStream_t s) {
+                                       int max_seq, int kv_ld, int n_heads, int n_kv_heads, float scale, int8_t* aq,
+                                       float* as, float* att_f32, hipStream_t s) {
+    const int n_vt = attn_v_tiles(max_seq);
+    if (n_vt < 2) return hipErrorInvalidValue;
     const size_t smem = attn_decode_lds_bytes(max_seq);
     if (smem > 65536) {
-        // long contexts: opt in to more than the default 64 KiB of LDS
+        // opt in to more than the default 64 KiB of LDS
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<QF, HD>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((k_attn_decode<QF, HD>), dim3(n_heads, HD / kDecDims), dim3(kDecThreads), smem, s, sq, kc, vc,
-                       st, n_heads, n_kv_heads, scale, max_seq, aq, as, att_f32);
+                       st, n_heads, n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32);
     return hipGetLastError();
 }
 
 template <int QF>
 static hipError_t launch_attn_decode_q(const float* sq, const float* kc, const float* vc, const StepState* st,
-                                       int max_seq, int n_heads, int n_kv_heads, int hd, float scale, int8_t* aq,
-                                       float* as, float* att_f32, hipStream_t s) {
+                                       int max_seq, int kv_ld, int n_heads, int n_kv_heads, int hd, float scale,
+                                       int8_t* aq, float* as, float* att_f32, hipStream_t s) {
     switch (hd) {
-    case 32: return launch_attn_decode_k<QF, 32>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
-    case 64: return launch_attn_decode_k<QF, 64>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
-    case 128: return launch_attn_decode_k<QF, 128>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 32: return launch_attn_decode_k<QF, 32>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 64: return launch_attn_decode_k<QF, 64>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 128: return launch_attn_decode_k<QF, 128>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st, int max_seq,
-                              int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, int8_t* aq, float* as,
-                              float* att_f32, hipStream_t s) {
+                              int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, int8_t* aq,
+                              float* as, float* att_f32, hipStream_t s) {
+    if (kv_ld % 4 || kv_ld < max_seq) return hipErrorInvalidValue;
     if (qfmt == kQ8)
-        return launch_attn_decode_q<kQ8>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as,
-                                         att_f32, s);
+        return launch_attn_decode_q<kQ8>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
+                                         as, att_f32, s);
     if (qfmt == kQ4)
-        return launch_attn_decode_q<kQ4>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as,
-                                         att_f32, s);
-    return launch_attn_decode_q<-1>(sq, kc, vc, st, max_seq, n_heads, n_kv_heads, head_size, scale, aq, as, att_f32,
-                                    s);
+        return launch_attn_decode_q<kQ4>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
+                                         as, att_f32, s);
+    return launch_attn_decode_q<-1>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq, as,
+                                    att_f32, s);
 }
 
 }  // namespace yl

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
             const bool is_k = er >= att && er < att + kv, is_v = er >= att + kv;
             const int c = is_v ? er - att - kv : (is_k ? er - att : 0);
             ep_acc = (is_k || is_v) && c < (kv / 4) * 4;
-            ep0 = (is_v ? a.v_cache : a.k_cache)[(size_t)pos * kv + c];
+            ep0 = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
             const int col = er < att ? er : c;
             const int pair = (col % hd) >> 1;
             ep1 = a.rope_cos[(size_t)pos * (hd >> 1) + pair];
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
                     const float v0 = accs[tw & ~1], v1 = accs[tw | 1];
                     const float r = (tw & 1) ? fadd(fmul(v0, s), fmul(v1, c)) : fmul(v0, c) - fmul(v1, s);
                     if (row < att) a.q_out[(size_t)t * att + col] = r;
-                    else a.k_cache[(size_t)pos * kv + col] = r;
+                    else a.k_cache[(size_t)col * a.kv_ld + pos] = r;
                 }
             }
         }

@@ -15,8 +15,12 @@
 //     eq : uint8 [vocab/64][dim/16][64][16], holding u = q + 128 (so the
 //          logits pass widens it with one unsigned-byte conversion)
 //     ed : f16   [vocab/64][dim/32][64]
-//   KV cache: f32 [n_layers][ctx_len][kv_dim] for keys and for values
-//   (InferenceSession, base_transformer.rs:81-98).
+//   KV cache (InferenceSession, base_transformer.rs:81-98), f32:
+//     values [n_layers][ctx_len][kv_dim] (the reference's layout);
+//     keys   [n_layers][kv_dim][kv_ld], transposed (kv_ld = ctx_len rounded
+//            up to a multiple of 4), so that decode attention loads one key
+//            dimension of 4 consecutive positions per 16-byte lane access.
+//   Both caches hold n_layers * kv_ld * kv_dim floats.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -72,8 +76,8 @@ struct GemvArgs {
     // kEpiStore
     float* out; int accumulate_cols;           // columns < accumulate_cols start from out[]
     // kEpiQkvRope
-    float* q_out; float* k_cache; float* v_cache;
-    int att_dim, kv_dim, head_size;
+    float* q_out; float* k_cache; float* v_cache;   // k_cache [kv_dim][kv_ld], v_cache [positions][kv_dim]
+    int att_dim, kv_dim, head_size, kv_ld;
     const float* rope_cos; const float* rope_sin;  // [ctx][head_size/2]
     const StepState* state;
     // kEpiSwiglu
@@ -83,16 +87,20 @@ struct GemvArgs {
 // kernel launchers; all return the hipError_t of the launch
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s);
+// out[c * out_ld + r] = in[r][c] for an in[rows][cols] f32 matrix
+hipError_t launch_transpose(const float* in, float* out, int rows, int cols, int out_ld, hipStream_t s);
 hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, float eps, int batch,
                           float* xn, int8_t* xq, float* xs, hipStream_t s);
 hipError_t launch_embed(const EmbQ8& e, const uint32_t* tokens, int batch, float* x, hipStream_t s);
+// kc: keys [kv_dim][kv_ld] (transposed), vc: values [max_seq][kv_dim]
 hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st,
-                            int batch, int max_seq, int n_heads, int n_kv_heads, int head_size,
+                            int batch, int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size,
                             float scale, int qfmt, int8_t* aq, float* as, float* att_f32,
                             hipStream_t s);
 size_t attn_decode_lds_bytes(int max_seq);
+bool attn_decode_fits(int max_seq);   // LDS holds the decode kernel's row and >= 2 V tiles
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st,
-                              int max_seq, int n_heads, int n_kv_heads, int head_size, float scale,
+                              int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
                               int qfmt, int8_t* aq, float* as, float* att_f32, hipStream_t s);
 hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,
                        float* q, float* k, int n_heads, int n_kv_heads, int head_size, hipStream_t s);

@@ -78,6 +78,22 @@ __global__ void k_quantize(int8_t* __restrict__ q, float* __restrict__ s, const 
     }
 }
 
+// out[c * out_ld + r] = in[r][c], 32x32 tiles through LDS.
+__global__ __launch_bounds__(kThreads) void k_transpose(const float* __restrict__ in, float* __restrict__ out, int rows,
+                                                        int cols, int out_ld) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    for (int i = threadIdx.x; i < 32 * 32; i += kThreads) {
+        const int r = r0 + i / 32, c = c0 + i % 32;
+        if (r < rows && c < cols) tile[i / 32][i % 32] = in[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 32 * 32; i += kThreads) {
+        const int c = c0 + i / 32, r = r0 + i % 32;
+        if (r < rows && c < cols) out[(size_t)c * out_ld + r] = tile[i % 32][i / 32];
+    }
+}
+
 // RoPE on q [batch][n_heads*hd] and k [batch][n_kv_heads*hd] at positions
 // pos+t, one thread per (head, pair).
 __global__ void k_rope(const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -161,6 +177,14 @@ hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, flo
         hipLaunchKernelGGL((k_rmsnorm<kQ4>), dim3(batch), dim3(kThreads), smem, s, x, w, dim, eps, xn, xq, xs);
     else
         hipLaunchKernelGGL((k_rmsnorm<-1>), dim3(batch), dim3(kThreads), smem, s, x, w, dim, eps, xn, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const float* in, float* out, int rows, int cols, int out_ld, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (out_ld < rows) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_transpose, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(kThreads), 0, s, in, out, rows, cols,
+                       out_ld);
     return hipGetLastError();
 }
 

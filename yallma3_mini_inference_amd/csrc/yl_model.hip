@@ -7,14 +7,17 @@
 //   attention -> quantize -> WO -> residual -> RMSNorm -> quantize ->
 //   W1,W3 -> SwiGLU -> quantize -> W2 -> residual,
 // then the final RMSNorm and the tied-embedding logits of the last token.
-// Kernel fusion (same arithmetic, fewer launches):
-//   embed + RMSNorm + quantize                      k_embed_norm
-//   Q/K/V matmul + K/V cache accumulate + RoPE      k_gemv<..., kEpiQkvRope>
-//   attention + quantize                            k_attention
-//   WO matmul + residual + RMSNorm + quantize       k_gemv<..., kEpiResid>
-//   W1/W3 matmul + SwiGLU + quantize                k_gemv<..., kEpiSwiglu>
-//   W2 matmul + residual + next RMSNorm + quantize  k_gemv<..., kEpiResid>
-//   logits + argmax                                 k_logits
+// Kernel fusion (same arithmetic, fewer launches), per layer:
+//   (layer 0: token embedding +) RMSNorm + quantize + Q/K/V matmul
+//     + K/V cache accumulate + RoPE                   k_gemv<..., kEpiQkvRope>
+//   attention + quantize                              k_attn_decode (one token),
+//                                                     k_attention (prompt batch)
+//   WO matmul + residual                              k_gemv<..., kEpiResid>
+//   RMSNorm + quantize + W1/W3 matmul + SwiGLU
+//     + quantize                                      k_gemv<..., kEpiSwiglu>
+//   W2 matmul + residual                              k_gemv<..., kEpiResid>
+// then final RMSNorm + logits + argmax (k_logits) and the step bookkeeping
+// (k_finalize).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdlib.h>
@@ -247,6 +250,7 @@ struct Layer {
 struct yl_model {
     yl_shape shape{};
     int dim = 0, hidden = 0, n_layers = 0, n_heads = 0, n_kv = 0, hd = 0, vocab = 0, ctx = 0;
+    int kv_ld = 0;   // cache positions: ctx rounded up to a multiple of 4 (key row stride)
     int att = 0, kv = 0;
     float eps = 0.0f, attn_scale = 0.0f;
     yl_rope_params rope{};
@@ -388,6 +392,7 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     if (m->n_heads <= 0 || m->dim % m->n_heads) { set_error("dim must be divisible by n_heads"); return nullptr; }
     m->hd = m->dim / m->n_heads;
     m->ctx = (int)((uint32_t)seq_len < max_ctx_len ? (uint32_t)seq_len : max_ctx_len);
+    m->kv_ld = (m->ctx + 3) & ~3;
     const GgufValue* toks = g.get("tokenizer.ggml.tokens");
     if (!toks) { set_error("tokenizer.ggml.tokens metadata key not found"); return nullptr; }
     if (toks->type != 9) { set_error("tokenizer.ggml.tokens must be an array of strings"); return nullptr; }
@@ -571,7 +576,7 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
     hipStream_t st = s->stream;
     hipError_t e;
 #define YL_TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
-    const size_t lay_kv = (size_t)m->ctx * m->kv;
+    const size_t lay_kv = (size_t)m->kv_ld * m->kv;
     for (int l = 0; l < m->n_layers; l++) {
         const Layer& L = m->layers[l];
         float* kc = s->kc + (size_t)l * lay_kv;
@@ -582,7 +587,7 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
         a.x = s->x; a.norm_w = L.rms_att; a.eps = m->eps;
         if (l == 0) { a.emb = m->emb; a.tokens = tok; }
         a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
-        a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd;
+        a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
         a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
         if (prof) prof->begin(0);
         YL_TRY(launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st));
@@ -591,10 +596,10 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
         // attention (+ quantize of its output)
         if (prof) prof->begin(1);
         if (batch == 1)
-            YL_TRY(launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->n_heads, m->n_kv, m->hd, m->attn_scale,
+            YL_TRY(launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale,
                                       L.wo.fmt, s->aq, s->as_, nullptr, st));
         else
-            YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->n_heads, m->n_kv, m->hd,
+            YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                     m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st));
         if (prof) prof->end(1, 0);
 
@@ -840,24 +845,32 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
         set_error("attention: seq_len too long for one workgroup");
         return YL_ERR_UNSUPPORTED;
     }
-    if (batch == 1 && (hd % 32 || attn_decode_lds_bytes((int)seq) > 160 * 1024)) {
+    if (batch == 1 && (hd % 32 || !attn_decode_fits((int)seq))) {
         set_error("attention: unsupported head size or seq_len for the decode kernel");
         return YL_ERR_UNSUPPORTED;
     }
     StepState* dst = nullptr;
+    float* kt = nullptr;
     StepState hst{};
     hst.pos = (int32_t)start_pos;
     hipStream_t strm = (hipStream_t)stream;
+    const int kv_dim = (int)(n_kv_heads * hd);
+    const int ld = ((int)seq + 3) & ~3;
+    // the kernels read keys transposed ([kv_dim][ld]); the caller's are in
+    // the reference layout [seq][kv_dim]
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
+    if (e == hipSuccess) e = hipMalloc(&kt, (size_t)ld * kv_dim * 4 + 256);
     if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, kv_dim, ld, strm);
     if (e == hipSuccess && batch == 1)
-        e = launch_attn_decode(q, kc, vc, dst, (int)seq, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
+        e = launch_attn_decode(q, kt, vc, dst, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
                                nullptr, nullptr, out, strm);
     else if (e == hipSuccess)
-        e = launch_attention(q, kc, vc, dst, (int)batch, (int)seq, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale,
-                             -1, nullptr, nullptr, out, strm);
+        e = launch_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
+                             attn_scale, -1, nullptr, nullptr, out, strm);
     if (e == hipSuccess) e = hipStreamSynchronize(strm);
     if (dst) hipFree(dst);
+    if (kt) hipFree(kt);
     return e == hipSuccess ? YL_OK : hip_fail(e, "attention");
 }
 
@@ -920,7 +933,7 @@ yl_session* yl_create_session(const yl_model* m) {
     if (!m) { set_error("null model"); return nullptr; }
     auto* s = new yl_session();
     s->m = m;
-    s->kv_floats = (size_t)m->n_layers * m->ctx * m->kv;
+    s->kv_floats = (size_t)m->n_layers * m->kv_ld * m->kv;
     s->ring_cap = (uint32_t)m->ctx;
     bool ok = hipStreamCreate(&s->stream) == hipSuccess &&
               hipMalloc(&s->kc, s->kv_floats * 4 + 256) == hipSuccess &&

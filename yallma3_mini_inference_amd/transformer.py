@@ -48,23 +48,39 @@ class InferenceSession:
         return k.value, v.value, n.value
 
     def key_cache(self) -> np.ndarray:
-        return self._download(self._kv()[0])
+        """Keys [n_layers][ctx_len][kv_dim] (the device holds them transposed)."""
+        ctx = self.model.shape.ctx_len
+        k = self._download(self._kv()[0], transposed=True)
+        return np.ascontiguousarray(k[:, :, :ctx].transpose(0, 2, 1))
 
     def value_cache(self) -> np.ndarray:
-        return self._download(self._kv()[1])
+        """Values [n_layers][ctx_len][kv_dim]."""
+        return np.ascontiguousarray(self._download(self._kv()[1])[:, :self.model.shape.ctx_len])
 
-    def _download(self, ptr) -> np.ndarray:
+    def _shape(self, transposed=False):
+        """Device cache shape; kv_ld = ctx_len rounded up to a multiple of 4."""
         m = self.model
-        shp = (m.shape.n_layers, m.shape.ctx_len, m.shape.n_kv_heads * m.shape.head_size)
-        out = np.empty(shp, np.float32)
+        ld, kv = (m.shape.ctx_len + 3) & ~3, m.shape.n_kv_heads * m.shape.head_size
+        return (m.shape.n_layers, kv, ld) if transposed else (m.shape.n_layers, ld, kv)
+
+    def _download(self, ptr, transposed=False) -> np.ndarray:
+        out = np.empty(self._shape(transposed), np.float32)
         check(lib().yl_memcpy_d2h(out.ctypes.data, ptr, out.nbytes))
         return out
 
     def upload_kv(self, key: np.ndarray, value: np.ndarray) -> None:
-        """Overwrite the device KV cache (tests and benchmarks pre-fill it)."""
+        """Overwrite the device KV cache from [n_layers][ctx_len][kv_dim]
+        arrays (tests and benchmarks pre-fill it)."""
         kp, vp, n = self._kv()
-        for ptr, a in ((kp, key), (vp, value)):
-            a = np.ascontiguousarray(a, np.float32)
+        m = self.model
+        ctx = m.shape.ctx_len
+        shp = (m.shape.n_layers, ctx, m.shape.n_kv_heads * m.shape.head_size)
+        dev = self._shape()
+        kd = np.zeros(self._shape(True), np.float32)
+        kd[:, :, :ctx] = np.asarray(key, np.float32).reshape(shp).transpose(0, 2, 1)
+        vd = np.zeros(dev, np.float32)
+        vd[:, :ctx] = np.asarray(value, np.float32).reshape(shp)
+        for ptr, a in ((kp, kd), (vp, vd)):
             if a.size != n:
                 raise ValueError("cache shape mismatch")
             check(lib().yl_memcpy_h2d(ptr, a.ctypes.data, a.nbytes))
