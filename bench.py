@@ -11,11 +11,21 @@ of one token plus the device argmax that feeds the next step (one HIP graph
 launch; tokens stay on the device).
 
 Also reported (same JSON line):
-  roofline      the quantized GEMV kernels (all seven projections): their
-                algorithmic bytes (quantized weights + f16 scales + int8
-                activations + outputs) / their HIP-event time, measured on
-                the session's stream over P decode steps run eagerly with an
-                event pair around every GEMV launch, against 8 TB/s.
+  kernels       per kernel class (QKV / Wo / gate-up / down GEMV, attention,
+                logits): the class's launches of one decode step (one per
+                layer) captured back to back in a HIP graph and replayed
+                between two HIP events on the session's stream, after the
+                timed steps, at the last decoded position; average us per
+                launch and algorithmic bytes per launch (quantized weights +
+                f16 scales + activations read + outputs written).
+  roofline      the dominant kernel (the GEMV class with the most time per
+                token): its bytes per launch / its average launch time,
+                against 8 TB/s; `traffic` = the HBM bytes per launch measured
+                by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated on a
+                copy kernel) from profiles/pmc_traffic_llama32_1b_decode.json
+                when that file covers this kernel, else null.
+  gemv_all      all four GEMV classes together: weight bytes per token / GEMV
+                time per token (the 60%-of-8-TB/s target's figure).
   cpu_baseline  the oracle (C restatement of the reference's Rayon CPU path,
                 OpenMP) decoding a bounded sample of the same workload on this
                 host's cores.
@@ -31,6 +41,12 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s + quant GEMV HBM GB/s (% of 8 TB/s peak), Llama-3.2-1B shape"
 HBM_PEAK_GBS = 8000.0
+KERNEL_NAMES = {
+    "qkv": "k_gemv (QKV, RMSNorm prologue, RoPE/KV epilogue)",
+    "wo": "k_gemv (Wo, residual epilogue)",
+    "w13": "k_gemv (gate/up, RMSNorm prologue, SwiGLU + quantize epilogue)",
+    "w2": "k_gemv (down, residual epilogue)",
+}
 
 
 def log(msg):
@@ -69,10 +85,12 @@ def main():
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--config", default="llama32_1b")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB (the known-size kernel that "
+                         "calibrates rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (the decode path is "
@@ -86,6 +104,19 @@ def main():
     if Y.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy_mib:
+        # the runtime's plain copy kernel over a known number of bytes
+        nbytes = args.calibrate_copy_mib << 20
+        L = Y.lib()
+        src, dst = L.yl_malloc(nbytes), L.yl_malloc(nbytes)
+        if not src or not dst:
+            raise SystemExit("calibration buffers: allocation failed")
+        Y.check(L.yl_memset_d(src, 1, nbytes))
+        Y.check(L.yl_memcpy_d2d(dst, src, nbytes))
+        Y.check(L.yl_synchronize())
+        L.yl_free(src)
+        L.yl_free(dst)
+        log(f"calibration copy: {nbytes} B read + {nbytes} B written")
     t0 = time.perf_counter()
     path = synth.ensure(args.config)
     log(f"model {path} ready in {time.perf_counter() - t0:.1f}s")
@@ -119,15 +150,32 @@ def main():
     tok_s = args.steps / elapsed
     log(f"decode: {args.steps} steps in {elapsed * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
 
-    # roofline of the quantized GEMV kernels (event pairs around every launch)
-    ms, launches, nbytes = model.profile_decode(sess, nxt, args.prompt, args.profile_steps, 0)
-    gemv_gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"GEMV: {launches} launches, {nbytes / launches / 1e6:.2f} MB avg, {ms / launches * 1e3:.2f} us avg "
-        f"-> {gemv_gbs:.0f} GB/s")
-    a_ms, a_n, _ = model.profile_decode(sess, nxt, args.prompt, 8, 1)
-    l_ms, l_n, l_bytes = model.profile_decode(sess, nxt, args.prompt, 8, 2)
-    log(f"attention avg {a_ms / a_n * 1e3:.2f} us; logits avg {l_ms / l_n * 1e3:.2f} us "
-        f"({l_bytes / (l_ms * 1e-3) / 1e9:.0f} GB/s)")
+    # per-class kernel timing: each class's launches of one decode step replayed
+    # as a graph between two HIP events on the session's stream (at the last
+    # decoded position; this modifies the session, which is not used again)
+    ppos = pos + args.steps - 1
+    kern = {}
+    for cls, reps in (("qkv", 20), ("attention", 20), ("wo", 20), ("w13", 20), ("w2", 20), ("logits", 10)):
+        us, nb, n = model.profile_kernel(sess, nxt, ppos, cls, reps)
+        kern[cls] = {"us": round(us, 3), "bytes": int(nb), "launches_per_step": int(n)}
+        if nb:
+            kern[cls]["gbs"] = round(nb / (us * 1e-6) / 1e9, 1)
+        log(f"{cls}: {us:.2f} us/launch x {n}/step" + (f", {nb / 1e6:.2f} MB -> {nb / (us * 1e3):.0f} GB/s" if nb else ""))
+    gemv = ("qkv", "wo", "w13", "w2")
+    gemv_us = sum(kern[c]["us"] * kern[c]["launches_per_step"] for c in gemv)
+    gemv_bytes = sum(kern[c]["bytes"] * kern[c]["launches_per_step"] for c in gemv)
+    gemv_gbs = gemv_bytes / (gemv_us * 1e-6) / 1e9
+    log(f"GEMVs: {gemv_us:.1f} us/token for {gemv_bytes / 1e6:.1f} MB -> {gemv_gbs:.0f} GB/s "
+        f"({gemv_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    dom = max(gemv, key=lambda c: kern[c]["us"] * kern[c]["launches_per_step"])
+    dom_gbs = kern[dom]["bytes"] / (kern[dom]["us"] * 1e-6) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "pmc_traffic_llama32_1b_decode.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            t = json.load(f)
+        if t.get("class") == dom:
+            traffic = t.get("traffic_bytes_per_launch")
 
     result = {
         "metric": METRIC,
@@ -150,14 +198,15 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv (quantized GEMV, all projections)",
-            "avg_launch_us": round(ms / launches * 1e3, 3), "bytes_per_launch": int(nbytes // launches),
+            "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": KERNEL_NAMES[dom], "class": dom,
+            "avg_launch_us": kern[dom]["us"], "bytes_per_launch": kern[dom]["bytes"],
         },
+        "gemv_all": {"us_per_token": round(gemv_us, 2), "bytes_per_token": gemv_bytes,
+                     "achieved_gbs": round(gemv_gbs, 1), "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+        "kernels": kern,
         "prefill_ms": round(prefill_s * 1e3, 2),
-        "attention_avg_us": round(a_ms / a_n * 1e3, 3),
-        "logits_avg_us": round(l_ms / l_n * 1e3, 3),
         "tokens_head": [int(t) for t in toks[:8]],
     }
     if not args.no_cpu_baseline:

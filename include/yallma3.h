@@ -82,6 +82,7 @@ void *yl_malloc(size_t bytes);                      /* device memory, 256-B alig
 void yl_free(void *p);
 yl_status yl_memcpy_h2d(void *dst_dev, const void *src_host, size_t bytes);
 yl_status yl_memcpy_d2h(void *dst_host, const void *src_dev, size_t bytes);
+yl_status yl_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes);
 yl_status yl_memset_d(void *dst_dev, int value, size_t bytes);
 yl_status yl_synchronize(void);
 
@@ -211,15 +212,20 @@ yl_status yl_generate_greedy(const yl_model *m, yl_session *s, uint32_t token, u
                              uint32_t n_steps, uint32_t *out_tokens);
 
 /* ------------------------------------------------------------ profiling */
-/* Per-kernel-class timing of greedy decode steps with HIP events recorded
- * around every launch of the class on the session's stream (steps run
- * eagerly, not as a graph).  kernel_class: 0 = quantized GEMV (all seven
- * projections), 1 = attention, 2 = logits.  Returns the summed event time
- * (ms), the launch count and the algorithmic bytes those launches read or
- * wrote.  Also advances the session like yl_generate_greedy. */
-yl_status yl_profile_decode(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
-                            uint32_t n_steps, int32_t kernel_class, double *ms, uint64_t *launches,
-                            uint64_t *bytes);
+/* Timing of one kernel class of a decode step at position start_pos:
+ * the class's launches of one step (one per layer; one for logits) are
+ * captured back to back in a HIP graph, replayed `reps` times between two
+ * HIP events on the session's stream, and the elapsed time is divided by
+ * the launches.  kernel_class: 0 = QKV GEMV (RMSNorm prologue, RoPE/KV
+ * epilogue), 1 = decode attention, 2 = Wo GEMV, 3 = gate/up GEMV (RMSNorm
+ * prologue, SwiGLU epilogue), 4 = down GEMV, 5 = logits.  Returns the
+ * average launch time (us), the algorithmic bytes one launch reads and
+ * writes (0 for attention) and the launches per step.  Leaves the session's
+ * KV cache at start_pos, its residual stream and its activations modified
+ * (the replays repeat the `+=` steps): reset the session afterwards. */
+yl_status yl_profile_kernel(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
+                            int32_t kernel_class, uint32_t reps, double *us_per_launch,
+                            uint64_t *bytes_per_launch, uint32_t *launches);
 
 /* Elementwise probe of the device arithmetic the path relies on (device
  * pointers, n floats): exp, sqrt(|x|), 1/x and f16 widening of (i & 0xffff). */

@@ -11,14 +11,14 @@ reference's API over it:
   ops.*                                                util.rs, forward.rs
   synth                                                seeded GGUF models
 """
-from ._lib import LIB_PATH, YlError, lib
+from ._lib import LIB_PATH, YlError, check, lib
 from .device import DeviceBuffer, device_count
 from .transformer import (InferenceSession, Transformer, TransformerLlamaGguf, infer_ffi, load_transformer,
                           load_transformer_ffi)
 from .weight_type import QuantizedWeight, WeightFormat, matmul, matmul_device, quantize, quantize_device
 
 __all__ = [
-    "LIB_PATH", "YlError", "lib", "DeviceBuffer", "device_count", "InferenceSession", "Transformer",
+    "LIB_PATH", "YlError", "check", "lib", "DeviceBuffer", "device_count", "InferenceSession", "Transformer",
     "TransformerLlamaGguf", "infer_ffi", "load_transformer", "load_transformer_ffi", "QuantizedWeight",
     "WeightFormat", "matmul", "matmul_device", "quantize", "quantize_device",
 ]

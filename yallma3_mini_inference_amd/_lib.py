@@ -21,13 +21,13 @@ STATUS_NAMES = {
 # every symbol include/yallma3.h declares
 EXPORTS = [
     "yl_last_error", "load_transformer_ffi", "infer_ffi", "free_string", "yl_device_count", "yl_malloc",
-    "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memset_d", "yl_synchronize", "yl_quantize",
+    "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memcpy_d2d", "yl_memset_d", "yl_synchronize", "yl_quantize",
     "yl_weight_upload", "yl_weight_upload_gguf", "yl_weight_free", "yl_weight_bytes", "yl_matmul",
     "yl_rmsnorm_quantize", "yl_rope_gguf", "yl_attention", "yl_swiglu_quantize", "yl_load",
     "yl_model_free", "yl_model_name", "yl_model_shape", "yl_vocab_size", "yl_max_ctx_len", "yl_bos_token",
     "yl_eos_token", "yl_model_weight_bytes", "yl_model_embedding_bytes", "yl_get_embeddings",
     "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_pos", "yl_session_set_pos",
-    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_decode", "yl_math_selftest",
+    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest",
     "yl_write_synthetic_gguf", "yl_synthetic_normal",
 ]
 
@@ -86,6 +86,7 @@ def lib():
         "yl_free": (None, [vp]),
         "yl_memcpy_h2d": (st, [vp, vp, sz]),
         "yl_memcpy_d2h": (st, [vp, vp, sz]),
+        "yl_memcpy_d2d": (st, [vp, vp, sz]),
         "yl_memset_d": (st, [vp, C.c_int, sz]),
         "yl_synchronize": (st, []),
         "yl_quantize": (st, [C.c_int, vp, vp, vp, sz, u32, vp]),
@@ -117,8 +118,8 @@ def lib():
         "yl_session_kv": (st, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz)]),
         "yl_forward_x": (st, [vp, vp, sz, u32, vp, vp, vp]),
         "yl_generate_greedy": (st, [vp, vp, u32, u32, u32, vp]),
-        "yl_profile_decode": (st, [vp, vp, u32, u32, u32, st, C.POINTER(C.c_double), C.POINTER(u64),
-                                   C.POINTER(u64)]),
+        "yl_profile_kernel": (st, [vp, vp, u32, u32, st, u32, C.POINTER(C.c_double), C.POINTER(u64),
+                                   C.POINTER(u32)]),
         "yl_math_selftest": (st, [vp, sz, vp, vp, vp, vp]),
         "yl_write_synthetic_gguf": (st, [C.c_char_p, C.POINTER(SynthConfig)]),
         "yl_synthetic_normal": (st, [u64, u64, u64, sz, f32, vp]),

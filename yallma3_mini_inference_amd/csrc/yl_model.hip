@@ -529,112 +529,84 @@ bool session_grow(yl_session* s, int batch) {
     return true;
 }
 
-// Event timing of one kernel class inside eager steps.
-struct Prof {
-    int cls = -1;
-    std::vector<hipEvent_t> ev;
-    int used = 0;
-    double ms = 0.0;
-    uint64_t launches = 0, bytes = 0;
-    hipStream_t stream = nullptr;
-    void begin(int c) {
-        if (c != cls) return;
-        if ((size_t)used + 2 > ev.size()) {
-            hipEvent_t a, b;
-            hipEventCreate(&a); hipEventCreate(&b);
-            ev.push_back(a); ev.push_back(b);
-        }
-        hipEventRecord(ev[used], stream);
-    }
-    void end(int c, uint64_t nbytes) {
-        if (c != cls) return;
-        hipEventRecord(ev[used + 1], stream);
-        used += 2;
-        launches += 1;
-        bytes += nbytes;
-    }
-    void collect() {
-        if (used) hipEventSynchronize(ev[used - 1]);
-        for (int i = 0; i < used; i += 2) {
-            float t = 0.0f;
-            hipEventElapsedTime(&t, ev[i], ev[i + 1]);
-            ms += t;
-        }
-        used = 0;
-    }
-    ~Prof() { for (auto e : ev) hipEventDestroy(e); }
-};
-
 uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
     return (uint64_t)w.bytes() + (uint64_t)batch * ((uint64_t)w.n + (uint64_t)w.nb * 4 + (uint64_t)out_elems * 4);
 }
 
-// One forward pass over `batch` tokens whose ids are at `tok` (device) and
-// whose first position is st->pos (device).  Enqueued on s->stream only.
-hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance,
-                           Prof* prof) {
+// Kernel classes of a forward pass, in step order (also the profiling
+// classes of yl_profile_kernel).
+enum OpClass : int { kOpQkv = 0, kOpAttn = 1, kOpWo = 2, kOpW13 = 3, kOpW2 = 4, kOpLogits = 5 };
+
+// Enqueues op `cls` of layer l for `batch` tokens whose ids are at `tok`
+// (device) and whose first position is st->pos (device), on s->stream.
+// `bytes` (nullable) receives the algorithmic bytes the launch reads and
+// writes.
+hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok, int advance,
+                      uint64_t* bytes) {
     hipStream_t st = s->stream;
-    hipError_t e;
-#define YL_TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
     const size_t lay_kv = (size_t)m->kv_ld * m->kv;
-    for (int l = 0; l < m->n_layers; l++) {
-        const Layer& L = m->layers[l];
-        float* kc = s->kc + (size_t)l * lay_kv;
-        float* vc = s->vc + (size_t)l * lay_kv;
+    if (cls == kOpLogits) {
+        // final RMSNorm + logits of the last token + argmax + step bookkeeping
+        if (bytes) *bytes = (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4;
+        return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->keys,
+                             s->st, s->ring, s->ring_cap, advance, st);
+    }
+    const Layer& L = m->layers[l];
+    float* kc = s->kc + (size_t)l * lay_kv;
+    float* vc = s->vc + (size_t)l * lay_kv;
+    GemvArgs a{};
+    switch (cls) {
+    case kOpQkv:
         // RMSNorm + quantize (prologue) -> Q,K,V -> K/V += into the cache -> RoPE
-        GemvArgs a{};
         a.qs = L.qkv.qs; a.d = L.qkv.d; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
         a.x = s->x; a.norm_w = L.rms_att; a.eps = m->eps;
         if (l == 0) { a.emb = m->emb; a.tokens = tok; }
         a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
         a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
         a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
-        if (prof) prof->begin(0);
-        YL_TRY(launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st));
-        if (prof) prof->end(0, gemv_bytes(L.qkv, L.qkv.o, batch));
-
+        if (bytes) *bytes = gemv_bytes(L.qkv, L.qkv.o, batch);
+        return launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st);
+    case kOpAttn:
         // attention (+ quantize of its output)
-        if (prof) prof->begin(1);
+        if (bytes) *bytes = 0;
         if (batch == 1)
-            YL_TRY(launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale,
-                                      L.wo.fmt, s->aq, s->as_, nullptr, st));
-        else
-            YL_TRY(launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                    m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st));
-        if (prof) prof->end(1, 0);
-
+            return launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                      m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
+        return launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
+    case kOpWo:
         // WO -> residual add
-        GemvArgs b{};
-        b.qs = L.wo.qs; b.d = L.wo.d; b.n = L.wo.n; b.o = L.wo.o; b.nb = L.wo.nb;
-        b.xq = s->aq; b.xs = s->as_; b.x = s->x;
-        if (prof) prof->begin(0);
-        YL_TRY(launch_gemv(b, L.wo.fmt, kEpiResid, batch, st));
-        if (prof) prof->end(0, gemv_bytes(L.wo, L.wo.o, batch));
-
+        a.qs = L.wo.qs; a.d = L.wo.d; a.n = L.wo.n; a.o = L.wo.o; a.nb = L.wo.nb;
+        a.xq = s->aq; a.xs = s->as_; a.x = s->x;
+        if (bytes) *bytes = gemv_bytes(L.wo, L.wo.o, batch);
+        return launch_gemv(a, L.wo.fmt, kEpiResid, batch, st);
+    case kOpW13:
         // RMSNorm + quantize (prologue) -> W1, W3 -> SwiGLU -> quantize
-        GemvArgs c{};
-        c.qs = L.w13.qs; c.d = L.w13.d; c.n = L.w13.n; c.o = L.w13.o; c.nb = L.w13.nb;
-        c.x = s->x; c.norm_w = L.rms_ffn; c.eps = m->eps;
-        c.hq = s->hq; c.hs = s->hs; c.h_f32 = nullptr; c.hidden = m->hidden; c.h_fmt = L.w2.fmt;
-        if (prof) prof->begin(0);
-        YL_TRY(launch_gemv(c, L.w13.fmt, kEpiSwiglu, batch, st));
-        if (prof) prof->end(0, gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch));
-
+        a.qs = L.w13.qs; a.d = L.w13.d; a.n = L.w13.n; a.o = L.w13.o; a.nb = L.w13.nb;
+        a.x = s->x; a.norm_w = L.rms_ffn; a.eps = m->eps;
+        a.hq = s->hq; a.hs = s->hs; a.h_f32 = nullptr; a.hidden = m->hidden; a.h_fmt = L.w2.fmt;
+        if (bytes) *bytes = gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch);
+        return launch_gemv(a, L.w13.fmt, kEpiSwiglu, batch, st);
+    case kOpW2:
         // W2 -> residual add
-        GemvArgs d{};
-        d.qs = L.w2.qs; d.d = L.w2.d; d.n = L.w2.n; d.o = L.w2.o; d.nb = L.w2.nb;
-        d.xq = s->hq; d.xs = s->hs; d.x = s->x;
-        if (prof) prof->begin(0);
-        YL_TRY(launch_gemv(d, L.w2.fmt, kEpiResid, batch, st));
-        if (prof) prof->end(0, gemv_bytes(L.w2, L.w2.o, batch));
+        a.qs = L.w2.qs; a.d = L.w2.d; a.n = L.w2.n; a.o = L.w2.o; a.nb = L.w2.nb;
+        a.xq = s->hq; a.xs = s->hs; a.x = s->x;
+        if (bytes) *bytes = gemv_bytes(L.w2, L.w2.o, batch);
+        return launch_gemv(a, L.w2.fmt, kEpiResid, batch, st);
+    default:
+        return hipErrorInvalidValue;
     }
-    // final RMSNorm + logits of the last token + argmax + step bookkeeping
-    if (prof) prof->begin(2);
-    YL_TRY(launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->keys,
-                         s->st, s->ring, s->ring_cap, advance, st));
-    if (prof) prof->end(2, (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4);
-#undef YL_TRY
-    return hipSuccess;
+}
+
+// One forward pass over `batch` tokens whose ids are at `tok` (device) and
+// whose first position is st->pos (device).  Enqueued on s->stream only.
+hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+    for (int l = 0; l < m->n_layers; l++)
+        for (int c = kOpQkv; c <= kOpW2; c++) {
+            const hipError_t e = enqueue_op(m, s, c, l, batch, tok, advance, nullptr);
+            if (e != hipSuccess) return e;
+        }
+    return enqueue_op(m, s, kOpLogits, 0, batch, tok, advance, nullptr);
 }
 
 bool ensure_graph(const yl_model* m, yl_session* s) {
@@ -644,7 +616,7 @@ bool ensure_graph(const yl_model* m, yl_session* s) {
         set_error("hipStreamBeginCapture failed");
         return false;
     }
-    const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1, nullptr);
+    const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1);
     const hipError_t e2 = hipStreamEndCapture(s->stream, &g);
     if (e != hipSuccess || e2 != hipSuccess) {
         set_error(std::string("decode graph capture failed: ") + hipGetErrorString(e != hipSuccess ? e : e2));
@@ -705,6 +677,11 @@ yl_status yl_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 yl_status yl_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
     return e == hipSuccess ? YL_OK : hip_fail(e, "hipMemcpy D2H");
+}
+
+yl_status yl_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "hipMemcpy D2D");
 }
 yl_status yl_memset_d(void* dst, int value, size_t bytes) {
     const hipError_t e = hipMemset(dst, value, bytes);
@@ -1006,7 +983,7 @@ yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint
         if (!session_grow(s, (int)n)) return YL_ERR_NOMEM;
         e = hipMemcpyAsync(s->tokens, tokens, n * 4, hipMemcpyHostToDevice, s->stream);
         if (e != hipSuccess) return hip_fail(e, "token upload");
-        e = enqueue_forward(m, s, (int)n, s->tokens, 0, nullptr);
+        e = enqueue_forward(m, s, (int)n, s->tokens, 0);
         if (e != hipSuccess) return hip_fail(e, "forward launch");
     }
     if (logits) {
@@ -1041,25 +1018,54 @@ yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, u
     return e == hipSuccess ? YL_OK : hip_fail(e, "generate");
 }
 
-yl_status yl_profile_decode(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, uint32_t n_steps,
-                            int32_t kernel_class, double* ms, uint64_t* launches, uint64_t* bytes) {
-    if (!m || !s || s->m != m || kernel_class < 0 || kernel_class > 2) { set_error("profile: bad arguments"); return YL_ERR_ARG; }
-    if ((uint64_t)start_pos + n_steps > (uint64_t)m->ctx) { set_error("profile: positions beyond ctx_len"); return YL_ERR_RANGE; }
+yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos,
+                            int32_t kernel_class, uint32_t reps, double* us_per_launch, uint64_t* bytes_per_launch,
+                            uint32_t* launches) {
+    if (!m || !s || s->m != m || kernel_class < kOpQkv || kernel_class > kOpLogits || reps == 0) {
+        set_error("profile: bad arguments");
+        return YL_ERR_ARG;
+    }
+    if ((uint64_t)start_pos + 1 > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
     yl_status rs = put_state(s, (int32_t)start_pos, token);
     if (rs != YL_OK) return rs;
-    Prof prof;
-    prof.cls = kernel_class;
-    prof.stream = s->stream;
-    for (uint32_t i = 0; i < n_steps; i++) {
-        const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1, &prof);
-        if (e != hipSuccess) return hip_fail(e, "profile step");
-        prof.collect();
+    // one graph: this class's launches of one decode step, back to back
+    const int n_launch = kernel_class == kOpLogits ? 1 : m->n_layers;
+    uint64_t nbytes = 0;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "profile capture");
+    hipError_t ec = hipSuccess;
+    for (int l = 0; l < n_launch && ec == hipSuccess; l++) {
+        uint64_t b = 0;
+        ec = enqueue_op(m, s, kernel_class, l, 1, &s->st->token, 0, &b);
+        nbytes += b;
     }
-    const hipError_t e = hipStreamSynchronize(s->stream);
+    e = hipStreamEndCapture(s->stream, &g);
+    if (ec != hipSuccess || e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return hip_fail(ec != hipSuccess ? ec : e, "profile capture");
+    }
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "profile instantiate");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    for (int w = 0; w < 2 && e == hipSuccess; w++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, s->stream);
+    for (uint32_t r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, s->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    hipGraphExecDestroy(ge);
     if (e != hipSuccess) return hip_fail(e, "profile");
-    if (ms) *ms = prof.ms;
-    if (launches) *launches = prof.launches;
-    if (bytes) *bytes = prof.bytes;
+    if (us_per_launch) *us_per_launch = (double)ms * 1000.0 / ((double)reps * n_launch);
+    if (bytes_per_launch) *bytes_per_launch = nbytes / (uint64_t)n_launch;
+    if (launches) *launches = (uint32_t)n_launch;
     return YL_OK;
 }
 

@@ -1,0 +1,107 @@
+"""Summaries of rocprofv3 output for the decode benchmark.
+
+    python -m yallma3_mini_inference_amd.rocprof trace KERNEL_TRACE.csv > summary.md
+        Per kernel (name, grid): dispatch count, mean / median / min duration
+        (us).  Decode launches (grid y = 1) and prompt launches (grid y > 1,
+        one row per token) are listed apart, since the bench's per-launch
+        figures are for decode launches only.
+
+    python -m yallma3_mini_inference_amd.rocprof pmc FETCH.csv WRITE.csv MIB CLASS OUT.json
+        HBM bytes per launch of one GEMV class from the counter_collection.csv
+        files of `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`
+        runs of `bench.py --calibrate-copy-mib MIB`.  Both counters are KiB per
+        dispatch; the plain copy of MIB MiB (the largest dispatch whose name
+        contains "copy" or "elementwise") scales each counter to real bytes.
+        Writes the median scaled FETCH + WRITE bytes per decode dispatch (the
+        class's dispatches with the smallest grid).
+"""
+import csv
+import collections
+import json
+import statistics
+import sys
+
+# template signatures of the decode GEMV kernels at the Llama-3.2-1B shape
+# (format, rows per workgroup, threads)
+CLASS_KERNELS = {
+    "qkv": "k_gemv<0, 8, 320",
+    "wo": "k_gemv<0, 8, 256",
+    "w13": "k_gemv<0, 64, 576",
+    "w2": "k_gemv<0, 4, 256",
+}
+
+
+def _short(name):
+    name = name.replace("void ", "").replace("yl::", "")
+    return name.split("(")[0]
+
+
+def trace(path):
+    rows = list(csv.DictReader(open(path)))
+    by = collections.defaultdict(list)
+    for r in rows:
+        kind = "decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in r["Kernel_Name"] else "prompt"
+        key = (kind, _short(r["Kernel_Name"]), r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"],
+               r["VGPR_Count"], r["LDS_Block_Size"], r["Scratch_Size"])
+        by[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| launches | kernel | grid (x, y) | threads | VGPRs | LDS B | scratch | mean us | median us | min us | total us |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    for kind in ("decode", "prompt"):
+        items = [(k, v) for k, v in by.items() if k[0] == kind]
+        items.sort(key=lambda kv: -sum(kv[1]))
+        for k, v in items:
+            print(f"| {len(v)} {kind} | `{k[1]}` | {k[2]}, {k[3]} | {k[4]} | {k[5]} | {k[6]} | {k[7]} | "
+                  f"{statistics.mean(v):.2f} | {statistics.median(v):.2f} | {min(v):.2f} | {sum(v):.0f} |")
+
+
+def _per_dispatch(path, counter):
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            d = r["Dispatch_Id"]
+            grid = int(r.get("Grid_Size", "0"))
+            prev = out.get(d)
+            out[d] = (r["Kernel_Name"], float(r["Counter_Value"]) + (prev[1] if prev else 0.0), grid)
+    return out
+
+
+def _scaled(path, counter, calib_bytes, pattern):
+    rows = _per_dispatch(path, counter)
+    copies = [v for n, v, _ in rows.values() if "copy" in n.lower() or "elementwise" in n.lower()]
+    if not copies:
+        raise SystemExit(f"{path}: no copy kernel for calibration")
+    factor = calib_bytes / (max(copies) * 1024.0)
+    match = [(v, g) for n, v, g in rows.values() if pattern in n]
+    if not match:
+        raise SystemExit(f"{path}: no dispatch matching {pattern!r}")
+    # decode launches have the smallest grid (prompt launches add one row of
+    # workgroups per token)
+    gmin = min(g for _, g in match)
+    vals = [v * 1024.0 * factor for v, g in match if g == gmin]
+    return statistics.median(vals), factor, len(vals)
+
+
+def pmc(fetch_csv, write_csv, mib, cls, out):
+    pat = CLASS_KERNELS[cls]
+    calib = mib * 1024 * 1024
+    fb, ff, nf = _scaled(fetch_csv, "FETCH_SIZE", calib, pat)
+    wb, wf, nw = _scaled(write_csv, "WRITE_SIZE", calib, pat)
+    res = {"class": cls, "kernel_pattern": pat, "fetch_bytes_per_launch": int(fb),
+           "write_bytes_per_launch": int(wb), "traffic_bytes_per_launch": int(fb + wb),
+           "fetch_scale": round(ff, 4), "write_scale": round(wf, 4), "dispatches": [nf, nw],
+           "calibration": f"plain device copy of {mib} MiB (reads {calib} B, writes {calib} B)"}
+    with open(out, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    if len(sys.argv) >= 3 and sys.argv[1] == "trace":
+        trace(sys.argv[2])
+    elif len(sys.argv) >= 7 and sys.argv[1] == "pmc":
+        pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]), sys.argv[5], sys.argv[6])
+    else:
+        print(__doc__)
+        sys.exit(2)
