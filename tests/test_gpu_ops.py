@@ -146,6 +146,28 @@ def test_matmul_q4_parity(gpu, oracle, batch, n, o):
     assert_bits(out, ref)
 
 
+@pytest.mark.parametrize("fmt,batch,n,o", [(0, 16, 2048, 256), (0, 130, 576, 190), (0, 257, 8192, 128),
+                                           (1, 64, 2048, 384), (1, 200, 1536, 96)])
+def test_matmul_mfma_parity(gpu, oracle, fmt, batch, n, o):
+    # batches of >= 16 rows run the int8-MFMA GEMM: partial token and row
+    # tiles, the `+=` columns and the `=` tail columns, both formats
+    from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul
+    rng = np.random.default_rng(11 * n + o + batch)
+    if fmt == 0:
+        wf = rng.normal(0, 0.02, o * n).astype(np.float32)
+        blk, wq, ws = _gguf_q8_blocks(wf)
+        w = QuantizedWeight.upload_gguf(WeightFormat.Q8_0, blk, o, n)
+    else:
+        wq = rng.integers(0, 16, o * n).astype(np.int8)
+        ws = (rng.normal(0, 0.003, o * n // 32)).astype(np.float16).astype(np.float32)
+        w = QuantizedWeight.upload(WeightFormat.Q4_0, wq, ws, o, n)
+    xq, xs = oracle.quantize(fmt, rng.normal(0, 1, batch * n).astype(np.float32))
+    init = rng.normal(0, 1, batch * o).astype(np.float32)
+    out = matmul(init.copy(), xq, xs, w, n, o, fmt=WeightFormat(fmt))
+    ref = oracle.matmul_q8_slices(init.copy(), xq, xs, wq, ws, n, o)
+    assert_bits(out, ref)
+
+
 def test_matmul_format_mismatch_raises(gpu):
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, YlError, matmul
     w = QuantizedWeight.upload(WeightFormat.Q8_0, np.ones(64, np.int8), np.ones(2, np.float32), 2, 32)

@@ -1,0 +1,340 @@
+// yl_gemm.hip -- quantized matmul over many tokens (prompt prefill, and
+// yl_matmul with a large batch) on int8 MFMA, bit-identical to
+// matmul_q8_slices (weight_type.rs:122-226).
+//
+// The reference sums, for each output (token t, row c), the block terms
+//     term_b = ((float)isum_b * w_scale[c][b]) * x_scale[t][b]
+// in ascending block order into an f32 accumulator, where isum_b is the
+// exact int32 dot of one 32-element block.  v_mfma_i32_32x32x32_i8 has
+// K = 32: one instruction yields exactly the 32x32 block dots of one block,
+// and each lane then folds its 16 dots into its 16 f32 accumulators in
+// block order with the reference's two roundings.  The f32 work (convert,
+// two products, one sum per output and block) is the bound, not the MFMA.
+//
+// Tile: a 256-thread workgroup owns 128 tokens x 128 weight rows; wavefront
+// w covers tokens 64*(w&1) .. +63 and rows 64*(w>>1) .. +63 as 2x2 MFMA
+// tiles.  MFMA lane layout (gfx950): operand lane l holds row l%32 (token
+// for A, weight row for B) and k = 16*(l/32) .. +15 of the block; result
+// register i of lane l is (token (i%4) + 8*(i/4) + 4*(l/32), row l%32).
+// Stages of 2 blocks (activations 8 KiB, weights 8/4 KiB, both scale
+// vectors) stream into LDS by LDS DMA, 4 stages deep, so no register holds
+// data in flight.  Q4_0 weights keep the reference nibble order and are
+// unpacked in registers to int8 in k order (values 0..15, no offset).
+#include <hip/hip_runtime.h>
+
+#include "yl_blocks.h"
+#include "yl_device.h"
+#include "yl_internal.h"
+
+namespace yl {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kGmThreads = 256;
+constexpr int kGmTM = 128;      // tokens per workgroup
+constexpr int kGmTN = 128;      // weight rows per workgroup
+constexpr int kGmBK = 2;        // blocks per stage
+constexpr int kGmStages = 4;    // stages in flight
+
+template <int WF>
+struct GmStage {
+    static constexpr int kRowB = WF == kQ8 ? 32 : 16;         // weight bytes per row and block
+    static constexpr int A = kGmBK * kGmTM * 32;              // [blk][token][32] int8
+    static constexpr int B = kGmBK * kGmTN * kRowB;           // [blk][row][32 | 16]
+    static constexpr int XS = kGmBK * kGmTM * 4;              // [blk][token] f32
+    static constexpr int WS = kGmTN * 4;                      // [row][2] f16 (the stage's 2 blocks)
+    static constexpr int bytes = A + B + XS + WS;
+    // LDS DMA instructions per wavefront and stage (16-byte lanes move 1 KiB,
+    // 4-byte lanes 256 B); every wavefront issues the same number
+    static constexpr int dmaA = A / 1024 / 4;
+    static constexpr int dmaB = B / 1024 / 4;
+    static constexpr int dma = dmaA + dmaB + 1 + 1;
+    static_assert(A % 4096 == 0 && B % 4096 == 0, "16-byte DMA split over 4 wavefronts");
+    static_assert(XS == 4 * 256 && WS == 2 * 256, "scale DMA shapes");
+};
+
+size_t gemm_lds_bytes(int wfmt) {
+    return (size_t)kGmStages * (wfmt == kQ8 ? GmStage<kQ8>::bytes : GmStage<kQ4>::bytes);
+}
+
+template <int D>
+__device__ __forceinline__ void gm_wait(int later) {
+    // this wavefront's DMA of the current stage is done when at most
+    // `later` younger stages (D instructions each) are still in flight
+    static_assert(kGmStages - 2 == 2, "wait counts below cover two younger stages");
+    if (later <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(D) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * D) : "memory");
+}
+
+// 8 Q4_0 bytes (16 nibbles, byte j = elements 2j | 2j+1 << 4) -> 16 int8
+// in element order
+__device__ __forceinline__ v4i q4_unpack16(uint2 p) {
+    const uint32_t lo0 = p.x & 0x0f0f0f0fu, hi0 = (p.x >> 4) & 0x0f0f0f0fu;
+    const uint32_t lo1 = p.y & 0x0f0f0f0fu, hi1 = (p.y >> 4) & 0x0f0f0f0fu;
+    // v_perm_b32(hi, lo, sel): byte k of the result = byte sel_k of {hi:lo}
+    // (lo = bytes 0..3, hi = bytes 4..7)
+    v4i r;
+    r.x = (int)__builtin_amdgcn_perm(hi0, lo0, 0x05010400u);   // lo0.b0 hi0.b0 lo0.b1 hi0.b1
+    r.y = (int)__builtin_amdgcn_perm(hi0, lo0, 0x07030602u);   // lo0.b2 hi0.b2 lo0.b3 hi0.b3
+    r.z = (int)__builtin_amdgcn_perm(hi1, lo1, 0x05010400u);
+    r.w = (int)__builtin_amdgcn_perm(hi1, lo1, 0x07030602u);
+    return r;
+}
+
+template <int WF, int EPI>
+__global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemvArgs a, int M) {
+    // (device pass only: the host pass has no gfx950 MFMA builtins and
+    // needs just the launch stub)
+#if defined(__HIP_DEVICE_COMPILE__)
+    using S = GmStage<WF>;
+    extern __shared__ __align__(16) unsigned char gsm[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int c0 = blockIdx.x * kGmTN, t0 = blockIdx.y * kGmTM;
+    const int nst = a.nb / kGmBK;
+
+    // accumulators: acc[tm][tn][i] = (token t0 + 64wm + 32tm + (i%4) + 8(i/4) + 4lh,
+    //                                 row c0 + 64wn + 32tn + li)
+    float acc[2][2][16];
+    int pos = 0;
+    if constexpr (EPI == kEpiQkvRope) pos = a.state->pos;
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float v = 0.0f;
+                const int t = t0 + 64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
+                const int c = c0 + 64 * wn + 32 * tn + li;
+                if (t < M && c < a.o) {
+                    if constexpr (EPI == kEpiStore) {
+                        if (c < a.accumulate_cols) v = a.out[(size_t)t * a.o + c];
+                    } else if constexpr (EPI == kEpiQkvRope) {
+                        // K/V rows accumulate into the cache (forward.rs:166-169)
+                        const int att = a.att_dim, kv = a.kv_dim;
+                        if (c >= att && c < att + kv) {
+                            const int cc = c - att;
+                            if (cc < (kv / 4) * 4) v = a.k_cache[(size_t)cc * a.kv_ld + pos + t];
+                        } else if (c >= att + kv) {
+                            const int cc = c - att - kv;
+                            if (cc < (kv / 4) * 4) v = a.v_cache[(size_t)(pos + t) * kv + cc];
+                        }
+                    }
+                }
+                acc[tm][tn][i] = v;
+            }
+
+    // DMA of stage s (blocks 2s, 2s+1) into LDS buffer `buf`.  Token and
+    // row indices past the matrix re-read the last valid one (results unused).
+    auto issue = [&](unsigned char* buf, int s) {
+        const int b0 = s * kGmBK;
+        // activations: instruction j covers block j/4, tokens 32*(j%4) .. +31;
+        // lane i -> token i/2, half i%2
+#pragma unroll
+        for (int k = 0; k < S::dmaA; k++) {
+            const int j = wave * S::dmaA + k;
+            const int blk = j / 4, tok = min(t0 + 32 * (j % 4) + (lane >> 1), M - 1);
+            const int8_t* src = a.xq + (size_t)tok * a.n + (size_t)(b0 + blk) * 32 + 16 * (lane & 1);
+            __builtin_amdgcn_global_load_lds(src, buf + j * 1024, 16, 0, 0);
+        }
+        // weights: Q8 as activations; Q4 instruction j covers block j/2, rows
+        // 64*(j%2) .. +63, one 16-byte block per lane
+#pragma unroll
+        for (int k = 0; k < S::dmaB; k++) {
+            const int j = wave * S::dmaB + k;
+            const uint8_t* src;
+            if constexpr (WF == kQ8) {
+                const int blk = j / 4, row = min(c0 + 32 * (j % 4) + (lane >> 1), a.o - 1);
+                src = a.qs + (size_t)row * a.n + (size_t)(b0 + blk) * 32 + 16 * (lane & 1);
+            } else {
+                const int blk = j / 2, row = min(c0 + 64 * (j % 2) + lane, a.o - 1);
+                src = a.qs + (size_t)row * (a.n / 2) + (size_t)(b0 + blk) * 16;
+            }
+            __builtin_amdgcn_global_load_lds(src, buf + S::A + j * 1024, 16, 0, 0);
+        }
+        // activation scales: wavefront w -> block w/2, tokens 64*(w%2) + lane
+        {
+            const int tok = min(t0 + 64 * (wave & 1) + lane, M - 1);
+            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * a.nb + b0 + (wave >> 1),
+                                             buf + S::A + S::B + wave * 256, 4, 0, 0);
+        }
+        // weight scales: rows 64*(w%2) + lane, the stage's two f16 as one dword
+        // (wavefronts 2 and 3 repeat 0 and 1)
+        {
+            const int row = min(c0 + 64 * (wave & 1) + lane, a.o - 1);
+            __builtin_amdgcn_global_load_lds(a.d + (size_t)row * a.nb + b0, buf + S::A + S::B + S::XS + (wave & 1) * 256,
+                                             4, 0, 0);
+        }
+    };
+
+    // the initial values have landed before any DMA is issued, so the
+    // stage waits below count DMA instructions only
+    wait_vm_all();
+    // prologue: the first kGmStages - 1 stages in flight
+#pragma unroll
+    for (int s = 0; s < kGmStages - 1; s++)
+        if (s < nst) issue(gsm + s * S::bytes, s);
+
+    for (int s = 0; s < nst; s++) {
+        gm_wait<S::dma>(min(kGmStages - 2, nst - 1 - s));
+        __syncthreads();   // every wavefront's DMA of stage s landed; stage s-1's buffer is free
+        if (s + kGmStages - 1 < nst)
+            issue(gsm + ((s + kGmStages - 1) % kGmStages) * S::bytes, s + kGmStages - 1);
+        const unsigned char* buf = gsm + (s % kGmStages) * S::bytes;
+        const float* xsl = reinterpret_cast<const float*>(buf + S::A + S::B);
+        const uint16_t* wsl = reinterpret_cast<const uint16_t*>(buf + S::A + S::B + S::XS);
+#pragma unroll
+        for (int blk = 0; blk < kGmBK; blk++) {
+            const unsigned char* Ab = buf + blk * (kGmTM * 32);
+            const unsigned char* Bb = buf + S::A + blk * (kGmTN * S::kRowB);
+            v4i av[2], bv[2];
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+                av[tm] = *reinterpret_cast<const v4i*>(Ab + (64 * wm + 32 * tm + li) * 32 + 16 * lh);
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++) {
+                if constexpr (WF == kQ8) {
+                    bv[tn] = *reinterpret_cast<const v4i*>(Bb + (64 * wn + 32 * tn + li) * 32 + 16 * lh);
+                } else {
+                    bv[tn] = q4_unpack16(*reinterpret_cast<const uint2*>(Bb + (64 * wn + 32 * tn + li) * 16 + 8 * lh));
+                }
+            }
+            float wsc[2];
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++) wsc[tn] = f16_to_f32(wsl[(64 * wn + 32 * tn + li) * 2 + blk]);
+            vf4 xv[2][4];
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    xv[tm][g] = *reinterpret_cast<const vf4*>(xsl + blk * kGmTM + 64 * wm + 32 * tm + 8 * g + 4 * lh);
+            // the four tiles' dots first (in separate registers), so the f32
+            // work of one tile does not wait on the next tile's MFMA
+            v16i dots[2][2];
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) {
+                    const v16i zero = {};
+                    dots[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[tm], bv[tn], zero, 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const float term = fmul(fmul((float)dots[tm][tn][i], wsc[tn]), xv[tm][i >> 2][i & 3]);
+                        acc[tm][tn][i] = fadd(acc[tm][tn][i], term);
+                    }
+        }
+    }
+
+    // epilogues
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int t = t0 + 64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
+            const bool tok_ok = t < M;
+            if constexpr (EPI == kEpiSwiglu) {
+                // SwiGLU (forward.rs:220-237) over the 64-row group [32 gate |
+                // 32 up] of this wavefront, then the 32-group quantization of h
+                const int grp = (c0 + 64 * wn) / 64;
+                const bool grp_ok = c0 + 64 * wn < a.o;
+                const float g = acc[tm][0][i], u = acc[tm][1][i];
+                const float den = fadd(1.0f, expf_rn(-g));
+                const float h = fmul(g / den, u);
+                float am = group_max(fabsf(h), 32);
+                am = fmaxf(am, 0.0f);
+                const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
+                const int q = a.h_fmt == kQ4 ? quant_one<kQ4>(h, sc) : quant_one<kQ8>(h, sc);
+                if (tok_ok && grp_ok) {
+                    const size_t base = (size_t)t * a.hidden + (size_t)grp * kGroup;
+                    if (a.h_f32) a.h_f32[base + li] = h;
+                    a.hq[base + li] = (int8_t)q;
+                    if (li == 0) a.hs[(size_t)t * (a.hidden / kGroup) + grp] = sc;
+                }
+            } else {
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) {
+                    const int c = c0 + 64 * wn + 32 * tn + li;
+                    const float v = acc[tm][tn][i];
+                    if constexpr (EPI == kEpiQkvRope) {
+                        // rope_gguf (util.rs:653-718) on q and k pairs (2j, 2j+1):
+                        // the pair partner is the neighbouring lane
+                        const float other = dpp_mov<0xB1>(v);
+                        if (tok_ok && c < a.o) {
+                            const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
+                            if (c >= att + kv) {
+                                a.v_cache[(size_t)(pos + t) * kv + (c - att - kv)] = v;
+                            } else {
+                                const int col = c < att ? c : c - att;
+                                const int pair = (col % hd) >> 1;
+                                const float cs = a.rope_cos[(size_t)(pos + t) * (hd >> 1) + pair];
+                                const float sn = a.rope_sin[(size_t)(pos + t) * (hd >> 1) + pair];
+                                const float v0 = (li & 1) ? other : v, v1 = (li & 1) ? v : other;
+                                const float r = (li & 1) ? fadd(fmul(v0, sn), fmul(v1, cs)) : fmul(v0, cs) - fmul(v1, sn);
+                                if (c < att) a.q_out[(size_t)t * att + col] = r;
+                                else a.k_cache[(size_t)col * a.kv_ld + pos + t] = r;
+                            }
+                        }
+                    } else if (tok_ok && c < a.o) {
+                        if constexpr (EPI == kEpiStore) a.out[(size_t)t * a.o + c] = v;
+                        if constexpr (EPI == kEpiResid) {
+                            // residual add (forward.rs:196-204 / 245-253)
+                            float* xp = a.x + (size_t)t * a.o + c;
+                            *xp = fadd(*xp, v);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+#endif
+}
+
+template <int WF, int EPI>
+static hipError_t launch_gemm_k(const GemvArgs& a, int M, hipStream_t st) {
+    const size_t smem = gemm_lds_bytes(WF);
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm<WF, EPI>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const dim3 grid((a.o + kGmTN - 1) / kGmTN, (M + kGmTM - 1) / kGmTM);
+    hipLaunchKernelGGL((k_gemm<WF, EPI>), grid, dim3(kGmThreads), smem, st, a, M);
+    return hipGetLastError();
+}
+
+bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M) {
+    if (M < 1 || a.n % 32 || a.nb != a.n / 32 || a.nb % kGmBK || (wfmt != kQ8 && wfmt != kQ4)) return false;
+    if (epi == kEpiSwiglu && (a.o % 64 || a.hidden * 2 != a.o)) return false;
+    if (epi == kEpiQkvRope && (a.head_size % 2 || a.att_dim % 32)) return false;
+    return true;
+}
+
+hipError_t launch_gemm(const GemvArgs& a, int wfmt, int epi, int M, hipStream_t st) {
+    if (!gemm_supported(a, wfmt, epi, M)) return hipErrorInvalidValue;
+#define YL_GEMM_EPI(WF)                                                        \
+    switch (epi) {                                                             \
+    case kEpiStore: return launch_gemm_k<WF, kEpiStore>(a, M, st);            \
+    case kEpiQkvRope: return launch_gemm_k<WF, kEpiQkvRope>(a, M, st);        \
+    case kEpiResid: return launch_gemm_k<WF, kEpiResid>(a, M, st);            \
+    case kEpiSwiglu: return launch_gemm_k<WF, kEpiSwiglu>(a, M, st);          \
+    default: return hipErrorInvalidValue;                                      \
+    }
+    if (wfmt == kQ8) { YL_GEMM_EPI(kQ8) }
+    YL_GEMM_EPI(kQ4)
+#undef YL_GEMM_EPI
+}
+
+}  // namespace yl

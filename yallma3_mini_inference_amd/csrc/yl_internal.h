@@ -87,6 +87,11 @@ struct GemvArgs {
 // kernel launchers; all return the hipError_t of the launch
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s);
+// many-token matmul on int8 MFMA (same epilogues and results as the GEMV;
+// activations always pre-quantized in xq/xs, M = tokens)
+bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M);
+size_t gemm_lds_bytes(int wfmt);
+hipError_t launch_gemm(const GemvArgs& a, int wfmt, int epi, int M, hipStream_t s);
 // out[c * out_ld + r] = in[r][c] for an in[rows][cols] f32 matrix
 hipError_t launch_transpose(const float* in, float* out, int rows, int cols, int out_ld, hipStream_t s);
 hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, float eps, int batch,

@@ -276,8 +276,8 @@ struct yl_session {
     StepState* st_host = nullptr;   // pinned
     int cap_b = 0;
     float *x = nullptr, *sq = nullptr, *logits = nullptr;
-    int8_t *aq = nullptr, *hq = nullptr;
-    float *as_ = nullptr, *hs = nullptr;
+    int8_t *aq = nullptr, *hq = nullptr, *nq = nullptr;   // nq/ns: normalized, quantized rows (prompt)
+    float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
     unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
@@ -515,7 +515,7 @@ bool session_grow(yl_session* s, int batch) {
     hipStreamSynchronize(s->stream);
     if (s->graph) { hipGraphExecDestroy(s->graph); s->graph = nullptr; }
     auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
-    rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens);
+    rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens); rel(s->nq); rel(s->ns);
     const size_t B = (size_t)batch;
     bool ok = hipMalloc(&s->x, B * m->dim * 4 + 256) == hipSuccess &&
               hipMalloc(&s->sq, B * m->att * 4 + 256) == hipSuccess &&
@@ -523,7 +523,9 @@ bool session_grow(yl_session* s, int batch) {
               hipMalloc(&s->hq, B * m->hidden + 256) == hipSuccess &&
               hipMalloc(&s->as_, B * m->att / 8 + 256) == hipSuccess &&
               hipMalloc(&s->hs, B * m->hidden / 8 + 256) == hipSuccess &&
-              hipMalloc(&s->tokens, B * 4 + 256) == hipSuccess;
+              hipMalloc(&s->tokens, B * 4 + 256) == hipSuccess &&
+              hipMalloc(&s->nq, B * m->dim + 256) == hipSuccess &&
+              hipMalloc(&s->ns, B * m->dim / 8 + 256) == hipSuccess;
     if (!ok) { set_error("hipMalloc failed for session buffers"); s->cap_b = 0; return false; }
     s->cap_b = batch;
     return true;
@@ -536,6 +538,58 @@ uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
 // Kernel classes of a forward pass, in step order (also the profiling
 // classes of yl_profile_kernel).
 enum OpClass : int { kOpQkv = 0, kOpAttn = 1, kOpWo = 2, kOpW13 = 3, kOpW2 = 4, kOpLogits = 5 };
+
+// Prompt batches from this many tokens run the projections on the int8
+// MFMA GEMM (activations normalized and quantized once per row first).
+constexpr int kGemmMinTokens = 16;
+
+// The projections of op `cls` of layer l over `batch` tokens on the GEMM;
+// hipErrorNotSupported when a shape needs the GEMV instead.
+hipError_t enqueue_op_gemm(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
+                           float* kc, float* vc, uint64_t* bytes) {
+    hipStream_t st = s->stream;
+    const Layer& L = m->layers[l];
+    GemvArgs a{};
+    const QMat* w = nullptr;
+    int epi = 0;
+    switch (cls) {
+    case kOpQkv:
+        w = &L.qkv; epi = kEpiQkvRope;
+        a.xq = s->nq; a.xs = s->ns;
+        a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
+        a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
+        a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
+        break;
+    case kOpWo:
+        w = &L.wo; epi = kEpiResid;
+        a.xq = s->aq; a.xs = s->as_; a.x = s->x;
+        break;
+    case kOpW13:
+        w = &L.w13; epi = kEpiSwiglu;
+        a.xq = s->nq; a.xs = s->ns;
+        a.hq = s->hq; a.hs = s->hs; a.h_f32 = nullptr; a.hidden = m->hidden; a.h_fmt = L.w2.fmt;
+        break;
+    case kOpW2:
+        w = &L.w2; epi = kEpiResid;
+        a.xq = s->hq; a.xs = s->hs; a.x = s->x;
+        break;
+    default:
+        return hipErrorNotSupported;
+    }
+    a.qs = w->qs; a.d = w->d; a.n = w->n; a.o = w->o; a.nb = w->nb;
+    if (!gemm_supported(a, w->fmt, epi, batch)) return hipErrorNotSupported;
+    hipError_t e = hipSuccess;
+    if (cls == kOpQkv || cls == kOpW13) {
+        // RMSNorm (+ the layer-0 embedding lookup) and quantization of every row
+        if (cls == kOpQkv && l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
+        if (e == hipSuccess)
+            e = launch_rmsnorm(w->fmt, s->x, cls == kOpQkv ? L.rms_att : L.rms_ffn, m->dim, m->eps, batch, nullptr,
+                               s->nq, s->ns, st);
+        if (e != hipSuccess) return e;
+    }
+    if (bytes) *bytes = gemv_bytes(*w, w->o, batch);
+    return launch_gemm(a, w->fmt, epi, batch, st);
+}
 
 // Enqueues op `cls` of layer l for `batch` tokens whose ids are at `tok`
 // (device) and whose first position is st->pos (device), on s->stream.
@@ -554,6 +608,10 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     const Layer& L = m->layers[l];
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
+    if (batch >= kGemmMinTokens && cls != kOpAttn) {
+        hipError_t e = enqueue_op_gemm(m, s, cls, l, batch, tok, kc, vc, bytes);
+        if (e != hipErrorNotSupported) return e;
+    }
     GemvArgs a{};
     switch (cls) {
     case kOpQkv:
@@ -770,7 +828,9 @@ yl_status yl_matmul(float* out, yl_format fmt, const int8_t* xq, const float* xs
     GemvArgs a{};
     a.qs = w->m.qs; a.d = w->m.d; a.n = w->m.n; a.o = w->m.o; a.nb = w->m.nb;
     a.xq = xq; a.xs = xs; a.out = out; a.accumulate_cols = (int)(o / 4 * 4);
-    const hipError_t e = launch_gemv(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream);
+    const bool mfma = batch >= (size_t)kGemmMinTokens && gemm_supported(a, w->m.fmt, kEpiStore, (int)batch);
+    const hipError_t e = mfma ? launch_gemm(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream)
+                              : launch_gemv(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream);
     return e == hipSuccess ? YL_OK : hip_fail(e, "matmul launch");
 }
 
