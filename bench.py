@@ -79,6 +79,125 @@ def cpu_baseline(path, prompt_len, seconds):
                       f"model, KV cache below {prompt_len} random-filled, {el:.1f}s"}
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0
+
+
+def run_prefill(args):
+    """Llama-3.2-1B-shaped Q4_0 (Q4_0 activations, reference semantics): a prompt of
+    --prefill-tokens random ids in one forward_x (projections on the int8-MFMA
+    GEMM), then --steps greedy decode steps.  Per-class GEMM times come from graph
+    replays of each projection's 16 launches at the prompt's batch."""
+    import numpy as np
+    import yallma3_mini_inference_amd as Y
+    from yallma3_mini_inference_amd import synth
+    M = args.prefill_tokens
+    path = synth.ensure("llama32_1b_q4")
+    model = Y.Transformer(path)
+    sess = model.create_session()
+    sh = model.shape
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, model.vocab_size(), M).astype(np.uint32)
+    model.forward_argmax(prompt, 0, sess)          # first use: kernel set-up, buffers
+    sess.reset()
+    Y.lib().yl_synchronize()
+    t0 = time.perf_counter()
+    first = model.forward_argmax(prompt, 0, sess)
+    Y.lib().yl_synchronize()
+    pre_s = time.perf_counter() - t0
+    log(f"prefill {M} tokens: {pre_s * 1e3:.1f} ms -> {M / pre_s:.0f} tok/s")
+    steps = min(args.steps, 256)
+    t0 = time.perf_counter()
+    toks = model.generate_greedy(sess, first, M, steps)
+    Y.lib().yl_synchronize()
+    dec_s = time.perf_counter() - t0
+    log(f"decode after prefill: {steps} steps in {dec_s * 1e3:.1f} ms -> {steps / dec_s:.1f} tok/s")
+    dim, hid, att, kv = sh.dimension, sh.hidden_dimension, sh.n_heads * sh.head_size, sh.n_kv_heads * sh.head_size
+    shapes = {"qkv": (att + 2 * kv, dim), "wo": (dim, att), "w13": (2 * hid, dim), "w2": (dim, hid)}
+    kern, gemm_us, gemm_ops = {}, 0.0, 0
+    for cls in ("qkv", "wo", "w13", "w2", "attention"):
+        us, _, n = model.profile_kernel(sess, first, 0, cls, reps=3, batch=M)
+        kern[cls] = {"us": round(us, 1), "launches_per_step": n}
+        if cls in shapes:
+            o, k = shapes[cls]
+            ops = 2 * M * o * k
+            kern[cls]["tops"] = round(ops / (us * 1e-6) / 1e12, 1)
+            gemm_us += us * n
+            gemm_ops += ops * n
+        log(f"{cls}: {us:.1f} us/launch" + (f" -> {kern[cls]['tops']} TOP/s" if cls in shapes else ""))
+    tops = gemm_ops / (gemm_us * 1e-6) / 1e12
+    log(f"GEMMs: {gemm_ops / 1e12:.3f} T int8 ops in {gemm_us / 1e3:.2f} ms -> {tops:.0f} TOP/s "
+        f"({tops / MFMA_INT8_PEAK_TOPS * 100:.1f}% of {MFMA_INT8_PEAK_TOPS:.0f})")
+    print(json.dumps({
+        "metric": f"prefill tok/s, Llama-3.2-1B-shaped Q4_0, {M}-token prompt (int8-MFMA GEMM)",
+        "value": round(M / pre_s, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "int8", "data": "synthetic (seeded N(0,0.02) weights, GGUF Q4_0; random prompt ids)",
+        "config": {"workload": f"Llama-3.2-1B-shaped Q4_0 prefill of {M} tokens, then {steps} greedy steps",
+                   "prompt_tokens": M},
+        "prefill_ms": round(pre_s * 1e3, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "k_gemm (int8 MFMA, all four projections)",
+                     "int_ops_per_prefill": gemm_ops, "gemm_ms": round(gemm_us / 1e3, 3)},
+        "kernels": kern,
+        "decode_tok_s_after_prefill": round(steps / dec_s, 1),
+        "tokens_head": [int(t) for t in toks[:8]],
+    }), flush=True)
+
+
+def run_matvec(args):
+    """The isolated Q8_0 matvec: W 8192x2048 ~N(0,0.02) as GGUF Q8_0 blocks, x 2048
+    ~N(0,1) quantized Q8_0, out 8192 f32, seed 0; 1000 launches rotating through 24
+    device copies of W (408 MiB, beyond the 256 MiB MALL)."""
+    import ctypes as C
+    import numpy as np
+    import yallma3_mini_inference_amd as Y
+    from oracle import oracle as O
+    L = Y.lib()
+    o, n, copies, iters = 8192, 2048, 24, 1000
+    wf = np.zeros(o * n, np.float32)
+    xf = np.zeros(n, np.float32)
+    Y.check(L.yl_synthetic_normal(0, 0, 0, wf.size, C.c_float(0.02), wf.ctypes.data))
+    Y.check(L.yl_synthetic_normal(0, 1, 0, xf.size, C.c_float(1.0), xf.ctypes.data))
+    blocks = wf.reshape(-1, 32)
+    d = (np.abs(blocks).max(axis=1) / np.float32(127.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    q = np.round(blocks * inv[:, None]).astype(np.int8)
+    raw = np.zeros((blocks.shape[0], 34), np.uint8)
+    raw[:, :2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    raw[:, 2:] = q.view(np.uint8)
+    ws = [Y.QuantizedWeight.upload_gguf(Y.WeightFormat.Q8_0, raw.ravel(), o, n) for _ in range(copies)]
+    xq, xs = Y.quantize(Y.WeightFormat.Q8_0, xf)
+    dq, ds = Y.DeviceBuffer.from_numpy(xq), Y.DeviceBuffer.from_numpy(xs)
+    dout = Y.DeviceBuffer.from_numpy(np.zeros(o, np.float32))
+    handles = (C.c_void_p * copies)(*[w._h for w in ws])
+    us = C.c_double()
+    Y.check(L.yl_matmul_bench(handles, copies, dq.ptr, ds.ptr, 1, dout.ptr, max(1, iters // copies), C.byref(us)))
+    nbytes = o * n + (o * n // 32) * 2 + n + (n // 32) * 4 + o * 4
+    gbs = nbytes / (us.value * 1e-6) / 1e9
+    # parity of the last launch against the oracle
+    out = dout.numpy()
+    ref = O.matmul_q8_slices(np.zeros(o, np.float32), xq, xs, q.ravel(),
+                             d.astype(np.float16).astype(np.float32), n, o)
+    same = bool((out.view(np.uint32) == ref.view(np.uint32)).all())
+    log(f"matvec 8192x2048 Q8_0: {us.value:.2f} us/launch, {nbytes} B -> {gbs:.0f} GB/s; bit-exact: {same}")
+    t0, k = time.perf_counter(), 0
+    while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) and k < iters:
+        O.matmul_q8_slices(np.zeros(o, np.float32), xq, xs, q.ravel(), d.astype(np.float16).astype(np.float32), n, o)
+        k += 1
+    cpu_us = (time.perf_counter() - t0) / k * 1e6
+    print(json.dumps({
+        "metric": "isolated Q8_0 matvec 8192x2048 GB/s", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "higher_is_better": True, "dtype": "int8", "data": "synthetic (seed 0, W ~N(0,0.02) GGUF Q8_0, x ~N(0,1))",
+        "config": {"workload": f"8192x2048 Q8_0 matvec, {iters} launches over {copies} weight copies"},
+        "us_per_launch": round(us.value, 3), "bit_exact": same,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv (store epilogue)", "bytes_per_launch": nbytes},
+        "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us/matvec", "cores": O.num_threads(), "kind": "port",
+                         "sample": f"{k} oracle matmul_q8_slices calls on the same inputs"},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,6 +207,11 @@ def main():
     ap.add_argument("--config", default="llama32_1b")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("decode", "prefill", "matvec"), default="decode",
+                    help="decode: the headline Llama-3.2-1B Q8_0 decode (default); prefill: Llama-3.2-1B Q4_0 "
+                         "prompt of --prefill-tokens on the int8-MFMA GEMM, then greedy decode; matvec: the "
+                         "isolated 8192x2048 Q8_0 matvec")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -117,6 +241,10 @@ def main():
         L.yl_free(src)
         L.yl_free(dst)
         log(f"calibration copy: {nbytes} B read + {nbytes} B written")
+    if args.workload == "prefill":
+        return run_prefill(args)
+    if args.workload == "matvec":
+        return run_matvec(args)
     t0 = time.perf_counter()
     path = synth.ensure(args.config)
     log(f"model {path} ready in {time.perf_counter() - t0:.1f}s")

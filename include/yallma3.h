@@ -117,6 +117,15 @@ size_t yl_weight_bytes(const yl_weight *w);
 yl_status yl_matmul(float *out, yl_format fmt, const int8_t *xq, const float *xs, size_t batch,
                     const yl_weight *w, size_t n, size_t o, uint32_t gs, void *stream);
 
+/* Timing of yl_matmul (`=` into out, no accumulation): the count weights
+ * (same format and shape, device-resident) are multiplied by the same
+ * activations one after another in a HIP graph, the graph is replayed `reps`
+ * times between two HIP events, and the elapsed time is divided by the
+ * launches.  Rotating through distinct weight copies larger in total than
+ * the 256 MiB MALL measures HBM, not cache.  xq/xs/out: device. */
+yl_status yl_matmul_bench(const yl_weight *const *ws, size_t count, const int8_t *xq, const float *xs,
+                          size_t batch, float *out, uint32_t reps, double *us_per_launch);
+
 /* util::rmsnorm per row (batch rows of size floats, device), optionally
  * followed by quantization of the normalized row.  qfmt: YL_Q8_0 / YL_Q4_0
  * to quantize into q/scale, or -1 for none.  xn (nullable) receives the f32
@@ -212,19 +221,23 @@ yl_status yl_generate_greedy(const yl_model *m, yl_session *s, uint32_t token, u
                              uint32_t n_steps, uint32_t *out_tokens);
 
 /* ------------------------------------------------------------ profiling */
-/* Timing of one kernel class of a decode step at position start_pos:
- * the class's launches of one step (one per layer; one for logits) are
+/* Timing of one kernel class of a forward step over `batch` tokens at
+ * positions start_pos..start_pos+batch-1 (batch 1: a decode step): the
+ * class's launches of one step (one per layer; one for logits) are
  * captured back to back in a HIP graph, replayed `reps` times between two
  * HIP events on the session's stream, and the elapsed time is divided by
- * the launches.  kernel_class: 0 = QKV GEMV (RMSNorm prologue, RoPE/KV
- * epilogue), 1 = decode attention, 2 = Wo GEMV, 3 = gate/up GEMV (RMSNorm
- * prologue, SwiGLU epilogue), 4 = down GEMV, 5 = logits.  Returns the
- * average launch time (us), the algorithmic bytes one launch reads and
- * writes (0 for attention) and the launches per step.  Leaves the session's
- * KV cache at start_pos, its residual stream and its activations modified
- * (the replays repeat the `+=` steps): reset the session afterwards. */
+ * the launches.  kernel_class: 0 = QKV projection (RoPE/KV epilogue; at
+ * batch 1 with its RMSNorm prologue), 1 = attention, 2 = Wo projection,
+ * 3 = gate/up projection (SwiGLU epilogue; at batch 1 with its RMSNorm
+ * prologue), 4 = down projection, 5 = logits.  For batch >= 16 the
+ * projections are the int8-MFMA GEMM alone (the row normalization before
+ * it is not captured).  Returns the average launch time (us), the
+ * algorithmic bytes one launch reads and writes (0 for attention) and the
+ * launches per step.  Leaves the session's KV cache at those positions, its
+ * residual stream and its activations modified (the replays repeat the `+=`
+ * steps): reset the session afterwards. */
 yl_status yl_profile_kernel(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
-                            int32_t kernel_class, uint32_t reps, double *us_per_launch,
+                            uint32_t batch, int32_t kernel_class, uint32_t reps, double *us_per_launch,
                             uint64_t *bytes_per_launch, uint32_t *launches);
 
 /* Elementwise probe of the device arithmetic the path relies on (device

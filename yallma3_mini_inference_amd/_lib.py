@@ -21,7 +21,7 @@ STATUS_NAMES = {
 # every symbol include/yallma3.h declares
 EXPORTS = [
     "yl_last_error", "load_transformer_ffi", "infer_ffi", "free_string", "yl_device_count", "yl_malloc",
-    "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memcpy_d2d", "yl_memset_d", "yl_synchronize", "yl_quantize",
+    "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memcpy_d2d", "yl_matmul_bench", "yl_memset_d", "yl_synchronize", "yl_quantize",
     "yl_weight_upload", "yl_weight_upload_gguf", "yl_weight_free", "yl_weight_bytes", "yl_matmul",
     "yl_rmsnorm_quantize", "yl_rope_gguf", "yl_attention", "yl_swiglu_quantize", "yl_load",
     "yl_model_free", "yl_model_name", "yl_model_shape", "yl_vocab_size", "yl_max_ctx_len", "yl_bos_token",
@@ -87,6 +87,7 @@ def lib():
         "yl_memcpy_h2d": (st, [vp, vp, sz]),
         "yl_memcpy_d2h": (st, [vp, vp, sz]),
         "yl_memcpy_d2d": (st, [vp, vp, sz]),
+        "yl_matmul_bench": (st, [vp, sz, vp, vp, sz, vp, u32, C.POINTER(C.c_double)]),
         "yl_memset_d": (st, [vp, C.c_int, sz]),
         "yl_synchronize": (st, []),
         "yl_quantize": (st, [C.c_int, vp, vp, vp, sz, u32, vp]),
@@ -118,7 +119,7 @@ def lib():
         "yl_session_kv": (st, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz)]),
         "yl_forward_x": (st, [vp, vp, sz, u32, vp, vp, vp]),
         "yl_generate_greedy": (st, [vp, vp, u32, u32, u32, vp]),
-        "yl_profile_kernel": (st, [vp, vp, u32, u32, st, u32, C.POINTER(C.c_double), C.POINTER(u64),
+        "yl_profile_kernel": (st, [vp, vp, u32, u32, u32, st, u32, C.POINTER(C.c_double), C.POINTER(u64),
                                    C.POINTER(u32)]),
         "yl_math_selftest": (st, [vp, sz, vp, vp, vp, vp]),
         "yl_write_synthetic_gguf": (st, [C.c_char_p, C.POINTER(SynthConfig)]),

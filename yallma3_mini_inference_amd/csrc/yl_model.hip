@@ -543,10 +543,11 @@ enum OpClass : int { kOpQkv = 0, kOpAttn = 1, kOpWo = 2, kOpW13 = 3, kOpW2 = 4, 
 // MFMA GEMM (activations normalized and quantized once per row first).
 constexpr int kGemmMinTokens = 16;
 
-// The projections of op `cls` of layer l over `batch` tokens on the GEMM;
+// The projections of op `cls` of layer l over `batch` tokens on the GEMM
+// (prologue: the row normalization the QKV and gate/up GEMMs read first);
 // hipErrorNotSupported when a shape needs the GEMV instead.
 hipError_t enqueue_op_gemm(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
-                           float* kc, float* vc, uint64_t* bytes) {
+                           float* kc, float* vc, uint64_t* bytes, bool prologue) {
     hipStream_t st = s->stream;
     const Layer& L = m->layers[l];
     GemvArgs a{};
@@ -579,7 +580,7 @@ hipError_t enqueue_op_gemm(const yl_model* m, yl_session* s, int cls, int l, int
     a.qs = w->qs; a.d = w->d; a.n = w->n; a.o = w->o; a.nb = w->nb;
     if (!gemm_supported(a, w->fmt, epi, batch)) return hipErrorNotSupported;
     hipError_t e = hipSuccess;
-    if (cls == kOpQkv || cls == kOpW13) {
+    if (prologue && (cls == kOpQkv || cls == kOpW13)) {
         // RMSNorm (+ the layer-0 embedding lookup) and quantization of every row
         if (cls == kOpQkv && l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
         if (e == hipSuccess)
@@ -596,7 +597,7 @@ hipError_t enqueue_op_gemm(const yl_model* m, yl_session* s, int cls, int l, int
 // `bytes` (nullable) receives the algorithmic bytes the launch reads and
 // writes.
 hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok, int advance,
-                      uint64_t* bytes) {
+                      uint64_t* bytes, bool prologue = true) {
     hipStream_t st = s->stream;
     const size_t lay_kv = (size_t)m->kv_ld * m->kv;
     if (cls == kOpLogits) {
@@ -609,7 +610,7 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
     if (batch >= kGemmMinTokens && cls != kOpAttn) {
-        hipError_t e = enqueue_op_gemm(m, s, cls, l, batch, tok, kc, vc, bytes);
+        hipError_t e = enqueue_op_gemm(m, s, cls, l, batch, tok, kc, vc, bytes, prologue);
         if (e != hipErrorNotSupported) return e;
     }
     GemvArgs a{};
@@ -832,6 +833,55 @@ yl_status yl_matmul(float* out, yl_format fmt, const int8_t* xq, const float* xs
     const hipError_t e = mfma ? launch_gemm(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream)
                               : launch_gemv(a, w->m.fmt, kEpiStore, (int)batch, (hipStream_t)stream);
     return e == hipSuccess ? YL_OK : hip_fail(e, "matmul launch");
+}
+
+yl_status yl_matmul_bench(const yl_weight* const* ws, size_t count, const int8_t* xq, const float* xs, size_t batch,
+                          float* out, uint32_t reps, double* us_per_launch) {
+    if (!ws || count == 0 || !xq || !xs || !out || reps == 0 || batch == 0 || batch > 65535) {
+        set_error("matmul_bench: bad arguments");
+        return YL_ERR_ARG;
+    }
+    for (size_t i = 0; i < count; i++)
+        if (!ws[i] || ws[i]->m.n != ws[0]->m.n || ws[i]->m.o != ws[0]->m.o || ws[i]->m.fmt != ws[0]->m.fmt) {
+            set_error("matmul_bench: weights must share format and shape");
+            return YL_ERR_ARG;
+        }
+    hipStream_t st = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "matmul_bench stream");
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    hipError_t ec = hipSuccess;
+    for (size_t i = 0; i < count && e == hipSuccess && ec == hipSuccess; i++) {
+        const QMat& w = ws[i]->m;
+        GemvArgs a{};
+        a.qs = w.qs; a.d = w.d; a.n = w.n; a.o = w.o; a.nb = w.nb;
+        a.xq = xq; a.xs = xs; a.out = out; a.accumulate_cols = 0;
+        const bool mfma = batch >= (size_t)kGemmMinTokens && gemm_supported(a, w.fmt, kEpiStore, (int)batch);
+        ec = mfma ? launch_gemm(a, w.fmt, kEpiStore, (int)batch, st) : launch_gemv(a, w.fmt, kEpiStore, (int)batch, st);
+    }
+    if (e == hipSuccess) e = hipStreamEndCapture(st, &g);
+    if (e == hipSuccess) e = ec;
+    if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipGraphLaunch(ge, st);
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
+    for (uint32_t r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, st);
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (ge) hipGraphExecDestroy(ge);
+    if (g) hipGraphDestroy(g);
+    hipStreamDestroy(st);
+    if (e != hipSuccess) return hip_fail(e, "matmul_bench");
+    if (us_per_launch) *us_per_launch = (double)ms * 1000.0 / ((double)reps * (double)count);
+    return YL_OK;
 }
 
 yl_status yl_rmsnorm_quantize(const float* x, const float* weight, size_t size, float eps, size_t batch, float* xn,
@@ -1078,17 +1128,19 @@ yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, u
     return e == hipSuccess ? YL_OK : hip_fail(e, "generate");
 }
 
-yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos,
+yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, uint32_t batch,
                             int32_t kernel_class, uint32_t reps, double* us_per_launch, uint64_t* bytes_per_launch,
                             uint32_t* launches) {
-    if (!m || !s || s->m != m || kernel_class < kOpQkv || kernel_class > kOpLogits || reps == 0) {
+    if (!m || !s || s->m != m || kernel_class < kOpQkv || kernel_class > kOpLogits || reps == 0 || batch == 0 ||
+        batch > 65535) {
         set_error("profile: bad arguments");
         return YL_ERR_ARG;
     }
-    if ((uint64_t)start_pos + 1 > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
+    if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
+    if (batch > 1 && !session_grow(s, (int)batch)) return YL_ERR_NOMEM;
     yl_status rs = put_state(s, (int32_t)start_pos, token);
     if (rs != YL_OK) return rs;
-    // one graph: this class's launches of one decode step, back to back
+    // one graph: this class's launches of one step, back to back
     const int n_launch = kernel_class == kOpLogits ? 1 : m->n_layers;
     uint64_t nbytes = 0;
     hipGraph_t g = nullptr;
@@ -1098,7 +1150,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     hipError_t ec = hipSuccess;
     for (int l = 0; l < n_launch && ec == hipSuccess; l++) {
         uint64_t b = 0;
-        ec = enqueue_op(m, s, kernel_class, l, 1, &s->st->token, 0, &b);
+        ec = enqueue_op(m, s, kernel_class, l, (int)batch, batch == 1 ? &s->st->token : s->tokens, 0, &b, false);
         nbytes += b;
     }
     e = hipStreamEndCapture(s->stream, &g);
@@ -1124,6 +1176,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     hipGraphExecDestroy(ge);
     if (e != hipSuccess) return hip_fail(e, "profile");
     if (us_per_launch) *us_per_launch = (double)ms * 1000.0 / ((double)reps * n_launch);
+    // (the replays leave the prompt buffers of the session in use)
     if (bytes_per_launch) *bytes_per_launch = nbytes / (uint64_t)n_launch;
     if (launches) *launches = (uint32_t)n_launch;
     return YL_OK;

@@ -154,13 +154,13 @@ class Transformer:
     PROFILE_CLASSES = {"qkv": 0, "attention": 1, "wo": 2, "w13": 3, "w2": 4, "logits": 5}
 
     def profile_kernel(self, session: InferenceSession, token: int, start_pos: int, kernel_class: str,
-                       reps: int = 20):
+                       reps: int = 20, batch: int = 1):
         """Average launch time (us), bytes per launch and launches per step of one
-        kernel class, from a graph of that class's launches of one decode step
-        replayed `reps` times between two HIP events.  Modifies the session's
-        state at start_pos (reset it afterwards)."""
+        kernel class, from a graph of that class's launches of one step over
+        `batch` tokens replayed `reps` times between two HIP events.  Modifies
+        the session's state at those positions (reset it afterwards)."""
         us, nbytes, n = C.c_double(), C.c_uint64(), C.c_uint32()
-        check(lib().yl_profile_kernel(self._h, session._h, int(token), int(start_pos),
+        check(lib().yl_profile_kernel(self._h, session._h, int(token), int(start_pos), int(batch),
                                       self.PROFILE_CLASSES[kernel_class], int(reps), C.byref(us),
                                       C.byref(nbytes), C.byref(n)))
         return us.value, nbytes.value, n.value
