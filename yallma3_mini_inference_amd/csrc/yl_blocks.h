@@ -280,6 +280,46 @@ __device__ __forceinline__ void rowq_squares_wave(int dim, float* sq) {
     for (int i = tm.idx; i < 8 * pad; i += 64) sq[(i / pad) * S + n8 + i % pad] = 0.0f;
 }
 
+// acc += every element of nbatch batches of 8 float4s in LDS, in order (a
+// serial f32 chain).  Three register batches rotate: each batch's reads are
+// issued two batches (64 dependent adds, ~270 cycles) before its adds --
+// about the LDS latency of a 16-byte read -- and the scheduling barriers
+// keep the reads there.  Reads past the last batch re-read it (unused).
+__device__ __forceinline__ void add_batch8(float& acc, const vf4 (&v)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        acc = fadd(acc, v[k].x);
+        acc = fadd(acc, v[k].y);
+        acc = fadd(acc, v[k].z);
+        acc = fadd(acc, v[k].w);
+    }
+}
+__device__ __forceinline__ void load_batch8(vf4 (&v)[8], const vf4* t4, int bt, int nbatch) {
+    const int b = bt < nbatch ? bt : nbatch - 1;
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = t4[b * 8 + k];
+}
+__device__ __forceinline__ float lds_serial_sum(const vf4* t4, int nbatch, float acc) {
+    if (nbatch <= 0) return acc;
+    vf4 v0[8], v1[8], v2[8];
+    load_batch8(v0, t4, 0, nbatch);
+    load_batch8(v1, t4, 1, nbatch);
+    for (int bt = 0; bt < nbatch; bt += 3) {
+        load_batch8(v2, t4, bt + 2, nbatch);
+        __builtin_amdgcn_sched_barrier(0);
+        add_batch8(acc, v0);
+        if (bt + 1 >= nbatch) break;
+        load_batch8(v0, t4, bt + 3, nbatch);
+        __builtin_amdgcn_sched_barrier(0);
+        add_batch8(acc, v1);
+        if (bt + 2 >= nbatch) break;
+        load_batch8(v1, t4, bt + 4, nbatch);
+        __builtin_amdgcn_sched_barrier(0);
+        add_batch8(acc, v2);
+    }
+    return acc;
+}
+
 // RMSNorm (util.rs:389-426) of a staged row, in two parts.
 //
 // rowq_chain: the sum of squares (the 8 serial chains, run by lanes 0-7 of
@@ -290,36 +330,8 @@ __device__ __forceinline__ float rowq_chain(int dim, float eps, const float* sq)
     const int S = rowq_stride(dim);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     float l = 0.0f;
-    if ((threadIdx.x & 63) < 8) {
-        // blocks of 8 vf4s; the next block's reads are issued before the
-        // current block's adds (the read after the last block is a re-read)
-        const vf4* r4 = reinterpret_cast<const vf4*>(sq + (threadIdx.x & 7) * S);
-        const int nblk = rowq_chain_len(dim) / 32;
-        vf4 va[8], vb[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) va[k] = r4[k];
-        for (int b = 0; b < nblk; b += 2) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) vb[k] = r4[(b + 1) * 8 + k];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                l = fadd(l, va[k].x);
-                l = fadd(l, va[k].y);
-                l = fadd(l, va[k].z);
-                l = fadd(l, va[k].w);
-            }
-            const int nb2 = b + 2 < nblk ? b + 2 : b;
-#pragma unroll
-            for (int k = 0; k < 8; k++) va[k] = r4[nb2 * 8 + k];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                l = fadd(l, vb[k].x);
-                l = fadd(l, vb[k].y);
-                l = fadd(l, vb[k].z);
-                l = fadd(l, vb[k].w);
-            }
-        }
-    }
+    if ((threadIdx.x & 63) < 8)
+        l = lds_serial_sum(reinterpret_cast<const vf4*>(sq + (threadIdx.x & 7) * S), rowq_chain_len(dim) / 32, 0.0f);
     float part[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) part[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), j));

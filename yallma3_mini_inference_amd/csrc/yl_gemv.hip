@@ -4,10 +4,11 @@
 // A workgroup owns R consecutive output rows of one batch row (blockIdx.y).
 // Its threads split the R*nb (row, block) pairs.  Every thread first issues
 // the loads of all its pairs' weights (two 16-byte loads per Q8_0 block, one
-// per Q4_0 block, plus the f16 scale) into registers; only then does the
-// workgroup prepare the activation row in LDS -- either staging an already
-// quantized row, or (QKV and gate/up matmuls) computing RMSNorm + quantize of
-// the f32 residual stream itself -- so that work overlaps the HBM latency.
+// per Q4_0 block, plus the f16 scale) into registers, right after its share
+// of the activation row; the workgroup then prepares the activation row in
+// LDS -- either staging an already quantized row, or (QKV and gate/up
+// matmuls) computing RMSNorm + quantize of the f32 residual stream itself --
+// while the weights are in flight.
 //
 // Each pair's exact int32 block dot (v_dot4_i32_i8) becomes the f32 term
 //     ((float)isum * w_scale) * x_scale
@@ -86,13 +87,29 @@ static size_t gemv_smem(int n, int nb, int R, int epi, int dim) {
     size_t s = (size_t)n + (size_t)nb * 4;
     s = (s + 15) & ~(size_t)15;
     s += (size_t)R * terms_stride(nb) * 4 + 64 * 4;
-    if (epi == kEpiQkvRope || epi == kEpiSwiglu) s += rowq_lds_floats(dim) * 4;
+    if (epi == kEpiQkvRope || epi == kEpiSwiglu) s += (size_t)8 * rowq_stride(dim) * 4;   // chain rows
     return s;
 }
 
-// Few wavefronts per SIMD (2, or 3 for 9-wavefront workgroups): a decode
-// launch has 1-2 workgroups per CU, so registers go to loads in flight
-// rather than to occupancy.
+// Block terms of one row added in block order onto acc (the reference's
+// `xout += term` sequence).
+__device__ __forceinline__ float ordered_row_sum(const float* tr, int nb, float acc) {
+    const vf4* t4 = reinterpret_cast<const vf4*>(tr);
+    const int nq = nb >> 2, nfull = nq >> 3;   // whole batches of 8 float4s
+    acc = lds_serial_sum(t4, nfull, acc);
+    for (int q = nfull * 8; q < nq; q++) {
+        const vf4 v = t4[q];
+        acc = fadd(acc, v.x);
+        acc = fadd(acc, v.y);
+        acc = fadd(acc, v.z);
+        acc = fadd(acc, v.w);
+    }
+    for (int b = nq * 4; b < nb; b++) acc = fadd(acc, tr[b]);
+    return acc;
+}
+
+// Few wavefronts per SIMD: a decode launch has 1-2 workgroups per CU, so
+// registers go to loads in flight rather than to occupancy.
 template <int WF, int R, int TPB, int PMAX, int EPI, bool EMB>
 __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 512 ? 3 : 2))) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -112,19 +129,15 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
     // inputs (recently written, cache-hot) before weights, weights before
     // what only the epilogue reads.  Vector-memory loads retire in order, so
     // waiting for the activations leaves the weights in flight.
-    // With an RMSNorm prologue, wavefront 0 loads the row and runs the serial
-    // sum of squares while the other wavefronts issue weight loads: a
-    // workgroup barrier completes only once every wavefront has issued all
-    // its loads, so only the short, parallel quantization waits for one.
+    // With an RMSNorm prologue every thread loads its slices of the row
+    // first, so they land early; the squares, the serial sum (one wavefront)
+    // and the quantization then run while the weights stream in.
     // All loads are unconditional (out-of-range indices are clamped and their
     // data ignored): a load under a divergent branch makes the compiler wait
     // for it at the branch join, which would serialize the HBM round trips.
     const int dim = n;
-    constexpr int WT = kNorm ? TPB - 64 : TPB;   // threads that load weights
-    // the gate/up matmul issues many loads per thread, so its wavefront 0
-    // also quantizes (a barrier would wait for all those loads to issue)
-    constexpr bool kWaveQuant = EPI == kEpiSwiglu;
-    const int tw = kNorm ? tid - 64 : tid;       // weight-thread index
+    constexpr int WT = TPB;                      // threads that load weights
+    const int tw = tid;                          // weight-thread index
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int total = R * nb;
     WBlock<WF> wv[PMAX];
@@ -175,58 +188,128 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
     };
 
     if constexpr (kNorm) {
-        if (wave == 0) {
-            // 1 (wavefront 0). residual row (or, in layer 0, the token's
-            // embedding row) + norm weights -> LDS; the serial sum of squares
-            constexpr int MP = 8;   // dim <= 4096
-            const RowTeam tm = team_wave();
-            const int passes = rowq_passes(dim, 64);
-            float* xrow = xt + 8 * rowq_stride(dim);
-            float* wrow = xrow + rowq_row_len(dim);
-            EmbRegs<EMB ? MP : 1> er_;
-            bool in_vocab = true;
+        // 1. every thread: its 8-element groups of the residual row (or, in
+        // layer 0, of the token's embedding row) and of the norm weights,
+        // then the epilogue values and its weight pairs, all issued before
+        // any wait.  Loads retire in order, so the row groups arrive first
+        // while the weights stream on.
+        constexpr int MP = (4096 / 8 + TPB - 1) / TPB;   // dim <= 4096
+        const int ng = dim / 8;
+        vf4 xg[2 * MP], wg[2 * MP];
+        uint2 eq[EMB ? MP : 1];
+        uint16_t ed[EMB ? MP : 1];
+        uint32_t tok = 0;
+        bool in_vocab = true;
+        if constexpr (EMB) {
+            tok = a.tokens[t];
+            in_vocab = tok < (uint32_t)a.emb.vocab;
+        }
+#pragma unroll
+        for (int p = 0; p < MP; p++) {
+            if (p * TPB >= ng) break;
+            const int e = 8 * min(tid + p * TPB, ng - 1);
             if constexpr (EMB) {
-                const uint32_t tok = a.tokens[t];
-                in_vocab = tok < (uint32_t)a.emb.vocab;
-                rowq_load_emb<MP>(tm, er_, a.emb, tok, passes);
+                // interleaved Q8_0 table: bytes q+128 at [vocab/64][dim/16][64][16],
+                // f16 scales at [vocab/64][dim/32][64]; ids outside the vocabulary
+                // read row 0 and become zeros below
+                const size_t tile = in_vocab ? tok >> 6 : 0;
+                const int ln = (int)(tok & 63u);
+                const uint8_t* q = reinterpret_cast<const uint8_t*>(a.emb.q);
+                eq[p] = *reinterpret_cast<const uint2*>(q + ((tile * (dim / 16) + (e >> 4)) * 64 + ln) * 16 + (e & 15));
+                ed[p] = a.emb.d[(tile * (dim / 32) + (e >> 5)) * 64 + ln];
             } else {
-                rowq_dma_f32(xrow, a.x + (size_t)t * dim, dim);
+                const vf4* x4 = reinterpret_cast<const vf4*>(a.x + (size_t)t * dim + e);
+                xg[2 * p] = x4[0];
+                xg[2 * p + 1] = x4[1];
             }
-            rowq_dma_f32(wrow, a.norm_w, dim);
-            wait_vm_all();
+            const vf4* w4 = reinterpret_cast<const vf4*>(a.norm_w + e);
+            wg[2 * p] = w4[0];
+            wg[2 * p + 1] = w4[1];
+        }
+        if (wave == 0) load_epilogue();
+        load_weights();
+        // (nothing below may be scheduled before the weight loads are issued)
+        __builtin_amdgcn_sched_barrier(0);
+
+        // 2. squares -> the 8 transposed chain rows in LDS (zero padded)
+        const int S = rowq_stride(dim);
+        float* sq = xt;
+#pragma unroll
+        for (int p = 0; p < MP; p++) {
+            const int g = tid + p * TPB;
+            if (p * TPB >= ng || g >= ng) break;
             if constexpr (EMB) {
                 // the residual stream starts as the embedding row
-                vf4 xv[2 * MP];
-                rowq_embed_values<MP>(xv, er_, in_vocab, passes);
+                // (transformer_llama_gguf.rs:459-473, base_transformer.rs:143-161)
+                const float sc = f16_to_f32(ed[p]);
+                float v[8];
 #pragma unroll
-                for (int p = 0; p < MP; p++)
-                    if (p < passes && rowq_live(tm, p, dim)) {
-                        const int e = rowq_elem(tm, p, dim);
-                        *reinterpret_cast<vf4*>(xrow + e) = xv[2 * p];
-                        *reinterpret_cast<vf4*>(xrow + e + 4) = xv[2 * p + 1];
-                        if (blockIdx.x == 0) {
-                            vf4* xo = reinterpret_cast<vf4*>(a.x + (size_t)t * dim + e);
-                            xo[0] = xv[2 * p];
-                            xo[1] = xv[2 * p + 1];
-                        }
-                    }
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t w = k < 4 ? eq[p].x : eq[p].y;
+                    const int u = (int)((w >> (8 * (k & 3))) & 0xffu);
+                    v[k] = in_vocab ? fmul((float)(u - 128), sc) : 0.0f;
+                }
+                xg[2 * p] = vf4{v[0], v[1], v[2], v[3]};
+                xg[2 * p + 1] = vf4{v[4], v[5], v[6], v[7]};
+                if (blockIdx.x == 0) {
+                    vf4* xo = reinterpret_cast<vf4*>(a.x + (size_t)t * dim + 8 * g);
+                    xo[0] = xg[2 * p];
+                    xo[1] = xg[2 * p + 1];
+                }
             }
-            rowq_squares_wave(dim, xt);
-            const float ss = rowq_chain(dim, a.eps, xt);
-            if constexpr (kWaveQuant) rowq_quant<WF, WF == kQ4>(tm, dim, ss, xt, xl, xsl, nullptr);
-            else if (tid == 0) accs[0] = ss;
-        } else {
-            // 1 (other wavefronts). weights -> registers
-            load_weights();
-            if (wave == 1) load_epilogue();
+            const vf4 x0 = xg[2 * p], x1 = xg[2 * p + 1];
+            sq[0 * S + g] = fmul(x0.x, x0.x);
+            sq[1 * S + g] = fmul(x0.y, x0.y);
+            sq[2 * S + g] = fmul(x0.z, x0.z);
+            sq[3 * S + g] = fmul(x0.w, x0.w);
+            sq[4 * S + g] = fmul(x1.x, x1.x);
+            sq[5 * S + g] = fmul(x1.y, x1.y);
+            sq[6 * S + g] = fmul(x1.z, x1.z);
+            sq[7 * S + g] = fmul(x1.w, x1.w);
+        }
+        {
+            const int pad = rowq_chain_len(dim) - ng;
+            for (int i = tid; i < 8 * pad; i += TPB) sq[(i / pad) * S + ng + i % pad] = 0.0f;
         }
         __syncthreads();
-        if constexpr (!kWaveQuant) {
-            // 2. the whole workgroup quantizes the normalized row (the
-            // barrier costs little when every thread issues few weight loads)
-            rowq_quant<WF, WF == kQ4>(team_workgroup(), dim, accs[0], xt, xl, xsl, nullptr);
-            __syncthreads();
+
+        // 3. the serial sum of squares (wavefront 0, lanes 0-7) -> ss
+        if (wave == 0) {
+            const float ss = rowq_chain(dim, a.eps, sq);
+            if (tid == 0) accs[0] = ss;
         }
+        __syncthreads();
+
+        // 4. o = w * (ss * x) and the 32-group quantization, each thread on
+        // its own groups (the 4 threads of a quad hold one 32-group)
+        const float ss = accs[0];
+#pragma unroll
+        for (int p = 0; p < MP; p++) {
+            if (p * TPB >= ng) break;
+            const int g = tid + p * TPB;
+            const bool live = g < ng;
+            const vf4 x0 = xg[2 * p], x1 = xg[2 * p + 1], w0 = wg[2 * p], w1 = wg[2 * p + 1];
+            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            float am = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                v[k] = fmul(w[k], fmul(ss, v[k]));
+                am = fmaxf(am, fabsf(v[k]));
+            }
+            am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
+            am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
+            const float sc = group_scale<WF>(am);
+            int q[8];
+            quant8<WF>(v, sc, q);
+            if (live) {
+                *reinterpret_cast<uint2*>(xl + 8 * g) =
+                    WF == kQ4 ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
+                              : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
+                if ((g & 3) == 0) xsl[g >> 2] = sc;
+            }
+        }
+        __syncthreads();
     } else {
         // 1a. quantized activation row -> registers
         constexpr int kMaxStage = 16384 / 8 / TPB;   // staged int8 rows: n <= 16384
@@ -245,9 +328,9 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
             const int i = tid + k * TPB;
             if (k * TPB < nb) sv[k] = xsg[i < nb ? i : 0];
         }
-        // 1b. weights, 1c. epilogue values
-        load_weights();
+        // 1b. epilogue values, weights -> registers
         load_epilogue();
+        load_weights();
         // 2. activation row -> LDS (int8 values + f32 group scales)
         uint2* xd = reinterpret_cast<uint2*>(xl);
 #pragma unroll
@@ -268,7 +351,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
     }
 
     // 3. exact block dots -> f32 terms in LDS
-    if (!kNorm || wave != 0) {
+    {
         const int dr = WT / nb, db = WT % nb;
         int r = tw / nb, b = tw - (tw / nb) * nb;
         if (db == 0) {
@@ -309,19 +392,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
     if (tw >= 0 && tw < R) {
         const int row = row0 + tw;
         if (row < o) {
-            float acc = ep_acc ? ep0 : 0.0f;
-            const float* tr = terms + tw * TS;
-            const float4* t4 = reinterpret_cast<const float4*>(tr);
-            int b = 0;
-#pragma unroll 4
-            for (; b < nb / 4; b++) {
-                const float4 v = t4[b];
-                acc = fadd(acc, v.x);
-                acc = fadd(acc, v.y);
-                acc = fadd(acc, v.z);
-                acc = fadd(acc, v.w);
-            }
-            for (int bb = b * 4; bb < nb; bb++) acc = fadd(acc, tr[bb]);
+            const float acc = ordered_row_sum(terms + tw * TS, nb, ep_acc ? ep0 : 0.0f);
             accs[tw] = acc;
             if constexpr (EPI == kEpiStore) a.out[(size_t)t * o + row] = acc;
             if constexpr (EPI == kEpiResid) {
@@ -365,9 +436,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 51
             const int grp = blockIdx.x;
             const size_t base = (size_t)t * a.hidden + (size_t)grp * kGroup;
             if (a.h_f32) a.h_f32[base + tw] = h;
-            float am = fabsf(h);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+            float am = group_max(fabsf(h), 32);   // lanes 0-31 (rows 0 and 1) all active
             am = fmaxf(am, 0.0f);
             const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
             const int q = a.h_fmt == kQ4 ? quant_one<kQ4>(h, sc) : quant_one<kQ8>(h, sc);
@@ -438,9 +507,9 @@ static hipError_t launch_epi(const GemvArgs& a, int batch, hipStream_t st) {
     const GemvShape s = pick_shape(a.o, a.nb, EPI);
     if (s.PMAX == 0) return hipErrorInvalidValue;
     if constexpr (EPI == kEpiSwiglu) {
-        return launch_r<WF, 64, 512 + 64, EPI>(a, s.PMAX, batch, st);
+        return launch_r<WF, 64, 512, EPI>(a, s.PMAX, batch, st);
     } else {
-        constexpr int T = EPI == kEpiQkvRope ? 256 + 64 : 256;
+        constexpr int T = 256;
         if (s.R == 4) return launch_r<WF, 4, T, EPI>(a, s.PMAX, batch, st);
         if (s.R == 16) return launch_r<WF, 16, T, EPI>(a, s.PMAX, batch, st);
         return launch_r<WF, 8, T, EPI>(a, s.PMAX, batch, st);
