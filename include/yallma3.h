@@ -245,6 +245,12 @@ yl_status yl_profile_kernel(const yl_model *m, yl_session *s, uint32_t token, ui
 yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt_out,
                            float *recip_out, float *f16_out);
 
+/* Probe of the one-wavefront serial sum behind the decode softmax
+ * denominator (forward.rs:356-361): out[c] = ((0 + v[a]) + v[a+1]) + ... +
+ * v[b-1] in f32 for a = offsets[c], b = offsets[c+1], values >= 0 (device
+ * pointers; offsets holds cases + 1 entries). */
+yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, float *out);
+
 /* ----------------------------------------------------- synthetic models */
 typedef struct {
     uint32_t dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx_len;

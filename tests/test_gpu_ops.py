@@ -255,3 +255,15 @@ def test_swiglu_quantize(gpu, oracle, hidden, batch, qfmt):
         oq, os_ = oracle.quantize(qfmt, ref.ravel())
         np.testing.assert_array_equal(q, oq)
         assert_bits(s, os_)
+
+
+def test_serial_sum_exact(gpu):
+    # the softmax denominator's serial sum by one wavefront (forward.rs:356-361)
+    import sys, os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from serial_sum_cases import cases, sequential
+    from yallma3_mini_inference_amd import ops
+    segs = cases(seed=7)
+    got = ops.serial_sum_selftest(segs)
+    ref = np.array([sequential(v) for v in segs], np.float32)
+    assert_bits(got, ref)

@@ -147,6 +147,85 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// DPP move with out-of-row (or masked-off) lanes reading 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_zero(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, CTRL, ROW_MASK, 0xF, true));
+}
+
+// Inclusive prefix sum over the 64 lanes (every lane active): shifts by 1,
+// 2, 4, 8 within each row of 16, then row 0's total into row 1 and row 2's
+// into row 3 (row_bcast:15), then lane 31's total into rows 2 and 3
+// (row_bcast:31).  Exact when every partial sum is an integer below 2^24.
+__device__ __forceinline__ float wave_scan_add(float x) {
+    x = x + dpp_zero<0x111, 0xF>(x);   // row_shr:1
+    x = x + dpp_zero<0x112, 0xF>(x);   // row_shr:2
+    x = x + dpp_zero<0x114, 0xF>(x);   // row_shr:4
+    x = x + dpp_zero<0x118, 0xF>(x);   // row_shr:8
+    x = x + dpp_zero<0x142, 0xA>(x);   // row_bcast:15 into rows 1, 3
+    x = x + dpp_zero<0x143, 0xC>(x);   // row_bcast:31 into rows 2, 3
+    return x;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// The serial f32 sum ((0 + v[0]) + v[1]) + ... + v[n-1] of n nonnegative
+// values in LDS, bit-identical to the one-at-a-time loop, computed by one
+// whole wavefront (all 64 lanes active, the same n and v on every lane).
+//
+// While the running sum s stays inside one binade it is a multiple of the
+// binade's ulp u, and the step fl(s + v) equals s + rn_u(v) -- v rounded to
+// the nearest multiple of u -- unless v/u lies exactly halfway between two
+// integers (the tie is broken by the last bit of s).  So each round takes the
+// next 64 values at once: r = rint(v/u) (an integer below 2^24), the
+// inclusive prefix sums of r (exact), and the candidates s + prefix*u
+// (exact).  Candidates hold up to the first lane whose value is a tie, does
+// not lie below the binade's top B, or whose candidate reaches B; that lane's
+// value is added by one ordinary f32 add, and the next round starts after it.
+// A zero sum takes the next nonzero value exactly (0 + v = v).  For the
+// softmax denominators here a round consumes 40-64 values.
+__device__ __forceinline__ float wave_serial_sum(const float* v_lds, int n) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+    int t = 0;
+    while (t < n) {
+        const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
+        if (s == 0.0f) {
+            const unsigned long long nz = __ballot(v != 0.0f);
+            if (nz == 0ull) { t += 64; continue; }
+            const int L = __builtin_ctzll(nz);
+            s = lane_value(v, L);
+            t += L + 1;
+            continue;
+        }
+        // s = m * 2^ex with m in [0.5, 1): u = 2^k, binade top B
+        const int ex = __builtin_amdgcn_frexp_expf(s);
+        const int k = ex - 24 > -149 ? ex - 24 : -149;
+        const float B = ex - 1 >= -126 ? __builtin_amdgcn_ldexpf(1.0f, ex) : 0x1p-126f;
+        bool bad = !(v < B);
+        const float q = __builtin_amdgcn_ldexpf(v, -k);
+        const float r = __builtin_rintf(q);
+        bad = bad || __builtin_fabsf(q - r) == 0.5f;
+        const float pre = wave_scan_add(bad ? 0.0f : r);
+        const float cand = s + __builtin_amdgcn_ldexpf(pre, k);
+        bad = bad || !(cand < B);
+        const unsigned long long m = __ballot(bad);
+        if (m == 0ull) {
+            s = lane_value(cand, 63);
+            t += 64;
+        } else {
+            const int L = __builtin_ctzll(m);
+            const float sp = L > 0 ? lane_value(cand, L - 1) : s;
+            s = fadd(sp, lane_value(v, L));
+            t += L + 1;
+        }
+    }
+    return s;
+}
+
 // Orderable 64-bit argmax key: larger key = larger value, ties broken toward
 // the smaller index (Sampler::sample_argmax keeps the first maximum,
 // sampler.rs:67-79).  NaN maps to the smallest key so it never wins.

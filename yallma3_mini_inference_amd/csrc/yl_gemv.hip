@@ -1,20 +1,38 @@
 // yl_gemv.hip -- quantized GEMV / batched matvec (weight_type.rs:122-226)
 // with the neighbouring elementwise work of forward.rs fused in.
 //
-// A workgroup owns R consecutive output rows of one batch row (blockIdx.y).
-// Its threads split the R*nb (row, block) pairs.  Every thread first issues
-// the loads of all its pairs' weights (two 16-byte loads per Q8_0 block, one
-// per Q4_0 block, plus the f16 scale) into registers, right after its share
-// of the activation row; the workgroup then prepares the activation row in
-// LDS -- either staging an already quantized row, or (QKV and gate/up
-// matmuls) computing RMSNorm + quantize of the f32 residual stream itself --
-// while the weights are in flight.
+// Workgroup layout: wavefronts 0..NA-1 are activation wavefronts (NA = 4
+// with an RMSNorm prologue, else 1); the rest are weight wavefronts.  Each
+// weight wavefront owns RW consecutive
+// output rows of one batch row (blockIdx.y) and every block of them:
+//   lane l works on row r = l / LPR, blocks b = k*LPR + l % LPR for slots
+//   k = 0..PPL-1 (LPR lanes per row, RW = 64/LPR rows per wavefront),
+// so slot k covers the same block range [k*LPR, (k+1)*LPR) of every row.
 //
-// Each pair's exact int32 block dot (v_dot4_i32_i8) becomes the f32 term
-//     ((float)isum * w_scale) * x_scale
-// in LDS, and thread r sums row r's terms in block order from the row's
-// initial value: the reference's `xout += term` sequence, so every output is
-// bit-identical to matmul_q8_slices for any grid shape.
+// 1. The activation wavefronts issue their loads first; after one barrier
+//    each weight wavefront issues the loads of its first LA slots (two
+//    16-byte loads per Q8_0 block or one per Q4_0 block, plus the f16 scale,
+//    through buffer descriptors: one VGPR offset per lane, slot offsets in
+//    scalar registers) and waits for the activation row.
+// 2. The activation wavefronts (no weight loads) stage the row in LDS:
+//    either the already quantized row (LDS DMA), or -- for the QKV and
+//    gate/up matmuls -- RMSNorm + quantize of the f32 residual stream (in
+//    layer 0, of the token's embedding row), shared by four wavefronts.
+//    They also stage the values the rows' sums start from (K/V cache entries
+//    for the `+=` columns) and the RoPE angles, then count themselves done
+//    in an LDS counter.  No further workgroup barrier is involved: a barrier
+//    would complete only once every wavefront has issued its loads, which
+//    under full HBM load is most of the kernel.
+// 3. Per slot, as its loads land: each lane's exact int32 block dot
+//    (v_dot4_i32_i8) becomes the f32 term ((float)isum * w_scale) * x_scale,
+//    and the row's first lane adds the slot's terms of its row in block
+//    order onto the row's accumulator, reading lane j's term through DPP
+//    (row_shl:j) -- the reference's `xout += term` sequence, so every output
+//    is bit-identical to matmul_q8_slices.  The sums advance while later
+//    slots are in flight; the loads of slot k + LA go out after slot k.
+// 4. Epilogues: residual add (WO, W2), RoPE + K/V cache (QKV), SwiGLU +
+//    quantize of h (gate/up; the only cross-wavefront step, after one
+//    workgroup barrier at the end), or a plain store.
 //
 // Q4_0 weights keep the reference nibble order (low nibble of byte j is
 // element 2j, high nibble 2j+1, unsigned 0..15); the activation row is
@@ -43,493 +61,555 @@ struct WBlock<kQ8> { uint4 a, b; };
 template <>
 struct WBlock<kQ4> { uint4 a; };
 
+constexpr int kBufRaw = 0x00020000;   // buffer descriptor word 3: raw 32-bit data
+
+// A buffer descriptor built from values the compiler must keep in scalar
+// registers (a descriptor in vector registers turns every load into a
+// readfirstlane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int bytes) {
+    const uint64_t p = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    void* q = (void*)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, __builtin_amdgcn_readfirstlane(bytes), kBufRaw);
+}
+
+__device__ __forceinline__ uint4 buf_u4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 template <int WF>
-__device__ __forceinline__ void load_block(WBlock<WF>& w, const uint8_t* __restrict__ p) {
+__device__ __forceinline__ void load_block(WBlock<WF>& w, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
     if constexpr (WF == kQ8) {
-        const uint4* q = reinterpret_cast<const uint4*>(p);
-        w.a = q[0];
-        w.b = q[1];
+        w.a = buf_u4(r, voff, soff);
+        w.b = buf_u4(r, voff + 16, soff);
     } else {
-        w.a = *reinterpret_cast<const uint4*>(p);
+        w.a = buf_u4(r, voff, soff);
     }
 }
 
+// Exact int32 dot of one block (|sum| < 2^24, integer adds in any order):
+// two independent v_dot4 chains of four, then one add.
 template <int WF>
 __device__ __forceinline__ int block_dot(const WBlock<WF>& w, const int32_t* xw) {
-    int acc = 0;
+    int a0 = 0, a1 = 0;
     if constexpr (WF == kQ8) {
-        acc = __builtin_amdgcn_sdot4((int)w.a.x, xw[0], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.a.y, xw[1], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.a.z, xw[2], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.a.w, xw[3], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.b.x, xw[4], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.b.y, xw[5], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.b.z, xw[6], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)w.b.w, xw[7], acc, false);
+        a0 = __builtin_amdgcn_sdot4((int)w.a.x, xw[0], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)w.b.x, xw[4], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)w.a.y, xw[1], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)w.b.y, xw[5], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)w.a.z, xw[2], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)w.b.z, xw[6], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)w.a.w, xw[3], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)w.b.w, xw[7], a1, false);
     } else {
         const uint32_t m = 0x0f0f0f0fu;
-        acc = __builtin_amdgcn_sdot4((int)(w.a.x & m), xw[0], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)((w.a.x >> 4) & m), xw[1], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)(w.a.y & m), xw[2], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)((w.a.y >> 4) & m), xw[3], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)(w.a.z & m), xw[4], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)((w.a.z >> 4) & m), xw[5], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)(w.a.w & m), xw[6], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)((w.a.w >> 4) & m), xw[7], acc, false);
+        a0 = __builtin_amdgcn_sdot4((int)(w.a.x & m), xw[0], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)(w.a.z & m), xw[4], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)((w.a.x >> 4) & m), xw[1], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)((w.a.z >> 4) & m), xw[5], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)(w.a.y & m), xw[2], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)(w.a.w & m), xw[6], a1, false);
+        a0 = __builtin_amdgcn_sdot4((int)((w.a.y >> 4) & m), xw[3], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)((w.a.w >> 4) & m), xw[7], a1, false);
     }
-    return acc;
+    return a0 + a1;
 }
 
-// terms row stride (floats): float4-aligned rows for the ordered sums
-__host__ __device__ inline int terms_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+constexpr int kMaxWeightWaves = 8;
+constexpr int kNormWaves = 4;         // activation wavefronts of the RMSNorm kernels
+constexpr int kGemvMaxThreads = 64 * (kMaxWeightWaves + kNormWaves);
 
-static size_t gemv_smem(int n, int nb, int R, int epi, int dim) {
-    size_t s = (size_t)n + (size_t)nb * 4;
-    s = (s + 15) & ~(size_t)15;
-    s += (size_t)R * terms_stride(nb) * 4 + 64 * 4;
-    if (epi == kEpiQkvRope || epi == kEpiSwiglu) s += (size_t)8 * rowq_stride(dim) * 4;   // chain rows
-    return s;
+// ----------------------------------------------------------- LDS layout ----
+// act row   : n bytes (int8, Q4 8-groups reordered), rounded up to 1 KiB
+//             (whole LDS DMA rows)
+// act scales: nb floats, rounded up to 1 KiB
+// sync      : 4 ints (counters of the activation wavefronts, ss)
+// init      : R floats (the value each row's sum starts from)
+// outs      : R floats (finished sums, for the SwiGLU step)
+// rope      : 2R floats + 4 (the QKV epilogue's angles and position)
+// norm      : 8 transposed chain rows of squares (RMSNorm kernels only)
+struct GemvLds {
+    size_t act, scales, sync, init, outs, rope, norm, total;
+};
+__host__ __device__ inline GemvLds gemv_lds(int n, int nb, int R, bool norm) {
+    GemvLds l{};
+    size_t o = 0;
+    l.act = o;
+    o += ((size_t)n + 1023) & ~(size_t)1023;
+    l.scales = o;
+    o += ((size_t)nb * 4 + 1023) & ~(size_t)1023;
+    l.sync = o;
+    o += 16;
+    l.init = o;
+    o += (size_t)R * 4;
+    l.outs = o;
+    o += (size_t)R * 4;
+    l.rope = o;
+    o += (size_t)R * 8 + 16;
+    o = (o + 15) & ~(size_t)15;
+    l.norm = o;
+    if (norm) o += (size_t)8 * rowq_stride(n) * 4;
+    l.total = o;
+    return l;
 }
 
-// Block terms of one row added in block order onto acc (the reference's
-// `xout += term` sequence).
-__device__ __forceinline__ float ordered_row_sum(const float* tr, int nb, float acc) {
-    const vf4* t4 = reinterpret_cast<const vf4*>(tr);
-    const int nq = nb >> 2, nfull = nq >> 3;   // whole batches of 8 float4s
-    acc = lds_serial_sum(t4, nfull, acc);
-    for (int q = nfull * 8; q < nq; q++) {
-        const vf4 v = t4[q];
-        acc = fadd(acc, v.x);
-        acc = fadd(acc, v.y);
-        acc = fadd(acc, v.z);
-        acc = fadd(acc, v.w);
+// Hand-offs between wavefronts of one workgroup through LDS counters
+// (relaxed atomics: a volatile LDS access would make the compiler wait for
+// every outstanding global load first).  LDS serves one wavefront's
+// accesses in order, and a waiter's reads of the published data are issued
+// only after it saw the count.  The waits are bounded: the counted
+// wavefronts always arrive within microseconds, the bound only keeps a
+// defect from hanging the device.
+__device__ __forceinline__ void lds_arrive(int* ctr) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's LDS writes done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_wait_count(int* ctr, int target) {
+    for (int i = 0; __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && i < (1 << 22); i++)
+        __builtin_amdgcn_s_sleep(1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// `bytes` bytes from global memory into LDS by LDS DMA: EB bytes per lane
+// (16 or 4), 64*EB bytes per instruction.  `bytes` is a multiple of EB and
+// src is EB-aligned; lanes past the end re-read the last EB bytes into the
+// padding of the region (rounded up to 64*EB).  No registers hold the data,
+// so no wait is implied; the caller waits (wait_vm_all) before reading it.
+template <int EB>
+__device__ __forceinline__ void dma_bytes(void* dst, const void* src, int bytes) {
+    const int lane = threadIdx.x & 63;
+    const uint8_t* s8 = reinterpret_cast<const uint8_t*>(src);
+    uint8_t* d8 = reinterpret_cast<uint8_t*>(dst);
+    for (int j = 0; j * 64 * EB < bytes; j++) {
+        const int e = min(j * 64 * EB + lane * EB, bytes - EB);
+        if constexpr (EB == 16) __builtin_amdgcn_global_load_lds(s8 + e, d8 + j * 64 * EB, 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(s8 + e, d8 + j * 64 * EB, 4, 0, 0);
     }
-    for (int b = nq * 4; b < nb; b++) acc = fadd(acc, tr[b]);
-    return acc;
 }
 
-// Few wavefronts per SIMD: a decode launch has 1-2 workgroups per CU, so
-// registers go to loads in flight rather than to occupancy.
-template <int WF, int R, int TPB, int PMAX, int EPI, bool EMB>
-__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(1, TPB > 512 ? 3 : 2))) void k_gemv(GemvArgs a) {
+// acc + v with v taken from lane (this lane + I) of the same 16-lane row.
+template <int I>
+__device__ __forceinline__ float add_from_lane_plus(float acc, float v) {
+    if constexpr (I == 0) return fadd(acc, v);
+    else return fadd(acc, dpp_zero<0x100 + I, 0xF>(v));   // row_shl:I
+}
+
+// Chain step of one slot (LPR <= 16): the row's first lane adds the slot's
+// terms of its row in block order, reading lane j's term by row_shl:j.
+template <int LPR, int I = 0>
+__device__ __forceinline__ float chain_slot_full(float acc, float term) {
+    if constexpr (I < LPR) return chain_slot_full<LPR, I + 1>(add_from_lane_plus<I>(acc, term), term);
+    else return acc;
+}
+// The same for the row's last, partial slot: `valid` (< LPR) terms.
+template <int LPR, int I = 0>
+__device__ __forceinline__ float chain_slot_part(float acc, float term, int valid) {
+    if constexpr (I < LPR) {
+        if (I >= valid) return acc;
+        return chain_slot_part<LPR, I + 1>(add_from_lane_plus<I>(acc, term), term, valid);
+    } else {
+        return acc;
+    }
+}
+template <int LPR>
+__device__ __forceinline__ float chain_slot_dpp(float acc, float term, int first_block, int nb) {
+    const int valid = nb - first_block;   // uniform
+    if (valid >= LPR) return chain_slot_full<LPR>(acc, term);
+    if (valid <= 0) return acc;
+    return chain_slot_part<LPR>(acc, term, valid);
+}
+
+// Few wavefronts per SIMD: registers go to loads in flight rather than to
+// occupancy.
+template <int WF, int EPI, bool EMB, int LPR, int PPL>
+__global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu(1, 3))) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
+    static_assert(LPR == 8 || LPR == 16, "a row's lanes share one 16-lane DPP row");
+    constexpr int RW = 64 / LPR;          // rows per weight wavefront
+    constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
+    constexpr int NA = kNorm ? kNormWaves : 1;   // activation wavefronts
     const int n = a.n, nb = a.nb, o = a.o;
-    const int tid = threadIdx.x;
+    const int nww = (int)(blockDim.x >> 6) - NA;
+    const int R = RW * nww;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = blockIdx.y;
     const int row0 = blockIdx.x * R;
-    const int TS = terms_stride(nb);
-    int8_t* xl = reinterpret_cast<int8_t*>(smem);
-    float* xsl = reinterpret_cast<float*>(smem + n);
-    float* terms = reinterpret_cast<float*>(smem + (((size_t)n + (size_t)nb * 4 + 15) & ~(size_t)15));
-    float* accs = terms + R * TS;
-    float* xt = accs + 64;
-    constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
+    const GemvLds L = gemv_lds(n, nb, R, kNorm);
+    int8_t* xl = reinterpret_cast<int8_t*>(smem + L.act);
+    float* xsl = reinterpret_cast<float*>(smem + L.scales);
+    int* ctr_sq = reinterpret_cast<int*>(smem + L.sync);       // squares written
+    int* ctr_ss = ctr_sq + 1;                                    // ss published
+    int* ctr_row = ctr_sq + 2;                                   // activation row ready
+    float* ssl = reinterpret_cast<float*>(ctr_sq + 3);
+    float* initl = reinterpret_cast<float*>(smem + L.init);
+    float* outl = reinterpret_cast<float*>(smem + L.outs);
 
-    // Global loads are issued in the order they are needed: activation
-    // inputs (recently written, cache-hot) before weights, weights before
-    // what only the epilogue reads.  Vector-memory loads retire in order, so
-    // waiting for the activations leaves the weights in flight.
-    // With an RMSNorm prologue every thread loads its slices of the row
-    // first, so they land early; the squares, the serial sum (one wavefront)
-    // and the quantization then run while the weights stream in.
-    // All loads are unconditional (out-of-range indices are clamped and their
-    // data ignored): a load under a divergent branch makes the compiler wait
-    // for it at the branch join, which would serialize the HBM round trips.
-    const int dim = n;
-    constexpr int WT = TPB;                      // threads that load weights
-    const int tw = tid;                          // weight-thread index
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int total = R * nb;
-    WBlock<WF> wv[PMAX];
-    uint16_t dv[PMAX];
-    float ep0 = 0.0f, ep1 = 1.0f, ep2 = 0.0f;
-    bool ep_acc = false;
-    int pos = 0;
+    // The activation wavefronts issue their loads before this barrier and
+    // the weight wavefronts theirs after it, so the row reaches the CU ahead
+    // of the weights.  The counters start at zero (LDS holds whatever the
+    // previous workgroup left).
+    if (tid < 3) __hip_atomic_store(ctr_sq + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
-    auto load_weights = [&]() {
-        const size_t row_bytes = WF == kQ8 ? (size_t)n : (size_t)n / 2;
-        const int dr = WT / nb, db = WT % nb;
-        int r = tw / nb, b = tw - (tw / nb) * nb;
-#pragma unroll
-        for (int k = 0; k < PMAX; k++) {
-            const bool ok = tw + k * WT < total && row0 + r < o;
-            const size_t row = ok ? (size_t)(row0 + r) : 0;
-            load_block<WF>(wv[k], a.qs + row * row_bytes + (size_t)b * (WF == kQ8 ? 32 : 16));
-            dv[k] = a.d[row * nb + b];
-            r += dr;
-            b += db;
-            if (b >= nb) { b -= nb; r += 1; }
-        }
-    };
-    // values the epilogue reads (cache initial values and RoPE angles at the
-    // decode position, the residual row, the accumulate-into output); row r
-    // of the workgroup is finished by weight thread r (R <= 64: one
-    // wavefront), which issues these loads right after its weight loads
-    auto load_epilogue = [&]() {
-        pos = (EPI == kEpiQkvRope) ? a.state->pos + t : 0;
-        const int er = min(row0 + (tw >= 0 && tw < R ? tw : 0), o - 1);
-        if constexpr (EPI == kEpiQkvRope) {
-            // K/V rows accumulate into the cache (forward.rs:166-169)
-            const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
-            const bool is_k = er >= att && er < att + kv, is_v = er >= att + kv;
-            const int c = is_v ? er - att - kv : (is_k ? er - att : 0);
-            ep_acc = (is_k || is_v) && c < (kv / 4) * 4;
-            ep0 = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
-            const int col = er < att ? er : c;
-            const int pair = (col % hd) >> 1;
-            ep1 = a.rope_cos[(size_t)pos * (hd >> 1) + pair];
-            ep2 = a.rope_sin[(size_t)pos * (hd >> 1) + pair];
-        } else if constexpr (EPI == kEpiResid) {
-            ep0 = a.x[(size_t)t * o + er];
-        } else if constexpr (EPI == kEpiStore) {
-            ep_acc = er < a.accumulate_cols;
-            ep0 = a.out[(size_t)t * o + er];
-        }
-    };
-
-    if constexpr (kNorm) {
-        // 1. every thread: its 8-element groups of the residual row (or, in
-        // layer 0, of the token's embedding row) and of the norm weights,
-        // then the epilogue values and its weight pairs, all issued before
-        // any wait.  Loads retire in order, so the row groups arrive first
-        // while the weights stream on.
-        constexpr int MP = (4096 / 8 + TPB - 1) / TPB;   // dim <= 4096
-        const int ng = dim / 8;
-        vf4 xg[2 * MP], wg[2 * MP];
-        uint2 eq[EMB ? MP : 1];
-        uint16_t ed[EMB ? MP : 1];
-        uint32_t tok = 0;
-        bool in_vocab = true;
-        if constexpr (EMB) {
-            tok = a.tokens[t];
-            in_vocab = tok < (uint32_t)a.emb.vocab;
-        }
-#pragma unroll
-        for (int p = 0; p < MP; p++) {
-            if (p * TPB >= ng) break;
-            const int e = 8 * min(tid + p * TPB, ng - 1);
+    if (wave < NA) {
+        // ---------------------------------------------- activation wavefronts
+        if constexpr (kNorm) {
+            // RMSNorm (util.rs:389-426) + quantize of the residual row,
+            // shared by the NA wavefronts: member i of the team holds the 8
+            // elements from 8*(p*team + i) in pass p
+            constexpr int MP = 2;   // dim <= 4096 = 2 passes of 256 x 8
+            const int dim = n;
+            const RowTeam tm{tid, 64 * NA};
+            const int passes = rowq_passes(dim, 64 * NA);
+            vf4 xv[2 * MP], wv_n[2 * MP];
+            EmbRegs<EMB ? MP : 1> er_;
+            bool in_vocab = true;
             if constexpr (EMB) {
-                // interleaved Q8_0 table: bytes q+128 at [vocab/64][dim/16][64][16],
-                // f16 scales at [vocab/64][dim/32][64]; ids outside the vocabulary
-                // read row 0 and become zeros below
-                const size_t tile = in_vocab ? tok >> 6 : 0;
-                const int ln = (int)(tok & 63u);
-                const uint8_t* q = reinterpret_cast<const uint8_t*>(a.emb.q);
-                eq[p] = *reinterpret_cast<const uint2*>(q + ((tile * (dim / 16) + (e >> 4)) * 64 + ln) * 16 + (e & 15));
-                ed[p] = a.emb.d[(tile * (dim / 32) + (e >> 5)) * 64 + ln];
+                const uint32_t tok = a.tokens[t];
+                in_vocab = tok < (uint32_t)a.emb.vocab;
+                rowq_load_emb<MP>(tm, er_, a.emb, tok, passes);
             } else {
-                const vf4* x4 = reinterpret_cast<const vf4*>(a.x + (size_t)t * dim + e);
-                xg[2 * p] = x4[0];
-                xg[2 * p + 1] = x4[1];
+                rowq_load_f32<MP>(tm, xv, a.x + (size_t)t * dim, dim, passes);
             }
-            const vf4* w4 = reinterpret_cast<const vf4*>(a.norm_w + e);
-            wg[2 * p] = w4[0];
-            wg[2 * p + 1] = w4[1];
-        }
-        if (wave == 0) load_epilogue();
-        load_weights();
-        // (nothing below may be scheduled before the weight loads are issued)
-        __builtin_amdgcn_sched_barrier(0);
-
-        // 2. squares -> the 8 transposed chain rows in LDS (zero padded)
-        const int S = rowq_stride(dim);
-        float* sq = xt;
-#pragma unroll
-        for (int p = 0; p < MP; p++) {
-            const int g = tid + p * TPB;
-            if (p * TPB >= ng || g >= ng) break;
+            rowq_load_f32<MP>(tm, wv_n, a.norm_w, dim, passes);
+            __syncthreads();
             if constexpr (EMB) {
                 // the residual stream starts as the embedding row
                 // (transformer_llama_gguf.rs:459-473, base_transformer.rs:143-161)
-                const float sc = f16_to_f32(ed[p]);
-                float v[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const uint32_t w = k < 4 ? eq[p].x : eq[p].y;
-                    const int u = (int)((w >> (8 * (k & 3))) & 0xffu);
-                    v[k] = in_vocab ? fmul((float)(u - 128), sc) : 0.0f;
-                }
-                xg[2 * p] = vf4{v[0], v[1], v[2], v[3]};
-                xg[2 * p + 1] = vf4{v[4], v[5], v[6], v[7]};
+                rowq_embed_values<MP>(xv, er_, in_vocab, passes);
                 if (blockIdx.x == 0) {
-                    vf4* xo = reinterpret_cast<vf4*>(a.x + (size_t)t * dim + 8 * g);
-                    xo[0] = xg[2 * p];
-                    xo[1] = xg[2 * p + 1];
+#pragma unroll
+                    for (int p = 0; p < MP; p++)
+                        if (p < passes && rowq_live(tm, p, dim)) {
+                            vf4* xo = reinterpret_cast<vf4*>(a.x + (size_t)t * dim + rowq_elem(tm, p, dim));
+                            xo[0] = xv[2 * p];
+                            xo[1] = xv[2 * p + 1];
+                        }
                 }
             }
-            const vf4 x0 = xg[2 * p], x1 = xg[2 * p + 1];
-            sq[0 * S + g] = fmul(x0.x, x0.x);
-            sq[1 * S + g] = fmul(x0.y, x0.y);
-            sq[2 * S + g] = fmul(x0.z, x0.z);
-            sq[3 * S + g] = fmul(x0.w, x0.w);
-            sq[4 * S + g] = fmul(x1.x, x1.x);
-            sq[5 * S + g] = fmul(x1.y, x1.y);
-            sq[6 * S + g] = fmul(x1.z, x1.z);
-            sq[7 * S + g] = fmul(x1.w, x1.w);
-        }
-        {
-            const int pad = rowq_chain_len(dim) - ng;
-            for (int i = tid; i < 8 * pad; i += TPB) sq[(i / pad) * S + ng + i % pad] = 0.0f;
-        }
-        __syncthreads();
-
-        // 3. the serial sum of squares (wavefront 0, lanes 0-7) -> ss
-        if (wave == 0) {
-            const float ss = rowq_chain(dim, a.eps, sq);
-            if (tid == 0) accs[0] = ss;
-        }
-        __syncthreads();
-
-        // 4. o = w * (ss * x) and the 32-group quantization, each thread on
-        // its own groups (the 4 threads of a quad hold one 32-group)
-        const float ss = accs[0];
+            // squares -> the 8 transposed chain rows (zero padded)
+            float* sq = reinterpret_cast<float*>(smem + L.norm);
+            const int S = rowq_stride(dim);
 #pragma unroll
-        for (int p = 0; p < MP; p++) {
-            if (p * TPB >= ng) break;
-            const int g = tid + p * TPB;
-            const bool live = g < ng;
-            const vf4 x0 = xg[2 * p], x1 = xg[2 * p + 1], w0 = wg[2 * p], w1 = wg[2 * p + 1];
-            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-            float am = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                v[k] = fmul(w[k], fmul(ss, v[k]));
-                am = fmaxf(am, fabsf(v[k]));
-            }
-            am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
-            am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
-            const float sc = group_scale<WF>(am);
-            int q[8];
-            quant8<WF>(v, sc, q);
-            if (live) {
-                *reinterpret_cast<uint2*>(xl + 8 * g) =
-                    WF == kQ4 ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
-                              : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
-                if ((g & 3) == 0) xsl[g >> 2] = sc;
-            }
-        }
-        __syncthreads();
-    } else {
-        // 1a. quantized activation row -> registers
-        constexpr int kMaxStage = 16384 / 8 / TPB;   // staged int8 rows: n <= 16384
-        constexpr int kMaxScale = (512 + TPB - 1) / TPB;
-        uint2 qv[kMaxStage];
-        float sv[kMaxScale];
-        const uint2* __restrict__ xg = reinterpret_cast<const uint2*>(a.xq + (size_t)t * n);
-        const float* __restrict__ xsg = a.xs + (size_t)t * nb;
-#pragma unroll
-        for (int k = 0; k < kMaxStage; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < n / 8) qv[k] = xg[i < n / 8 ? i : 0];
-        }
-#pragma unroll
-        for (int k = 0; k < kMaxScale; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < nb) sv[k] = xsg[i < nb ? i : 0];
-        }
-        // 1b. epilogue values, weights -> registers
-        load_epilogue();
-        load_weights();
-        // 2. activation row -> LDS (int8 values + f32 group scales)
-        uint2* xd = reinterpret_cast<uint2*>(xl);
-#pragma unroll
-        for (int k = 0; k < kMaxStage; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < n / 8 && i < n / 8) {
-                uint2 v = qv[k];
-                if constexpr (WF == kQ4) v = q4_reorder8(v);
-                xd[i] = v;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kMaxScale; k++) {
-            const int i = tid + k * TPB;
-            if (k * TPB < nb && i < nb) xsl[i] = sv[k];
-        }
-        __syncthreads();
-    }
-
-    // 3. exact block dots -> f32 terms in LDS
-    {
-        const int dr = WT / nb, db = WT % nb;
-        int r = tw / nb, b = tw - (tw / nb) * nb;
-        if (db == 0) {
-            // every pair of this thread uses the same activation block
-            int32_t xw[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) xw[j] = reinterpret_cast<const int32_t*>(xl + b * 32)[j];
-            const float xs_b = xsl[b];
-#pragma unroll
-            for (int k = 0; k < PMAX; k++) {
-                if (tw + k * WT < total) {
-                    float term = 0.0f;
-                    if (row0 + r < o) term = fmul(fmul((float)block_dot<WF>(wv[k], xw), f16_to_f32(dv[k])), xs_b);
-                    terms[r * TS + b] = term;
+            for (int p = 0; p < MP; p++)
+                if (p < passes && rowq_live(tm, p, dim)) {
+                    const int i = rowq_elem(tm, p, dim) >> 3;
+                    const vf4 u = xv[2 * p], v = xv[2 * p + 1];
+                    sq[0 * S + i] = fmul(u.x, u.x);
+                    sq[1 * S + i] = fmul(u.y, u.y);
+                    sq[2 * S + i] = fmul(u.z, u.z);
+                    sq[3 * S + i] = fmul(u.w, u.w);
+                    sq[4 * S + i] = fmul(v.x, v.x);
+                    sq[5 * S + i] = fmul(v.y, v.y);
+                    sq[6 * S + i] = fmul(v.z, v.z);
+                    sq[7 * S + i] = fmul(v.w, v.w);
                 }
-                r += dr;
+            {
+                const int n8 = dim / 8, pad = rowq_chain_len(dim) - n8;
+                for (int i = tid; i < 8 * pad; i += 64 * NA) sq[(i / pad) * S + n8 + i % pad] = 0.0f;
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < PMAX; k++) {
-                if (tw + k * WT < total) {
-                    float term = 0.0f;
-                    if (row0 + r < o) {
-                        const int isum = block_dot<WF>(wv[k], reinterpret_cast<const int32_t*>(xl + b * 32));
-                        term = fmul(fmul((float)isum, f16_to_f32(dv[k])), xsl[b]);
+            // initial values of the rows' sums: the K/V `+=` columns start
+            // from the cache (forward.rs:166-169, weight_type.rs:190-201)
+            if (wave == NA - 1) {
+                if constexpr (EPI == kEpiQkvRope) {
+                    // the epilogue's position and the RoPE angles of the rows
+                    // (util.rs:653-718; the table row of the position)
+                    const int pos = a.state->pos + t;
+                    const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
+                    float* ropel = reinterpret_cast<float*>(smem + L.rope);
+                    for (int i = lane; i < R; i += 64) {
+                        const int row = min(row0 + i, o - 1);
+                        const int col = row < att ? row : (row < att + kv ? row - att : row - att - kv);
+                        const int pair = (col % hd) >> 1;
+                        ropel[2 * i] = a.rope_cos[(size_t)pos * (hd >> 1) + pair];
+                        ropel[2 * i + 1] = a.rope_sin[(size_t)pos * (hd >> 1) + pair];
                     }
-                    terms[r * TS + b] = term;
+                    if (lane == 0) reinterpret_cast<int*>(ropel)[2 * R] = pos;
                 }
-                r += dr;
-                b += db;
-                if (b >= nb) { b -= nb; r += 1; }
+                for (int i = lane; i < R; i += 64) {
+                    float v = 0.0f;
+                    if constexpr (EPI == kEpiQkvRope) {
+                        const int row = min(row0 + i, o - 1);
+                        const int pos = a.state->pos + t;
+                        const int att = a.att_dim, kv = a.kv_dim;
+                        const bool is_k = row >= att && row < att + kv, is_v = row >= att + kv;
+                        const int c = is_v ? row - att - kv : (is_k ? row - att : 0);
+                        if ((is_k || is_v) && c < (kv / 4) * 4)
+                            v = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
+                    }
+                    initl[i] = v;
+                }
             }
-        }
-    }
-    __syncthreads();
-
-    // 4. ordered per-row sums
-    if (tw >= 0 && tw < R) {
-        const int row = row0 + tw;
-        if (row < o) {
-            const float acc = ordered_row_sum(terms + tw * TS, nb, ep_acc ? ep0 : 0.0f);
-            accs[tw] = acc;
-            if constexpr (EPI == kEpiStore) a.out[(size_t)t * o + row] = acc;
-            if constexpr (EPI == kEpiResid) {
-                // residual add (forward.rs:196-204 / 245-253)
-                a.x[(size_t)t * o + row] = fadd(ep0, acc);
+            lds_arrive(ctr_sq);
+            // the serial sum of squares (wavefront 0, lanes 0-7) -> ss
+            if (wave == 0) {
+                lds_wait_count(ctr_sq, NA);
+                const float ss = rowq_chain(dim, a.eps, sq);
+                if (lane == 0) *ssl = ss;
+                lds_arrive(ctr_ss);
             }
+            lds_wait_count(ctr_ss, 1);
+            const float ss = *ssl;
+            // o = w * (ss * x) and the 32-group quantization of the member's
+            // slices (the 4 lanes of a quad hold one 32-group)
+#pragma unroll
+            for (int p = 0; p < MP; p++)
+                if (p < passes && rowq_live(tm, p, dim)) {
+                    const int e = rowq_elem(tm, p, dim);
+                    const vf4 x0 = xv[2 * p], x1 = xv[2 * p + 1], w0 = wv_n[2 * p], w1 = wv_n[2 * p + 1];
+                    float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    float am = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        v[k] = fmul(w8[k], fmul(ss, v[k]));
+                        am = fmaxf(am, fabsf(v[k]));
+                    }
+                    am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
+                    am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
+                    const float sc = group_scale<WF>(am);
+                    int q[8];
+                    quant8<WF>(v, sc, q);
+                    *reinterpret_cast<uint2*>(xl + e) =
+                        WF == kQ4 ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
+                                  : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
+                    if ((tid & 3) == 0) xsl[e >> 5] = sc;
+                }
+            lds_arrive(ctr_row);
+        } else {
+            // the quantized row and its scales by LDS DMA and, for the plain
+            // store, the initial values of the `+=` columns
+            // (int8 rows: n % 32 == 0, so 16-byte pieces; scale rows start at
+            // any 4-byte boundary)
+            dma_bytes<16>(xl, a.xq + (size_t)t * n, n);
+            dma_bytes<4>(xsl, a.xs + (size_t)t * nb, nb * 4);
+            float iv = 0.0f;
+            if constexpr (EPI == kEpiStore) {
+                const int row = min(row0 + lane, o - 1);
+                iv = row < a.accumulate_cols ? a.out[(size_t)t * o + row] : 0.0f;
+            }
+            __syncthreads();
+            wait_vm_all();
+            if constexpr (WF == kQ4) {
+                // Q4_0: each 8-group reordered to (even, odd) elements, in place
+                uint2* xd = reinterpret_cast<uint2*>(xl);
+                for (int i = lane; i < n / 8; i += 64) xd[i] = q4_reorder8(xd[i]);
+            }
+            if (lane < R) initl[lane] = iv;   // R <= 64
+            lds_arrive(ctr_row);
         }
-    }
-    if constexpr (EPI == kEpiStore || EPI == kEpiResid) return;
-    __syncthreads();
+    } else {
+        // -------------------------------------------------- weight wavefronts
+        __syncthreads();
+        const int w = wave - NA;
+        const int wrow0 = row0 + w * RW;                    // this wavefront's first row
+        const int r = lane / LPR, j = lane - (lane / LPR) * LPR;
+        const int rows_here = max(0, min(RW, o - wrow0));
+        const size_t row_bytes = WF == kQ8 ? (size_t)n : (size_t)n / 2;
+        constexpr int kBlockBytes = WF == kQ8 ? 32 : 16;
+        // descriptors over this wavefront's rows: rows past the matrix read 0
+        const __amdgpu_buffer_rsrc_t qr =
+            uniform_rsrc(a.qs + (size_t)min(wrow0, o - 1) * row_bytes, (int)(rows_here * row_bytes));
+        const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(a.d + (size_t)min(wrow0, o - 1) * nb, rows_here * nb * 2);
+        const int qv = (int)(r * row_bytes) + j * kBlockBytes;
+        const int dv_off = (r * nb + j) * 2;
+        // Slot by slot (loads complete in issue order, so slot k's wait
+        // leaves the later slots in flight; the scheduling barriers keep the
+        // compiler from regrouping them).  LA slots go out first, then slot
+        // k + LA right after slot k is consumed, into the registers slot k
+        // used: under full HBM load a load waits for queue space, and a
+        // wavefront that issued everything up front would start its first
+        // slot only when most data had arrived.
+        constexpr int LA = PPL <= 4 ? PPL : (PPL / 2 < 8 ? PPL / 2 : 8);
+        WBlock<WF> wv[LA];
+        uint16_t dv[LA];
+        auto issue = [&](int k) {
+            load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
+            dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+#pragma unroll
+        for (int k = 0; k < LA; k++) issue(k);
+        // the row's first lane holds its sum
+        const int my_r = r;
+        const bool chain_lane = j == 0;
+        const int my_row = wrow0 + my_r;
+        // epilogue operand of the residual add (needed only at the end)
+        float resid = 0.0f;
+        if constexpr (EPI == kEpiResid) resid = a.x[(size_t)t * o + min(my_row, o - 1)];
+        __builtin_amdgcn_sched_barrier(0);
 
-    // 5. epilogues over neighbouring rows
-    if constexpr (EPI == kEpiQkvRope) {
-        // rope_gguf (util.rs:653-718): pair (2i, 2i+1) of a head rotated by the
-        // angle table row `pos`; v rows are stored as summed.
-        if (tw >= 0 && tw < R) {
-            const int row = row0 + tw;
-            if (row < o) {
-                const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
-                const float v = accs[tw];
-                if (row >= att + kv) {
-                    a.v_cache[(size_t)pos * kv + (row - att - kv)] = v;
+        lds_wait_count(ctr_row, NA);
+        float acc = initl[min(w * RW + my_r, R - 1)];
+#pragma unroll
+        for (int k = 0; k < PPL; k++) {
+            // exact block dot -> f32 term
+            const int b = k * LPR + j;
+            const int bb = b < nb ? b : nb - 1;
+            const int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
+            const float term = fmul(fmul((float)isum, f16_to_f32(dv[k % LA])), xsl[bb]);
+            acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
+            if (k + LA < PPL) issue(k + LA);
+        }
+
+        // epilogues on the finished sums (chain lanes hold row my_row)
+        const bool live = chain_lane && my_row < o;
+        if constexpr (EPI == kEpiStore) {
+            if (live) a.out[(size_t)t * o + my_row] = acc;
+        } else if constexpr (EPI == kEpiResid) {
+            // residual add (forward.rs:196-204 / 245-253)
+            if (live) a.x[(size_t)t * o + my_row] = fadd(resid, acc);
+        } else if constexpr (EPI == kEpiQkvRope) {
+            // rope_gguf (util.rs:653-718): pair (2i, 2i+1) of a head rotated
+            // by the angle table row `pos`; v rows are stored as summed.
+            // The rows of a pair are in this wavefront (RW even).
+            const float other = __shfl_xor(acc, LPR, 64);
+            if (live) {
+                const float* ropel = reinterpret_cast<const float*>(smem + L.rope);
+                const int pos = reinterpret_cast<const int*>(ropel)[2 * R];
+                const int att = a.att_dim, kv = a.kv_dim;
+                const bool odd = my_row & 1;
+                if (my_row >= att + kv) {
+                    a.v_cache[(size_t)pos * kv + (my_row - att - kv)] = acc;
                 } else {
-                    const int col = row < att ? row : row - att;
-                    const float c = ep1, s = ep2;
-                    const float v0 = accs[tw & ~1], v1 = accs[tw | 1];
-                    const float r = (tw & 1) ? fadd(fmul(v0, s), fmul(v1, c)) : fmul(v0, c) - fmul(v1, s);
-                    if (row < att) a.q_out[(size_t)t * att + col] = r;
-                    else a.k_cache[(size_t)col * a.kv_ld + pos] = r;
+                    const int col = my_row < att ? my_row : my_row - att;
+                    const int li = w * RW + my_r;
+                    const float c = ropel[2 * li];
+                    const float s = ropel[2 * li + 1];
+                    const float v0 = odd ? other : acc, v1 = odd ? acc : other;
+                    const float rr = odd ? fadd(fmul(v0, s), fmul(v1, c)) : fmul(v0, c) - fmul(v1, s);
+                    if (my_row < att) a.q_out[(size_t)t * att + col] = rr;
+                    else a.k_cache[(size_t)col * a.kv_ld + pos] = rr;
                 }
             }
+        } else if constexpr (EPI == kEpiSwiglu) {
+            if (chain_lane) outl[w * RW + my_r] = acc;
         }
-    } else if constexpr (EPI == kEpiSwiglu) {
-        // SwiGLU (forward.rs:220-237): h = (g / (1 + exp(-g))) * u, then this
-        // 32-group of h is quantized for the down projection.
-        if (tw >= 0 && tw < 32) {
-            const float g = accs[tw];
-            const float u = accs[32 + tw];
+    }
+
+    if constexpr (EPI == kEpiSwiglu) {
+        // SwiGLU (forward.rs:220-237) of the workgroup's 32 outputs: rows
+        // [32 gate | 32 up] of one 64-row group, h = (g / (1 + exp(-g))) * u,
+        // then this 32-group of h is quantized for the down projection.
+        __syncthreads();
+        if (wave == 0 && lane < 32) {
+            const float g = outl[lane];
+            const float u = outl[32 + lane];
             const float den = fadd(1.0f, expf_rn(-g));
             const float h = fmul(g / den, u);
             const int grp = blockIdx.x;
             const size_t base = (size_t)t * a.hidden + (size_t)grp * kGroup;
-            if (a.h_f32) a.h_f32[base + tw] = h;
+            if (a.h_f32) a.h_f32[base + lane] = h;
             float am = group_max(fabsf(h), 32);   // lanes 0-31 (rows 0 and 1) all active
             am = fmaxf(am, 0.0f);
             const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
             const int q = a.h_fmt == kQ4 ? quant_one<kQ4>(h, sc) : quant_one<kQ8>(h, sc);
-            a.hq[base + tw] = (int8_t)q;
-            if (tw == 0) a.hs[(size_t)t * (a.hidden / kGroup) + grp] = sc;
+            a.hq[base + lane] = (int8_t)q;
+            if (lane == 0) a.hs[(size_t)t * (a.hidden / kGroup) + grp] = sc;
         }
     }
 }
 
 // ------------------------------------------------------------ dispatch ----
 
-struct GemvShape {
-    int R, WT, PMAX;   // rows per workgroup, weight-loading threads, pairs per thread
+// Lanes per row and slots per lane for a row of nb blocks: 8 lanes per row
+// (8 rows per wavefront) up to 64 blocks, then 16 lanes (4 rows) with 8, 16
+// or 32 slots.  A row's lanes stay inside one 16-lane DPP row, where the
+// row sums gather the terms.  The gate/up matmul needs 64 rows per
+// workgroup (8 weight wavefronts of 8 rows), so it keeps 8 lanes per row and
+// takes 16 slots up to 128 blocks.
+struct GemvPlan {
+    int lpr, ppl, nww;
 };
-
-// Rows per workgroup and threads: enough workgroups to cover the 256 CUs,
-// 32-128 KiB of weights in flight per CU, and every pair of a thread loaded
-// before its first use.  Kernels with an RMSNorm prologue launch one more
-// wavefront (the normalizing one) than WT.
-static GemvShape pick_shape(int o, int nb, int epi) {
-    GemvShape s;
-    s.WT = epi == kEpiSwiglu ? 512 : 256;
-    if (epi == kEpiSwiglu) s.R = 64;
-    else if (nb >= 192) s.R = 4;
-    else if (o >= 8192) s.R = 16;
-    else s.R = 8;
-    const int p = (s.R * nb + s.WT - 1) / s.WT;
-    s.PMAX = p <= 1 ? 1 : p <= 2 ? 2 : p <= 4 ? 4 : p <= 8 ? 8 : p <= 16 ? 16 : 0;
-    return s;
+static bool plan_gemv(int o, int nb, int epi, GemvPlan* p) {
+    if (nb <= 0) return false;
+    if (epi == kEpiSwiglu) {
+        if (o % 64 || nb > 128) return false;
+        p->lpr = 8;
+        p->ppl = nb <= 8 ? 1 : nb <= 16 ? 2 : nb <= 32 ? 4 : nb <= 64 ? 8 : 16;
+        p->nww = 8;
+        return true;
+    }
+    if (nb <= 64) {
+        p->lpr = 8;
+        p->ppl = nb <= 8 ? 1 : nb <= 16 ? 2 : nb <= 32 ? 4 : 8;
+    } else {
+        p->lpr = 16;
+        p->ppl = nb <= 128 ? 8 : nb <= 256 ? 16 : nb <= 512 ? 32 : 0;
+        if (!p->ppl) return false;
+    }
+    // one round of workgroups on the 256 CUs: the fewest weight wavefronts
+    // per workgroup that keep the grid within 256 workgroups
+    const int rw = 64 / p->lpr;
+    p->nww = 1;
+    while (p->nww < kMaxWeightWaves && (o + rw * p->nww - 1) / (rw * p->nww) > 256) p->nww *= 2;
+    return true;
 }
 
-template <int WF, int R, int TPB, int PMAX, int EPI, bool EMB>
-static hipError_t launch_k(const GemvArgs& a, dim3 grid, size_t smem, hipStream_t st) {
-    if (smem > 65536) {
-        // rows longer than 4096 need more than the default 64 KiB of LDS
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<WF, R, TPB, PMAX, EPI, EMB>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+template <int WF, int EPI, bool EMB, int LPR, int PPL>
+static hipError_t launch_k(const GemvArgs& a, int nww, int batch, hipStream_t st) {
+    constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
+    constexpr int NA = kNorm ? kNormWaves : 1;
+    const int R = (64 / LPR) * nww;
+    const GemvLds L = gemv_lds(a.n, a.nb, R, kNorm);
+    if (L.total > 160 * 1024) return hipErrorInvalidValue;
+    if (L.total > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<WF, EPI, EMB, LPR, PPL>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_gemv<WF, R, TPB, PMAX, EPI, EMB>), grid, dim3(TPB), smem, st, a);
+    const dim3 grid((a.o + R - 1) / R, batch);
+    hipLaunchKernelGGL((k_gemv<WF, EPI, EMB, LPR, PPL>), grid, dim3(64 * (nww + NA)), L.total, st, a);
     return hipGetLastError();
 }
 
-template <int WF, int R, int TPB, int EPI, bool EMB>
-static hipError_t launch_r2(const GemvArgs& a, int pmax, int batch, hipStream_t st) {
-    const size_t smem = gemv_smem(a.n, a.nb, R, EPI, a.n);
-    const dim3 grid((a.o + R - 1) / R, batch);
-    switch (pmax) {
-    case 1: return launch_k<WF, R, TPB, 1, EPI, EMB>(a, grid, smem, st);
-    case 2: return launch_k<WF, R, TPB, 2, EPI, EMB>(a, grid, smem, st);
-    case 4: return launch_k<WF, R, TPB, 4, EPI, EMB>(a, grid, smem, st);
-    case 8: return launch_k<WF, R, TPB, 8, EPI, EMB>(a, grid, smem, st);
-    case 16: return launch_k<WF, R, TPB, 16, EPI, EMB>(a, grid, smem, st);
-    default: return hipErrorInvalidValue;
+template <int WF, int EPI, bool EMB>
+static hipError_t launch_plan(const GemvArgs& a, const GemvPlan& p, int batch, hipStream_t st) {
+    if (p.lpr == 8) {
+        switch (p.ppl) {
+        case 1: return launch_k<WF, EPI, EMB, 8, 1>(a, p.nww, batch, st);
+        case 2: return launch_k<WF, EPI, EMB, 8, 2>(a, p.nww, batch, st);
+        case 4: return launch_k<WF, EPI, EMB, 8, 4>(a, p.nww, batch, st);
+        case 8: return launch_k<WF, EPI, EMB, 8, 8>(a, p.nww, batch, st);
+        case 16:
+            if constexpr (EPI == kEpiSwiglu) return launch_k<WF, EPI, EMB, 8, 16>(a, p.nww, batch, st);
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+        }
     }
-}
-
-template <int WF, int R, int TPB, int EPI>
-static hipError_t launch_r(const GemvArgs& a, int pmax, int batch, hipStream_t st) {
-    if constexpr (EPI == kEpiQkvRope) {
-        if (a.emb.q) return launch_r2<WF, R, TPB, EPI, true>(a, pmax, batch, st);
+    if constexpr (EPI != kEpiSwiglu) {
+        if (p.lpr == 16) {
+            switch (p.ppl) {
+            case 8: return launch_k<WF, EPI, EMB, 16, 8>(a, p.nww, batch, st);
+            case 16: return launch_k<WF, EPI, EMB, 16, 16>(a, p.nww, batch, st);
+            case 32: return launch_k<WF, EPI, EMB, 16, 32>(a, p.nww, batch, st);
+            default: return hipErrorInvalidValue;
+            }
+        }
     }
-    return launch_r2<WF, R, TPB, EPI, false>(a, pmax, batch, st);
-}
-
-template <int WF, int EPI>
-static hipError_t launch_epi(const GemvArgs& a, int batch, hipStream_t st) {
-    const GemvShape s = pick_shape(a.o, a.nb, EPI);
-    if (s.PMAX == 0) return hipErrorInvalidValue;
-    if constexpr (EPI == kEpiSwiglu) {
-        return launch_r<WF, 64, 512, EPI>(a, s.PMAX, batch, st);
-    } else {
-        constexpr int T = 256;
-        if (s.R == 4) return launch_r<WF, 4, T, EPI>(a, s.PMAX, batch, st);
-        if (s.R == 16) return launch_r<WF, 16, T, EPI>(a, s.PMAX, batch, st);
-        return launch_r<WF, 8, T, EPI>(a, s.PMAX, batch, st);
-    }
+    return hipErrorInvalidValue;
 }
 
 template <int WF>
 static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t st) {
+    GemvPlan p{};
+    if (!plan_gemv(a.o, a.nb, epi, &p)) return hipErrorInvalidValue;
     switch (epi) {
-    case kEpiStore: return launch_epi<WF, kEpiStore>(a, batch, st);
-    case kEpiQkvRope: return launch_epi<WF, kEpiQkvRope>(a, batch, st);
-    case kEpiResid: return launch_epi<WF, kEpiResid>(a, batch, st);
-    case kEpiSwiglu: return launch_epi<WF, kEpiSwiglu>(a, batch, st);
+    case kEpiStore: return launch_plan<WF, kEpiStore, false>(a, p, batch, st);
+    case kEpiQkvRope:
+        if (a.emb.q) return launch_plan<WF, kEpiQkvRope, true>(a, p, batch, st);
+        return launch_plan<WF, kEpiQkvRope, false>(a, p, batch, st);
+    case kEpiResid: return launch_plan<WF, kEpiResid, false>(a, p, batch, st);
+    case kEpiSwiglu: return launch_plan<WF, kEpiSwiglu, false>(a, p, batch, st);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s) {
     if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (a.n % 32 || a.n > 4096)) return hipErrorInvalidValue;
-    if (a.n % 32 || a.n > 16384) return hipErrorInvalidValue;
+    if (a.n % 32 || a.n > 16384 || a.o <= 0) return hipErrorInvalidValue;
     if (wfmt == kQ8) return launch_wf<kQ8>(a, epi, batch, s);
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);
     return hipErrorInvalidValue;

@@ -120,6 +120,8 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
 hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
                                 float* div_out, float* f16_out, hipStream_t s);
 
+hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, float* out, hipStream_t s);
+
 // error reporting shared by the C ABI
 void set_error(const std::string& msg);
 

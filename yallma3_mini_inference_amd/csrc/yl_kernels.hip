@@ -155,6 +155,15 @@ __global__ void k_math_selftest(const float* __restrict__ x, int n, float* exp_o
     f16_out[i] = f16_to_f32((uint16_t)(i & 0xffff));
 }
 
+// One wavefront per case: the serial sum of v[offs[c] .. offs[c+1]).
+__global__ __launch_bounds__(64) void k_serial_sum_selftest(const float* __restrict__ v,
+                                                            const uint32_t* __restrict__ offs, float* out) {
+    const int c = blockIdx.x;
+    const uint32_t a = offs[c], b = offs[c + 1];
+    const float s = wave_serial_sum(v + a, (int)(b - a));
+    if (threadIdx.x == 0) out[c] = s;
+}
+
 // ------------------------------------------------------------- launchers --
 
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s) {
@@ -217,6 +226,12 @@ hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sq
                                 float* f16_out, hipStream_t s) {
     hipLaunchKernelGGL(k_math_selftest, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s, x, n, exp_out,
                        sqrt_out, div_out, f16_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, float* out, hipStream_t s) {
+    if (cases <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_serial_sum_selftest, dim3(cases), dim3(64), 0, s, v, offs, out);
     return hipGetLastError();
 }
 

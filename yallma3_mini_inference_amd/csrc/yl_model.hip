@@ -977,6 +977,13 @@ yl_status yl_math_selftest(const float* x, size_t n, float* exp_out, float* sqrt
     return e == hipSuccess ? YL_OK : hip_fail(e, "math selftest");
 }
 
+yl_status yl_serial_sum_selftest(const float* v, const uint32_t* offsets, size_t cases, float* out) {
+    if ((!v || !offsets || !out) && cases) return YL_ERR_ARG;
+    hipError_t e = launch_serial_sum_selftest(v, offsets, (int)cases, out, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    return e == hipSuccess ? YL_OK : hip_fail(e, "serial sum self-test");
+}
+
 // ---------------------------------------------------------------- model
 
 yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) {

@@ -7,6 +7,7 @@ it mirrors:
   attention         forward.rs fused_attention (forward.rs:299-400)
   swiglu_quantize   forward.rs:220-237 + quantize
   math_selftest     device exp / sqrt / division / f16 widening probes
+  serial_sum_selftest  the one-wavefront exact serial f32 sum (softmax denominator)
 """
 from __future__ import annotations
 
@@ -75,3 +76,15 @@ def math_selftest(x: np.ndarray):
     outs = [DeviceBuffer.zeros(x.size, np.float32) for _ in range(4)]
     check(lib().yl_math_selftest(dx.ptr, x.size, *[o.ptr for o in outs]))
     return tuple(o.numpy() for o in outs)
+
+
+def serial_sum_selftest(segments):
+    """Device serial f32 sums ((0 + v0) + v1) + ... of each nonnegative segment."""
+    segs = [np.ascontiguousarray(s, np.float32).ravel() for s in segments]
+    offs = np.zeros(len(segs) + 1, np.uint32)
+    offs[1:] = np.cumsum([s.size for s in segs])
+    v = np.concatenate(segs) if segs else np.zeros(1, np.float32)
+    dv, do = DeviceBuffer.from_numpy(v if v.size else np.zeros(1, np.float32)), DeviceBuffer.from_numpy(offs)
+    out = DeviceBuffer.zeros(max(1, len(segs)), np.float32)
+    check(lib().yl_serial_sum_selftest(dv.ptr, do.ptr, len(segs), out.ptr))
+    return out.numpy()[: len(segs)]
