@@ -49,10 +49,17 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     rowq_load_f32<MP>(tm, xv, x, dim, passes);
     rowq_load_f32<MP>(tm, wv, norm_w, dim, passes);
     __syncthreads();
+    // embedding chunks (16 bytes per lane) and their f16 block scales (one
+    // per two chunks) in one ring, each scale issued right behind its chunks:
+    // loads retire in issue order, so a scale loaded just in time would wait
+    // for every chunk prefetched before it
     int4 qv[kLogitChunks];
+    uint16_t sv[kLogitChunks / 2];
 #pragma unroll
-    for (int k = 0; k < kLogitChunks; k++)
-        if (k < k16n) qv[k] = qp[(size_t)k * 64];
+    for (int k = 0; k < kLogitChunks; k++) {
+        qv[k] = qp[(size_t)min(k, k16n - 1) * 64];
+        if (k & 1) sv[k >> 1] = dp[(size_t)min(k >> 1, nbE - 1) * 64];
+    }
     rowq_stage<MP>(tm, xv, wv, dim, passes, sq);
     rowq_norm_quant<-1, false>(dim, eps, sq, nullptr, nullptr, xn);
 
@@ -65,8 +72,12 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                 const int k = k0 + kk2;
                 if (k < k16n) {
                     const int4 q4 = qv[kk2];
-                    if (k + kLogitChunks < k16n) qv[kk2] = qp[(size_t)(k + kLogitChunks) * 64];
-                    const float scv = f16_to_f32(dp[(size_t)(k >> 1) * 64]);
+                    const float scv = f16_to_f32(sv[kk2 >> 1]);
+                    // refill: chunk k + kLogitChunks, and after an odd chunk
+                    // the scale of the block kLogitChunks/2 ahead (clamped
+                    // reads past the row are never used)
+                    qv[kk2] = qp[(size_t)min(k + kLogitChunks, k16n - 1) * 64];
+                    if (kk2 & 1) sv[kk2 >> 1] = dp[(size_t)min((k + kLogitChunks) >> 1, nbE - 1) * 64];
                     const float nsc = -128.0f * scv;   // exact: power-of-two multiple
                     const float* xk = xn + k * 16;
                     const uint32_t w[4] = {(uint32_t)q4.x, (uint32_t)q4.y, (uint32_t)q4.z, (uint32_t)q4.w};
