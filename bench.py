@@ -81,6 +81,16 @@ def cpu_baseline(path, prompt_len, seconds):
 
 MFMA_INT8_PEAK_TOPS = 5000.0
 
+# Decode workloads (--config): prompt length, decode steps (warmup + timed),
+# and the description that names them in the result line.
+DECODE = {
+    "llama32_1b": (512, 256, "Llama-3.2-1B-shaped Q8_0 greedy decode, batch 1, 512-token prompt then 256 steps, "
+                             "KV f32 ctx 4096"),
+    "smollm2_135m": (256, 128, "SmolLM2-135M-shaped Q8_0 greedy decode, batch 1, 256-token prompt then 128 steps"),
+    "llama3_8b_mixed": (8192, 256, "Llama-3-8B-shaped decode (Q4_0 FFN, Q8_0 attention/output), batch 1, KV cache "
+                                   "prefilled to 8192 positions, then 256 steps"),
+}
+
 
 def run_prefill(args):
     """Llama-3.2-1B-shaped Q4_0 (Q4_0 activations, reference semantics): a prompt of
@@ -201,10 +211,11 @@ def run_matvec(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default: the workload's steps - warmup)")
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="llama32_1b")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
+    ap.add_argument("--config", default="llama32_1b", choices=sorted(DECODE),
+                    help="decode workload: llama32_1b (the headline), smollm2_135m, llama3_8b_mixed")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("decode", "prefill", "matvec"), default="decode",
@@ -242,9 +253,16 @@ def main():
         L.yl_free(dst)
         log(f"calibration copy: {nbytes} B read + {nbytes} B written")
     if args.workload == "prefill":
+        if args.steps is None:
+            args.steps = 32
         return run_prefill(args)
     if args.workload == "matvec":
         return run_matvec(args)
+    d_prompt, d_steps, d_desc = DECODE[args.config]
+    if args.prompt is None:
+        args.prompt = d_prompt
+    if args.steps is None:
+        args.steps = d_steps - args.warmup
     t0 = time.perf_counter()
     path = synth.ensure(args.config)
     log(f"model {path} ready in {time.perf_counter() - t0:.1f}s")
@@ -299,14 +317,14 @@ def main():
     dom_gbs = kern[dom]["bytes"] / (kern[dom]["us"] * 1e-6) / 1e9
     traffic = None
     tf = os.path.join(ROOT, "profiles", "pmc_traffic_llama32_1b_decode.json")
-    if os.path.exists(tf):
+    if args.config == "llama32_1b" and os.path.exists(tf):
         with open(tf) as f:
             t = json.load(f)
         if t.get("class") == dom:
             traffic = t.get("traffic_bytes_per_launch")
 
     result = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == "llama32_1b" else f"decode tok/s, {args.config} shape",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -317,10 +335,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights, GGUF Q8_0; random prompt ids)",
+        "data": "synthetic (seeded N(0,0.02) weights, GGUF blocks; random prompt ids)",
         "config": {
-            "workload": "Llama-3.2-1B-shaped Q8_0 greedy decode, batch 1, 512-token prompt then 256 steps, "
-                        "KV f32 ctx 4096",
+            "workload": d_desc,
             "batch": 1, "prompt_tokens": args.prompt,
             "decode_positions": f"{args.prompt + args.warmup}..{args.prompt + args.warmup + args.steps - 1}",
             "parallelism": "single GPU",

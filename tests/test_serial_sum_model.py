@@ -1,9 +1,10 @@
 """CPU model of the device's one-wavefront serial sum (wave_serial_sum in
-csrc/yl_device.h), round by round, held to the sequential f32 loop it
-replaces: while the running sum s stays in one binade it is a multiple of
-that binade's ulp u, so a step adds v rounded to a multiple of u unless v/u
-is an exact tie; each round takes 64 values as integers, prefix-sums them
-and stops at the first tie, binade exit, or value that leaves the binade."""
+csrc/yl_device.h), row by row, held to the sequential f32 loop it replaces:
+while the running sum s stays in one binade it is a multiple of that
+binade's ulp u, so a step adds v rounded to a multiple of u unless v/u is an
+exact tie; rows of 64 values are taken as integers and prefix-summed onto a
+running total until the first tie, binade exit, or value that leaves the
+binade, where one ordinary add restarts the binade."""
 import numpy as np
 
 from serial_sum_cases import cases, sequential
@@ -15,10 +16,10 @@ def model_sum(v):
     v = np.asarray(v, F)
     n, s, t = v.size, F(0.0), 0
     while t < n:
-        lanes = np.zeros(64, F)
-        k_ = min(64, n - t)
-        lanes[:k_] = v[t:t + k_]
         if s == 0:
+            lanes = np.zeros(64, F)
+            c = min(64, n - t)
+            lanes[:c] = v[t:t + c]
             nz = np.nonzero(lanes != 0)[0]
             if nz.size == 0:
                 t += 64
@@ -29,22 +30,31 @@ def model_sum(v):
         ex = int(np.frexp(s)[1])
         k = max(ex - 24, -149)
         B = F(np.ldexp(1.0, ex)) if ex - 1 >= -126 else F(2.0 ** -126)
-        bad = ~(lanes < B)
-        with np.errstate(over="ignore", invalid="ignore"):   # only lanes already marked bad overflow
-            q = np.ldexp(lanes, -k).astype(F)
-            r = np.rint(q).astype(F)
-            bad |= np.abs(q - r) == F(0.5)
-        pre = np.cumsum(np.where(bad, F(0), r), dtype=F)   # exact: integers < 2^24
-        cand = (s + np.ldexp(pre, k).astype(F)).astype(F)
-        bad |= ~(cand < B)
-        if not bad.any():
-            s = cand[63]
-            t += 64
-        else:
+        off = F(0.0)   # running total of the rows taken, in units of u
+        while True:
+            lanes = np.zeros(64, F)
+            c = min(64, n - t)
+            lanes[:c] = v[t:t + c]
+            bad = ~(lanes < B)
+            with np.errstate(over="ignore", invalid="ignore"):   # only lanes already marked bad overflow
+                q = np.ldexp(lanes, -k).astype(F)
+                r = np.rint(q).astype(F)
+                bad |= np.abs(q - r) == F(0.5)
+            pre = (np.cumsum(np.where(bad, F(0), r), dtype=F) + off).astype(F)   # exact: integers < 2^24
+            cand = (s + np.ldexp(pre, k).astype(F)).astype(F)
+            bad |= ~(cand < B)
+            if not bad.any():
+                off = pre[63]
+                t += 64
+                if t >= n:
+                    s = cand[63]
+                    break
+                continue
             L = int(np.argmax(bad))
-            sp = cand[L - 1] if L > 0 else s
+            sp = cand[L - 1] if L > 0 else F(s + F(np.ldexp(off, k)))
             s = F(sp + lanes[L])
             t += L + 1
+            break
     return s
 
 

@@ -179,21 +179,23 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
 // While the running sum s stays inside one binade it is a multiple of the
 // binade's ulp u, and the step fl(s + v) equals s + rn_u(v) -- v rounded to
 // the nearest multiple of u -- unless v/u lies exactly halfway between two
-// integers (the tie is broken by the last bit of s).  So each round takes the
-// next 64 values at once: r = rint(v/u) (an integer below 2^24), the
-// inclusive prefix sums of r (exact), and the candidates s + prefix*u
-// (exact).  Candidates hold up to the first lane whose value is a tie, does
-// not lie below the binade's top B, or whose candidate reaches B; that lane's
-// value is added by one ordinary f32 add, and the next round starts after it.
-// A zero sum takes the next nonzero value exactly (0 + v = v).  For the
-// softmax denominators here a round consumes 40-64 values.
+// integers (the tie is broken by the last bit of s).  So the wavefront
+// streams rows of 64 values: r = rint(v/u) (an integer below 2^24), their
+// inclusive prefix sums by DPP plus the running total of the earlier rows
+// (exact), and the candidates s + prefix*u (exact).  A row whose candidates
+// all hold advances only the running total; at the first lane whose value
+// is a tie, does not lie below the binade's top B, or whose candidate
+// reaches B, that lane's value is added by one ordinary f32 add, and the
+// binade is taken afresh from the new sum.  A zero sum takes the next
+// nonzero value exactly (0 + v = v).  A softmax denominator over n
+// positions takes about n/64 rows plus one restart per binade (10-20).
 __device__ __forceinline__ float wave_serial_sum(const float* v_lds, int n) {
     const int lane = threadIdx.x & 63;
     float s = 0.0f;
     int t = 0;
     while (t < n) {
-        const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
         if (s == 0.0f) {
+            const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
             const unsigned long long nz = __ballot(v != 0.0f);
             if (nz == 0ull) { t += 64; continue; }
             const int L = __builtin_ctzll(nz);
@@ -205,22 +207,31 @@ __device__ __forceinline__ float wave_serial_sum(const float* v_lds, int n) {
         const int ex = __builtin_amdgcn_frexp_expf(s);
         const int k = ex - 24 > -149 ? ex - 24 : -149;
         const float B = ex - 1 >= -126 ? __builtin_amdgcn_ldexpf(1.0f, ex) : 0x1p-126f;
-        bool bad = !(v < B);
-        const float q = __builtin_amdgcn_ldexpf(v, -k);
-        const float r = __builtin_rintf(q);
-        bad = bad || __builtin_fabsf(q - r) == 0.5f;
-        const float pre = wave_scan_add(bad ? 0.0f : r);
-        const float cand = s + __builtin_amdgcn_ldexpf(pre, k);
-        bad = bad || !(cand < B);
-        const unsigned long long m = __ballot(bad);
-        if (m == 0ull) {
-            s = lane_value(cand, 63);
-            t += 64;
-        } else {
-            const int L = __builtin_ctzll(m);
-            const float sp = L > 0 ? lane_value(cand, L - 1) : s;
-            s = fadd(sp, lane_value(v, L));
-            t += L + 1;
+        float off = 0.0f;   // running total of the rows taken, in units of u
+        while (true) {
+            const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
+            bool bad = !(v < B);
+            const float q = __builtin_amdgcn_ldexpf(v, -k);
+            const float r = __builtin_rintf(q);
+            bad = bad || __builtin_fabsf(q - r) == 0.5f;
+            const float pre = wave_scan_add(bad ? 0.0f : r) + off;
+            const float cand = s + __builtin_amdgcn_ldexpf(pre, k);
+            bad = bad || !(cand < B);
+            const unsigned long long m = __ballot(bad);
+            if (m == 0ull) {
+                off = lane_value(pre, 63);
+                t += 64;
+                if (t >= n) {
+                    s = lane_value(cand, 63);
+                    break;
+                }
+            } else {
+                const int L = __builtin_ctzll(m);
+                const float sp = L > 0 ? lane_value(cand, L - 1) : s + __builtin_amdgcn_ldexpf(off, k);
+                s = fadd(sp, lane_value(v, L));
+                t += L + 1;
+                break;
+            }
         }
     }
     return s;
