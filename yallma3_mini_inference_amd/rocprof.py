@@ -22,12 +22,12 @@ import statistics
 import sys
 
 # template signatures of the decode GEMV kernels at the Llama-3.2-1B shape
-# (format, rows per workgroup, threads)
+# (weight format, epilogue, embedding prologue, lanes per row, slots)
 CLASS_KERNELS = {
-    "qkv": "k_gemv<0, 8, 320",
-    "wo": "k_gemv<0, 8, 256",
-    "w13": "k_gemv<0, 64, 576",
-    "w2": "k_gemv<0, 4, 256",
+    "qkv": "k_gemv<0, 1, false, 8, 8>",
+    "wo": "k_gemv<0, 2, false, 8, 8>",
+    "w13": "k_gemv<0, 3, false, 8, 8>",
+    "w2": "k_gemv<0, 2, false, 16, 16>",
 }
 
 
