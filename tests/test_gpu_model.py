@@ -110,3 +110,27 @@ def test_smollm2_shape_short(gpu, oracle, model_dir):
         tok = oracle.argmax(o.forward_x([tok], 24 + i, os_))
         ref.append(tok)
     assert list(toks) == ref
+
+
+def test_long_context_decode(gpu, oracle, model_dir):
+    """ctx 4096: decode steps take the scores kernel + the decode kernel, whose
+    softmax sum runs on one lane up to 2048 positions and on one wavefront
+    (rows of 64) beyond; the greedy graph replays the same kernels."""
+    g, o, _ = _models(gpu, oracle, model_dir, "tiny_long")
+    rng = np.random.default_rng(4096)
+    toks = rng.integers(0, o.vocab, 2100).astype(np.uint32)
+    gs, os_ = g.create_session(), o.create_session()
+    assert_bits(g.forward_x(toks[:30], 0, gs), o.forward_x(toks[:30], 0, os_), "prefill 30")
+    for i in range(30, 34):
+        assert_bits(g.forward_x(toks[i:i + 1], i, gs), o.forward_x(toks[i:i + 1], i, os_), f"decode at {i}")
+    assert_bits(g.forward_x(toks[34:2093], 34, gs), o.forward_x(toks[34:2093], 34, os_), "prefill to 2093")
+    for i in range(2093, 2100):
+        lo = o.forward_x(toks[i:i + 1], i, os_)
+        assert_bits(g.forward_x(toks[i:i + 1], i, gs), lo, f"decode at {i}")
+    tok = oracle.argmax(lo)
+    toks_g = g.generate_greedy(gs, tok, 2100, 4)
+    ref = []
+    for i in range(4):
+        tok = oracle.argmax(o.forward_x([tok], 2100 + i, os_))
+        ref.append(tok)
+    assert list(toks_g) == ref

@@ -228,7 +228,8 @@ def test_rope(gpu, oracle, hd, nh, nkv, theta, pos, batch):
 
 
 @pytest.mark.parametrize("batch,start,nh,nkv,hd", [(1, 0, 4, 2, 64), (1, 700, 32, 8, 64), (7, 13, 9, 3, 64),
-                                                   (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128)])
+                                                   (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128),
+                                                   (1, 3000, 9, 3, 64), (1, 2100, 2, 2, 32), (1, 5119, 8, 8, 64)])
 def test_attention(gpu, oracle, batch, start, nh, nkv, hd):
     from yallma3_mini_inference_amd import ops
     rng = np.random.default_rng(batch * 1000 + start)
@@ -264,6 +265,15 @@ def test_serial_sum_exact(gpu):
     from serial_sum_cases import cases, sequential
     from yallma3_mini_inference_amd import ops
     segs = cases(seed=7)
+    # +inf and NaN among the values (the sum stays +inf, or turns NaN)
+    base = np.exp(-np.linspace(0, 4, 900)).astype(np.float32)
+    for spots in ((700, np.inf), (700, np.nan), (20, np.inf), (40, np.inf, 800, np.nan)):
+        w = base.copy()
+        for i in range(0, len(spots), 2):
+            w[spots[i]] = spots[i + 1]
+        segs.append(w)
     got = ops.serial_sum_selftest(segs)
     ref = np.array([sequential(v) for v in segs], np.float32)
-    assert_bits(got, ref)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bits(got[~nan], ref[~nan])

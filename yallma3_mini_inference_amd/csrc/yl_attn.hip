@@ -61,6 +61,10 @@ constexpr int kVTileFloats = kVTileRows * kDecDims;
 constexpr int kMaxVTiles = 4;                  // V tiles in flight
 constexpr int kDecLdsBudget = 156 * 1024;      // LDS bytes one workgroup may use
 constexpr int kBufFlags = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
+// softmax sums over more positions than this take one wavefront's row
+// streaming; shorter ones one lane (the restarts at binade changes cost more
+// than the rows save)
+constexpr int kWaveSumSeq = 2560;
 
 // pt row stride: positions up to max_seq rounded to 64 (the serial sum
 // reads zero padding to that length), + 4 floats to spread banks
@@ -87,40 +91,119 @@ __device__ __forceinline__ vf4 buf_load_f32x4(__amdgpu_buffer_rsrc_t r, int voff
 
 // LDS DMA of V rows [r0, r0 + kVTileRows) of 32 columns from col0 into an
 // LDS tile [kVTileRows][32]: one instruction moves 8 rows (64 lanes x 16
-// bytes); each wavefront issues exactly kVTileDmaPerWave of them.  Rows
-// past `rows` re-read the last one (never used).
-constexpr int kVTileDmaPerWave = kVTileRows / 8 / (kDecThreads / 64);
+// bytes).  Only the last kDmaWaves wavefronts issue them (kVTileDmaPerWave
+// each per tile); they have no P.V chains and are idle while wavefront 0
+// sums the softmax denominator.  Rows past `rows` re-read the last one
+// (never used).
+constexpr int kDmaWaves = 4;
+constexpr int kDmaWave0 = kDecThreads / 64 - kDmaWaves;
+constexpr int kVTileDmaPerWave = kVTileRows / 8 / kDmaWaves;
+static_assert(kDecChains <= kDmaWave0 * 64, "the DMA wavefronts hold no P.V chain");
 __device__ __forceinline__ void v_tile_dma(float* tile, const float* __restrict__ vc, int kv_dim, int col0, int r0,
                                            int rows) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) - kDmaWave0;
 #pragma unroll
     for (int k = 0; k < kVTileDmaPerWave; k++) {
-        const int g = wave + k * (kDecThreads / 64);
+        const int g = w + k * kDmaWaves;
         const int row = min(r0 + g * 8 + (lane >> 3), rows - 1);
         __builtin_amdgcn_global_load_lds(vc + (size_t)row * kv_dim + col0 + (lane & 7) * 4, tile + g * 8 * kDecDims,
                                          16, 0, 0);
     }
 }
-// Waits until at most `later` tiles' DMA of this wavefront is in flight.
+// Waits until at most `later` tiles' DMA of this (DMA) wavefront is in flight.
 __device__ __forceinline__ void wait_v_tiles(int later) {
-    static_assert(kVTileDmaPerWave == 4, "wait counts below assume 4 DMA instructions per tile");
+    static_assert(kVTileDmaPerWave == 8, "wait counts below assume 8 DMA instructions per tile");
     switch (later) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
     }
 }
 
-template <int QF, int HD>
+template <int NV>
+__device__ __forceinline__ void exp_row(float* pt, int PCS, int b0, int seq, int pad, float mx) {
+    float ev[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int t2 = min(b0 + (int)threadIdx.x + i * kDecThreads, pad - 1);
+        ev[i] = pt[(t2 & 7) * PCS + (t2 >> 3)];
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int t2 = b0 + (int)threadIdx.x + i * kDecThreads;
+        const float e = t2 < seq ? expf_rn(ev[i] - mx) : 0.0f;
+        if (t2 < pad) pt[(t2 & 7) * PCS + (t2 >> 3)] = e;
+    }
+}
+
+constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decode kernel)
+constexpr int kScoreRows = 256;   // positions per scores workgroup
+constexpr int kLongQuads = 8;     // score quads per decode thread: max_seq <= 8 * 4 * kDecThreads
+
+template <int HD>
+__global__ __launch_bounds__(kDecThreads) void k_attn_scores(const float* __restrict__ sq,
+                                                             const float* __restrict__ kc,
+                                                             const StepState* __restrict__ st, int n_heads,
+                                                             int n_kv_heads, float attn_scale, int kv_ld,
+                                                             float* __restrict__ sc, int sc_ld) {
+    extern __shared__ __align__(16) float lds[];
+    const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int j = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int seq = st->pos + 1;
+    const int p0 = blockIdx.y * kScoreRows;
+    if (p0 >= seq) return;
+    const int r = n_heads / n_kv_heads;
+    // quads start at most at the last position and rows are kv_ld >= seq (a
+    // multiple of 4) long, so every 16-byte read stays inside its row
+    const int quad = min(p0 / 4 + lane, (seq + 3) / 4 - 1);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(kc + (size_t)g * HD * kv_ld), (short)0, HD * kv_ld * 4, kBufFlags);
+    vf4 k4[HD / 8];
+#pragma unroll
+    for (int s = 0; s < HD / 8; s++) k4[s] = buf_load_f32x4(krs, quad * 16, (8 * s + j) * kv_ld * 4);
+    for (int hh = 0; hh < r; hh++) {
+        const float* qp = sq + (size_t)(g * r + hh) * HD + j;
+        float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < HD / 8; s++) {
+            const float qv = qp[8 * s];
+            l[0] = fadd(l[0], fmul(qv, k4[s].x));
+            l[1] = fadd(l[1], fmul(qv, k4[s].y));
+            l[2] = fadd(l[2], fmul(qv, k4[s].z));
+            l[3] = fadd(l[3], fmul(qv, k4[s].w));
+        }
+        *reinterpret_cast<vf4*>(lds + (hh * 8 + j) * kScoreRows + 4 * lane) = vf4{l[0], l[1], l[2], l[3]};
+    }
+    __syncthreads();
+    const int n = min(kScoreRows, seq - p0);
+    for (int i = tid; i < r * kScoreRows; i += kDecThreads) {
+        const int hh = i / kScoreRows, p = i % kScoreRows;
+        float lj[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) lj[jj] = lds[(hh * 8 + jj) * kScoreRows + p];
+        if (p < n) sc[(size_t)(g * r + hh) * sc_ld + p0 + p] = fmul(reduce_add8(lj), attn_scale);
+    }
+}
+
+template <int QF, int HD, bool LONG>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_decode(
     const float* __restrict__ sq, const float* __restrict__ kc, const float* __restrict__ vc,
     const StepState* __restrict__ st, int n_heads, int n_kv_heads, float attn_scale, int max_seq, int kv_ld,
-    int n_vt, int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32) {
+    int n_vt, int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32,
+    const float* __restrict__ sc, int sc_ld) {
     extern __shared__ __align__(16) float lds[];
-    const int h = blockIdx.x, ds = blockIdx.y, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kvh = h / (n_heads / n_kv_heads);
+    // Workgroups are dealt to the 8 XCDs round-robin by index (each XCD has
+    // its own L2).  Order the (kv head, dims, query head) tuples so that
+    // each XCD receives a contiguous run of them: the query heads that read
+    // the same keys and V columns then share one L2.
+    const int r = n_heads / n_kv_heads, nb = gridDim.x;
+    const int lg = (nb & 7) ? (int)blockIdx.x : (int)(blockIdx.x & 7) * (nb >> 3) + (int)(blockIdx.x >> 3);
+    const int kvh = lg / (r * (HD / kDecDims));
+    const int ds = (lg / r) % (HD / kDecDims);
+    const int h = kvh * r + lg % r;
     const int kv_dim = n_kv_heads * HD;
     const int seq = st->pos + 1;
     const int n_chunks = seq / 8;
@@ -151,91 +234,110 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // 1. scores -> pt (transposed)
     const int n_quads = (seq + 3) / 4;
     float lmax = -1e10f;
-    // each wavefront walks its own 64-quad slices (wavefronts past the last
-    // quad do not enter)
     const int lane = tid & 63;
-    for (int q0 = wave * 64; q0 < n_quads; q0 += kDecThreads) {
-        const int quad = min(q0 + lane, n_quads - 1);
-        const int voff = quad * 16;
-        float l[4][8];
+    if constexpr (LONG) {
+        // the scores kernel's row of this head (rows are sc_ld >= max_seq, a
+        // multiple of 4, floats long)
+        // every load is issued before the first is used (quads past the row
+        // re-read its last quad)
+        const float* __restrict__ sh = sc + (size_t)h * sc_ld;
+        vf4 s4[kLongQuads];
 #pragma unroll
-        for (int pp = 0; pp < 4; pp++)
+        for (int i = 0; i < kLongQuads; i++)
+            s4[i] = *reinterpret_cast<const vf4*>(sh + 4 * min(tid + i * kDecThreads, n_quads - 1));
 #pragma unroll
-            for (int j = 0; j < 8; j++) l[pp][j] = 0.0f;
-        // the query pointer and the row offset are made opaque per slice, so
-        // the per-dimension query values and row offsets are not hoisted
-        // out of the slice loop (they would need a scalar register each)
-        // (readfirstlane: asm results count as divergent, and a divergent
-        // index would turn the scalar query loads into vector ones)
-        int row_off = 0, q_off = 0;
-        asm volatile("" : "+s"(row_off), "+s"(q_off));
-        row_off = __builtin_amdgcn_readfirstlane(row_off);
-        const float* qp = qh + __builtin_amdgcn_readfirstlane(q_off);
-        const int row_step = kv_ld * 4;
-        vf4 kq[2][8];
-        float qg[2][8];
+        for (int i = 0; i < kLongQuads; i++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            kq[0][j] = buf_load_f32x4(krs, voff, row_off + j * row_step);
-            qg[0][j] = qp[j];
-        }
-#pragma unroll
-        for (int s = 0; s < HD / 8; s++) {
-            if (s + 1 < HD / 8) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    kq[(s + 1) & 1][j] = buf_load_f32x4(krs, voff, row_off + (8 * (s + 1) + j) * row_step);
-                    qg[(s + 1) & 1][j] = qp[8 * (s + 1) + j];
-                }
+            for (int pp = 0; pp < 4; pp++) {
+                const int p = 4 * (tid + i * kDecThreads) + pp;
+                const bool live = p < seq;
+                *(live ? pt + (p & 7) * PCS + (p >> 3) : red + 15) = s4[i][pp];
+                lmax = fmaxf(lmax, live ? s4[i][pp] : -1e10f);
             }
-            // one group ahead only
+    } else {
+        // wavefront j computes lane partial j (key dimensions 8s + j, s in
+        // order) of every position, 4 per lane: a round takes NCH chunks of
+        // 256 positions with all their key rows in flight (HD/8 16-byte
+        // loads per chunk), and the partials meet in the V tile area
+        // ([8][RP], free until the V DMA starts) for reduce_add8 and the scale
+        constexpr int NCH = kScoreLoads / (HD / 8);
+        constexpr int RP = NCH * 256;
+        static_assert(8 * RP <= 2 * kVTileFloats, "partials must fit two V tiles");
+        float* part = vt;
+        const float* qp = qh + wave;   // wave = j, uniform: scalar query loads
+        const int row_step = kv_ld * 4;
+        for (int r0 = 0; r0 < seq; r0 += RP) {
+            vf4 k4[NCH][HD / 8];
+#pragma unroll
+            for (int ch = 0; ch < NCH; ch++) {
+                const int quad = min(r0 / 4 + ch * 64 + lane, n_quads - 1);
+#pragma unroll
+                for (int s = 0; s < HD / 8; s++) k4[ch][s] = buf_load_f32x4(krs, quad * 16, (8 * s + wave) * row_step);
+            }
+            // every load of the round is issued before the first product
+            // (left free, the scheduler keeps a dozen in flight)
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float qv = qg[s & 1][j];
-                const vf4 k4 = kq[s & 1][j];
-                l[0][j] = fadd(l[0][j], fmul(qv, k4.x));
-                l[1][j] = fadd(l[1][j], fmul(qv, k4.y));
-                l[2][j] = fadd(l[2][j], fmul(qv, k4.z));
-                l[3][j] = fadd(l[3][j], fmul(qv, k4.w));
+            for (int ch = 0; ch < NCH; ch++) {
+                float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < HD / 8; s++) {
+                    const float qv = qp[8 * s];
+                    l[0] = fadd(l[0], fmul(qv, k4[ch][s].x));
+                    l[1] = fadd(l[1], fmul(qv, k4[ch][s].y));
+                    l[2] = fadd(l[2], fmul(qv, k4[ch][s].z));
+                    l[3] = fadd(l[3], fmul(qv, k4[ch][s].w));
+                }
+                *reinterpret_cast<vf4*>(part + wave * RP + ch * 256 + 4 * lane) = vf4{l[0], l[1], l[2], l[3]};
             }
-            // the group's products are complete here: left free, the
-            // compiler defers the .y/.z/.w lanes and keeps every key vector
-            // of every group alive
+            lds_barrier();
+            for (int i = tid; i < RP; i += kDecThreads) {
+                float lj[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) asm volatile("" : "+v"(l[0][j]), "+v"(l[1][j]), "+v"(l[2][j]), "+v"(l[3][j]));
-        }
-#pragma unroll
-        for (int pp = 0; pp < 4; pp++) {
-            const int p = (q0 + lane) * 4 + pp;
-            const float sv = fmul(reduce_add8(l[pp]), attn_scale);
-            // unconditional store (positions past seq go to a spare slot):
-            // a conditional one would let the compiler sink the K loads
-            // into a divergent branch and wait for them at its end
-            const bool live = p < seq;
-            *(live ? pt + (p & 7) * PCS + (p >> 3) : red + 15) = sv;
-            lmax = fmaxf(lmax, live ? sv : -1e10f);
+                for (int jj = 0; jj < 8; jj++) lj[jj] = part[jj * RP + i];
+                const int p = r0 + i;
+                const float sv = fmul(reduce_add8(lj), attn_scale);
+                const bool live = p < seq;
+                *(live ? pt + (p & 7) * PCS + (p >> 3) : red + 15) = sv;
+                lmax = fmaxf(lmax, live ? sv : -1e10f);
+            }
+            lds_barrier();   // part is rewritten by the next round, then by the V DMA
         }
     }
-    // the first V tiles start now; their latency overlaps the softmax
     const int n_tiles = (8 * n_chunks + kVTileRows - 1) / kVTileRows;
-    for (int t = 0; t < n_tiles && t < n_vt; t++) v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
+    const bool dma_wave = wave >= kDmaWave0;
 
     // 2. softmax: max from -1e10 (forward.rs:351-356), e = exp(s - max),
     // sum_exp serial in position order, p = e * (1 / sum_exp)
     lmax = wave_max(lmax);
     if ((tid & 63) == 0) red[tid >> 6] = lmax;
-    __syncthreads();
+    lds_barrier();   // the V tiles stay in flight
     float mx = red[0];
 #pragma unroll
     for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
     const int pad = (seq + 63) & ~63;
-    for (int t2 = tid; t2 < pad; t2 += kDecThreads) {
-        float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
-        *e = t2 < seq ? expf_rn(*e - mx) : 0.0f;
+    {
+        // up to 8 independent exponentials per thread and round (the
+        // polynomial is a chain of dependent double-precision steps)
+        const int nv = (pad + kDecThreads - 1) / kDecThreads;
+        if (nv <= 1) exp_row<1>(pt, PCS, 0, seq, pad, mx);
+        else if (nv == 2) exp_row<2>(pt, PCS, 0, seq, pad, mx);
+        else if (nv <= 4) exp_row<4>(pt, PCS, 0, seq, pad, mx);
+        else
+            for (int b0 = 0; b0 < pad; b0 += 8 * kDecThreads) exp_row<8>(pt, PCS, b0, seq, pad, mx);
     }
-    __syncthreads();
-    if (tid == 0) {
+    lds_barrier();
+    // the first V tiles start now, issued by the DMA wavefronts while
+    // wavefront 0 sums
+    if (dma_wave)
+        for (int t = 0; t < n_tiles && t < n_vt; t++)
+            v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
+    const bool wave_sum = seq > kWaveSumSeq;
+    if (wave_sum && tid < 64) {
+        // one wavefront, rows of 64 positions (see wave_serial_sum)
+        const float sum = wave_serial_sum_at([pt, PCS](int i) { return pt[(i & 7) * PCS + (i >> 3)]; }, seq);
+        if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    } else if (!wave_sum && tid == 0) {
         // blocks of 32 positions = 4 columns of the 8 rows, read as 8 vf4s;
         // each block's reads are issued before the previous block is added
         // (the scheduling barriers keep that order); the number of blocks
@@ -264,7 +366,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         }
         red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
     const float inv = red[8];
     for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
         float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
@@ -278,8 +380,8 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     for (int t = 0; t < n_tiles; t++) {
         // this wavefront's DMA into tile t; the later tiles already issued
         // may stay in flight
-        wait_v_tiles(min(n_vt - 1, n_tiles - 1 - t));
-        __syncthreads();    // everyone's DMA (and, for t = 0, the p row)
+        if (dma_wave) wait_v_tiles(min(n_vt - 1, n_tiles - 1 - t));
+        lds_barrier();    // the DMA of tile t (and, for t = 0, the p row)
         const float* tile = vt + (t % n_vt) * kVTileFloats;
         if (tid < kDecChains) {
             const int c0 = t * (kVTileRows / 8);
@@ -288,18 +390,30 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
             float vv[kVTileRows / 8];
 #pragma unroll
             for (int i = 0; i < kVTileRows / 8; i++) vv[i] = tile[(8 * i + cj) * kDecDims + cd];
+            if (steps == kVTileRows / 8) {
+                // a whole tile: no per-step bound
 #pragma unroll
-            for (int i = 0; i < kVTileRows / 8; i += 4) {
-                const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
-                if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vv[i + 0]));
-                if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vv[i + 1]));
-                if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vv[i + 2]));
-                if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                for (int i = 0; i < kVTileRows / 8; i += 4) {
+                    const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
+                    acc = fadd(acc, fmul(p4.x, vv[i + 0]));
+                    acc = fadd(acc, fmul(p4.y, vv[i + 1]));
+                    acc = fadd(acc, fmul(p4.z, vv[i + 2]));
+                    acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kVTileRows / 8; i += 4) {
+                    const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
+                    if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vv[i + 0]));
+                    if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vv[i + 1]));
+                    if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vv[i + 2]));
+                    if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                }
             }
         }
         if (t + n_vt < n_tiles) {
-            __syncthreads();    // tile t consumed before it is refilled
-            v_tile_dma(vt + (t % n_vt) * kVTileFloats, vc, kv_dim, col0, (t + n_vt) * kVTileRows, seq);
+            lds_barrier();    // tile t consumed before it is refilled
+            if (dma_wave) v_tile_dma(vt + (t % n_vt) * kVTileFloats, vc, kv_dim, col0, (t + n_vt) * kVTileRows, seq);
         }
     }
     if (tid < kDecChains) part[cj * kDecDims + cd] = acc;
@@ -444,50 +558,81 @@ hipError_t launch_attention(const float* sq, const float* kc, const float* vc, c
 }
 
 size_t attn_decode_lds_bytes(int max_seq) { return attn_decode_lds_floats(max_seq) * sizeof(float); }
-bool attn_decode_fits(int max_seq) { return attn_v_tiles(max_seq) >= 2; }
+
+
+// contexts longer than this take the scores kernel + the decode kernel
+constexpr int kAttnSplitSeq = 4096;
+bool attn_decode_split(int max_seq) { return max_seq > kAttnSplitSeq; }
+bool attn_decode_fits(int max_seq) {
+    return attn_v_tiles(max_seq) >= 2 && (!attn_decode_split(max_seq) || max_seq <= kLongQuads * 4 * kDecThreads);
+}
+static int attn_scores_ld(int max_seq) { return (max_seq + 63) & ~63; }
+size_t attn_scores_bytes(int n_heads, int max_seq) {
+    return attn_decode_split(max_seq) ? (size_t)n_heads * attn_scores_ld(max_seq) * sizeof(float) : 0;
+}
+
+template <class K>
+static hipError_t opt_in_lds(K* kern, size_t smem) {
+    if (smem <= 65536) return hipSuccess;
+    // more than the default 64 KiB of LDS
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)smem);
+}
 
 template <int QF, int HD>
 static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const float* vc, const StepState* st,
                                        int max_seq, int kv_ld, int n_heads, int n_kv_heads, float scale, int8_t* aq,
-                                       float* as, float* att_f32, hipStream_t s) {
+                                       float* as, float* att_f32, float* sc, hipStream_t s) {
     const int n_vt = attn_v_tiles(max_seq);
     if (n_vt < 2) return hipErrorInvalidValue;
     const size_t smem = attn_decode_lds_bytes(max_seq);
-    if (smem > 65536) {
-        // opt in to more than the default 64 KiB of LDS
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<QF, HD>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    const dim3 grid(n_heads * (HD / kDecDims));
+    if (sc && attn_decode_split(max_seq)) {
+        if (max_seq > kLongQuads * 4 * kDecThreads) return hipErrorInvalidValue;
+        const int r = n_heads / n_kv_heads;
+        const size_t smem_s = (size_t)r * 8 * kScoreRows * sizeof(float);
+        if (smem_s > kDecLdsBudget) return hipErrorInvalidValue;
+        const int sc_ld = attn_scores_ld(max_seq);
+        hipError_t e = opt_in_lds(&k_attn_scores<HD>, smem_s);
+        if (e == hipSuccess) e = opt_in_lds(&k_attn_decode<QF, HD, true>, smem);
         if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((k_attn_scores<HD>), dim3(n_kv_heads, (max_seq + kScoreRows - 1) / kScoreRows),
+                           dim3(kDecThreads), smem_s, s, sq, kc, st, n_heads, n_kv_heads, scale, kv_ld, sc, sc_ld);
+        hipLaunchKernelGGL((k_attn_decode<QF, HD, true>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
+                           n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, sc, sc_ld);
+        return hipGetLastError();
     }
-    hipLaunchKernelGGL((k_attn_decode<QF, HD>), dim3(n_heads, HD / kDecDims), dim3(kDecThreads), smem, s, sq, kc, vc,
-                       st, n_heads, n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32);
+    const hipError_t e = opt_in_lds(&k_attn_decode<QF, HD, false>, smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_attn_decode<QF, HD, false>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
+                       n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, nullptr, 0);
     return hipGetLastError();
 }
 
 template <int QF>
 static hipError_t launch_attn_decode_q(const float* sq, const float* kc, const float* vc, const StepState* st,
                                        int max_seq, int kv_ld, int n_heads, int n_kv_heads, int hd, float scale,
-                                       int8_t* aq, float* as, float* att_f32, hipStream_t s) {
+                                       int8_t* aq, float* as, float* att_f32, float* sc, hipStream_t s) {
     switch (hd) {
-    case 32: return launch_attn_decode_k<QF, 32>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
-    case 64: return launch_attn_decode_k<QF, 64>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
-    case 128: return launch_attn_decode_k<QF, 128>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, s);
+    case 32: return launch_attn_decode_k<QF, 32>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, sc, s);
+    case 64: return launch_attn_decode_k<QF, 64>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, sc, s);
+    case 128: return launch_attn_decode_k<QF, 128>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, sc, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st, int max_seq,
                               int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, int8_t* aq,
-                              float* as, float* att_f32, hipStream_t s) {
+                              float* as, float* att_f32, float* sc, hipStream_t s) {
     if (kv_ld % 4 || kv_ld < max_seq) return hipErrorInvalidValue;
     if (qfmt == kQ8)
         return launch_attn_decode_q<kQ8>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
-                                         as, att_f32, s);
+                                         as, att_f32, sc, s);
     if (qfmt == kQ4)
         return launch_attn_decode_q<kQ4>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
-                                         as, att_f32, s);
+                                         as, att_f32, sc, s);
     return launch_attn_decode_q<-1>(sq, kc, vc, st, max_seq, kv_ld, n_heads, n_kv_heads, head_size, scale, aq, as,
-                                    att_f32, s);
+                                    att_f32, sc, s);
 }
 
 }  // namespace yl

@@ -168,73 +168,132 @@ __device__ __forceinline__ float wave_scan_add(float x) {
     return x;
 }
 
+// Workgroup barrier ordering LDS traffic only: waits for this wavefront's
+// LDS operations, but not for its global loads or LDS DMA in flight (a
+// __syncthreads() is a release fence, and on this target waits for both).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float lane_value(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
 // The serial f32 sum ((0 + v[0]) + v[1]) + ... + v[n-1] of n nonnegative
-// values in LDS, bit-identical to the one-at-a-time loop, computed by one
-// whole wavefront (all 64 lanes active, the same n and v on every lane).
+// values, bit-identical to the one-at-a-time loop, computed by one whole
+// wavefront (all 64 lanes active, the same n and values on every lane); the
+// values are read as get(i), 0 <= i < n, in any layout.
 //
 // While the running sum s stays inside one binade it is a multiple of the
 // binade's ulp u, and the step fl(s + v) equals s + rn_u(v) -- v rounded to
 // the nearest multiple of u -- unless v/u lies exactly halfway between two
-// integers (the tie is broken by the last bit of s).  So the wavefront
-// streams rows of 64 values: r = rint(v/u) (an integer below 2^24), their
-// inclusive prefix sums by DPP plus the running total of the earlier rows
-// (exact), and the candidates s + prefix*u (exact).  A row whose candidates
-// all hold advances only the running total; at the first lane whose value
-// is a tie, does not lie below the binade's top B, or whose candidate
-// reaches B, that lane's value is added by one ordinary f32 add, and the
-// binade is taken afresh from the new sum.  A zero sum takes the next
-// nonzero value exactly (0 + v = v).  A softmax denominator over n
-// positions takes about n/64 rows plus one restart per binade (10-20).
-__device__ __forceinline__ float wave_serial_sum(const float* v_lds, int n) {
+// integers (the tie is broken by the last bit of s).  The first 32 values
+// are added one at a time: the early sum crosses a binade every few values.
+// Then the wavefront takes super-rows of 64 lanes x KV consecutive values:
+// r = rint(v/u) (integers below 2^24), each lane's running sums of its own
+// r, a DPP scan of the lane totals, and the candidates s + prefix*u (all
+// exact).  Candidates never decrease, so a super-row whose values hold no
+// tie and none at or above the binade's top B, and whose last candidate per
+// lane stays below B, is taken whole.  Otherwise the first offending value
+// in order is added by one ordinary f32 add onto the exact sum before it,
+// and the same super-row (still in registers) is scanned again from the
+// next value with the new binade.  A zero sum takes the next nonzero value
+// exactly (0 + v = v).  A softmax denominator over n positions costs about
+// n/512 super-row passes plus one pass per binade crossed after the 32nd
+// value (a handful).
+constexpr int kSerialSumPrologue = 32;
+
+// s is +inf or NaN and values from `start` on are still to be added: adding
+// nonnegative values keeps +inf, and a NaN among them gives NaN
+template <class Get>
+__device__ __forceinline__ float serial_sum_nonfinite(Get get, int n, int start, float s) {
+    if (s != s) return s;
+    bool nan = false;
+    for (int i = start + (int)(threadIdx.x & 63); i < n; i += 64) {
+        const float v = get(i);
+        nan = nan || v != v;
+    }
+    return __ballot(nan) ? __builtin_nanf("") : s;
+}
+
+template <int KV = 8, class Get>
+__device__ __forceinline__ float wave_serial_sum_at(Get get, int n) {
     const int lane = threadIdx.x & 63;
+    const int np0 = n < kSerialSumPrologue ? n : kSerialSumPrologue;
+    const float x0 = lane < np0 ? get(lane) : 0.0f;
     float s = 0.0f;
-    int t = 0;
-    while (t < n) {
-        if (s == 0.0f) {
-            const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
-            const unsigned long long nz = __ballot(v != 0.0f);
-            if (nz == 0ull) { t += 64; continue; }
-            const int L = __builtin_ctzll(nz);
-            s = lane_value(v, L);
-            t += L + 1;
-            continue;
-        }
-        // s = m * 2^ex with m in [0.5, 1): u = 2^k, binade top B
-        const int ex = __builtin_amdgcn_frexp_expf(s);
-        const int k = ex - 24 > -149 ? ex - 24 : -149;
-        const float B = ex - 1 >= -126 ? __builtin_amdgcn_ldexpf(1.0f, ex) : 0x1p-126f;
-        float off = 0.0f;   // running total of the rows taken, in units of u
-        while (true) {
-            const float v = t + lane < n ? v_lds[t + lane] : 0.0f;
-            bool bad = !(v < B);
-            const float q = __builtin_amdgcn_ldexpf(v, -k);
-            const float r = __builtin_rintf(q);
-            bad = bad || __builtin_fabsf(q - r) == 0.5f;
-            const float pre = wave_scan_add(bad ? 0.0f : r) + off;
-            const float cand = s + __builtin_amdgcn_ldexpf(pre, k);
-            bad = bad || !(cand < B);
-            const unsigned long long m = __ballot(bad);
-            if (m == 0ull) {
-                off = lane_value(pre, 63);
-                t += 64;
-                if (t >= n) {
-                    s = lane_value(cand, 63);
-                    break;
-                }
-            } else {
+#pragma unroll
+    for (int i = 0; i < kSerialSumPrologue; i++)
+        if (i < np0) s = fadd(s, lane_value(x0, i));
+    int start = np0;   // the first value not yet added
+    constexpr int W = 64 * KV;
+    for (int t0 = (start / W) * W; start < n; t0 += W) {
+        const int base = t0 + KV * lane;   // index of this lane's x[0]
+        float x[KV];
+#pragma unroll
+        for (int i = 0; i < KV; i++) x[i] = base + i < n ? get(base + i) : 0.0f;
+        const int end = n < t0 + W ? n : t0 + W;
+        while (start < end) {
+            if (!(s <= 0x1.fffffep127f)) return serial_sum_nonfinite(get, n, start, s);
+            if (s == 0.0f) {
+                int fi = KV;
+                float fv = 0.0f;
+#pragma unroll
+                for (int i = KV - 1; i >= 0; i--)
+                    if (base + i >= start && x[i] != 0.0f) { fi = i; fv = x[i]; }
+                const unsigned long long m = __ballot(fi < KV);
+                if (m == 0ull) { start = end; break; }
                 const int L = __builtin_ctzll(m);
-                const float sp = L > 0 ? lane_value(cand, L - 1) : s + __builtin_amdgcn_ldexpf(off, k);
-                s = fadd(sp, lane_value(v, L));
-                t += L + 1;
+                s = lane_value(fv, L);
+                start = t0 + KV * L + __builtin_amdgcn_readlane(fi, L) + 1;
+                continue;
+            }
+            // s = m * 2^ex with m in [0.5, 1): u = 2^k, binade top B
+            const int ex = __builtin_amdgcn_frexp_expf(s);
+            const int k = ex - 24 > -149 ? ex - 24 : -149;
+            const float B = ex - 1 >= -126 ? __builtin_amdgcn_ldexpf(1.0f, ex) : 0x1p-126f;
+            float P[KV];
+            bool bad1[KV];
+            float run = 0.0f;
+            bool any1 = false;
+#pragma unroll
+            for (int i = 0; i < KV; i++) {
+                const bool live = base + i >= start;
+                const float q = __builtin_amdgcn_ldexpf(x[i], -k);
+                const float r = __builtin_rintf(q);
+                bad1[i] = live && (!(x[i] < B) || __builtin_fabsf(q - r) == 0.5f);
+                run += live && !bad1[i] ? r : 0.0f;
+                P[i] = run;
+                any1 = any1 || bad1[i];
+            }
+            const float incl = wave_scan_add(run);
+            const float cand_last = s + __builtin_amdgcn_ldexpf(incl, k);
+            const unsigned long long m = __ballot(any1 || !(cand_last < B));
+            if (m == 0ull) {
+                s = lane_value(cand_last, 63);
+                start = end;
                 break;
             }
+            // the first offending value of each lane (lane L's is the one)
+            const int L = __builtin_ctzll(m);
+            const float E = incl - run;
+            float prev = s + __builtin_amdgcn_ldexpf(E, k);
+            int fb = KV;
+            float sp = 0.0f, xv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KV; i++) {
+                const float cand = s + __builtin_amdgcn_ldexpf(E + P[i], k);
+                const bool b = bad1[i] || (base + i >= start && !(cand < B));
+                if (fb == KV && b) { fb = i; sp = prev; xv = x[i]; }
+                prev = cand;
+            }
+            s = fadd(lane_value(sp, L), lane_value(xv, L));
+            start = t0 + KV * L + __builtin_amdgcn_readlane(fb, L) + 1;
         }
     }
+    if (!(s <= 0x1.fffffep127f)) return serial_sum_nonfinite(get, n, n, s);
     return s;
+}
+__device__ __forceinline__ float wave_serial_sum(const float* v, int n) {
+    return wave_serial_sum_at([v](int i) { return v[i]; }, n);
 }
 
 // Orderable 64-bit argmax key: larger key = larger value, ties broken toward

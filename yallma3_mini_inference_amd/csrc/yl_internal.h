@@ -106,7 +106,11 @@ size_t attn_decode_lds_bytes(int max_seq);
 bool attn_decode_fits(int max_seq);   // LDS holds the decode kernel's row and >= 2 V tiles
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st,
                               int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
-                              int qfmt, int8_t* aq, float* as, float* att_f32, hipStream_t s);
+                              int qfmt, int8_t* aq, float* as, float* att_f32, float* sc, hipStream_t s);
+// sc: scratch for the scores of long contexts, attn_scores_bytes() bytes
+// (0: the context is short enough for the single decode kernel; sc may be null)
+bool attn_decode_split(int max_seq);
+size_t attn_scores_bytes(int n_heads, int max_seq);
 hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,
                        float* q, float* k, int n_heads, int n_kv_heads, int head_size, hipStream_t s);
 hipError_t launch_swiglu_quant(int qfmt, const float* gate, const float* up, int hidden, int batch,

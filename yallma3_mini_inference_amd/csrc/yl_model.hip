@@ -279,6 +279,7 @@ struct yl_session {
     int8_t *aq = nullptr, *hq = nullptr, *nq = nullptr;   // nq/ns: normalized, quantized rows (prompt)
     float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
     unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
+    float* sc = nullptr;                 // attention scores of long contexts [n_heads][ctx]
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
     uint32_t ring_cap = 0;
@@ -630,7 +631,7 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         if (bytes) *bytes = 0;
         if (batch == 1)
             return launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                      m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
+                                      m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->sc, st);
         return launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                 m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
     case kOpWo:
@@ -937,7 +938,7 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
         return YL_ERR_UNSUPPORTED;
     }
     StepState* dst = nullptr;
-    float* kt = nullptr;
+    float *kt = nullptr, *sc = nullptr;
     StepState hst{};
     hst.pos = (int32_t)start_pos;
     hipStream_t strm = (hipStream_t)stream;
@@ -947,17 +948,20 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     // the reference layout [seq][kv_dim]
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&kt, (size_t)ld * kv_dim * 4 + 256);
+    const size_t sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq) : 0;
+    if (e == hipSuccess && sc_bytes) e = hipMalloc(&sc, sc_bytes);
     if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, kv_dim, ld, strm);
     if (e == hipSuccess && batch == 1)
         e = launch_attn_decode(q, kt, vc, dst, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
-                               nullptr, nullptr, out, strm);
+                               nullptr, nullptr, out, sc, strm);
     else if (e == hipSuccess)
         e = launch_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
                              attn_scale, -1, nullptr, nullptr, out, strm);
     if (e == hipSuccess) e = hipStreamSynchronize(strm);
     if (dst) hipFree(dst);
     if (kt) hipFree(kt);
+    if (sc) hipFree(sc);
     return e == hipSuccess ? YL_OK : hip_fail(e, "attention");
 }
 
@@ -1040,6 +1044,8 @@ yl_session* yl_create_session(const yl_model* m) {
               hipMalloc(&s->logits, (size_t)m->vocab * 4 + 256) == hipSuccess &&
               hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess &&
               hipMalloc(&s->keys, (size_t)logits_blocks(m->emb) * 8 + 256) == hipSuccess && session_grow(s, 1);
+    const size_t sc_bytes = attn_scores_bytes(m->n_heads, m->ctx);
+    if (ok && sc_bytes) ok = hipMalloc(&s->sc, sc_bytes) == hipSuccess;
     if (!ok) {
         if (yl_last_error()[0] == 0) set_error("session allocation failed");
         yl_session_free(s);
@@ -1053,7 +1059,7 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->graph) hipGraphExecDestroy(s->graph);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->keys, s->tokens};
+                   s->as_, s->hs, s->keys, s->tokens, s->sc};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);

@@ -48,6 +48,8 @@ CONFIGS = {
     "tiny": ModelConfig(128, 256, 2, 4, 2, 512, 256),
     "tiny_q4": ModelConfig(128, 256, 2, 4, 2, 512, 256, attn_format=Q4, ffn_format=Q4, file_type=2),
     "tiny_mixed": ModelConfig(128, 384, 3, 4, 1, 1000, 300, rope_theta=500000.0, ffn_format=Q4),
+    # a context long enough for the two-kernel decode attention (head size 64, 4 query heads per kv head)
+    "tiny_long": ModelConfig(256, 512, 2, 4, 1, 512, 4096, seed=7),
     # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
     "smollm2_135m": ModelConfig(576, 1536, 30, 9, 3, 49152, 2048),
     # Llama-3.2-1B shape: dim 2048, FFN 8192, 16 layers, 32/8 heads, vocab 128256
