@@ -21,7 +21,8 @@ def _models(gpu, oracle, model_dir, name):
     return Transformer(path), oracle.Model(path), path
 
 
-@pytest.mark.parametrize("name,prompt_len,steps", [("tiny", 20, 24), ("tiny_q4", 17, 16), ("tiny_mixed", 33, 20)])
+@pytest.mark.parametrize("name,prompt_len,steps", [("tiny", 20, 24), ("tiny_q4", 17, 16), ("tiny_mixed", 33, 20),
+                                                    ("tiny_pad", 9, 12)])
 def test_prefill_then_greedy_decode(gpu, oracle, model_dir, name, prompt_len, steps):
     g, o, _ = _models(gpu, oracle, model_dir, name)
     rng = np.random.default_rng(prompt_len)

@@ -179,14 +179,13 @@ __device__ __forceinline__ void rowq_load_emb(RowTeam tm, EmbRegs<MP>& r, const 
     const bool in_vocab = tok < (uint32_t)e.vocab;
     const size_t tile = in_vocab ? tok >> 6 : 0;
     const int lane = (int)(tok & 63u);
-    const int k16n = e.dim / 16, nbE = e.dim / 32;
     const uint8_t* q = reinterpret_cast<const uint8_t*>(e.q);
 #pragma unroll
     for (int p = 0; p < MP; p++)
         if (p < passes) {
             const int el = rowq_elem(tm, p, e.dim);
-            r.q[p] = *reinterpret_cast<const uint2*>(q + ((tile * k16n + (el >> 4)) * 64 + lane) * 16 + (el & 15));
-            r.d[p] = e.d[(tile * nbE + (el >> 5)) * 64 + lane];
+            r.q[p] = *reinterpret_cast<const uint2*>(q + emb_q_off(e.tiles, tile, el >> 4, lane) + (el & 15));
+            r.d[p] = e.d[emb_d_idx(e.tiles, tile, el >> 5, lane)];
         }
 }
 // Embedding values q*scale (transformer_llama_gguf.rs:459-473), zero for ids

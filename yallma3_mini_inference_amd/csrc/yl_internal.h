@@ -43,9 +43,22 @@ struct QMat {          // device-resident quantized matrix
 
 struct EmbQ8 {         // interleaved Q8_0 token embedding
     int vocab = 0, dim = 0, tiles = 0;
+    int dimp = 0;      // dim rounded up to 64: the padding has scale 0
     int8_t* q = nullptr;
     uint16_t* d = nullptr;
 };
+// Layout: vocabulary rows in tiles of 64 (lane = row % 64).  Chunk k (16
+// values, bytes u = q + 128) of every row of every tile lies together,
+// [k][tile][lane][16], and so do the f16 scales of 32-block b,
+// [b/2][tile][lane][2] (one 4-byte load per block pair): wavefronts that walk
+// their tiles chunk by chunk read neighbouring kibibytes, which HBM serves
+// much faster than one separate stream per wavefront.
+__host__ __device__ inline size_t emb_q_off(int tiles, size_t tile, int k16, int lane) {
+    return (((size_t)k16 * tiles + tile) * 64 + lane) * 16;
+}
+__host__ __device__ inline size_t emb_d_idx(int tiles, size_t tile, int b, int lane) {
+    return (((size_t)(b >> 1) * tiles + tile) * 64 + lane) * 2 + (b & 1);
+}
 
 // Per-session step state on the device: read by every kernel of a decode
 // step, advanced by the final kernel so greedy steps chain without the host.

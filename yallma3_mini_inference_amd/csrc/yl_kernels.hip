@@ -45,12 +45,11 @@ __global__ __launch_bounds__(kThreads) void k_embed(EmbQ8 e, const uint32_t* __r
     const uint32_t tok = tokens[t];
     const int lane = (int)(tok & 63u);
     const size_t tile = tok >> 6;
-    const int k16n = dim / 16, nbE = dim / kGroup;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         float v = 0.0f;
         if (tok < (uint32_t)e.vocab) {
-            const int q = (int)(uint8_t)e.q[((tile * k16n + (i >> 4)) * 64 + lane) * 16 + (i & 15)] - 128;
-            v = fmul((float)q, f16_to_f32(e.d[(tile * nbE + (i >> 5)) * 64 + lane]));
+            const int q = (int)(uint8_t)e.q[emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15)] - 128;
+            v = fmul((float)q, f16_to_f32(e.d[emb_d_idx(e.tiles, tile, i >> 5, lane)]));
         }
         x[(size_t)t * dim + i] = v;
     }

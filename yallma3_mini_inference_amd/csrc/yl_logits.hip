@@ -21,7 +21,7 @@
 namespace yl {
 
 constexpr int kLogitThreads = 256;
-constexpr int kLogitChunks = 8;   // 16-byte chunks in flight per lane
+constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each) in flight
 
 __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* __restrict__ x,
                                                           const float* __restrict__ norm_w, float eps,
@@ -30,18 +30,22 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     extern __shared__ __align__(16) float lds[];
     __shared__ unsigned long long wkey[kLogitThreads / 64];
     constexpr int MP = 8192 / 8 / kLogitThreads;   // dim <= 8192
+    constexpr int NG = kLogitGroups;
     const int dim = e.dim, tid = threadIdx.x;
-    float* xn = lds;
-    float* sq = lds + dim;
+    float* xn = lds;             // the normalized row, zero over the padding
+    float* sq = lds + e.dimp;
     const int wave = tid >> 6, lane = tid & 63;
     const int tile = blockIdx.x * (kLogitThreads / 64) + wave;
     const bool live = tile < e.tiles;
-    const int k16n = dim / 16, nbE = dim / kGroup;
-    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * k16n * 64 + lane;
-    const uint16_t* dp = e.d + (size_t)(live ? tile : 0) * nbE * 64 + lane;
+    const int ng = e.dimp / 64;   // groups: 4 chunks, one block pair
+    // chunk k of this row at qp[k * cs], the scales of block pair g at dp[g * cs]
+    const size_t cs = (size_t)e.tiles * 64;
+    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 + lane;
+    const uint32_t* dp = reinterpret_cast<const uint32_t*>(e.d) + (size_t)(live ? tile : 0) * 64 + lane;
+    for (int i = dim + tid; i < e.dimp; i += kLogitThreads) xn[i] = 0.0f;
 
     // the residual row and norm weights first (every wavefront's loads issued
-    // before the barrier), then the first embedding chunks, which stay in
+    // before the barrier), then the first embedding groups, which stay in
     // flight while the row is normalized (loads retire in issue order)
     const RowTeam tm = team_workgroup();
     const int passes = rowq_passes(dim, kLogitThreads);
@@ -49,16 +53,15 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     rowq_load_f32<MP>(tm, xv, x, dim, passes);
     rowq_load_f32<MP>(tm, wv, norm_w, dim, passes);
     __syncthreads();
-    // embedding chunks (16 bytes per lane) and their f16 block scales (one
-    // per two chunks) in one ring, each scale issued right behind its chunks:
-    // loads retire in issue order, so a scale loaded just in time would wait
-    // for every chunk prefetched before it
-    int4 qv[kLogitChunks];
-    uint16_t sv[kLogitChunks / 2];
+    // a ring of NG groups: each group's scale word, then its 4 chunks
+    int4 qv[NG][4];
+    uint32_t sv[NG];
 #pragma unroll
-    for (int k = 0; k < kLogitChunks; k++) {
-        qv[k] = qp[(size_t)min(k, k16n - 1) * 64];
-        if (k & 1) sv[k >> 1] = dp[(size_t)min(k >> 1, nbE - 1) * 64];
+    for (int gg = 0; gg < NG; gg++) {
+        const int g = min(gg, ng - 1);
+        sv[gg] = dp[(size_t)g * cs];
+#pragma unroll
+        for (int c = 0; c < 4; c++) qv[gg][c] = qp[(size_t)(4 * g + c) * cs];
     }
     rowq_stage<MP>(tm, xv, wv, dim, passes, sq);
     rowq_norm_quant<-1, false>(dim, eps, sq, nullptr, nullptr, xn);
@@ -66,21 +69,29 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     unsigned long long kk = 0ull;
     if (live) {
         float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int k0 = 0; k0 < k16n; k0 += kLogitChunks) {
+        for (int g0 = 0; g0 < ng; g0 += NG) {
 #pragma unroll
-            for (int kk2 = 0; kk2 < kLogitChunks; kk2++) {
-                const int k = k0 + kk2;
-                if (k < k16n) {
-                    const int4 q4 = qv[kk2];
-                    const float scv = f16_to_f32(sv[kk2 >> 1]);
-                    // refill: chunk k + kLogitChunks, and after an odd chunk
-                    // the scale of the block kLogitChunks/2 ahead (clamped
-                    // reads past the row are never used)
-                    qv[kk2] = qp[(size_t)min(k + kLogitChunks, k16n - 1) * 64];
-                    if (kk2 & 1) sv[kk2 >> 1] = dp[(size_t)min((k + kLogitChunks) >> 1, nbE - 1) * 64];
+            for (int gg = 0; gg < NG; gg++) {
+                const int g = g0 + gg;
+                if (NG > 1 && g >= ng) break;
+                const uint32_t sw = sv[gg];
+                int4 q4[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) q4[c] = qv[gg][c];
+                // refill with group g + NG (clamped re-reads past the row are
+                // never used)
+                const int gn = min(g + NG, ng - 1);
+                sv[gg] = dp[(size_t)gn * cs];
+#pragma unroll
+                for (int c = 0; c < 4; c++) qv[gg][c] = qp[(size_t)(4 * gn + c) * cs];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float scv = f16_to_f32((uint16_t)(c < 2 ? sw & 0xffffu : sw >> 16));
                     const float nsc = -128.0f * scv;   // exact: power-of-two multiple
-                    const float* xk = xn + k * 16;
-                    const uint32_t w[4] = {(uint32_t)q4.x, (uint32_t)q4.y, (uint32_t)q4.z, (uint32_t)q4.w};
+                    const float* xk = xn + (4 * g + c) * 16;
+                    const uint32_t w[4] = {(uint32_t)q4[c].x, (uint32_t)q4[c].y, (uint32_t)q4[c].z,
+                                           (uint32_t)q4[c].w};
 #pragma unroll
                     for (int m = 0; m < 4; m++) {
 #pragma unroll
@@ -142,7 +153,7 @@ __global__ __launch_bounds__(512) void k_finalize(const unsigned long long* __re
     st->pos += advance;
 }
 
-size_t logits_lds_bytes(int dim) { return ((size_t)dim + rowq_lds_floats(dim)) * sizeof(float); }
+size_t logits_lds_bytes(int dim) { return ((size_t)((dim + 63) & ~63) + rowq_lds_floats(dim)) * sizeof(float); }
 int logits_blocks(const EmbQ8& e) { return (e.tiles + kLogitThreads / 64 - 1) / (kLogitThreads / 64); }
 
 hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, float eps, float* logits,

@@ -311,9 +311,10 @@ bool upload_embedding(const GgufTensor* t, int dim, int vocab, EmbQ8* e, std::st
     if ((uint64_t)dim * vocab > t->n_elements) { *err = "token_embd.weight smaller than vocab*dim"; return false; }
     if (dim % 32) { *err = "embedding length must be a multiple of 32"; return false; }
     const int tiles = (vocab + 63) / 64;
-    const int k16n = dim / 16, nbE = dim / 32;
-    std::vector<int8_t> q((size_t)tiles * 64 * dim, 0);
-    std::vector<uint16_t> d((size_t)tiles * 64 * nbE, 0);
+    const int nbE = dim / 32, dimp = (dim + 63) & ~63;
+    // padding blocks (dim..dimp) keep scale 0: their values are exact zeros
+    std::vector<int8_t> q((size_t)tiles * 64 * dimp, 0);
+    std::vector<uint16_t> d((size_t)tiles * 64 * (dimp / 32), 0);
     const size_t blocks = (size_t)vocab * nbE;
     if (t->type == kGgmlQ8_0) {
         if (blocks * 34 > t->avail) { *err = "token_embd exceeds the file"; return false; }
@@ -340,15 +341,14 @@ bool upload_embedding(const GgufTensor* t, int dim, int vocab, EmbQ8* e, std::st
                     vals[2 * j + 1] = (int8_t)((blk[2 + j] >> 4) & 0x0f);
                 }
             }
-            d[(tile * nbE + b) * 64 + lane] = sc;
+            d[emb_d_idx(tiles, tile, b, (int)lane)] = sc;
             for (int h = 0; h < 2; h++) {
-                const size_t k16 = (size_t)2 * b + h;
-                int8_t* dst = &q[((tile * k16n + k16) * 64 + lane) * 16];
+                int8_t* dst = &q[emb_q_off(tiles, tile, 2 * b + h, (int)lane)];
                 for (int j = 0; j < 16; j++) dst[j] = (int8_t)((uint8_t)vals[16 * h + j] ^ 0x80u);  // u = q + 128
             }
         }
     }
-    e->vocab = vocab; e->dim = dim; e->tiles = tiles;
+    e->vocab = vocab; e->dim = dim; e->tiles = tiles; e->dimp = dimp;
     if (hipMalloc(&e->q, q.size() + 256) != hipSuccess || hipMalloc(&e->d, d.size() * 2 + 256) != hipSuccess ||
         hipMemcpy(e->q, q.data(), q.size(), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(e->d, d.data(), d.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {

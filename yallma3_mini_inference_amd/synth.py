@@ -48,6 +48,8 @@ CONFIGS = {
     "tiny": ModelConfig(128, 256, 2, 4, 2, 512, 256),
     "tiny_q4": ModelConfig(128, 256, 2, 4, 2, 512, 256, attn_format=Q4, ffn_format=Q4, file_type=2),
     "tiny_mixed": ModelConfig(128, 384, 3, 4, 1, 1000, 300, rope_theta=500000.0, ffn_format=Q4),
+    # dim 96: the embedding table's rows are padded to 128 (zero-scale blocks); vocab 300 ends in a partial tile
+    "tiny_pad": ModelConfig(96, 192, 2, 3, 1, 300, 128, seed=3),
     # a context long enough for the two-kernel decode attention (head size 64, 4 query heads per kv head)
     "tiny_long": ModelConfig(256, 512, 2, 4, 1, 512, 4096, seed=7),
     # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
