@@ -338,31 +338,37 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         const float sum = wave_serial_sum_at([pt, PCS](int i) { return pt[(i & 7) * PCS + (i >> 3)]; }, seq);
         if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     } else if (!wave_sum && tid == 0) {
-        // blocks of 32 positions = 4 columns of the 8 rows, read as 8 vf4s;
-        // each block's reads are issued before the previous block is added
-        // (the scheduling barriers keep that order); the number of blocks
-        // is even and the zero padding adds nothing
+        // blocks of 32 positions = 4 columns of the 8 rows, read as 8 vf4s.
+        // Per block: 7 of the next block's reads, the block's first column
+        // (8 adds), the next block's 8th read, the other 3 columns -- so the
+        // reads land under the adds, and no more than 15 LDS reads are ever
+        // outstanding (lgkmcnt counts to 15; beyond that the compiler can
+        // only wait for all of them).  The number of blocks is even and the
+        // zero padding adds nothing.
         const int nblk = pad / 32;
         float sum = 0.0f;
         vf4 va[8], vb[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) va[j] = *reinterpret_cast<const vf4*>(pt + j * PCS);
+        // the first block lands before the loop (reads pending at the loop
+        // head would make the compiler wait for all of them there)
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+        auto block = [&](vf4 (&cur)[8], vf4 (&nxt)[8], int bn) {
+#pragma unroll
+            for (int j = 0; j < 7; j++) nxt[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * bn);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 8; j++) sum = fadd(sum, cur[j][0]);
+            nxt[7] = *reinterpret_cast<const vf4*>(pt + 7 * PCS + 4 * bn);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 1; c < 4; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) sum = fadd(sum, cur[j][c]);
+        };
         for (int b = 0; b < nblk; b += 2) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) vb[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * (b + 1));
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) sum = fadd(sum, va[j][c]);
-            const int b2 = b + 2 < nblk ? b + 2 : b;
-#pragma unroll
-            for (int j = 0; j < 8; j++) va[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * b2);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) sum = fadd(sum, vb[j][c]);
+            block(va, vb, b + 1);
+            block(vb, va, b + 2 < nblk ? b + 2 : b);
         }
         red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
