@@ -22,7 +22,8 @@ def _models(gpu, oracle, model_dir, name):
 
 
 @pytest.mark.parametrize("name,prompt_len,steps", [("tiny", 20, 24), ("tiny_q4", 17, 16), ("tiny_mixed", 33, 20),
-                                                    ("tiny_pad", 9, 12)])
+                                                    ("tiny_pad", 9, 12), ("tiny", 100, 6), ("tiny_q4", 130, 4),
+                                                    ("tiny_mixed", 200, 4)])
 def test_prefill_then_greedy_decode(gpu, oracle, model_dir, name, prompt_len, steps):
     g, o, _ = _models(gpu, oracle, model_dir, name)
     rng = np.random.default_rng(prompt_len)

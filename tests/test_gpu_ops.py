@@ -229,7 +229,9 @@ def test_rope(gpu, oracle, hd, nh, nkv, theta, pos, batch):
 
 @pytest.mark.parametrize("batch,start,nh,nkv,hd", [(1, 0, 4, 2, 64), (1, 700, 32, 8, 64), (7, 13, 9, 3, 64),
                                                    (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128),
-                                                   (1, 3000, 9, 3, 64), (1, 2100, 2, 2, 32), (1, 5119, 8, 8, 64)])
+                                                   (1, 3000, 9, 3, 64), (1, 2100, 2, 2, 32), (1, 5119, 8, 8, 64),
+                                                   (64, 0, 4, 2, 64), (100, 37, 8, 2, 128), (130, 0, 9, 3, 64),
+                                                   (70, 5, 2, 2, 32), (257, 300, 4, 1, 64)])
 def test_attention(gpu, oracle, batch, start, nh, nkv, hd):
     from yallma3_mini_inference_amd import ops
     rng = np.random.default_rng(batch * 1000 + start)
@@ -241,6 +243,26 @@ def test_attention(gpu, oracle, batch, start, nh, nkv, hd):
     out = ops.attention(q, kc, vc, batch, start, nh, nkv, hd, scale)
     ref = oracle.fused_attention(q, kc, vc, seq, batch, nh, nkv, hd, start, nkv * hd, scale)
     assert_bits(out, ref)
+
+
+def test_prompt_attention_nonfinite_v(gpu, oracle):
+    # an infinity in V past some rows' causal bound: the reference still adds
+    # p * v there (p = 0), so those rows turn NaN; the tiled kernel must not
+    # skip the masked positions then
+    from yallma3_mini_inference_amd import ops
+    batch, start, nh, nkv, hd = 96, 10, 4, 2, 64
+    rng = np.random.default_rng(96)
+    seq = start + batch
+    q = rng.normal(0, 1, batch * nh * hd).astype(np.float32)
+    kc = rng.normal(0, 1, seq * nkv * hd).astype(np.float32)
+    vc = rng.normal(0, 1, seq * nkv * hd).astype(np.float32)
+    vc[(start + 80) * nkv * hd + 3] = np.inf
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    out = ops.attention(q, kc, vc, batch, start, nh, nkv, hd, scale)
+    ref = oracle.fused_attention(q, kc, vc, seq, batch, nh, nkv, hd, start, nkv * hd, scale)
+    nan = np.isnan(ref)
+    assert nan.any() and np.array_equal(np.isnan(out), nan)
+    assert_bits(out[~nan], ref[~nan])
 
 
 @pytest.mark.parametrize("hidden,batch,qfmt", [(8192, 1, 0), (1536, 2, 1), (96, 1, -1)])

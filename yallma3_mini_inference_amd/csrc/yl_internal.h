@@ -122,6 +122,13 @@ hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc,
                               int qfmt, int8_t* aq, float* as, float* att_f32, float* sc, hipStream_t s);
 // sc: scratch for the scores of long contexts, attn_scores_bytes() bytes
 // (0: the context is short enough for the single decode kernel; sc may be null)
+// Prompt batches of 64 or more tokens: tiled attention over a scratch of
+// prompt_attn_bytes(n_heads, seq_len, batch); seq_ld = pos + batch (host side)
+bool prompt_attn_applies(int batch);
+size_t prompt_attn_bytes(int n_heads, int seq_ld, int batch);
+hipError_t launch_prompt_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
+                                   int seq_ld, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
+                                   int qfmt, int8_t* aq, float* as, float* att_f32, float* scratch, hipStream_t s);
 bool attn_decode_split(int max_seq);
 size_t attn_scores_bytes(int n_heads, int max_seq);
 hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* st, int batch,

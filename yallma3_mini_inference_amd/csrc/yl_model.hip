@@ -280,6 +280,9 @@ struct yl_session {
     float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
     unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
     float* sc = nullptr;                 // attention scores of long contexts [n_heads][ctx]
+    float* psc = nullptr;                // prompt attention scratch (batches of 64+ tokens)
+    size_t psc_bytes = 0;
+    int pseq = 0;                        // seq_len of the prompt call being enqueued
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
     uint32_t ring_cap = 0;
@@ -508,6 +511,26 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     return m.release();
 }
 
+// The prompt attention scratch for `batch` tokens from `start_pos` (kept at
+// the largest size used; prompts below 64 tokens need none).
+bool prompt_scratch(yl_session* s, int batch, uint32_t start_pos) {
+    s->pseq = (int)start_pos + batch;
+    if (!prompt_attn_applies(batch)) return true;
+    const size_t need = prompt_attn_bytes(s->m->n_heads, s->pseq, batch);
+    if (need <= s->psc_bytes) return true;
+    hipStreamSynchronize(s->stream);
+    if (s->psc) hipFree(s->psc);
+    s->psc = nullptr;
+    s->psc_bytes = 0;
+    if (hipMalloc(&s->psc, need + 256) != hipSuccess) {
+        s->psc = nullptr;
+        set_error("hipMalloc failed for the prompt attention scratch");
+        return false;
+    }
+    s->psc_bytes = need;
+    return true;
+}
+
 bool session_grow(yl_session* s, int batch) {
     if (batch <= s->cap_b) return true;
     const yl_model* m = s->m;
@@ -632,6 +655,9 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         if (batch == 1)
             return launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                       m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->sc, st);
+        if (prompt_attn_applies(batch) && s->psc)
+            return launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                           m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->psc, st);
         return launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                 m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
     case kOpWo:
@@ -929,8 +955,12 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     const size_t seq = start_pos + batch;
     // one token: the decode kernel (as in a decode step); several: the
     // prompt kernel, whose workgroup holds a whole score row
-    if (batch > 1 && seq * 4 + (size_t)hd * 40 > 60 * 1024) {
+    if (batch > 1 && !prompt_attn_applies((int)batch) && seq * 4 + (size_t)hd * 40 > 60 * 1024) {
         set_error("attention: seq_len too long for one workgroup");
+        return YL_ERR_UNSUPPORTED;
+    }
+    if (prompt_attn_applies((int)batch) && hd != 32 && hd != 64 && hd != 128) {
+        set_error("attention: prompt batches of 64+ tokens need head_size 32, 64 or 128");
         return YL_ERR_UNSUPPORTED;
     }
     if (batch == 1 && (hd % 32 || !attn_decode_fits((int)seq))) {
@@ -948,13 +978,18 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     // the reference layout [seq][kv_dim]
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&kt, (size_t)ld * kv_dim * 4 + 256);
-    const size_t sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq) : 0;
+    const size_t sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq)
+                            : prompt_attn_applies((int)batch) ? prompt_attn_bytes((int)n_heads, (int)seq, (int)batch)
+                                                              : 0;
     if (e == hipSuccess && sc_bytes) e = hipMalloc(&sc, sc_bytes);
     if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, kv_dim, ld, strm);
     if (e == hipSuccess && batch == 1)
         e = launch_attn_decode(q, kt, vc, dst, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
                                nullptr, nullptr, out, sc, strm);
+    else if (e == hipSuccess && sc)
+        e = launch_prompt_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
+                                    attn_scale, -1, nullptr, nullptr, out, sc, strm);
     else if (e == hipSuccess)
         e = launch_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
                              attn_scale, -1, nullptr, nullptr, out, strm);
@@ -1059,7 +1094,7 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->graph) hipGraphExecDestroy(s->graph);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->keys, s->tokens, s->sc};
+                   s->as_, s->hs, s->keys, s->tokens, s->sc, s->psc};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
@@ -1103,7 +1138,7 @@ yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint
         e = hipGraphLaunch(s->graph, s->stream);
         if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
     } else {
-        if (!session_grow(s, (int)n)) return YL_ERR_NOMEM;
+        if (!session_grow(s, (int)n) || !prompt_scratch(s, (int)n, start_pos)) return YL_ERR_NOMEM;
         e = hipMemcpyAsync(s->tokens, tokens, n * 4, hipMemcpyHostToDevice, s->stream);
         if (e != hipSuccess) return hip_fail(e, "token upload");
         e = enqueue_forward(m, s, (int)n, s->tokens, 0);
@@ -1150,7 +1185,8 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
-    if (batch > 1 && !session_grow(s, (int)batch)) return YL_ERR_NOMEM;
+    if (batch > 1 && (!session_grow(s, (int)batch) || !prompt_scratch(s, (int)batch, start_pos)))
+        return YL_ERR_NOMEM;
     yl_status rs = put_state(s, (int32_t)start_pos, token);
     if (rs != YL_OK) return rs;
     // one graph: this class's launches of one step, back to back

@@ -1,0 +1,460 @@
+// yl_pattn.hip -- attention of prompt batches (forward.rs:299-400), tiled.
+//
+// A prompt of B >= 64 tokens attends in four kernels that share every K, V
+// and score tile among 64 query rows.  The arithmetic is the reference's,
+// operation by operation:
+//   score[t][t2] = reduce_add8(8 lane partials over head_size) * scale,
+//     positions past the row's causal bound t1 = pos + t are -1e10;
+//   max from -1e10; e = exp(score - max); sum_exp serial over all seq_len
+//     positions (masked ones add exp(-1e10 - max), zero unless every score
+//     of the row is at or below -1e10); p = e * (1 / sum_exp);
+//   out[t][d] = reduce_add8(lane j sums p * v over t2 = 8c + j in c order)
+//     + the seq_len % 8 tail in t2 order.
+//
+// 1. k_pattn_scores: workgroup (position tile, row tile, head) computes the
+//    64 x 64 scores with 4 x 4 register tiles, one lane partial j at a time
+//    (folded in reduce_add8's order), and the tile's row maxima.
+// 2. k_pattn_exp: the same tiles, e = exp(score - max) in place.
+// 3. k_pattn_sum: one lane per row walks the row in position order (the
+//    serial denominator), then inv = 1 / sum and the masked p.
+// 4. k_pattn_pv: workgroup (row tile, head) chains p * v for its 64 rows and
+//    every dimension (4 rows x 4 dimensions x 8 lane chains per thread),
+//    then the 32-group quantization of the output projection's input.
+// Scores live in a scratch [head][position][row] (rows contiguous, so a
+// wavefront reading one position of 64 rows reads 256 contiguous bytes).
+#include <hip/hip_runtime.h>
+
+#include "yl_blocks.h"
+#include "yl_device.h"
+#include "yl_internal.h"
+
+namespace yl {
+
+constexpr int kPT = 64;         // rows (and positions) per tile
+constexpr int kPTS = kPT + 4;   // LDS row stride of a 64-wide tile (16-byte aligned, banks spread)
+constexpr int kBufRawP = 0x00020000;
+
+__host__ __device__ inline int pattn_rows_ld(int batch) { return (batch + kPT - 1) / kPT * kPT; }
+__host__ __device__ inline int pattn_tiles(int seq) { return (seq + kPT - 1) / kPT; }
+
+// Scratch: scores [n_heads][seq_ld][Bp], tile maxima [n_heads][tiles][Bp],
+// then per row: max, 1/sum, masked p ([n_heads][Bp] each).
+struct PromptScratch {
+    float *sc, *tm, *mx, *inv, *pm;
+};
+__host__ __device__ inline PromptScratch pattn_carve(float* base, int n_heads, int seq_ld, int batch) {
+    const size_t Bp = pattn_rows_ld(batch);
+    PromptScratch p;
+    p.sc = base;
+    p.tm = p.sc + (size_t)n_heads * seq_ld * Bp;
+    p.mx = p.tm + (size_t)n_heads * pattn_tiles(seq_ld) * Bp;
+    p.inv = p.mx + (size_t)n_heads * Bp;
+    p.pm = p.inv + (size_t)n_heads * Bp;
+    return p;
+}
+size_t prompt_attn_bytes(int n_heads, int seq_ld, int batch) {
+    const size_t Bp = pattn_rows_ld(batch);
+    return (size_t)n_heads * Bp * ((size_t)seq_ld + pattn_tiles(seq_ld) + 3) * sizeof(float);
+}
+bool prompt_attn_applies(int batch) { return batch >= kPT; }
+
+// ---------------------------------------------------------------------------
+// 1. scores and tile row maxima.  Thread (ty, tx) of 16 x 16: rows 4ty..+3,
+//    positions 4tx..+3 of the tile.  Lane partial j (dimensions 8s + j, s in
+//    order) of all 16 scores, then folded: a = ((l0 + l1) + l2) + l3,
+//    b = ((l4 + l5) + l6) + l7, score = (a + b) * scale.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ sq, const float* __restrict__ kc,
+                                                      const StepState* __restrict__ st, int batch, int seq_ld,
+                                                      int kv_ld, int n_heads, int n_kv_heads, float scale,
+                                                      float* __restrict__ scratch) {
+    __shared__ __align__(16) float qT[HD * kPTS];   // [dim][row]
+    __shared__ __align__(16) float kT[HD * kPTS];   // [dim][position]
+    const int pt = blockIdx.x, rt = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    const int pos0 = st->pos, seq = pos0 + batch;
+    const int row0 = rt * kPT, p0 = pt * kPT;
+    if (seq > seq_ld || p0 >= seq || p0 > pos0 + row0 + kPT - 1) return;   // past the sequence, or all masked
+    const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
+    const int Bp = pattn_rows_ld(batch);
+    const int kvh = h / (n_heads / n_kv_heads), att_dim = n_heads * HD;
+    // every load first (q rows as 16-byte pieces, key quads), then the LDS
+    // stores: keys transposed, dimension d of position p at
+    // kc[(kvh*HD + d) * kv_ld + p]; quads past the row (kv_ld is a multiple
+    // of 4) re-read its last quad (positions past seq are never stored)
+    constexpr int NV = HD / 16;   // 16-byte pieces per thread, q and keys each
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(kc + (size_t)kvh * HD * kv_ld), (short)0, HD * kv_ld * 4, kBufRawP);
+    vf4 qa[NV], ka[NV];
+    // (q pieces: consecutive lanes take consecutive rows, so the transposed
+    // LDS stores below hit consecutive banks)
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
+        qa[i] = *reinterpret_cast<const vf4*>(sq + (size_t)min(row0 + r, batch - 1) * att_dim + (size_t)h * HD + 4 * d4);
+        const int d = idx / (kPT / 4), q4 = idx % (kPT / 4);
+        const int p = min(p0 + 4 * q4, kv_ld - 4);
+        ka[i] = __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(krs, p * 4, d * kv_ld * 4, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
+        const bool live = row0 + r < batch;
+#pragma unroll
+        for (int c = 0; c < 4; c++) qT[(4 * d4 + c) * kPTS + r] = live ? qa[i][c] : 0.0f;
+        const int d = idx / (kPT / 4), q4 = idx % (kPT / 4);
+        *reinterpret_cast<vf4*>(kT + d * kPTS + 4 * q4) = ka[i];
+    }
+    __syncthreads();
+    const int ty = tid >> 4, tx = tid & 15;
+    float A[4][4], Bh[4][4];
+    // one lane partial at a time (unrolled, the compiler would hoist every
+    // partial's LDS reads and run out of registers)
+#pragma unroll 1
+    for (int j = 0; j < 8; j++) {
+        float l[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) l[a][b] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < HD / 8; s++) {
+            const vf4 qv = *reinterpret_cast<const vf4*>(qT + (8 * s + j) * kPTS + 4 * ty);
+            const vf4 kv = *reinterpret_cast<const vf4*>(kT + (8 * s + j) * kPTS + 4 * tx);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) l[a][b] = fadd(l[a][b], fmul(qv[a], kv[b]));
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (j == 0) A[a][b] = l[a][b];
+                else if (j < 4) A[a][b] = fadd(A[a][b], l[a][b]);
+                else if (j == 4) Bh[a][b] = l[a][b];
+                else Bh[a][b] = fadd(Bh[a][b], l[a][b]);
+            }
+    }
+    float rmax[4] = {-1e10f, -1e10f, -1e10f, -1e10f};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int p = p0 + 4 * tx + b;
+        float v[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            v[a] = fmul(fadd(A[a][b], Bh[a][b]), scale);
+            if (p <= pos0 + row0 + 4 * ty + a) rmax[a] = fmaxf(rmax[a], v[a]);
+        }
+        if (p < seq)
+            *reinterpret_cast<vf4*>(S.sc + ((size_t)h * seq_ld + p) * Bp + row0 + 4 * ty) = vf4{v[0], v[1], v[2], v[3]};
+    }
+    // row maxima over the 16 threads of a row group (tx = the low 4 bits)
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) rmax[a] = fmaxf(rmax[a], __shfl_xor(rmax[a], off, 16));
+    if (tx == 0)
+#pragma unroll
+        for (int a = 0; a < 4; a++) S.tm[((size_t)h * pattn_tiles(seq_ld) + pt) * Bp + row0 + 4 * ty + a] = rmax[a];
+}
+
+// ---------------------------------------------------------------------------
+// 2. e = exp(score - max) in place over the causal entries of a tile; the
+//    row max folds the tile maxima from -1e10 (the position-0 tile stores it)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__ st, int batch, int seq_ld,
+                                                   int n_heads, float* __restrict__ scratch) {
+    __shared__ float mxl[kPT];
+    const int pt = blockIdx.x, rt = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    const int pos0 = st->pos, seq = pos0 + batch;
+    const int row0 = rt * kPT, p0 = pt * kPT;
+    if (seq > seq_ld || p0 >= seq || p0 > pos0 + row0 + kPT - 1) return;
+    const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
+    const int Bp = pattn_rows_ld(batch), ntl = pattn_tiles(seq_ld);
+    {
+        // row r = tid % 64 folds tile maxima q = tid / 64 + 4k (loads issued
+        // 8 at a time), then the 4 partial maxima meet in LDS
+        __shared__ float mxp[4][kPT];
+        const int r = tid & 63, part = tid >> 6, t = row0 + r;
+        const int last = min(pos0 + t, seq - 1) / kPT;
+        const float* tmr = S.tm + (size_t)h * ntl * Bp + t;
+        float mx = -1e10f;
+        for (int q0 = part; q0 <= last; q0 += 32) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = tmr[(size_t)min(q0 + 4 * k, last) * Bp];
+#pragma unroll
+            for (int k = 0; k < 8; k++) mx = fmaxf(mx, v[k]);
+        }
+        mxp[part][r] = mx;
+        __syncthreads();
+        if (tid < kPT) {
+            mx = fmaxf(fmaxf(mxp[0][tid], mxp[1][tid]), fmaxf(mxp[2][tid], mxp[3][tid]));
+            mxl[tid] = mx;
+            if (pt == 0) S.mx[(size_t)h * Bp + row0 + tid] = mx;
+        }
+    }
+    __syncthreads();
+    // 16 entries per thread: position pp = idx / 64, row r = idx % 64
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int idx = tid + 256 * k, pp = idx >> 6, r = idx & 63;
+        const int p = min(p0 + pp, seq - 1);
+        v[k] = S.sc[((size_t)h * seq_ld + p) * Bp + row0 + r];
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int idx = tid + 256 * k, pp = idx >> 6, r = idx & 63;
+        const int p = p0 + pp, t = row0 + r;
+        const bool live = p < seq && t < batch && p <= pos0 + t;
+        const float e = expf_rn(v[k] - mxl[r]);
+        if (live) S.sc[((size_t)h * seq_ld + p) * Bp + t] = e;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 3. serial denominators, one lane per row, positions in order; 8 loads in
+//    flight per lane (the adds stay in order)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pattn_sum(const StepState* __restrict__ st, int batch, int seq_ld,
+                                                   int n_heads, float* __restrict__ scratch) {
+    const int h = blockIdx.y, tid = threadIdx.x;
+    const int t = blockIdx.x * 256 + tid;
+    const int pos0 = st->pos, seq = pos0 + batch;
+    if (seq > seq_ld) return;
+    const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
+    const int Bp = pattn_rows_ld(batch);
+    const int tc = min(t, Bp - 1);
+    const int t1 = pos0 + t;
+    // the wavefront walks to the last causal position of its last row
+    const int wlast = min(pos0 + min((int)(blockIdx.x * 256 + (tid & ~63) + 63), batch - 1), seq - 1);
+    const float* col = S.sc + (size_t)h * seq_ld * Bp + tc;
+    float sum = 0.0f;
+    // a ring of two 8-position groups: the next group's loads are in flight
+    // while the current one is added
+    float ea[8], eb[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) ea[i] = col[(size_t)min(i, wlast) * Bp];
+    for (int t2 = 0; t2 <= wlast; t2 += 16) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) eb[i] = col[(size_t)min(t2 + 8 + i, wlast) * Bp];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (t2 + i <= t1 && t2 + i <= wlast) sum = fadd(sum, ea[i]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) ea[i] = col[(size_t)min(t2 + 16 + i, wlast) * Bp];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (t2 + 8 + i <= t1 && t2 + 8 + i <= wlast) sum = fadd(sum, eb[i]);
+    }
+    if (t >= batch) return;
+    // masked positions t1+1 .. seq-1 add exp(-1e10 - max) each
+    const float em = t1 < seq - 1 ? expf_rn(-1e10f - S.mx[(size_t)h * Bp + t]) : 0.0f;
+    if (em != 0.0f)
+        for (int i = t1 + 1; i < seq; i++) sum = fadd(sum, em);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    S.inv[(size_t)h * Bp + t] = inv;
+    S.pm[(size_t)h * Bp + t] = fmul(em, inv);
+}
+
+// ---------------------------------------------------------------------------
+// 4. P.V chains and the output.  Thread (ty, tx): rows 4ty..+3, dimensions
+//    4tx..+3, 8 lane chains each (acc[row][dim][j] += p * v over t2 = 8c + j,
+//    c in order).  Positions run to the tile's causal bound (the last row's
+//    t1) unless a row's masked p is nonzero or the V rows past the bound hold
+//    an infinity or NaN (0 * v would then not vanish): masked positions add
+//    p * v = +-0 to a partial that starts at +0, which changes nothing.
+// ---------------------------------------------------------------------------
+template <int QF, int HD>
+__global__ __launch_bounds__(HD * 4) void k_pattn_pv(const float* __restrict__ vc, const StepState* __restrict__ st,
+                                                     int batch, int seq_ld, int n_heads, int n_kv_heads,
+                                                     float* __restrict__ scratch, int8_t* __restrict__ aq,
+                                                     float* __restrict__ as, float* __restrict__ att_f32) {
+    constexpr int NT = HD * 4, NX = HD / 4;   // threads; dimension groups
+    constexpr int VS = HD + 4;                // LDS row stride of a V tile
+    __shared__ __align__(16) float pT[kPT * kPTS];   // [position][row]
+    __shared__ __align__(16) float vT[kPT * VS];     // [position][dim]
+    __shared__ float invl[kPT], pml[kPT];
+    __shared__ int full_sh;
+    const int rt = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int pos0 = st->pos, seq = pos0 + batch;
+    if (seq > seq_ld) return;
+    const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
+    const int Bp = pattn_rows_ld(batch);
+    const int kvh = h / (n_heads / n_kv_heads), kv_dim = n_kv_heads * HD, att_dim = n_heads * HD;
+    const int row0 = rt * kPT;
+    const int n_chunks = seq / 8;
+    const int bound = min(seq, pos0 + row0 + kPT);   // positions < bound hold every row's causal part
+    if (tid == 0) full_sh = 0;
+    __syncthreads();
+    bool full = false;
+    if (tid < kPT) {
+        const int t = row0 + tid;
+        invl[tid] = t < batch ? S.inv[(size_t)h * Bp + t] : 0.0f;
+        pml[tid] = t < batch ? S.pm[(size_t)h * Bp + t] : 0.0f;
+        full = pml[tid] != 0.0f;
+    }
+    // V past the bound (only the chunked part is chained), 16-byte pieces,
+    // 8 loads in flight per thread
+    const float* vh = vc + (size_t)kvh * HD;
+    const int n_scan = max(0, n_chunks * 8 - bound) * NX;
+    for (int i0 = tid; i0 < n_scan; i0 += 8 * NT) {
+        vf4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = min(i0 + k * NT, n_scan - 1);
+            v[k] = *reinterpret_cast<const vf4*>(vh + (size_t)(bound + i / NX) * kv_dim + 4 * (i % NX));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) full = full || !(__builtin_fabsf(v[k][c]) <= 3.402823466e38f);
+    }
+    if (full) atomicOr(&full_sh, 1);
+    __syncthreads();
+    const int end_c = full_sh ? n_chunks : min(n_chunks, (bound + 7) / 8);
+
+    const int ty = tid / NX, tx = tid % NX;
+    float acc[4][4][8];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[a][b][j] = 0.0f;
+    const float* sch = S.sc + (size_t)h * seq_ld * Bp + row0;
+    // tiles of 64 positions: the next tile's scores and V rows are loaded
+    // into registers while the current tile is chained
+    constexpr int SV = kPT * kPT / 4 / NT, VV = kPT * NX / NT;
+    vf4 sreg[SV], vreg[VV];
+    auto load_tile = [&](int q0) {
+#pragma unroll
+        for (int i = 0; i < SV; i++) {
+            const int idx = tid + NT * i, pp = idx / (kPT / 4), r4 = idx % (kPT / 4);
+            sreg[i] = *reinterpret_cast<const vf4*>(sch + (size_t)min(q0 + pp, seq - 1) * Bp + 4 * r4);
+        }
+#pragma unroll
+        for (int i = 0; i < VV; i++) {
+            const int idx = tid + NT * i, pp = idx / NX, d4 = idx % NX;
+            vreg[i] = *reinterpret_cast<const vf4*>(vh + (size_t)min(q0 + pp, seq - 1) * kv_dim + 4 * d4);
+        }
+    };
+    // p = e * inv on the causal entries, the row's masked p elsewhere
+    auto store_tile = [&](int q0) {
+#pragma unroll
+        for (int i = 0; i < SV; i++) {
+            const int idx = tid + NT * i, pp = idx / (kPT / 4), r4 = idx % (kPT / 4);
+            float pv[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int r = 4 * r4 + c;
+                pv[c] = q0 + pp <= pos0 + row0 + r ? fmul(sreg[i][c], invl[r]) : pml[r];
+            }
+            *reinterpret_cast<vf4*>(pT + pp * kPTS + 4 * r4) = vf4{pv[0], pv[1], pv[2], pv[3]};
+        }
+#pragma unroll
+        for (int i = 0; i < VV; i++) {
+            const int idx = tid + NT * i, pp = idx / NX, d4 = idx % NX;
+            *reinterpret_cast<vf4*>(vT + pp * VS + 4 * d4) = vreg[i];
+        }
+    };
+    if (end_c > 0) load_tile(0);
+    for (int q0 = 0; q0 < 8 * end_c; q0 += kPT) {
+        store_tile(q0);
+        lds_barrier();   // (the next tile's loads, issued below, stay in flight across both barriers)
+        if (q0 + kPT < 8 * end_c) load_tile(q0 + kPT);
+        const int nc = min(kPT / 8, end_c - q0 / 8);
+        for (int c = 0; c < nc; c++) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const vf4 pv = *reinterpret_cast<const vf4*>(pT + (8 * c + j) * kPTS + 4 * ty);
+                const vf4 vv = *reinterpret_cast<const vf4*>(vT + (8 * c + j) * VS + 4 * tx);
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) acc[a][b][j] = fadd(acc[a][b][j], fmul(pv[a], vv[b]));
+            }
+        }
+        lds_barrier();
+    }
+    // out = reduce_add8 + the seq % 8 tail in order, then the 32-groups
+    // (8 threads of consecutive tx hold one group of a row)
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int r = 4 * ty + a, t = row0 + r;
+        const int tcl = min(t, batch - 1);
+        float o[4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            o[b] = reduce_add8(acc[a][b]);
+            for (int t2 = n_chunks * 8; t2 < seq; t2++) {
+                const float p = t2 <= pos0 + tcl ? fmul(sch[(size_t)t2 * Bp + r], invl[r]) : pml[r];
+                o[b] = fadd(o[b], fmul(p, vh[(size_t)t2 * kv_dim + 4 * tx + b]));
+            }
+        }
+        const size_t col = (size_t)t * att_dim + (size_t)h * HD + 4 * tx;
+        if (t < batch && att_f32)
+#pragma unroll
+            for (int b = 0; b < 4; b++) att_f32[col + b] = o[b];
+        if constexpr (QF >= 0) {
+            float am = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 4; b++) am = fmaxf(am, fabsf(o[b]));
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, 8));
+            const float s = group_scale<QF>(am);
+            if (t < batch) {
+#pragma unroll
+                for (int b = 0; b < 4; b++) aq[col + b] = (int8_t)quant_one<QF>(o[b], s);
+                if ((tx & 7) == 0) as[col / kGroup] = s;
+            }
+        }
+    }
+}
+
+template <int QF, int HD>
+static hipError_t launch_pattn_hd(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
+                                  int seq_ld, int kv_ld, int n_heads, int n_kv_heads, float scale, int8_t* aq,
+                                  float* as, float* att_f32, float* scratch, hipStream_t s) {
+    const dim3 tiles(pattn_tiles(seq_ld), pattn_tiles(batch), n_heads);
+    hipLaunchKernelGGL((k_pattn_scores<HD>), tiles, dim3(256), 0, s, sq, kc, st, batch, seq_ld, kv_ld, n_heads,
+                       n_kv_heads, scale, scratch);
+    hipLaunchKernelGGL(k_pattn_exp, tiles, dim3(256), 0, s, st, batch, seq_ld, n_heads, scratch);
+    hipLaunchKernelGGL(k_pattn_sum, dim3((pattn_rows_ld(batch) + 255) / 256, n_heads), dim3(256), 0, s, st, batch,
+                       seq_ld, n_heads, scratch);
+    hipLaunchKernelGGL((k_pattn_pv<QF, HD>), dim3(pattn_tiles(batch), n_heads), dim3(HD * 4), 0, s, vc, st, batch,
+                       seq_ld, n_heads, n_kv_heads, scratch, aq, as, att_f32);
+    return hipGetLastError();
+}
+
+template <int QF>
+static hipError_t launch_pattn_q(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
+                                 int seq_ld, int kv_ld, int n_heads, int n_kv_heads, int hd, float scale, int8_t* aq,
+                                 float* as, float* att_f32, float* scratch, hipStream_t s) {
+    switch (hd) {
+    case 32: return launch_pattn_hd<QF, 32>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, scratch, s);
+    case 64: return launch_pattn_hd<QF, 64>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, scratch, s);
+    case 128: return launch_pattn_hd<QF, 128>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, scale, aq, as, att_f32, scratch, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prompt_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
+                                   int seq_ld, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
+                                   int qfmt, int8_t* aq, float* as, float* att_f32, float* scratch, hipStream_t s) {
+    if (!scratch || batch < kPT || seq_ld < batch || kv_ld < seq_ld || kv_ld % 4) return hipErrorInvalidValue;
+    if (qfmt == kQ8)
+        return launch_pattn_q<kQ8>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
+                                   as, att_f32, scratch, s);
+    if (qfmt == kQ4)
+        return launch_pattn_q<kQ4>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
+                                   as, att_f32, scratch, s);
+    return launch_pattn_q<-1>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, head_size, scale, aq, as,
+                              att_f32, scratch, s);
+}
+
+}  // namespace yl
