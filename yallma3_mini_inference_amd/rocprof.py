@@ -40,7 +40,9 @@ def trace(path):
     rows = list(csv.DictReader(open(path)))
     by = collections.defaultdict(list)
     for r in rows:
-        kind = "decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in r["Kernel_Name"] else "prompt"
+        name = r["Kernel_Name"]
+        kind = ("decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in name or "k_attn_scores" in name
+                else "prompt")
         key = (kind, _short(r["Kernel_Name"]), r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"],
                r["VGPR_Count"], r["LDS_Block_Size"], r["Scratch_Size"])
         by[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
