@@ -138,6 +138,38 @@ __device__ __forceinline__ void exp_row(float* pt, int PCS, int b0, int seq, int
 }
 
 constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decode kernel)
+
+// One round of the decode kernel's scores: wavefront `wave` = lane partial
+// j computes partial j (key dimensions 8s + j, s in order) of NC chunks of
+// 256 positions starting at r0 (4 positions per lane), every key load of
+// the round issued before the first product; partials go to
+// part[j][RP].  Quads past the row re-read its last quad (never used).
+template <int HD, int NC>
+__device__ __forceinline__ void score_round(__amdgpu_buffer_rsrc_t krs, const float* qp, int r0, int n_quads,
+                                            int lane, int wave, int row_step, float* part, int RP) {
+    vf4 k4[NC][HD / 8];
+#pragma unroll
+    for (int ch = 0; ch < NC; ch++) {
+        const int quad = min(r0 / 4 + ch * 64 + lane, n_quads - 1);
+#pragma unroll
+        for (int s = 0; s < HD / 8; s++) k4[ch][s] = buf_load_f32x4(krs, quad * 16, (8 * s + wave) * row_step);
+    }
+    // (left free, the scheduler keeps a dozen loads in flight)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ch = 0; ch < NC; ch++) {
+        float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < HD / 8; s++) {
+            const float qv = qp[8 * s];
+            l[0] = fadd(l[0], fmul(qv, k4[ch][s].x));
+            l[1] = fadd(l[1], fmul(qv, k4[ch][s].y));
+            l[2] = fadd(l[2], fmul(qv, k4[ch][s].z));
+            l[3] = fadd(l[3], fmul(qv, k4[ch][s].w));
+        }
+        *reinterpret_cast<vf4*>(part + wave * RP + ch * 256 + 4 * lane) = vf4{l[0], l[1], l[2], l[3]};
+    }
+}
 constexpr int kScoreRows = 256;   // positions per scores workgroup
 constexpr int kLongQuads = 8;     // score quads per decode thread: max_seq <= 8 * 4 * kDecThreads
 
@@ -267,31 +299,23 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         const float* qp = qh + wave;   // wave = j, uniform: scalar query loads
         const int row_step = kv_ld * 4;
         for (int r0 = 0; r0 < seq; r0 += RP) {
-            vf4 k4[NCH][HD / 8];
-#pragma unroll
-            for (int ch = 0; ch < NCH; ch++) {
-                const int quad = min(r0 / 4 + ch * 64 + lane, n_quads - 1);
-#pragma unroll
-                for (int s = 0; s < HD / 8; s++) k4[ch][s] = buf_load_f32x4(krs, quad * 16, (8 * s + wave) * row_step);
-            }
-            // every load of the round is issued before the first product
-            // (left free, the scheduler keeps a dozen in flight)
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int ch = 0; ch < NCH; ch++) {
-                float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int s = 0; s < HD / 8; s++) {
-                    const float qv = qp[8 * s];
-                    l[0] = fadd(l[0], fmul(qv, k4[ch][s].x));
-                    l[1] = fadd(l[1], fmul(qv, k4[ch][s].y));
-                    l[2] = fadd(l[2], fmul(qv, k4[ch][s].z));
-                    l[3] = fadd(l[3], fmul(qv, k4[ch][s].w));
-                }
-                *reinterpret_cast<vf4*>(part + wave * RP + ch * 256 + 4 * lane) = vf4{l[0], l[1], l[2], l[3]};
+            // only the chunks holding positions (loads past the last one
+            // would all re-read its last quad, still costing memory-pipe
+            // cycles); one straight-line variant per chunk count
+            const int nlive = min(NCH, (n_quads - r0 / 4 + 63) / 64);
+            auto round = [&](auto nc) {
+                score_round<HD, decltype(nc)::value>(krs, qp, r0, n_quads, lane, wave, row_step, part, RP);
+            };
+            switch (nlive) {
+            case 1: round(std::integral_constant<int, 1>{}); break;
+            case 2: if constexpr (NCH >= 2) round(std::integral_constant<int, 2>{}); break;
+            case 3: if constexpr (NCH >= 3) round(std::integral_constant<int, 3>{}); break;
+            case 4: if constexpr (NCH >= 4) round(std::integral_constant<int, 4>{}); break;
+            default: if constexpr (NCH >= 8) round(std::integral_constant<int, NCH>{}); break;
             }
             lds_barrier();
-            for (int i = tid; i < RP; i += kDecThreads) {
+            const int nr = min(RP, seq - r0);
+            for (int i = tid; i < nr; i += kDecThreads) {
                 float lj[8];
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) lj[jj] = part[jj * RP + i];
