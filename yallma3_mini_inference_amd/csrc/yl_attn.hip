@@ -474,6 +474,244 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
 }
 
 // ---------------------------------------------------------------------------
+// Long contexts, head sizes 64 and 128, 2/4/8 query heads per kv head: the
+// softmax and the P.V chains as three more kernels after k_attn_scores.
+// Scratch after the scores: p transposed [n_heads][8][pcs] (p[8c + j] at
+// (h*8 + j)*pcs + c, pcs = sc_ld / 8), then the lane partials
+// [n_heads][HD][8].
+// ---------------------------------------------------------------------------
+constexpr int kPvRows = 64;     // V rows (one lane j) per LDS slot
+constexpr int kPvSlots = 8;     // slots in flight
+
+// Waits until at most n of this wavefront's vector memory operations are
+// in flight (n < 64; the immediate must be a constant).
+// 32-bit LDS offset of a pointer into shared memory
+__device__ __forceinline__ unsigned lds_addr(const float* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) float*)p;
+}
+
+// rows O and O + 1 (64 floats apart) at LDS offset a, untracked by the
+// compiler's waits: the caller waits with lgkm_wait_tie before the use
+template <int O>
+__device__ __forceinline__ vf2 lds_read2st64(unsigned a) {
+    static_assert(O >= 0 && O + 1 < 256, "offset field");
+    vf2 r;
+    asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(r) : "v"(a), "n"(O), "n"(O + 1) : "memory");
+    return r;
+}
+
+// 16 bytes at LDS offset a + O (a broadcast when a is uniform), untracked
+template <int O>
+__device__ __forceinline__ vf4 lds_read_b128(unsigned a) {
+    static_assert(O >= 0 && O < 65536, "offset field");
+    vf4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(O) : "memory");
+    return r;
+}
+
+// s_waitcnt lgkmcnt(N), tied to the registers it makes valid so that no use
+// of them is scheduled above it
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tie(vf2& a, vf2& b, vf2& c, vf2& d, vf4& e, vf4& f) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%6)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f) : "n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// vmcnt <= k * D for a run-time k in [0, 7]
+template <int D>
+__device__ __forceinline__ void wait_vm_slots(int k) {
+    switch (k) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<D>(); break;
+    case 2: wait_vm<2 * D>(); break;
+    case 3: wait_vm<3 * D>(); break;
+    case 4: wait_vm<4 * D>(); break;
+    case 5: wait_vm<5 * D>(); break;
+    case 6: wait_vm<6 * D>(); break;
+    default: wait_vm<7 * D>(); break;
+    }
+}
+
+// Softmax of one head: max from -1e10, e = exp(score - max) into LDS, the
+// serial sum (one lane up to kWaveSumSeq positions, one wavefront beyond),
+// p = e * (1 / sum) written transposed for the P.V kernel.
+__global__ __launch_bounds__(kDecThreads) void k_attn_softmax(const StepState* __restrict__ st, int sc_ld,
+                                                              int n_heads, float* __restrict__ scratch) {
+    extern __shared__ __align__(16) float el[];
+    __shared__ float red[16];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int seq = st->pos + 1, n_quads = (seq + 3) / 4;
+    const float* __restrict__ sh = scratch + (size_t)h * sc_ld;
+    float* __restrict__ pt = scratch + (size_t)n_heads * sc_ld + (size_t)h * sc_ld;   // [8][pcs] of this head
+    const int pcs = sc_ld / 8;
+    vf4 s4[kLongQuads];
+#pragma unroll
+    for (int i = 0; i < kLongQuads; i++) s4[i] = *reinterpret_cast<const vf4*>(sh + 4 * min(tid + i * kDecThreads, n_quads - 1));
+    float lmax = -1e10f;
+#pragma unroll
+    for (int i = 0; i < kLongQuads; i++)
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++)
+            lmax = fmaxf(lmax, 4 * (tid + i * kDecThreads) + pp < seq ? s4[i][pp] : -1e10f);
+    lmax = wave_max(lmax);
+    if ((tid & 63) == 0) red[tid >> 6] = lmax;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
+#pragma unroll
+    for (int i = 0; i < kLongQuads; i++)
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) {
+            const int p = 4 * (tid + i * kDecThreads) + pp;
+            if (p < seq) el[p] = expf_rn(s4[i][pp] - mx);
+        }
+    __syncthreads();
+    if (seq > kWaveSumSeq) {
+        if (tid < 64) {
+            const float sum = wave_serial_sum(el, seq);
+            if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+        }
+    } else if (tid == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < seq; i++) sum = fadd(sum, el[i]);
+        red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = red[8];
+    for (int p = tid; p < seq; p += kDecThreads) pt[(p & 7) * pcs + (p >> 3)] = fmul(el[p], inv);
+}
+
+// P.V chains of one lane j: workgroup (kv head g, 64-dimension part, j),
+// wavefront w = query head g*r + w, lane = dimension.  p[8c + j] is the same
+// for the whole wavefront (scalar loads); V rows 8c + j (256 bytes of the
+// part) stream through an LDS ring of kPvSlots slots of kPvRows rows, every
+// wavefront issuing 16/r of each slot's 16 DMA instructions.
+template <int HD, int R>
+__global__ __launch_bounds__(64 * R) void k_attn_pv_j(const float* __restrict__ vc, const StepState* __restrict__ st,
+                                                      int n_heads, int n_kv_heads, int sc_ld,
+                                                      float* __restrict__ scratch) {
+    extern __shared__ __align__(16) float ring[];   // [kPvSlots][kPvRows][64] V, then [kPvSlots][R][64] p
+    static_assert(kPvRows == 64 && kPvSlots == 8 && 16 % R == 0, "one p per lane and slot");
+    constexpr int NP = HD / 64;
+    constexpr int DPW = 16 / R + 1;   // DMA instructions per wavefront and slot: V rows, then p
+    const int g = blockIdx.x / NP, part = blockIdx.x % NP, j = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = g * R + wave;
+    const int kv_dim = n_kv_heads * HD;
+    const int seq = st->pos + 1, n_chunks = seq / 8;
+    const int pcs = sc_ld / 8;
+    const float* __restrict__ ph = scratch + (size_t)n_heads * sc_ld + ((size_t)h * 8 + j) * pcs;
+    const float* __restrict__ vcol = vc + (size_t)g * HD + part * 64;
+    float* __restrict__ pring = ring + kPvSlots * kPvRows * 64;
+    const int n_slots = (n_chunks + kPvRows - 1) / kPvRows;
+    // slot sl: V rows c = sl*kPvRows + 4*k + (lane >> 4), k = wave + R*i, 16-byte
+    // piece lane & 15; p of chunk sl*kPvRows + lane for this wavefront's head
+    auto dma = [&](int sl) {
+        float* dst = ring + (sl % kPvSlots) * kPvRows * 64;
+#pragma unroll
+        for (int i = 0; i < 16 / R; i++) {
+            const int k = wave + R * i;
+            const int c = min(sl * kPvRows + 4 * k + (lane >> 4), n_chunks - 1);
+            __builtin_amdgcn_global_load_lds(vcol + (size_t)(8 * c + j) * kv_dim + (lane & 15) * 4,
+                                             dst + k * 4 * 64, 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(ph + min(sl * kPvRows + lane, n_chunks - 1),
+                                         pring + ((sl % kPvSlots) * R + wave) * 64, 4, 0, 0);
+    };
+    for (int sl = 0; sl < n_slots && sl < kPvSlots; sl++) dma(sl);
+    float acc = 0.0f;
+    for (int sl = 0; sl < n_slots; sl++) {
+        wait_vm_slots<DPW>(min(kPvSlots - 1, n_slots - 1 - sl));
+        lds_barrier();   // every wavefront's DMA of slot sl
+        const float* tile = ring + (sl % kPvSlots) * kPvRows * 64;
+        const float* prow = pring + ((sl % kPvSlots) * R + wave) * 64;
+        const int steps = min(kPvRows, n_chunks - sl * kPvRows);
+        if (steps == kPvRows) {
+            // groups of 8 steps: the next group's V (4 two-row reads) and p
+            // (2 broadcast reads) are issued before this group's 16 VALU ops,
+            // so each LDS latency hides under the previous group.  The reads
+            // are inline assembly with explicit waits: the compiler counts
+            // the LDS DMA above as a pending flat access and would otherwise
+            // wait for every LDS read at each use.
+            const unsigned va = lds_addr(tile + lane), pa = lds_addr(prow);
+            vf2 vr[2][4];
+            vf4 pr[2][2];
+#define YL_PV_LOAD(gi, b)                                                                                       \
+            vr[b][0] = lds_read2st64<8 * (gi)>(va); vr[b][1] = lds_read2st64<8 * (gi) + 2>(va);                 \
+            vr[b][2] = lds_read2st64<8 * (gi) + 4>(va); vr[b][3] = lds_read2st64<8 * (gi) + 6>(va);             \
+            pr[b][0] = lds_read_b128<32 * (gi)>(pa); pr[b][1] = lds_read_b128<32 * (gi) + 16>(pa);
+#define YL_PV_STEP(gi, n)                                                                                       \
+            {                                                                                                   \
+                constexpr int b = (gi) & 1;                                                                     \
+                lgkm_wait_tie<n>(vr[b][0], vr[b][1], vr[b][2], vr[b][3], pr[b][0], pr[b][1]);                   \
+                _Pragma("unroll") for (int k = 0; k < 8; k++)                                                   \
+                    acc = fadd(acc, fmul(pr[b][k >> 2][k & 3], vr[b][k >> 1][k & 1]));                          \
+            }
+            YL_PV_LOAD(0, 0)
+            YL_PV_LOAD(1, 1) YL_PV_STEP(0, 6)
+            YL_PV_LOAD(2, 0) YL_PV_STEP(1, 6)
+            YL_PV_LOAD(3, 1) YL_PV_STEP(2, 6)
+            YL_PV_LOAD(4, 0) YL_PV_STEP(3, 6)
+            YL_PV_LOAD(5, 1) YL_PV_STEP(4, 6)
+            YL_PV_LOAD(6, 0) YL_PV_STEP(5, 6)
+            YL_PV_LOAD(7, 1) YL_PV_STEP(6, 6)
+            YL_PV_STEP(7, 0)
+#undef YL_PV_LOAD
+#undef YL_PV_STEP
+            static_assert(kPvRows == 64, "8 groups of 8 rows");
+        } else {
+            for (int i = 0; i < steps; i++) acc = fadd(acc, fmul(prow[i], tile[i * 64 + lane]));
+        }
+        if (sl + kPvSlots < n_slots) {
+            lds_barrier();   // slot consumed before it is refilled
+            dma(sl + kPvSlots);
+        }
+    }
+    float* __restrict__ lp = scratch + (size_t)n_heads * sc_ld * 2;
+    lp[((size_t)h * HD + part * 64 + lane) * 8 + j] = acc;
+}
+
+// out[d] = reduce_add8(lane partials) + the seq % 8 tail in order, then the
+// 32-group quantization of the output projection's input.
+template <int QF, int HD>
+__global__ __launch_bounds__(HD) void k_attn_pv_out(const float* __restrict__ vc, const StepState* __restrict__ st,
+                                                    int n_heads, int n_kv_heads, int sc_ld,
+                                                    const float* __restrict__ scratch, int8_t* __restrict__ aq,
+                                                    float* __restrict__ as, float* __restrict__ att_f32) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int kvh = h / (n_heads / n_kv_heads), kv_dim = n_kv_heads * HD;
+    const int seq = st->pos + 1, n_chunks = seq / 8, pcs = sc_ld / 8;
+    const float* __restrict__ lp = scratch + (size_t)n_heads * sc_ld * 2 + ((size_t)h * HD + d) * 8;
+    float lj[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) lj[jj] = lp[jj];
+    float out = reduce_add8(lj);
+    const float* __restrict__ pt = scratch + (size_t)n_heads * sc_ld + (size_t)h * 8 * pcs;
+    for (int i = 0; n_chunks * 8 + i < seq; i++)
+        out = fadd(out, fmul(pt[i * pcs + n_chunks], vc[(size_t)(n_chunks * 8 + i) * kv_dim + kvh * HD + d]));
+    const size_t col = (size_t)h * HD + d;
+    if (att_f32) att_f32[col] = out;
+    if constexpr (QF >= 0) {
+        float am = fabsf(out);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+        am = fmaxf(am, 0.0f);
+        const float sc = group_scale<QF>(am);
+        aq[col] = (int8_t)quant_one<QF>(out, sc);
+        if ((d & 31) == 0) as[col / kGroup] = sc;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prompt batches: one workgroup per (query head, token); seq_len = pos +
 // batch, the token's own position pos + t, later positions masked to -1e10.
 // LDS: scores seq_len | q head_size | partials 8*head_size | out head_size.
@@ -596,15 +834,19 @@ bool attn_decode_split(int max_seq) { return max_seq > kAttnSplitSeq; }
 bool attn_decode_fits(int max_seq) {
     return attn_v_tiles(max_seq) >= 2 && (!attn_decode_split(max_seq) || max_seq <= kLongQuads * 4 * kDecThreads);
 }
-static int attn_scores_ld(int max_seq) { return (max_seq + 63) & ~63; }
+static int attn_scores_ld(int max_seq) { return (max_seq + 127) & ~127; }
+// scores [n_heads][sc_ld], p [n_heads][8][sc_ld / 8], lane partials
+// [n_heads][128][8]
 size_t attn_scores_bytes(int n_heads, int max_seq) {
-    return attn_decode_split(max_seq) ? (size_t)n_heads * attn_scores_ld(max_seq) * sizeof(float) : 0;
+    return attn_decode_split(max_seq)
+               ? (size_t)n_heads * (2 * (size_t)attn_scores_ld(max_seq) + 128 * 8) * sizeof(float)
+               : 0;
 }
 
 template <class K>
 static hipError_t opt_in_lds(K* kern, size_t smem) {
-    if (smem <= 65536) return hipSuccess;
-    // more than the default 64 KiB of LDS
+    if (smem <= 60 * 1024) return hipSuccess;
+    // more than the default 64 KiB of LDS with the static part
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)smem);
 }
@@ -628,6 +870,21 @@ static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const f
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((k_attn_scores<HD>), dim3(n_kv_heads, (max_seq + kScoreRows - 1) / kScoreRows),
                            dim3(kDecThreads), smem_s, s, sq, kc, st, n_heads, n_kv_heads, scale, kv_ld, sc, sc_ld);
+        if constexpr (HD >= 64) if (r == 2 || r == 4 || r == 8) {
+            // softmax, P.V by lane j, output
+            const size_t smem_e = (size_t)sc_ld * sizeof(float);
+            const size_t smem_r = (size_t)kPvSlots * (kPvRows + r) * 64 * sizeof(float);
+            auto pv = r == 2 ? &k_attn_pv_j<HD, 2> : r == 4 ? &k_attn_pv_j<HD, 4> : &k_attn_pv_j<HD, 8>;
+            e = opt_in_lds(&k_attn_softmax, smem_e);
+            if (e == hipSuccess) e = opt_in_lds(pv, smem_r);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(kDecThreads), smem_e, s, st, sc_ld, n_heads, sc);
+            hipLaunchKernelGGL(pv, dim3(n_kv_heads * (HD / 64), 8), dim3(64 * r), smem_r, s, vc, st, n_heads,
+                               n_kv_heads, sc_ld, sc);
+            hipLaunchKernelGGL((k_attn_pv_out<QF, HD>), dim3(n_heads), dim3(HD), 0, s, vc, st, n_heads, n_kv_heads,
+                               sc_ld, sc, aq, as, att_f32);
+            return hipGetLastError();
+        }
         hipLaunchKernelGGL((k_attn_decode<QF, HD, true>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
                            n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, sc, sc_ld);
         return hipGetLastError();

@@ -18,6 +18,7 @@ constexpr int kGroup = 32;        // block size of Q8_0/Q4_0 (transformer_llama_
 // Native 4-float vector for register arrays: copies of HIP's float4 (a
 // struct) lower to memcpy, which can keep an array out of registers.
 typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef float vf2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float fadd(float a, float b) { return a + b; }
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }

@@ -41,7 +41,7 @@ def trace(path):
     by = collections.defaultdict(list)
     for r in rows:
         name = r["Kernel_Name"]
-        kind = ("decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in name or "k_attn_scores" in name
+        kind = ("decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in name or "k_attn_scores" in name or "k_attn_pv_j" in name
                 else "prompt")
         key = (kind, _short(r["Kernel_Name"]), r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"],
                r["VGPR_Count"], r["LDS_Block_Size"], r["Scratch_Size"])
