@@ -485,60 +485,6 @@ constexpr int kPvSlots = 8;     // slots in flight
 
 // Waits until at most n of this wavefront's vector memory operations are
 // in flight (n < 64; the immediate must be a constant).
-// 32-bit LDS offset of a pointer into shared memory
-__device__ __forceinline__ unsigned lds_addr(const float* p) {
-    return (unsigned)(size_t)(const __attribute__((address_space(3))) float*)p;
-}
-
-// rows O and O + 1 (64 floats apart) at LDS offset a, untracked by the
-// compiler's waits: the caller waits with lgkm_wait_tie before the use
-template <int O>
-__device__ __forceinline__ vf2 lds_read2st64(unsigned a) {
-    static_assert(O >= 0 && O + 1 < 256, "offset field");
-    vf2 r;
-    asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(r) : "v"(a), "n"(O), "n"(O + 1) : "memory");
-    return r;
-}
-
-// 16 bytes at LDS offset a + O (a broadcast when a is uniform), untracked
-template <int O>
-__device__ __forceinline__ vf4 lds_read_b128(unsigned a) {
-    static_assert(O >= 0 && O < 65536, "offset field");
-    vf4 r;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(O) : "memory");
-    return r;
-}
-
-// s_waitcnt lgkmcnt(N), tied to the registers it makes valid so that no use
-// of them is scheduled above it
-template <int N>
-__device__ __forceinline__ void lgkm_wait_tie(vf2& a, vf2& b, vf2& c, vf2& d, vf4& e, vf4& f) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt field");
-    asm volatile("s_waitcnt lgkmcnt(%6)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f) : "n"(N) : "memory");
-}
-
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
-}
-
-// vmcnt <= k * D for a run-time k in [0, 7]
-template <int D>
-__device__ __forceinline__ void wait_vm_slots(int k) {
-    switch (k) {
-    case 0: wait_vm<0>(); break;
-    case 1: wait_vm<D>(); break;
-    case 2: wait_vm<2 * D>(); break;
-    case 3: wait_vm<3 * D>(); break;
-    case 4: wait_vm<4 * D>(); break;
-    case 5: wait_vm<5 * D>(); break;
-    case 6: wait_vm<6 * D>(); break;
-    default: wait_vm<7 * D>(); break;
-    }
-}
-
 // Softmax of one head: max from -1e10, e = exp(score - max) into LDS, the
 // serial sum (one lane up to kWaveSumSeq positions, one wavefront beyond),
 // p = e * (1 / sum) written transposed for the P.V kernel.
