@@ -228,7 +228,7 @@ def test_rope(gpu, oracle, hd, nh, nkv, theta, pos, batch):
 
 
 @pytest.mark.parametrize("batch,start,nh,nkv,hd", [(1, 0, 4, 2, 64), (1, 700, 32, 8, 64), (7, 13, 9, 3, 64),
-                                                   (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128),
+                                                   (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128), (1, 4999, 8, 4, 64), (1, 6000, 16, 2, 128), (1, 8191, 32, 8, 128),
                                                    (1, 3000, 9, 3, 64), (1, 2100, 2, 2, 32), (1, 5119, 8, 8, 64),
                                                    (64, 0, 4, 2, 64), (100, 37, 8, 2, 128), (130, 0, 9, 3, 64),
                                                    (70, 5, 2, 2, 32), (257, 300, 4, 1, 64)])
