@@ -64,7 +64,8 @@ float yo_f16_to_f32(uint16_t h) {
 
 /* exp evaluated in binary64 and rounded once to binary32.
  * x*log2(e) -> k (nearest), r = (x - k*ln2_hi) - k*ln2_lo with the fdlibm
- * split of ln2 (e_exp.c), e^r by a degree-13 Taylor polynomial (Horner),
+ * split of ln2 (e_exp.c), e^r by a degree-13 Taylor polynomial (Horner, one
+ * fused multiply-add per degree, like the device's evaluation),
  * then scaled by 2^k.  Stands in for f32::exp (forward.rs:358) and
  * wide::f32x8::exp (forward.rs:230). */
 float yo_expf(float xf) {
@@ -78,19 +79,19 @@ float yo_expf(float xf) {
     double kd = nearbyint(x * log2e);
     double r = (x - kd * ln2_hi) - kd * ln2_lo;
     double p = 0x1.6124613a86d09p-33;          /* 1/13! */
-    p = p * r + 0x1.1eed8eff8d898p-29;         /* 1/12! */
-    p = p * r + 0x1.ae64567f544e4p-26;         /* 1/11! */
-    p = p * r + 0x1.27e4fb7789f5cp-22;         /* 1/10! */
-    p = p * r + 0x1.71de3a556c734p-19;         /* 1/9!  */
-    p = p * r + 0x1.a01a01a01a01ap-16;         /* 1/8!  */
-    p = p * r + 0x1.a01a01a01a01ap-13;         /* 1/7!  */
-    p = p * r + 0x1.6c16c16c16c17p-10;         /* 1/6!  */
-    p = p * r + 0x1.1111111111111p-7;          /* 1/5!  */
-    p = p * r + 0x1.5555555555555p-5;          /* 1/4!  */
-    p = p * r + 0x1.5555555555555p-3;          /* 1/3!  */
-    p = p * r + 0x1.0000000000000p-1;          /* 1/2!  */
-    p = p * r + 1.0;
-    p = p * r + 1.0;
+    p = fma(p, r, 0x1.1eed8eff8d898p-29);         /* 1/12! */
+    p = fma(p, r, 0x1.ae64567f544e4p-26);         /* 1/11! */
+    p = fma(p, r, 0x1.27e4fb7789f5cp-22);         /* 1/10! */
+    p = fma(p, r, 0x1.71de3a556c734p-19);         /* 1/9!  */
+    p = fma(p, r, 0x1.a01a01a01a01ap-16);         /* 1/8!  */
+    p = fma(p, r, 0x1.a01a01a01a01ap-13);         /* 1/7!  */
+    p = fma(p, r, 0x1.6c16c16c16c17p-10);         /* 1/6!  */
+    p = fma(p, r, 0x1.1111111111111p-7);          /* 1/5!  */
+    p = fma(p, r, 0x1.5555555555555p-5);          /* 1/4!  */
+    p = fma(p, r, 0x1.5555555555555p-3);          /* 1/3!  */
+    p = fma(p, r, 0x1.0000000000000p-1);          /* 1/2!  */
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
     return (float)ldexp(p, (int)kd);
 }
 

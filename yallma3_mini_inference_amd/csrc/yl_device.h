@@ -40,7 +40,8 @@ __device__ __forceinline__ float reduce_add8(const float l[8]) {
 
 // exp evaluated in binary64, rounded once to binary32: x*log2(e) -> k
 // (nearest), r = (x - k*ln2_hi) - k*ln2_lo with the fdlibm split of ln2,
-// e^r by the degree-13 Taylor polynomial (Horner), scaled by 2^k.  It is the
+// e^r by the degree-13 Taylor polynomial (Horner, one fused multiply-add per
+// degree, as in the oracle), scaled by 2^k.  It is the
 // correctly rounded expf except with probability ~1e-9 per input; it stands
 // in for f32::exp in the softmax (forward.rs:358) and wide::f32x8::exp in
 // SwiGLU (forward.rs:230).
@@ -55,19 +56,19 @@ __device__ __forceinline__ float expf_rn(float xf) {
     const double kd = __builtin_rint(x * log2e);
     const double r = (x - kd * ln2_hi) - kd * ln2_lo;
     double p = 0x1.6124613a86d09p-33;
-    p = p * r + 0x1.1eed8eff8d898p-29;
-    p = p * r + 0x1.ae64567f544e4p-26;
-    p = p * r + 0x1.27e4fb7789f5cp-22;
-    p = p * r + 0x1.71de3a556c734p-19;
-    p = p * r + 0x1.a01a01a01a01ap-16;
-    p = p * r + 0x1.a01a01a01a01ap-13;
-    p = p * r + 0x1.6c16c16c16c17p-10;
-    p = p * r + 0x1.1111111111111p-7;
-    p = p * r + 0x1.5555555555555p-5;
-    p = p * r + 0x1.5555555555555p-3;
-    p = p * r + 0x1.0000000000000p-1;
-    p = p * r + 1.0;
-    p = p * r + 1.0;
+    p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
+    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
+    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
+    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
+    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
+    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
+    p = __builtin_fma(p, r, 0x1.1111111111111p-7);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-5);
+    p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+    p = __builtin_fma(p, r, 0x1.0000000000000p-1);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
     return (float)__builtin_amdgcn_ldexp(p, (int)kd);
 }
 
