@@ -196,21 +196,30 @@ __global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__
         }
     }
     __syncthreads();
-    // 16 entries per thread: position pp = idx / 64, row r = idx % 64
-    float v[16];
+    // 4 positions x 4 consecutive rows per thread, as 16-byte accesses:
+    // position pp = tid / 16 + 16k, rows 4 * (tid % 16) + 0..3
+    const int r4 = 4 * (tid & 15);
+    vf4 v[4];
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int idx = tid + 256 * k, pp = idx >> 6, r = idx & 63;
-        const int p = min(p0 + pp, seq - 1);
-        v[k] = S.sc[((size_t)h * seq_ld + p) * Bp + row0 + r];
+    for (int k = 0; k < 4; k++) {
+        const int p = min(p0 + (tid >> 4) + 16 * k, seq - 1);
+        v[k] = *reinterpret_cast<const vf4*>(S.sc + ((size_t)h * seq_ld + p) * Bp + row0 + r4);
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int idx = tid + 256 * k, pp = idx >> 6, r = idx & 63;
-        const int p = p0 + pp, t = row0 + r;
-        const bool live = p < seq && t < batch && p <= pos0 + t;
-        const float e = expf_rn(v[k] - mxl[r]);
-        if (live) S.sc[((size_t)h * seq_ld + p) * Bp + t] = e;
+    for (int k = 0; k < 4; k++) {
+        const int p = p0 + (tid >> 4) + 16 * k, t = row0 + r4;
+        vf4 e;
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = expf_rn(v[k][i] - mxl[r4 + i]);
+        float* dst = S.sc + ((size_t)h * seq_ld + p) * Bp + t;
+        // live: p < seq, row < batch and p <= pos0 + row (rising with the row)
+        if (p < seq && t + 3 < batch && p <= pos0 + t) {
+            *reinterpret_cast<vf4*>(dst) = e;
+        } else if (p < seq) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (t + i < batch && p <= pos0 + t + i) dst[i] = e[i];
+        }
     }
 }
 
