@@ -107,12 +107,9 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
     }
     __syncthreads();
     const int ty = tid >> 4, tx = tid & 15;
-    float A[4][4], Bh[4][4];
-    // one lane partial at a time (unrolled, the compiler would hoist every
-    // partial's LDS reads and run out of registers)
-#pragma unroll 1
-    for (int j = 0; j < 8; j++) {
-        float l[4][4];
+    float A[4][4], Bh[4][4], l[4][4];
+    // lane partial j of the 4 x 4 pairs
+    auto partial = [&](int j) {
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -126,15 +123,36 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
 #pragma unroll
                 for (int b = 0; b < 4; b++) l[a][b] = fadd(l[a][b], fmul(qv[a], kv[b]));
         }
+    };
+    // reduce_add8: A = ((l0 + l1) + l2) + l3, Bh = ((l4 + l5) + l6) + l7.
+    // One partial at a time (unrolled, the compiler would hoist every
+    // partial's LDS reads and run out of registers); each fold is a loop of
+    // its own so that no per-element branch on j remains.
+    partial(0);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) A[a][b] = l[a][b];
+#pragma unroll 1
+    for (int j = 1; j < 4; j++) {
+        partial(j);
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                if (j == 0) A[a][b] = l[a][b];
-                else if (j < 4) A[a][b] = fadd(A[a][b], l[a][b]);
-                else if (j == 4) Bh[a][b] = l[a][b];
-                else Bh[a][b] = fadd(Bh[a][b], l[a][b]);
-            }
+            for (int b = 0; b < 4; b++) A[a][b] = fadd(A[a][b], l[a][b]);
+    }
+    partial(4);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) Bh[a][b] = l[a][b];
+#pragma unroll 1
+    for (int j = 5; j < 8; j++) {
+        partial(j);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) Bh[a][b] = fadd(Bh[a][b], l[a][b]);
     }
     float rmax[4] = {-1e10f, -1e10f, -1e10f, -1e10f};
 #pragma unroll
