@@ -396,14 +396,30 @@ __global__ __launch_bounds__(HD * 4) void k_pattn_pv(const float* __restrict__ v
         if (q0 + kPT < 8 * end_c) load_tile(q0 + kPT);
         const int nc = min(kPT / 8, end_c - q0 / 8);
         for (int c = 0; c < nc; c++) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const vf4 pv = *reinterpret_cast<const vf4*>(pT + (8 * c + j) * kPTS + 4 * ty);
-                const vf4 vv = *reinterpret_cast<const vf4*>(vT + (8 * c + j) * VS + 4 * tx);
+            // lane j's p and V reads alternate between two register sets, so
+            // that lane j + 1's reads are in flight while lane j's 32 ops run
+            auto rd = [&](int j, vf4& pv, vf4& vv) {
+                pv = *reinterpret_cast<const vf4*>(pT + (8 * c + j) * kPTS + 4 * ty);
+                vv = *reinterpret_cast<const vf4*>(vT + (8 * c + j) * VS + 4 * tx);
+            };
+            auto step = [&](int j, const vf4& pv, const vf4& vv) {
 #pragma unroll
                 for (int a = 0; a < 4; a++)
 #pragma unroll
                     for (int b = 0; b < 4; b++) acc[a][b][j] = fadd(acc[a][b][j], fmul(pv[a], vv[b]));
+            };
+            vf4 p0, v0, p1, v1;
+            rd(0, p0, v0);
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                rd(j + 1, p1, v1);
+                __builtin_amdgcn_sched_barrier(0);
+                step(j, p0, v0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (j + 2 < 8) rd(j + 2, p0, v0);
+                __builtin_amdgcn_sched_barrier(0);
+                step(j + 1, p1, v1);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         lds_barrier();
