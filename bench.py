@@ -29,6 +29,12 @@ Also reported (same JSON line):
   cpu_baseline  the oracle (C restatement of the reference's Rayon CPU path,
                 OpenMP) decoding a bounded sample of the same workload on this
                 host's cores.
+  parity        outside the timed region: the HIP path decodes the same
+                sample (same random-filled KV cache, same first token) one
+                forward_x at a time, and every step's logits and greedy token
+                are compared with the oracle's: bit-identical logits, the
+                largest relative logit difference (bar 1e-3) and whether the
+                greedy tokens are identical.
 """
 import argparse
 import json
@@ -53,30 +59,79 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(path, prompt_len, seconds):
-    """Oracle decode at positions prompt_len.. with a random-filled KV cache."""
+SAMPLE_STEPS = 64   # decode steps of the CPU-baseline and parity sample
+
+
+def sample_kv(shape, prompt_len):
+    """The sample's KV cache below prompt_len: N(0, 1), seed 0 (keys, values)."""
+    import numpy as np
+    rng = np.random.default_rng(0)
+    kv_dim = shape.n_kv_heads * shape.head_size
+    dims = (shape.n_layers, prompt_len, kv_dim)
+    return rng.standard_normal(dims, dtype=np.float32), rng.standard_normal(dims, dtype=np.float32)
+
+
+def gpu_sample(model, kv, prompt_len):
+    """The HIP path on the sample: forward_x one token at a time from token 1
+    at prompt_len, greedy; returns (per-step logits, tokens)."""
+    import numpy as np
+    import yallma3_mini_inference_amd as Y
+    sess = model.create_session()
+    sess.upload_kv(*kv)
+    tok, logits, toks = 1, [], []
+    for i in range(SAMPLE_STEPS):
+        lg = model.forward_x([tok], prompt_len + i, sess)
+        tok = int(np.argmax(lg))
+        logits.append(lg)
+        toks.append(tok)
+    sess.close()
+    Y.lib().yl_synchronize()
+    return logits, toks
+
+
+def cpu_baseline(path, prompt_len, seconds, kv):
+    """Oracle decode at positions prompt_len.. with the sample's KV cache;
+    returns the baseline record and the per-step logits and tokens."""
     import numpy as np
     from oracle import oracle as O
     t0 = time.perf_counter()
     m = O.Model(path)
     s = m.create_session()
-    rng = np.random.default_rng(0)
-    kc, vc = s.key_cache(), s.value_cache()
-    kc[:, :prompt_len] = rng.normal(0, 1, kc[:, :prompt_len].shape).astype(np.float32)
-    vc[:, :prompt_len] = rng.normal(0, 1, vc[:, :prompt_len].shape).astype(np.float32)
+    s.key_cache()[:, :prompt_len] = kv[0]
+    s.value_cache()[:, :prompt_len] = kv[1]
     log(f"cpu baseline: oracle load {time.perf_counter() - t0:.1f}s, threads {O.num_threads()}")
     tok, pos, n = 1, prompt_len, 0
+    logits, toks = [], []
     t0 = time.perf_counter()
     while True:
-        tok = O.argmax(m.forward_x([tok], pos, s))
+        lo = m.forward_x([tok], pos, s)
+        tok = O.argmax(lo)
+        logits.append(lo)
+        toks.append(tok)
         pos += 1
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 64:
+        if el >= seconds or n >= SAMPLE_STEPS:
             break
-    return {"value": n / el, "unit": "tok/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"{n} greedy decode steps at positions {prompt_len}..{prompt_len + n - 1} of the same "
-                      f"model, KV cache below {prompt_len} random-filled, {el:.1f}s"}
+    rec = {"value": n / el, "unit": "tok/s", "cores": O.num_threads(), "kind": "port",
+           "sample": f"{n} greedy decode steps at positions {prompt_len}..{prompt_len + n - 1} of the same "
+                     f"model, KV cache below {prompt_len} random-filled (N(0,1), seed 0), {el:.1f}s"}
+    return rec, logits, toks
+
+
+def parity_record(gpu, cpu):
+    """Step-by-step comparison of the HIP path's sample with the oracle's."""
+    import numpy as np
+    (gl, gt), (cl, ct) = gpu, cpu
+    n = len(cl)
+    worst, bits = 0.0, True
+    for a, b in zip(gl[:n], cl):
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        worst = max(worst, float(np.max(np.abs(a64 - b64)) / max(float(np.max(np.abs(b64))), 1e-30)))
+        bits = bits and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+    return {"steps_compared": n, "tokens_identical": list(gt[:n]) == list(ct), "logits_bit_identical": bits,
+            "max_rel_logit_diff": worst, "tolerance": 1e-3,
+            "sample": "the cpu_baseline sample, decoded on the GPU one forward_x per step"}
 
 
 MFMA_INT8_PEAK_TOPS = 5000.0
@@ -356,9 +411,13 @@ def main():
     }
     if not args.no_cpu_baseline:
         sess.close()
+        kv = sample_kv(model.shape, args.prompt)
+        gpu = gpu_sample(model, kv, args.prompt)
         model.close()
-        result["cpu_baseline"] = cpu_baseline(path, args.prompt, args.cpu_seconds)
-        log(f"cpu baseline {result['cpu_baseline']['value']:.3f} tok/s")
+        rec, cl, ct = cpu_baseline(path, args.prompt, args.cpu_seconds, kv)
+        result["cpu_baseline"] = rec
+        result["parity"] = parity_record(gpu, (cl, ct))
+        log(f"cpu baseline {rec['value']:.3f} tok/s; parity {result['parity']}")
     print(json.dumps(result), flush=True)
 
 

@@ -26,8 +26,8 @@
  *   yl_rope_gguf           util::rope_gguf, util.rs:653-718
  *   yl_attention           forward.rs fused_attention, forward.rs:299-400
  *   yl_swiglu_quantize     forward.rs:220-237 (+ quantize)
- *   yl_logits_argmax       forward.rs:261-279 + Sampler::sample_argmax,
- *                          sampler.rs:67-79
+ *   (greedy argmax, Sampler::sample_argmax sampler.rs:67-79, is the
+ *    `argmax` output of yl_forward_x and the chaining of yl_generate_greedy)
  *
  * Memory: functions documented "device" take pointers from yl_malloc (or
  * any HIP device allocation on the current device); "host" pointers are
@@ -64,6 +64,10 @@ const char *yl_last_error(void);
 /* WeightFormat, weight_type.rs:17-22 */
 typedef enum { YL_Q8_0 = 0, YL_Q4_0 = 1, YL_F16 = 2 } yl_format;
 
+/* Model and session handles (defined by the library). */
+typedef struct yl_model yl_model;
+typedef struct yl_session yl_session;
+
 /* ------------------------------------------------ product ABI (unchanged) */
 /* lib.rs:135-152: loads a model (".gguf") into the process-wide current
  * transformer, replacing the previous one.  false on NULL, unknown
@@ -75,6 +79,11 @@ bool load_transformer_ffi(const char *model_path);
 char *infer_ffi(const char *prompt);
 /* Releases a string returned by infer_ffi; NULL is ignored. */
 void free_string(char *s);
+/* The model load_transformer_ffi installed (the reference's `static mut`
+ * current transformer, lib.rs:135-152), or NULL before the first successful
+ * load; owned by the library and freed by the next successful load.  Lets a
+ * host that loads through the product ABI reach the model API above. */
+const yl_model *yl_ffi_model(void);
 
 /* ------------------------------------------------------- device helpers */
 yl_status yl_device_count(int *count);
@@ -159,8 +168,6 @@ yl_status yl_swiglu_quantize(const float *gate, const float *up, size_t hidden, 
                              float *h, int32_t qfmt, int8_t *q, float *scale, void *stream);
 
 /* --------------------------------------------------- model and session */
-typedef struct yl_model yl_model;
-typedef struct yl_session yl_session;
 
 typedef struct {                 /* TransformerShape, base_transformer.rs:25-44 */
     uint32_t dimension, hidden_dimension, n_heads, head_size, n_kv_heads, vocab_size;
@@ -232,7 +239,9 @@ yl_status yl_generate_greedy(const yl_model *m, yl_session *s, uint32_t token, u
  * prologue), 4 = down projection, 5 = logits.  For batch >= 16 the
  * projections are the int8-MFMA GEMM alone (the row normalization before
  * it is not captured).  Returns the average launch time (us), the
- * algorithmic bytes one launch reads and writes (0 for attention) and the
+ * algorithmic bytes one launch reads and writes (attention: the keys and
+ * values of all start_pos + batch positions, the queries and the quantized
+ * output) and the
  * launches per step.  Leaves the session's KV cache at those positions, its
  * residual stream and its activations modified (the replays repeat the `+=`
  * steps): reset the session afterwards. */
@@ -248,8 +257,11 @@ yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt
 /* Probe of the one-wavefront serial sum behind the decode softmax
  * denominator (forward.rs:356-361): out[c] = ((0 + v[a]) + v[a+1]) + ... +
  * v[b-1] in f32 for a = offsets[c], b = offsets[c+1], values >= 0 (device
- * pointers; offsets holds cases + 1 entries). */
-yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, float *out);
+ * pointers; offsets holds cases + 1 entries).  segment 0 sums each case in
+ * one pass; segment k > 0 in consecutive pieces of k values, each piece
+ * continuing from the previous piece's sum (the long-context path). */
+yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, uint32_t segment,
+                                 float *out);
 
 /* ----------------------------------------------------- synthetic models */
 typedef struct {

@@ -115,9 +115,9 @@ def test_smollm2_shape_short(gpu, oracle, model_dir):
 
 
 def test_long_context_decode(gpu, oracle, model_dir):
-    """ctx 4096: decode steps take the scores kernel + the decode kernel, whose
-    softmax sum runs on one lane up to 2048 positions and on one wavefront
-    (rows of 64) beyond; the greedy graph replays the same kernels."""
+    """ctx 4096: decode steps take the single decode attention kernel, whose
+    softmax sum runs on one lane up to 2560 positions and on one wavefront
+    (super-rows of 512) beyond; the greedy graph replays the same kernel."""
     g, o, _ = _models(gpu, oracle, model_dir, "tiny_long")
     rng = np.random.default_rng(4096)
     toks = rng.integers(0, o.vocab, 2100).astype(np.uint32)

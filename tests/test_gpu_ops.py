@@ -119,7 +119,8 @@ def _gguf_q8_blocks(wf):
     return out.ravel(), q.ravel(), d.astype(np.float16).astype(np.float32)
 
 
-@pytest.mark.parametrize("batch,n,o", [(1, 2048, 2048), (1, 8192, 1024), (3, 576, 190), (2, 4096, 37)])
+@pytest.mark.parametrize("batch,n,o", [(1, 2048, 2048), (1, 8192, 1024), (3, 576, 190), (2, 4096, 37),
+                                       (1, 14336, 128)])
 def test_matmul_q8_parity(gpu, oracle, batch, n, o):
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul
     rng = np.random.default_rng(n + o)
@@ -133,7 +134,7 @@ def test_matmul_q8_parity(gpu, oracle, batch, n, o):
     assert_bits(out, ref)
 
 
-@pytest.mark.parametrize("batch,n,o", [(1, 2048, 512), (2, 8192, 256), (1, 576, 36)])
+@pytest.mark.parametrize("batch,n,o", [(1, 2048, 512), (2, 8192, 256), (1, 576, 36), (1, 14336, 256)])
 def test_matmul_q4_parity(gpu, oracle, batch, n, o):
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul
     rng = np.random.default_rng(7 * n + o)
@@ -294,8 +295,12 @@ def test_serial_sum_exact(gpu):
         for i in range(0, len(spots), 2):
             w[spots[i]] = spots[i + 1]
         segs.append(w)
-    got = ops.serial_sum_selftest(segs)
     ref = np.array([sequential(v) for v in segs], np.float32)
     nan = np.isnan(ref)
-    assert np.array_equal(np.isnan(got), nan)
-    assert_bits(got[~nan], ref[~nan])
+    # whole rows, and rows summed in pieces that continue from the previous
+    # piece's sum (the softmax of contexts longer than LDS holds): pieces of
+    # 700 (partial super-rows), 37 (inside the one-at-a-time prologue), 8192
+    for piece in (0, 700, 37, 8192):
+        got = ops.serial_sum_selftest(segs, piece)
+        assert np.array_equal(np.isnan(got), nan), piece
+        assert_bits(got[~nan], ref[~nan])

@@ -20,7 +20,7 @@ STATUS_NAMES = {
 
 # every symbol include/yallma3.h declares
 EXPORTS = [
-    "yl_last_error", "load_transformer_ffi", "infer_ffi", "free_string", "yl_device_count", "yl_malloc",
+    "yl_last_error", "load_transformer_ffi", "infer_ffi", "free_string", "yl_ffi_model", "yl_device_count", "yl_malloc",
     "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memcpy_d2d", "yl_matmul_bench", "yl_memset_d", "yl_synchronize", "yl_quantize",
     "yl_weight_upload", "yl_weight_upload_gguf", "yl_weight_free", "yl_weight_bytes", "yl_matmul",
     "yl_rmsnorm_quantize", "yl_rope_gguf", "yl_attention", "yl_swiglu_quantize", "yl_load",
@@ -81,6 +81,7 @@ def lib():
         "load_transformer_ffi": (C.c_bool, [C.c_char_p]),
         "infer_ffi": (vp, [C.c_char_p]),
         "free_string": (None, [vp]),
+        "yl_ffi_model": (vp, []),
         "yl_device_count": (st, [C.POINTER(C.c_int)]),
         "yl_malloc": (vp, [sz]),
         "yl_free": (None, [vp]),
@@ -122,7 +123,7 @@ def lib():
         "yl_profile_kernel": (st, [vp, vp, u32, u32, u32, st, u32, C.POINTER(C.c_double), C.POINTER(u64),
                                    C.POINTER(u32)]),
         "yl_math_selftest": (st, [vp, sz, vp, vp, vp, vp]),
-        "yl_serial_sum_selftest": (st, [vp, vp, sz, vp]),
+        "yl_serial_sum_selftest": (st, [vp, vp, sz, u32, vp]),
         "yl_write_synthetic_gguf": (st, [C.c_char_p, C.POINTER(SynthConfig)]),
         "yl_synthetic_normal": (st, [u64, u64, u64, sz, f32, vp]),
     }

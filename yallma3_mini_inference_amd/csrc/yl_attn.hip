@@ -535,6 +535,55 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_softmax(const StepState* _
     for (int p = tid; p < seq; p += kDecThreads) pt[(p & 7) * pcs + (p >> 3)] = fmul(el[p], inv);
 }
 
+// The same softmax for rows longer than LDS holds (contexts beyond 16384):
+// the max over the scores row in global memory, e = exp(score - max) back
+// into the row, the serial sum in segments of kSoftSeg values staged into
+// LDS (double-buffered: the next segment is copied while wavefront 0 sums the
+// current one, each segment continuing from the previous segment's sum),
+// then p = e * (1 / sum) transposed as above.
+constexpr int kSoftSeg = 6144;
+__global__ __launch_bounds__(kDecThreads) void k_attn_softmax_long(const StepState* __restrict__ st, int sc_ld,
+                                                                   int n_heads, float* __restrict__ scratch) {
+    extern __shared__ __align__(16) float seg[];   // [2][kSoftSeg]
+    __shared__ float red[16];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int seq = st->pos + 1;
+    float* __restrict__ sh = scratch + (size_t)h * sc_ld;
+    float* __restrict__ pt = scratch + (size_t)n_heads * sc_ld + (size_t)h * sc_ld;
+    const int pcs = sc_ld / 8;
+    float lmax = -1e10f;
+    for (int p = tid; p < seq; p += kDecThreads) lmax = fmaxf(lmax, sh[p]);
+    lmax = wave_max(lmax);
+    if ((tid & 63) == 0) red[tid >> 6] = lmax;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
+    for (int p = tid; p < seq; p += kDecThreads) sh[p] = expf_rn(sh[p] - mx);
+    __syncthreads();   // (the row's e values, written by every wavefront)
+    const int nseg = (seq + kSoftSeg - 1) / kSoftSeg;
+    auto stage = [&](int k) {
+        float* d = seg + (k & 1) * kSoftSeg;
+        const int b = k * kSoftSeg, n = min(kSoftSeg, seq - b);
+        for (int i = tid; i < n; i += kDecThreads) d[i] = sh[b + i];
+    };
+    stage(0);
+    __syncthreads();
+    float sum = 0.0f;
+    for (int k = 0; k < nseg; k++) {
+        if (k + 1 < nseg) stage(k + 1);
+        if (tid < 64) {
+            const float* d = seg + (k & 1) * kSoftSeg;
+            sum = wave_serial_sum(d, min(kSoftSeg, seq - k * kSoftSeg), sum);
+        }
+        __syncthreads();   // segment k summed and segment k + 1 staged
+    }
+    if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    __syncthreads();
+    const float inv = red[8];
+    for (int p = tid; p < seq; p += kDecThreads) pt[(p & 7) * pcs + (p >> 3)] = fmul(sh[p], inv);
+}
+
 // P.V chains of one lane j: workgroup (kv head g, 64-dimension part, j),
 // wavefront w = query head g*r + w, lane = dimension.  p[8c + j] is the same
 // for the whole wavefront (scalar loads); V rows 8c + j (256 bytes of the
@@ -754,10 +803,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
         quantize_head_output<QF>(outl, hd, aq, as, (size_t)t * (att_dim / kGroup) + ((size_t)h * hd) / kGroup);
 }
 
+static size_t attention_lds_bytes(int seq_len, int head_size) {
+    return ((size_t)((seq_len + 3) & ~3) + 10 * (size_t)head_size) * sizeof(float);
+}
+bool attention_row_fits(int seq_len, int head_size) { return attention_lds_bytes(seq_len, head_size) <= 60 * 1024; }
+
 hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
                             int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale, int qfmt,
                             int8_t* aq, float* as, float* att_f32, hipStream_t s) {
-    const size_t smem = ((size_t)((max_seq + 3) & ~3) + 10 * (size_t)head_size) * sizeof(float);
+    // max_seq: the seq_len of this call (LDS holds its score row)
+    if (!attention_row_fits(max_seq, head_size)) return hipErrorInvalidValue;
+    const size_t smem = attention_lds_bytes(max_seq, head_size);
     const dim3 grid(n_heads, batch);
     if (qfmt == kQ8)
         hipLaunchKernelGGL((k_attention<kQ8>), grid, dim3(kAttnThreads), smem, s, sq, kc, vc, st, batch, kv_ld,
@@ -777,8 +833,17 @@ size_t attn_decode_lds_bytes(int max_seq) { return attn_decode_lds_floats(max_se
 // contexts longer than this take the scores kernel + the decode kernel
 constexpr int kAttnSplitSeq = 4096;
 bool attn_decode_split(int max_seq) { return max_seq > kAttnSplitSeq; }
-bool attn_decode_fits(int max_seq) {
-    return attn_v_tiles(max_seq) >= 2 && (!attn_decode_split(max_seq) || max_seq <= kLongQuads * 4 * kDecThreads);
+// Head size 64 or 128 with 2, 4 or 8 query heads per kv head runs the
+// four-kernel path, whose softmax streams rows of any length; every other
+// layout keeps the scores row of the decode kernel in LDS (16384 positions).
+int attn_decode_limit(int n_heads, int n_kv_heads, int head_size) {
+    const int r = n_kv_heads > 0 ? n_heads / n_kv_heads : 0;
+    if ((head_size == 64 || head_size == 128) && (r == 2 || r == 4 || r == 8)) return 0x7fffffff;
+    return kLongQuads * 4 * kDecThreads;
+}
+bool attn_decode_fits(int max_seq, int n_heads, int n_kv_heads, int head_size) {
+    return attn_v_tiles(max_seq < kAttnSplitSeq ? max_seq : kAttnSplitSeq) >= 2 &&
+           max_seq <= attn_decode_limit(n_heads, n_kv_heads, head_size);
 }
 static int attn_scores_ld(int max_seq) { return (max_seq + 127) & ~127; }
 // scores [n_heads][sc_ld], p [n_heads][8][sc_ld / 8], lane partials
@@ -801,40 +866,49 @@ template <int QF, int HD>
 static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const float* vc, const StepState* st,
                                        int max_seq, int kv_ld, int n_heads, int n_kv_heads, float scale, int8_t* aq,
                                        float* as, float* att_f32, float* sc, hipStream_t s) {
-    const int n_vt = attn_v_tiles(max_seq);
-    if (n_vt < 2) return hipErrorInvalidValue;
-    const size_t smem = attn_decode_lds_bytes(max_seq);
     const dim3 grid(n_heads * (HD / kDecDims));
-    if (sc && attn_decode_split(max_seq)) {
-        if (max_seq > kLongQuads * 4 * kDecThreads) return hipErrorInvalidValue;
+    if (max_seq > attn_decode_limit(n_heads, n_kv_heads, HD)) return hipErrorInvalidValue;
+    if (attn_decode_split(max_seq)) {
+        if (!sc) return hipErrorInvalidValue;   // the scores scratch of long contexts
         const int r = n_heads / n_kv_heads;
         const size_t smem_s = (size_t)r * 8 * kScoreRows * sizeof(float);
         if (smem_s > kDecLdsBudget) return hipErrorInvalidValue;
         const int sc_ld = attn_scores_ld(max_seq);
         hipError_t e = opt_in_lds(&k_attn_scores<HD>, smem_s);
-        if (e == hipSuccess) e = opt_in_lds(&k_attn_decode<QF, HD, true>, smem);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((k_attn_scores<HD>), dim3(n_kv_heads, (max_seq + kScoreRows - 1) / kScoreRows),
                            dim3(kDecThreads), smem_s, s, sq, kc, st, n_heads, n_kv_heads, scale, kv_ld, sc, sc_ld);
         if constexpr (HD >= 64) if (r == 2 || r == 4 || r == 8) {
             // softmax, P.V by lane j, output
-            const size_t smem_e = (size_t)sc_ld * sizeof(float);
+            // (rows up to 16384 positions are held in LDS whole)
+            const bool long_row = max_seq > kLongQuads * 4 * kDecThreads;
+            const size_t smem_e = long_row ? 2 * (size_t)kSoftSeg * sizeof(float) : (size_t)sc_ld * sizeof(float);
             const size_t smem_r = (size_t)kPvSlots * (kPvRows + r) * 64 * sizeof(float);
             auto pv = r == 2 ? &k_attn_pv_j<HD, 2> : r == 4 ? &k_attn_pv_j<HD, 4> : &k_attn_pv_j<HD, 8>;
-            e = opt_in_lds(&k_attn_softmax, smem_e);
+            auto softmax = long_row ? &k_attn_softmax_long : &k_attn_softmax;
+            e = opt_in_lds(softmax, smem_e);
             if (e == hipSuccess) e = opt_in_lds(pv, smem_r);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL(k_attn_softmax, dim3(n_heads), dim3(kDecThreads), smem_e, s, st, sc_ld, n_heads, sc);
+            hipLaunchKernelGGL(softmax, dim3(n_heads), dim3(kDecThreads), smem_e, s, st, sc_ld, n_heads, sc);
             hipLaunchKernelGGL(pv, dim3(n_kv_heads * (HD / 64), 8), dim3(64 * r), smem_r, s, vc, st, n_heads,
                                n_kv_heads, sc_ld, sc);
             hipLaunchKernelGGL((k_attn_pv_out<QF, HD>), dim3(n_heads), dim3(HD), 0, s, vc, st, n_heads, n_kv_heads,
                                sc_ld, sc, aq, as, att_f32);
             return hipGetLastError();
         }
+        // other layouts: the decode kernel reads the scores row back into LDS
+        const int n_vt = attn_v_tiles(max_seq);
+        if (n_vt < 2) return hipErrorInvalidValue;
+        const size_t smem = attn_decode_lds_bytes(max_seq);
+        e = opt_in_lds(&k_attn_decode<QF, HD, true>, smem);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((k_attn_decode<QF, HD, true>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
                            n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, sc, sc_ld);
         return hipGetLastError();
     }
+    const int n_vt = attn_v_tiles(max_seq);
+    if (n_vt < 2) return hipErrorInvalidValue;
+    const size_t smem = attn_decode_lds_bytes(max_seq);
     const hipError_t e = opt_in_lds(&k_attn_decode<QF, HD, false>, smem);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_attn_decode<QF, HD, false>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,

@@ -272,12 +272,14 @@ __device__ __forceinline__ float serial_sum_nonfinite(Get get, int n, int start,
     return __ballot(nan) ? __builtin_nanf("") : s;
 }
 
+// `s0` is the running sum before v[0] (0 for a whole row; a long row can be
+// summed in segments, each continuing from the previous segment's result).
 template <int KV = 8, class Get>
-__device__ __forceinline__ float wave_serial_sum_at(Get get, int n) {
+__device__ __forceinline__ float wave_serial_sum_at(Get get, int n, float s0 = 0.0f) {
     const int lane = threadIdx.x & 63;
     const int np0 = n < kSerialSumPrologue ? n : kSerialSumPrologue;
     const float x0 = lane < np0 ? get(lane) : 0.0f;
-    float s = 0.0f;
+    float s = s0;
 #pragma unroll
     for (int i = 0; i < kSerialSumPrologue; i++)
         if (i < np0) s = fadd(s, lane_value(x0, i));
@@ -350,15 +352,18 @@ __device__ __forceinline__ float wave_serial_sum_at(Get get, int n) {
     if (!(s <= 0x1.fffffep127f)) return serial_sum_nonfinite(get, n, n, s);
     return s;
 }
-__device__ __forceinline__ float wave_serial_sum(const float* v, int n) {
-    return wave_serial_sum_at([v](int i) { return v[i]; }, n);
+__device__ __forceinline__ float wave_serial_sum(const float* v, int n, float s0 = 0.0f) {
+    return wave_serial_sum_at([v](int i) { return v[i]; }, n, s0);
 }
 
 // Orderable 64-bit argmax key: larger key = larger value, ties broken toward
 // the smaller index (Sampler::sample_argmax keeps the first maximum,
-// sampler.rs:67-79).  NaN maps to the smallest key so it never wins.
+// sampler.rs:67-79).  The reference starts from row 0 and replaces the
+// maximum only on `p > max`, so a NaN in row 0 is never replaced (the
+// result is 0) and a NaN elsewhere never wins: row 0's NaN takes the largest
+// key, any other NaN the smallest.
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-    if (v != v) return 0ull;
+    if (v != v) return idx == 0 ? ~0ull : 0ull;
     if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
     uint32_t u = __float_as_uint(v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);

@@ -110,21 +110,27 @@ hipError_t launch_transpose(const float* in, float* out, int rows, int cols, int
 hipError_t launch_rmsnorm(int qfmt, const float* x, const float* w, int dim, float eps, int batch,
                           float* xn, int8_t* xq, float* xs, hipStream_t s);
 hipError_t launch_embed(const EmbQ8& e, const uint32_t* tokens, int batch, float* x, hipStream_t s);
-// kc: keys [kv_dim][kv_ld] (transposed), vc: values [max_seq][kv_dim]
+// kc: keys [kv_dim][kv_ld] (transposed), vc: values [max_seq][kv_dim];
+// max_seq = the call's seq_len, which attention_row_fits() must accept
+bool attention_row_fits(int seq_len, int head_size);
 hipError_t launch_attention(const float* sq, const float* kc, const float* vc, const StepState* st,
                             int batch, int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size,
                             float scale, int qfmt, int8_t* aq, float* as, float* att_f32,
                             hipStream_t s);
 size_t attn_decode_lds_bytes(int max_seq);
-bool attn_decode_fits(int max_seq);   // LDS holds the decode kernel's row and >= 2 V tiles
+// The longest context one decode step attends over for this head layout,
+// and whether a context of max_seq positions is within it.
+int attn_decode_limit(int n_heads, int n_kv_heads, int head_size);
+bool attn_decode_fits(int max_seq, int n_heads, int n_kv_heads, int head_size);
 hipError_t launch_attn_decode(const float* sq, const float* kc, const float* vc, const StepState* st,
                               int max_seq, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
                               int qfmt, int8_t* aq, float* as, float* att_f32, float* sc, hipStream_t s);
 // sc: scratch for the scores of long contexts, attn_scores_bytes() bytes
 // (0: the context is short enough for the single decode kernel; sc may be null)
-// Prompt batches of 64 or more tokens: tiled attention over a scratch of
+// Prompt batches of 64 or more tokens, and shorter ones whose seq_len is
+// too long for k_attention's LDS row: tiled attention over a scratch of
 // prompt_attn_bytes(n_heads, seq_len, batch); seq_ld = pos + batch (host side)
-bool prompt_attn_applies(int batch);
+bool prompt_attn_applies(int batch, int seq_len, int head_size);
 size_t prompt_attn_bytes(int n_heads, int seq_ld, int batch);
 hipError_t launch_prompt_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
                                    int seq_ld, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
@@ -144,7 +150,8 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
 hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
                                 float* div_out, float* f16_out, hipStream_t s);
 
-hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, float* out, hipStream_t s);
+hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
+                                      hipStream_t s);
 
 // error reporting shared by the C ABI
 void set_error(const std::string& msg);

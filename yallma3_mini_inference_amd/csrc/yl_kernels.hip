@@ -154,12 +154,21 @@ __global__ void k_math_selftest(const float* __restrict__ x, int n, float* exp_o
     f16_out[i] = f16_to_f32((uint16_t)(i & 0xffff));
 }
 
-// One wavefront per case: the serial sum of v[offs[c] .. offs[c+1]).
+// One wavefront per case: the serial sum of v[offs[c] .. offs[c+1]), in one
+// call (seg 0) or in consecutive segments of seg values, each continuing
+// from the previous segment's sum.
 __global__ __launch_bounds__(64) void k_serial_sum_selftest(const float* __restrict__ v,
-                                                            const uint32_t* __restrict__ offs, float* out) {
+                                                            const uint32_t* __restrict__ offs, int seg, float* out) {
     const int c = blockIdx.x;
     const uint32_t a = offs[c], b = offs[c + 1];
-    const float s = wave_serial_sum(v + a, (int)(b - a));
+    const int n = (int)(b - a);
+    float s;
+    if (seg <= 0) {
+        s = wave_serial_sum(v + a, n);
+    } else {
+        s = 0.0f;
+        for (int i = 0; i < n; i += seg) s = wave_serial_sum(v + a + i, min(seg, n - i), s);
+    }
     if (threadIdx.x == 0) out[c] = s;
 }
 
@@ -228,9 +237,10 @@ hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sq
     return hipGetLastError();
 }
 
-hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, float* out, hipStream_t s) {
+hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
+                                      hipStream_t s) {
     if (cases <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_serial_sum_selftest, dim3(cases), dim3(64), 0, s, v, offs, out);
+    hipLaunchKernelGGL(k_serial_sum_selftest, dim3(cases), dim3(64), 0, s, v, offs, seg, out);
     return hipGetLastError();
 }
 

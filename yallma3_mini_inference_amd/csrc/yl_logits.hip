@@ -146,7 +146,9 @@ __global__ __launch_bounds__(512) void k_finalize(const unsigned long long* __re
     if (threadIdx.x != 0) return;
     m = wk[0];
     for (int w = 1; w < 8; w++) m = wk[w] > m ? wk[w] : m;
-    const uint32_t tok = 0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull);
+    // (every key is nonzero: a row's key is zero only for a NaN past row 0,
+    // and row 0's key is never zero)
+    const uint32_t tok = m ? 0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull) : 0u;
     st->token = tok;
     if (ring && st->n_out < ring_cap) ring[st->n_out] = tok;
     st->n_out += 1;

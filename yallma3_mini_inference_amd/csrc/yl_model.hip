@@ -286,7 +286,15 @@ struct yl_session {
     uint32_t* tokens = nullptr;
     uint32_t* ring = nullptr;
     uint32_t ring_cap = 0;
-    hipGraphExec_t graph = nullptr;
+    // decode-step graphs, one per context bucket: decode attention is sized
+    // for the bucket's longest context (see decode_bucket)
+    struct DecodeGraph {
+        int max_seq;
+        hipGraphExec_t exec;
+    };
+    std::vector<DecodeGraph> graphs;
+    int dec_seq = 0;                     // bucket of the decode step being enqueued
+    uint64_t prof_seq = 0;               // seq_len of the step yl_profile_kernel times
     uint32_t pos = 0;
 };
 
@@ -436,8 +444,11 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
         *st = YL_ERR_UNSUPPORTED;
         return nullptr;
     }
-    if ((size_t)m->ctx * 4 + (size_t)m->hd * 40 > 60 * 1024) {
-        set_error("context too long for the single-pass attention kernel (ctx_len <= ~15000)");
+    // kernels address one layer's value cache (kv_ld x kv_dim floats) with
+    // 32-bit byte offsets
+    if ((uint64_t)m->kv_ld * (uint64_t)m->kv * 4 >= (1ull << 31)) {
+        set_error("context_length " + std::to_string(m->ctx) + " too long: one layer's KV cache must stay below "
+                  "2 GiB (cap it with max_ctx_len)");
         *st = YL_ERR_UNSUPPORTED;
         return nullptr;
     }
@@ -515,7 +526,7 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
 // the largest size used; prompts below 64 tokens need none).
 bool prompt_scratch(yl_session* s, int batch, uint32_t start_pos) {
     s->pseq = (int)start_pos + batch;
-    if (!prompt_attn_applies(batch)) return true;
+    if (!prompt_attn_applies(batch, s->pseq, s->m->hd)) return true;
     const size_t need = prompt_attn_bytes(s->m->n_heads, s->pseq, batch);
     if (need <= s->psc_bytes) return true;
     hipStreamSynchronize(s->stream);
@@ -534,10 +545,11 @@ bool prompt_scratch(yl_session* s, int batch, uint32_t start_pos) {
 bool session_grow(yl_session* s, int batch) {
     if (batch <= s->cap_b) return true;
     const yl_model* m = s->m;
-    // the decode graph holds the old buffer addresses: drop it, it is
-    // captured again on the next decode step
+    // the decode graphs hold the old buffer addresses: drop them, they are
+    // captured again on the next decode steps
     hipStreamSynchronize(s->stream);
-    if (s->graph) { hipGraphExecDestroy(s->graph); s->graph = nullptr; }
+    for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
+    s->graphs.clear();
     auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
     rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens); rel(s->nq); rel(s->ns);
     const size_t B = (size_t)batch;
@@ -650,15 +662,18 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         if (bytes) *bytes = gemv_bytes(L.qkv, L.qkv.o, batch);
         return launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st);
     case kOpAttn:
-        // attention (+ quantize of its output)
-        if (bytes) *bytes = 0;
+        // attention (+ quantize of its output).  Algorithmic bytes: the keys
+        // and values of every position, the queries, the quantized output.
+        if (bytes)
+            *bytes = 2ull * s->prof_seq * (uint64_t)m->kv * 4 +
+                     (uint64_t)batch * ((uint64_t)m->att * 4 + (uint64_t)m->att + (uint64_t)m->att / 8);
         if (batch == 1)
-            return launch_attn_decode(s->sq, kc, vc, s->st, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+            return launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                       m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->sc, st);
-        if (prompt_attn_applies(batch) && s->psc)
+        if (prompt_attn_applies(batch, s->pseq, m->hd))
             return launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                            m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->psc, st);
-        return launch_attention(s->sq, kc, vc, s->st, batch, m->ctx, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+        return launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                 m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
     case kOpWo:
         // WO -> residual add
@@ -695,28 +710,54 @@ hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const ui
     return enqueue_op(m, s, kOpLogits, 0, batch, tok, advance, nullptr);
 }
 
-bool ensure_graph(const yl_model* m, yl_session* s) {
-    if (s->graph) return true;
+// Decode attention is sized for a context bucket: 4096 positions (the one
+// kernel of short contexts), then powers of two, capped at ctx_len, so a
+// model loaded with a long context decodes short conversations on the same
+// kernels as a short-context model.
+int decode_bucket(const yl_model* m, uint64_t seq_end) {
+    uint64_t b = 4096;
+    while (b < seq_end) b *= 2;
+    return (int)(b < (uint64_t)m->ctx ? b : (uint64_t)m->ctx);
+}
+
+// The graph of one decode step whose context ends at seq_end (<= ctx_len),
+// captured on first use.
+hipGraphExec_t ensure_graph(const yl_model* m, yl_session* s, uint64_t seq_end) {
+    const int bucket = decode_bucket(m, seq_end);
+    for (const auto& dg : s->graphs)
+        if (dg.max_seq == bucket) return dg.exec;
+    s->dec_seq = bucket;
     hipGraph_t g = nullptr;
     if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         set_error("hipStreamBeginCapture failed");
-        return false;
+        return nullptr;
     }
     const hipError_t e = enqueue_forward(m, s, 1, &s->st->token, 1);
     const hipError_t e2 = hipStreamEndCapture(s->stream, &g);
     if (e != hipSuccess || e2 != hipSuccess) {
         set_error(std::string("decode graph capture failed: ") + hipGetErrorString(e != hipSuccess ? e : e2));
         if (g) hipGraphDestroy(g);
-        return false;
+        return nullptr;
     }
-    const hipError_t e3 = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+    hipGraphExec_t ge = nullptr;
+    const hipError_t e3 = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e3 != hipSuccess) {
         set_error(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(e3));
-        s->graph = nullptr;
-        return false;
+        return nullptr;
     }
-    return true;
+    s->graphs.push_back({bucket, ge});
+    return ge;
+}
+
+// Positions a decode step can attend over for this model's head layout.
+bool decode_in_range(const yl_model* m, uint64_t seq_end, const char* what) {
+    const int lim = attn_decode_limit(m->n_heads, m->n_kv, m->hd);
+    if (seq_end <= (uint64_t)lim) return true;
+    set_error(std::string(what) + ": decode attention for this head layout (head_size " + std::to_string(m->hd) +
+              ", " + std::to_string(m->n_heads / m->n_kv) + " query heads per kv head) reaches " +
+              std::to_string(lim) + " positions");
+    return false;
 }
 
 yl_status hip_fail(hipError_t e, const char* what) {
@@ -955,15 +996,16 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     const size_t seq = start_pos + batch;
     // one token: the decode kernel (as in a decode step); several: the
     // prompt kernel, whose workgroup holds a whole score row
-    if (batch > 1 && !prompt_attn_applies((int)batch) && seq * 4 + (size_t)hd * 40 > 60 * 1024) {
-        set_error("attention: seq_len too long for one workgroup");
+    if (seq >= (1u << 30) || (uint64_t)seq * n_kv_heads * hd * 4 >= (1ull << 31)) {
+        set_error("attention: the cache must stay below 2 GiB");
         return YL_ERR_UNSUPPORTED;
     }
-    if (prompt_attn_applies((int)batch) && hd != 32 && hd != 64 && hd != 128) {
-        set_error("attention: prompt batches of 64+ tokens need head_size 32, 64 or 128");
+    const bool tiled = prompt_attn_applies((int)batch, (int)seq, (int)hd);
+    if (tiled && hd != 32 && hd != 64 && hd != 128) {
+        set_error("attention: tiled prompt attention needs head_size 32, 64 or 128");
         return YL_ERR_UNSUPPORTED;
     }
-    if (batch == 1 && (hd % 32 || !attn_decode_fits((int)seq))) {
+    if (batch == 1 && (hd % 32 || hd > 128 || !attn_decode_fits((int)seq, (int)n_heads, (int)n_kv_heads, (int)hd))) {
         set_error("attention: unsupported head size or seq_len for the decode kernel");
         return YL_ERR_UNSUPPORTED;
     }
@@ -979,8 +1021,8 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
     if (e == hipSuccess) e = hipMalloc(&kt, (size_t)ld * kv_dim * 4 + 256);
     const size_t sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq)
-                            : prompt_attn_applies((int)batch) ? prompt_attn_bytes((int)n_heads, (int)seq, (int)batch)
-                                                              : 0;
+                            : tiled ? prompt_attn_bytes((int)n_heads, (int)seq, (int)batch)
+                                    : 0;
     if (e == hipSuccess && sc_bytes) e = hipMalloc(&sc, sc_bytes);
     if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, kv_dim, ld, strm);
@@ -1016,9 +1058,11 @@ yl_status yl_math_selftest(const float* x, size_t n, float* exp_out, float* sqrt
     return e == hipSuccess ? YL_OK : hip_fail(e, "math selftest");
 }
 
-yl_status yl_serial_sum_selftest(const float* v, const uint32_t* offsets, size_t cases, float* out) {
+yl_status yl_serial_sum_selftest(const float* v, const uint32_t* offsets, size_t cases, uint32_t segment,
+                                 float* out) {
     if ((!v || !offsets || !out) && cases) return YL_ERR_ARG;
-    hipError_t e = launch_serial_sum_selftest(v, offsets, (int)cases, out, nullptr);
+    if (segment > (1u << 30)) return YL_ERR_ARG;
+    hipError_t e = launch_serial_sum_selftest(v, offsets, (int)cases, (int)segment, out, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     return e == hipSuccess ? YL_OK : hip_fail(e, "serial sum self-test");
 }
@@ -1092,9 +1136,9 @@ yl_session* yl_create_session(const yl_model* m) {
 void yl_session_free(yl_session* s) {
     if (!s) return;
     if (s->stream) hipStreamSynchronize(s->stream);
-    if (s->graph) hipGraphExecDestroy(s->graph);
+    for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->keys, s->tokens, s->sc, s->psc};
+                   s->as_, s->hs, s->nq, s->ns, s->keys, s->tokens, s->sc, s->psc};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
@@ -1130,12 +1174,14 @@ yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint
         return YL_ERR_RANGE;
     }
     if (n > 65535) { set_error("forward_x: more than 65535 tokens in one call"); return YL_ERR_ARG; }
+    if (n == 1 && !decode_in_range(m, (uint64_t)start_pos + 1, "forward_x")) return YL_ERR_RANGE;
     yl_status rs = put_state(s, (int32_t)start_pos, tokens[0]);
     if (rs != YL_OK) return rs;
     hipError_t e;
     if (n == 1) {
-        if (!ensure_graph(m, s)) return YL_ERR_HIP;
-        e = hipGraphLaunch(s->graph, s->stream);
+        hipGraphExec_t ge = ensure_graph(m, s, (uint64_t)start_pos + 1);
+        if (!ge) return YL_ERR_HIP;
+        e = hipGraphLaunch(ge, s->stream);
         if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
     } else {
         if (!session_grow(s, (int)n) || !prompt_scratch(s, (int)n, start_pos)) return YL_ERR_NOMEM;
@@ -1163,12 +1209,21 @@ yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, u
         set_error("generate: positions beyond ctx_len " + std::to_string(m->ctx));
         return YL_ERR_RANGE;
     }
+    if (!decode_in_range(m, (uint64_t)start_pos + n_steps, "generate")) return YL_ERR_RANGE;
     yl_status rs = put_state(s, (int32_t)start_pos, token);
     if (rs != YL_OK) return rs;
-    if (!ensure_graph(m, s)) return YL_ERR_HIP;
-    for (uint32_t i = 0; i < n_steps; i++) {
-        const hipError_t e = hipGraphLaunch(s->graph, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    // steps of one context bucket replay that bucket's graph (the position
+    // and token live on the device, so the graphs hand over seamlessly)
+    for (uint32_t i = 0; i < n_steps;) {
+        const uint64_t seq = (uint64_t)start_pos + i + 1;
+        const int bucket = decode_bucket(m, seq);
+        hipGraphExec_t ge = ensure_graph(m, s, seq);
+        if (!ge) return YL_ERR_HIP;
+        const uint32_t end = (uint64_t)bucket - start_pos < n_steps ? (uint32_t)(bucket - start_pos) : n_steps;
+        for (; i < end; i++) {
+            const hipError_t e = hipGraphLaunch(ge, s->stream);
+            if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+        }
     }
     hipError_t e = hipSuccess;
     if (out_tokens) e = hipMemcpyAsync(out_tokens, s->ring, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s->stream);
@@ -1185,6 +1240,9 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
+    if (batch == 1 && !decode_in_range(m, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
+    s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
+    s->prof_seq = (uint64_t)start_pos + batch;
     if (batch > 1 && (!session_grow(s, (int)batch) || !prompt_scratch(s, (int)batch, start_pos)))
         return YL_ERR_NOMEM;
     yl_status rs = put_state(s, (int32_t)start_pos, token);
@@ -1253,6 +1311,11 @@ bool load_transformer_ffi(const char* model_path) {
     if (g_current) model_release(g_current);
     g_current = m;
     return true;
+}
+
+const yl_model* yl_ffi_model(void) {
+    std::lock_guard<std::mutex> lk(g_ffi_mu);
+    return g_current;
 }
 
 char* infer_ffi(const char* prompt) {

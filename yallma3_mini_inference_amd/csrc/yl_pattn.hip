@@ -56,7 +56,12 @@ size_t prompt_attn_bytes(int n_heads, int seq_ld, int batch) {
     const size_t Bp = pattn_rows_ld(batch);
     return (size_t)n_heads * Bp * ((size_t)seq_ld + pattn_tiles(seq_ld) + 3) * sizeof(float);
 }
-bool prompt_attn_applies(int batch) { return batch >= kPT; }
+// k_attention (one workgroup per head and token) holds the whole score row
+// in LDS; batches of 2..63 tokens whose seq_len does not fit take the tiled
+// path as one partial row tile
+bool prompt_attn_applies(int batch, int seq_len, int head_size) {
+    return batch >= kPT || (batch > 1 && !attention_row_fits(seq_len, head_size));
+}
 
 // ---------------------------------------------------------------------------
 // 1. scores and tile row maxima.  Thread (ty, tx) of 16 x 16: rows 4ty..+3,
@@ -489,7 +494,7 @@ static hipError_t launch_pattn_q(const float* sq, const float* kc, const float* 
 hipError_t launch_prompt_attention(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
                                    int seq_ld, int kv_ld, int n_heads, int n_kv_heads, int head_size, float scale,
                                    int qfmt, int8_t* aq, float* as, float* att_f32, float* scratch, hipStream_t s) {
-    if (!scratch || batch < kPT || seq_ld < batch || kv_ld < seq_ld || kv_ld % 4) return hipErrorInvalidValue;
+    if (!scratch || batch < 2 || seq_ld < batch || kv_ld < seq_ld || kv_ld % 4) return hipErrorInvalidValue;
     if (qfmt == kQ8)
         return launch_pattn_q<kQ8>(sq, kc, vc, st, batch, seq_ld, kv_ld, n_heads, n_kv_heads, head_size, scale, aq,
                                    as, att_f32, scratch, s);

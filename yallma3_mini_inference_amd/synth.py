@@ -50,8 +50,18 @@ CONFIGS = {
     "tiny_mixed": ModelConfig(128, 384, 3, 4, 1, 1000, 300, rope_theta=500000.0, ffn_format=Q4),
     # dim 96: the embedding table's rows are padded to 128 (zero-scale blocks); vocab 300 ends in a partial tile
     "tiny_pad": ModelConfig(96, 192, 2, 3, 1, 300, 128, seed=3),
-    # a context long enough for the two-kernel decode attention (head size 64, 4 query heads per kv head)
+    # ctx 4096, the longest context of the single decode attention kernel (head size 64, 4 query heads
+    # per kv head): its softmax sum runs on one lane up to 2560 positions and one wavefront beyond
     "tiny_long": ModelConfig(256, 512, 2, 4, 1, 512, 4096, seed=7),
+    # head size 64, 2 query heads per kv head, context_length 131072 (a Llama-3.x
+    # GGUF's): decode past 16384 positions streams the softmax row in segments
+    "tiny_ctx131k": ModelConfig(256, 512, 2, 4, 2, 512, 131072, rope_theta=500000.0, seed=11),
+    # head size 32 beside a 20000-position context: its decode attention keeps
+    # the scores row in LDS and stops at 16384 positions
+    "tiny_hd32_long": ModelConfig(128, 256, 2, 4, 2, 512, 20000, seed=12),
+    # ctx 8448 with 4 query heads per kv head (head size 64): decode beyond
+    # 4096 positions runs the four-kernel split attention inside the graph
+    "tiny_8k": ModelConfig(256, 512, 2, 4, 1, 512, 8448, seed=9),
     # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
     "smollm2_135m": ModelConfig(576, 1536, 30, 9, 3, 49152, 2048),
     # Llama-3.2-1B shape: dim 2048, FFN 8192, 16 layers, 32/8 heads, vocab 128256

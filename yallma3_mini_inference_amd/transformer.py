@@ -69,17 +69,22 @@ class InferenceSession:
         return out
 
     def upload_kv(self, key: np.ndarray, value: np.ndarray) -> None:
-        """Overwrite the device KV cache from [n_layers][ctx_len][kv_dim]
-        arrays (tests and benchmarks pre-fill it)."""
+        """Overwrite the device KV cache from [n_layers][P][kv_dim] arrays of
+        the first P <= ctx_len positions (the rest become zeros); tests and
+        benchmarks pre-fill it."""
         kp, vp, n = self._kv()
         m = self.model
-        ctx = m.shape.ctx_len
-        shp = (m.shape.n_layers, ctx, m.shape.n_kv_heads * m.shape.head_size)
-        dev = self._shape()
+        kv = m.shape.n_kv_heads * m.shape.head_size
+        key = np.asarray(key, np.float32)
+        value = np.asarray(value, np.float32)
+        P = key.size // (m.shape.n_layers * kv)
+        if key.size != m.shape.n_layers * P * kv or value.size != key.size or P > m.shape.ctx_len:
+            raise ValueError("cache shape mismatch")
+        shp = (m.shape.n_layers, P, kv)
         kd = np.zeros(self._shape(True), np.float32)
-        kd[:, :, :ctx] = np.asarray(key, np.float32).reshape(shp).transpose(0, 2, 1)
-        vd = np.zeros(dev, np.float32)
-        vd[:, :ctx] = np.asarray(value, np.float32).reshape(shp)
+        kd[:, :, :P] = key.reshape(shp).transpose(0, 2, 1)
+        vd = np.zeros(self._shape(), np.float32)
+        vd[:, :P] = value.reshape(shp)
         for ptr, a in ((kp, kd), (vp, vd)):
             if a.size != n:
                 raise ValueError("cache shape mismatch")
