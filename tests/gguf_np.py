@@ -341,7 +341,7 @@ def _rand_q4(rng, rows, cols, std):
     return q4_blocks(rng.integers(0, 16, (n, 32)), d)
 
 
-def random_llama(path, dim=64, hidden=128, n_layers=2, n_heads=4, n_kv_heads=2, vocab=96, ctx=64,
+def random_llama(path, dim=64, hidden=128, n_layers=2, n_heads=2, n_kv_heads=1, vocab=96, ctx=64,
                  attn_fmt=T_Q8_0, ffn_fmt=T_Q8_0, embd_fmt=T_Q8_0, seed=0, rope_theta=10000.0,
                  nan_embedding_rows=(), nan_output_norm=False, emb_std=0.5, w_std=0.05):
     """A random llama GGUF whose norm weights differ per tensor (so a swapped

@@ -8,11 +8,13 @@
   the oracle's dequantized table must equal value * scale element by element.
 * Composition (forward.rs:120-280): an independent float64 forward over the
   same bytes (tests/gguf_np.py, its own GGUF parser) must agree with the
-  oracle's logits to 1e-6 (relative, norm-wise), on random models with
+  oracle's logits to 1e-5 (relative, norm-wise; observed <= 3e-7, the
+  activation quantization's rare rounding flips), on random models with
   distinct norm weights in Q8_0, Q4_0 and mixed formats; and each of a set of
   plausible mistakes -- GGML's Q4_0 nibble order and offset, HF-layout RoPE
   pairs, gate and up exchanged, the two norms exchanged, no 1/sqrt(head_size)
-  scale -- computed the same way must disagree by more than 1e-4.
+  scale -- computed the same way must disagree by more than 1e-4 (observed
+  >= 1.1e-3).
 * The golden fixture: the oracle's logits and greedy ids on seeded models,
   frozen in tests/golden/forward_golden.npz by tests/golden/make_golden.py,
   must be reproduced bit for bit.
@@ -49,7 +51,7 @@ def _hand_embedding_model(path, fmt):
     else:
         vals = (7 * e + 3 * v) % 255 - 127
         blob = G.q8_blocks(vals.ravel(), d.ravel())
-    G.random_llama(path, dim=dim, vocab=vocab, seed=5)
+    G.random_llama(path, dim=dim, vocab=vocab, n_heads=2, n_kv_heads=1, seed=5)   # head size 32
     g = G.Gguf(path)
     tensors = []
     for name, (dims, typ, off) in g.tensors.items():
@@ -112,7 +114,7 @@ def _compare(oracle, path, variant, steps=4):
 def test_float64_forward_agrees_with_oracle(oracle, tmp_path, name):
     a, f, e = MODELS[name]
     path = G.random_llama(str(tmp_path / f"{name}.gguf"), attn_fmt=a, ffn_fmt=f, embd_fmt=e, seed=1)
-    assert _compare(oracle, path, "reference") < 1e-6
+    assert _compare(oracle, path, "reference") < 1e-5
 
 
 @pytest.mark.parametrize("variant", [v for v in G.VARIANTS if v != "reference"])
