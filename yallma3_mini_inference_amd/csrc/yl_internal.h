@@ -98,6 +98,7 @@ struct GemvArgs {
 };
 
 // kernel launchers; all return the hipError_t of the launch
+hipError_t launch_set_state(StepState* st, int32_t pos, uint32_t token, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s);
 // many-token matmul on int8 MFMA (same epilogues and results as the GEMV;

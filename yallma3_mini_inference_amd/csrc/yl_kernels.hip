@@ -172,7 +172,23 @@ __global__ __launch_bounds__(64) void k_serial_sum_selftest(const float* __restr
     if (threadIdx.x == 0) out[c] = s;
 }
 
+// The step state of an op call: its first position (and token).
+__global__ void k_set_state(StepState* st, int32_t pos, uint32_t token) {
+    if (threadIdx.x == 0) {
+        st->pos = pos;
+        st->token = token;
+        st->n_out = 0;
+        st->pad = 0;
+        st->argmax = 0ull;
+    }
+}
+
 // ------------------------------------------------------------- launchers --
+
+hipError_t launch_set_state(StepState* st, int32_t pos, uint32_t token, hipStream_t s) {
+    hipLaunchKernelGGL(k_set_state, dim3(1), dim3(64), 0, s, st, pos, token);
+    return hipGetLastError();
+}
 
 hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, size_t n, hipStream_t s) {
     const size_t groups = n / kGroup;

@@ -986,20 +986,32 @@ yl_status yl_rope_gguf(const yl_rope_params* p, float* q, float* k, size_t batch
     return e == hipSuccess ? YL_OK : hip_fail(e, "rope");
 }
 
-yl_status yl_attention(float* out, const float* q, const float* kc, const float* vc, size_t batch, uint32_t start_pos,
-                       uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, float attn_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Buffers an attention op call needs beyond its inputs and outputs: the
+// step state (the call's first position), the keys transposed to the
+// kernels' [kv_dim][ld] layout (the caller's are [seq][kv_dim]), and the
+// scores scratch of long decode contexts or of tiled prompt batches.
+struct AttnBuffers {
+    int ld = 0, kv_dim = 0;
+    size_t kt_bytes = 0, sc_bytes = 0;
+};
+
+yl_status attention_plan(const float* out, const float* q, const float* kc, const float* vc, size_t batch,
+                         uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, AttnBuffers* B) {
     if (!out || !q || !kc || !vc || !n_heads || !n_kv_heads || n_heads % n_kv_heads || hd % 8 || !hd) {
         set_error("attention: bad arguments");
         return YL_ERR_ARG;
     }
-    if (batch == 0) return YL_OK;
     const size_t seq = start_pos + batch;
-    // one token: the decode kernel (as in a decode step); several: the
-    // prompt kernel, whose workgroup holds a whole score row
     if (seq >= (1u << 30) || (uint64_t)seq * n_kv_heads * hd * 4 >= (1ull << 31)) {
         set_error("attention: the cache must stay below 2 GiB");
         return YL_ERR_UNSUPPORTED;
     }
+    // one token: the decode kernels (as in a decode step); several: the
+    // prompt kernels (one score row per workgroup, or tiled)
     const bool tiled = prompt_attn_applies((int)batch, (int)seq, (int)hd);
     if (tiled && hd != 32 && hd != 64 && hd != 128) {
         set_error("attention: tiled prompt attention needs head_size 32, 64 or 128");
@@ -1009,32 +1021,51 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
         set_error("attention: unsupported head size or seq_len for the decode kernel");
         return YL_ERR_UNSUPPORTED;
     }
+    B->kv_dim = (int)(n_kv_heads * hd);
+    B->ld = ((int)seq + 3) & ~3;
+    B->kt_bytes = ((size_t)B->ld * B->kv_dim * 4 + 255) & ~(size_t)255;
+    B->sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq)
+                  : tiled    ? prompt_attn_bytes((int)n_heads, (int)seq, (int)batch)
+                             : 0;
+    return YL_OK;
+}
+
+// Enqueues one attention op call on `strm` over the buffers of `B`.
+hipError_t attention_enqueue(float* out, const float* q, const float* kc, const float* vc, size_t batch,
+                             uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, float attn_scale,
+                             const AttnBuffers& B, StepState* dst, float* kt, float* sc, hipStream_t strm) {
+    const int seq = (int)(start_pos + batch);
+    hipError_t e = launch_set_state(dst, (int32_t)start_pos, 0u, strm);
+    if (e == hipSuccess) e = launch_transpose(kc, kt, seq, B.kv_dim, B.ld, strm);
+    if (e != hipSuccess) return e;
+    if (batch == 1)
+        return launch_attn_decode(q, kt, vc, dst, seq, B.ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
+                                  nullptr, nullptr, out, sc, strm);
+    if (sc)
+        return launch_prompt_attention(q, kt, vc, dst, (int)batch, seq, B.ld, (int)n_heads, (int)n_kv_heads, (int)hd,
+                                       attn_scale, -1, nullptr, nullptr, out, sc, strm);
+    return launch_attention(q, kt, vc, dst, (int)batch, seq, B.ld, (int)n_heads, (int)n_kv_heads, (int)hd,
+                            attn_scale, -1, nullptr, nullptr, out, strm);
+}
+
+}  // namespace
+
+extern "C" {
+
+yl_status yl_attention(float* out, const float* q, const float* kc, const float* vc, size_t batch, uint32_t start_pos,
+                       uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, float attn_scale, void* stream) {
+    AttnBuffers B;
+    const yl_status st = attention_plan(out, q, kc, vc, batch, start_pos, n_heads, n_kv_heads, hd, &B);
+    if (st != YL_OK || batch == 0) return st;
     StepState* dst = nullptr;
     float *kt = nullptr, *sc = nullptr;
-    StepState hst{};
-    hst.pos = (int32_t)start_pos;
     hipStream_t strm = (hipStream_t)stream;
-    const int kv_dim = (int)(n_kv_heads * hd);
-    const int ld = ((int)seq + 3) & ~3;
-    // the kernels read keys transposed ([kv_dim][ld]); the caller's are in
-    // the reference layout [seq][kv_dim]
     hipError_t e = hipMalloc(&dst, sizeof(StepState));
-    if (e == hipSuccess) e = hipMalloc(&kt, (size_t)ld * kv_dim * 4 + 256);
-    const size_t sc_bytes = batch == 1 ? attn_scores_bytes((int)n_heads, (int)seq)
-                            : tiled ? prompt_attn_bytes((int)n_heads, (int)seq, (int)batch)
-                                    : 0;
-    if (e == hipSuccess && sc_bytes) e = hipMalloc(&sc, sc_bytes);
-    if (e == hipSuccess) e = hipMemcpy(dst, &hst, sizeof hst, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, kv_dim, ld, strm);
-    if (e == hipSuccess && batch == 1)
-        e = launch_attn_decode(q, kt, vc, dst, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1,
-                               nullptr, nullptr, out, sc, strm);
-    else if (e == hipSuccess && sc)
-        e = launch_prompt_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
-                                    attn_scale, -1, nullptr, nullptr, out, sc, strm);
-    else if (e == hipSuccess)
-        e = launch_attention(q, kt, vc, dst, (int)batch, (int)seq, ld, (int)n_heads, (int)n_kv_heads, (int)hd,
-                             attn_scale, -1, nullptr, nullptr, out, strm);
+    if (e == hipSuccess) e = hipMalloc(&kt, B.kt_bytes);
+    if (e == hipSuccess && B.sc_bytes) e = hipMalloc(&sc, B.sc_bytes);
+    if (e == hipSuccess)
+        e = attention_enqueue(out, q, kc, vc, batch, start_pos, n_heads, n_kv_heads, hd, attn_scale, B, dst, kt, sc,
+                              strm);
     if (e == hipSuccess) e = hipStreamSynchronize(strm);
     if (dst) hipFree(dst);
     if (kt) hipFree(kt);
