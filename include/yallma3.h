@@ -162,6 +162,20 @@ yl_status yl_attention(float *out, const float *q, const float *key_cache, const
                        size_t batch, uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads,
                        uint32_t head_size, float attn_scale, void *stream);
 
+/* yl_attention without any allocation: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as yl_attention, but the step state, the transposed keys and the
+ * scores scratch live in a 64 MiB array the library holds per GPU for the
+ * life of the process; calls that would need more (keys of seq_len *
+ * n_kv_heads * head_size floats plus the scores) return YL_ERR_RANGE.  The
+ * work is enqueued on `stream` and not waited for: synchronize before
+ * reading `out`.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (different streams or threads) race. */
+yl_status yl_attention_noalloc(float *out, const float *q, const float *key_cache, const float *value_cache,
+                               size_t batch, uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads,
+                               uint32_t head_size, float attn_scale, void *stream);
+
 /* SwiGLU (forward.rs:220-237) of gate/up [batch][hidden] (device) into h
  * (nullable, f32), optionally quantized (qfmt -1 = none). */
 yl_status yl_swiglu_quantize(const float *gate, const float *up, size_t hidden, size_t batch,

@@ -1073,6 +1073,77 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     return e == hipSuccess ? YL_OK : hip_fail(e, "attention");
 }
 
+}  // extern "C"
+
+// ---------------------------------------------- allocation-free attention
+// yl_attention_noalloc keeps the step state, the transposed keys and the
+// scores scratch of a call in this array instead of hipMalloc'ed buffers.
+// Every GPU the library runs on holds its own copy until the process ends;
+// host code reaches a device's copy only through the address that
+// hipGetSymbolAddress returns with that device current (the array's name is
+// a host-side stand-in, not a device address).
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up on the first call on
+// each device.
+yl_status scratch_of_current_device(unsigned char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("attention_noalloc: device index beyond " + std::to_string(kMaxDevices));
+        return YL_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) {
+            set_error("hipGetSymbolAddress(scratch) returned a null address");
+            return YL_ERR_HIP;
+        }
+        g_scratch_dev[dev] = static_cast<unsigned char*>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return YL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+yl_status yl_attention_noalloc(float* out, const float* q, const float* kc, const float* vc, size_t batch,
+                               uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd,
+                               float attn_scale, void* stream) {
+    AttnBuffers B;
+    yl_status st = attention_plan(out, q, kc, vc, batch, start_pos, n_heads, n_kv_heads, hd, &B);
+    if (st != YL_OK || batch == 0) return st;
+    const size_t sc_off = 256 + B.kt_bytes;
+    const size_t need = sc_off + ((B.sc_bytes + 255) & ~(size_t)255);
+    if (need > kNoAllocScratchBytes) {
+        set_error("attention_noalloc: the call needs " + std::to_string(need) + " bytes of scratch, more than the " +
+                  std::to_string(kNoAllocScratchBytes) + " the library holds per GPU");
+        return YL_ERR_RANGE;
+    }
+    unsigned char* base = nullptr;
+    st = scratch_of_current_device(&base);
+    if (st != YL_OK) return st;
+    StepState* dst = reinterpret_cast<StepState*>(base);
+    float* kt = reinterpret_cast<float*>(base + 256);
+    float* sc = B.sc_bytes ? reinterpret_cast<float*>(base + sc_off) : nullptr;
+    const hipError_t e = attention_enqueue(out, q, kc, vc, batch, start_pos, n_heads, n_kv_heads, hd, attn_scale, B,
+                                           dst, kt, sc, (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "attention_noalloc");
+}
+
 yl_status yl_swiglu_quantize(const float* gate, const float* up, size_t hidden, size_t batch, float* h, int32_t qfmt,
                              int8_t* q, float* scale, void* stream) {
     if (!gate || !up || !hidden) { set_error("swiglu: bad arguments"); return YL_ERR_ARG; }
