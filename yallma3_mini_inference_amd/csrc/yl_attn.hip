@@ -145,17 +145,18 @@ constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decod
 // the round issued before the first product; partials go to
 // part[j][RP].  Quads past the row re-read its last quad (never used).
 template <int HD, int NC>
-__device__ __forceinline__ void score_round(__amdgpu_buffer_rsrc_t krs, const float* qp, int r0, int n_quads,
-                                            int lane, int wave, int row_step, float* part, int RP) {
-    vf4 k4[NC][HD / 8];
+__device__ __forceinline__ void score_loads(__amdgpu_buffer_rsrc_t krs, int r0, int n_quads, int lane, int wave,
+                                            int row_step, vf4 (&k4)[NC][HD / 8]) {
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
         const int quad = min(r0 / 4 + ch * 64 + lane, n_quads - 1);
 #pragma unroll
         for (int s = 0; s < HD / 8; s++) k4[ch][s] = buf_load_f32x4(krs, quad * 16, (8 * s + wave) * row_step);
     }
-    // (left free, the scheduler keeps a dozen loads in flight)
-    __builtin_amdgcn_sched_barrier(0);
+}
+template <int HD, int NC>
+__device__ __forceinline__ void score_products(const float* qp, const vf4 (&k4)[NC][HD / 8], int lane, int wave,
+                                               float* part, int RP) {
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
         float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -169,6 +170,15 @@ __device__ __forceinline__ void score_round(__amdgpu_buffer_rsrc_t krs, const fl
         }
         *reinterpret_cast<vf4*>(part + wave * RP + ch * 256 + 4 * lane) = vf4{l[0], l[1], l[2], l[3]};
     }
+}
+template <int HD, int NC>
+__device__ __forceinline__ void score_round(__amdgpu_buffer_rsrc_t krs, const float* qp, int r0, int n_quads,
+                                            int lane, int wave, int row_step, float* part, int RP) {
+    vf4 k4[NC][HD / 8];
+    score_loads<HD, NC>(krs, r0, n_quads, lane, wave, row_step, k4);
+    // (left free, the scheduler keeps a dozen loads in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    score_products<HD, NC>(qp, k4, lane, wave, part, RP);
 }
 constexpr int kScoreRows = 256;   // positions per scores workgroup
 constexpr int kLongQuads = 8;     // score quads per decode thread: max_seq <= 8 * 4 * kDecThreads
@@ -237,8 +247,6 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     const int ds = (lg / r) % (HD / kDecDims);
     const int h = kvh * r + lg % r;
     const int kv_dim = n_kv_heads * HD;
-    const int seq = st->pos + 1;
-    const int n_chunks = seq / 8;
     const int PCS = attn_pt_stride(max_seq);
     float* pt = lds;
     float* vt = pt + 8 * PCS;
@@ -250,12 +258,25 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // keys of this kv head through a buffer descriptor: a per-lane 32-bit
     // offset (4 positions) and a uniform offset per key dimension, so no
     // load needs a 64-bit address register; quads start at most at the last
-    // position, and rows are kv_ld >= seq (a multiple of 4) long, so every
-    // 16-byte read stays inside its row
+    // position, and rows are kv_ld >= max_seq (a multiple of 4) long, so
+    // every 16-byte read stays inside its row
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(kc + (size_t)kvh * HD * kv_ld), (short)0, HD * kv_ld * 4, kBufFlags);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(vc), (short)0, max_seq * kv_dim * 4, kBufFlags);
+    const int lane = tid & 63;
+
+    // The key loads of the first score round go out before the step's
+    // position is read (one dependent load later): they cover the first
+    // positions of the context up to one round (clamped to max_seq), and
+    // the scores of positions past seq are never used.
+    constexpr int NCH = kScoreLoads / (HD / 8);   // chunks of 256 positions per round
+    constexpr int RP = NCH * 256;
+    vf4 k0[LONG ? 1 : NCH][HD / 8];
+    if constexpr (!LONG)
+        score_loads<HD, NCH>(krs, 0, (min(max_seq, RP) + 3) / 4, lane, wave, kv_ld * 4, k0);
+    const int seq = st->pos + 1;
+    const int n_chunks = seq / 8;
 
     // the seq % 8 tail rows of V, for the output threads (tid < 32)
     float vtail[7];
@@ -266,7 +287,6 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // 1. scores -> pt (transposed)
     const int n_quads = (seq + 3) / 4;
     float lmax = -1e10f;
-    const int lane = tid & 63;
     if constexpr (LONG) {
         // the scores kernel's row of this head (rows are sc_ld >= max_seq, a
         // multiple of 4, floats long)
@@ -292,27 +312,16 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         // 256 positions with all their key rows in flight (HD/8 16-byte
         // loads per chunk), and the partials meet in the V tile area
         // ([8][RP], free until the V DMA starts) for reduce_add8 and the scale
-        constexpr int NCH = kScoreLoads / (HD / 8);
-        constexpr int RP = NCH * 256;
+        // round 0 from the keys already in flight, then rounds of only the
+        // chunks that hold positions (loads past the last one would all
+        // re-read its last quad, still costing memory-pipe cycles), one
+        // straight-line variant per chunk count
         static_assert(8 * RP <= 2 * kVTileFloats, "partials must fit two V tiles");
         float* part = vt;
         const float* qp = qh + wave;   // wave = j, uniform: scalar query loads
         const int row_step = kv_ld * 4;
-        for (int r0 = 0; r0 < seq; r0 += RP) {
-            // only the chunks holding positions (loads past the last one
-            // would all re-read its last quad, still costing memory-pipe
-            // cycles); one straight-line variant per chunk count
-            const int nlive = min(NCH, (n_quads - r0 / 4 + 63) / 64);
-            auto round = [&](auto nc) {
-                score_round<HD, decltype(nc)::value>(krs, qp, r0, n_quads, lane, wave, row_step, part, RP);
-            };
-            switch (nlive) {
-            case 1: round(std::integral_constant<int, 1>{}); break;
-            case 2: if constexpr (NCH >= 2) round(std::integral_constant<int, 2>{}); break;
-            case 3: if constexpr (NCH >= 3) round(std::integral_constant<int, 3>{}); break;
-            case 4: if constexpr (NCH >= 4) round(std::integral_constant<int, 4>{}); break;
-            default: if constexpr (NCH >= 8) round(std::integral_constant<int, NCH>{}); break;
-            }
+        // the round's partials -> scaled scores in pt and the running max
+        auto reduce_round = [&](int r0) {
             lds_barrier();
             const int nr = min(RP, seq - r0);
             for (int i = tid; i < nr; i += kDecThreads) {
@@ -326,6 +335,22 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
                 lmax = fmaxf(lmax, live ? sv : -1e10f);
             }
             lds_barrier();   // part is rewritten by the next round, then by the V DMA
+        };
+        score_products<HD, NCH>(qp, k0, lane, wave, part, RP);
+        reduce_round(0);
+        for (int r0 = RP; r0 < seq; r0 += RP) {
+            const int nlive = min(NCH, (n_quads - r0 / 4 + 63) / 64);
+            auto round = [&](auto nc) {
+                score_round<HD, decltype(nc)::value>(krs, qp, r0, n_quads, lane, wave, row_step, part, RP);
+            };
+            switch (nlive) {
+            case 1: round(std::integral_constant<int, 1>{}); break;
+            case 2: if constexpr (NCH >= 2) round(std::integral_constant<int, 2>{}); break;
+            case 3: if constexpr (NCH >= 3) round(std::integral_constant<int, 3>{}); break;
+            case 4: if constexpr (NCH >= 4) round(std::integral_constant<int, 4>{}); break;
+            default: if constexpr (NCH >= 8) round(std::integral_constant<int, NCH>{}); break;
+            }
+            reduce_round(r0);
         }
     }
     const int n_tiles = (8 * n_chunks + kVTileRows - 1) / kVTileRows;

@@ -74,8 +74,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
     return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, __builtin_amdgcn_readfirstlane(bytes), kBufRaw);
 }
 
+// Weights are read once per token, so they are loaded non-temporally
+// (cache policy `nt`): a decode step streams over a gigabyte of weights, and
+// loads that allocate normally would evict from the L2s and the 256 MiB
+// Infinity Cache the small data every kernel waits on -- its kernel
+// arguments, the step state, the activation rows, the KV cache.
+constexpr int kPolStream = 2;   // buffer load aux bit 1: nt
+
 __device__ __forceinline__ uint4 buf_u4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kPolStream));
 }
 
 template <int WF>
@@ -266,6 +273,11 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             vf4 xv[2 * MP], wv_n[2 * MP];
             EmbRegs<EMB ? MP : 1> er_;
             bool in_vocab = true;
+            // the position of the QKV epilogue, loaded first (the RoPE angles
+            // and the cache entries the K/V sums start from depend on it)
+            int pos = 0;
+            if constexpr (EPI == kEpiQkvRope)
+                if (wave == NA - 1) pos = a.state->pos + t;
             if constexpr (EMB) {
                 const uint32_t tok = a.tokens[t];
                 in_vocab = tok < (uint32_t)a.emb.vocab;
@@ -310,13 +322,15 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                 const int n8 = dim / 8, pad = rowq_chain_len(dim) - n8;
                 for (int i = tid; i < 8 * pad; i += 64 * NA) sq[(i / pad) * S + n8 + i % pad] = 0.0f;
             }
+            // the chain may start: it waits for the squares only
+            lds_arrive(ctr_sq);
             // initial values of the rows' sums: the K/V `+=` columns start
-            // from the cache (forward.rs:166-169, weight_type.rs:190-201)
+            // from the cache (forward.rs:166-169, weight_type.rs:190-201),
+            // published with the activation row (ctr_row) while the chain runs
             if (wave == NA - 1) {
                 if constexpr (EPI == kEpiQkvRope) {
                     // the epilogue's position and the RoPE angles of the rows
                     // (util.rs:653-718; the table row of the position)
-                    const int pos = a.state->pos + t;
                     const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
                     float* ropel = reinterpret_cast<float*>(smem + L.rope);
                     for (int i = lane; i < R; i += 64) {
@@ -332,7 +346,6 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                     float v = 0.0f;
                     if constexpr (EPI == kEpiQkvRope) {
                         const int row = min(row0 + i, o - 1);
-                        const int pos = a.state->pos + t;
                         const int att = a.att_dim, kv = a.kv_dim;
                         const bool is_k = row >= att && row < att + kv, is_v = row >= att + kv;
                         const int c = is_v ? row - att - kv : (is_k ? row - att : 0);
@@ -342,7 +355,6 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                     initl[i] = v;
                 }
             }
-            lds_arrive(ctr_sq);
             // the serial sum of squares (wavefront 0, lanes 0-7) -> ss
             if (wave == 0) {
                 lds_wait_count(ctr_sq, NA);
@@ -427,7 +439,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         uint16_t dv[LA];
         auto issue = [&](int k) {
             load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
-            dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, 0);
+            dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, kPolStream);
             __builtin_amdgcn_sched_barrier(0);
         };
 #pragma unroll

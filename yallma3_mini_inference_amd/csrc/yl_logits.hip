@@ -20,6 +20,15 @@
 
 namespace yl {
 
+// The embedding table is streamed once per token: non-temporal loads keep it
+// from evicting the data the next step's kernels wait on (see yl_gemv.hip).
+typedef int vi4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 load_stream(const int4* p) {
+    const vi4_t v = __builtin_nontemporal_load(reinterpret_cast<const vi4_t*>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t load_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
 constexpr int kLogitThreads = 256;
 constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each) in flight
 
@@ -59,9 +68,9 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
 #pragma unroll
     for (int gg = 0; gg < NG; gg++) {
         const int g = min(gg, ng - 1);
-        sv[gg] = dp[(size_t)g * cs];
+        sv[gg] = load_stream(dp + (size_t)g * cs);
 #pragma unroll
-        for (int c = 0; c < 4; c++) qv[gg][c] = qp[(size_t)(4 * g + c) * cs];
+        for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
     }
     rowq_stage<MP>(tm, xv, wv, dim, passes, sq);
     rowq_norm_quant<-1, false>(dim, eps, sq, nullptr, nullptr, xn);
@@ -81,9 +90,9 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                 // refill with group g + NG (clamped re-reads past the row are
                 // never used)
                 const int gn = min(g + NG, ng - 1);
-                sv[gg] = dp[(size_t)gn * cs];
+                sv[gg] = load_stream(dp + (size_t)gn * cs);
 #pragma unroll
-                for (int c = 0; c < 4; c++) qv[gg][c] = qp[(size_t)(4 * gn + c) * cs];
+                for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * gn + c) * cs);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int c = 0; c < 4; c++) {

@@ -28,7 +28,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/yallma3.h"
+#include "yallma3.h"
 #include "yl_gguf.h"
 #include "yl_internal.h"
 

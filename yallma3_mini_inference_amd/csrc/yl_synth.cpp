@@ -16,7 +16,7 @@
 #include <thread>
 #include <vector>
 
-#include "../../include/yallma3.h"
+#include "yallma3.h"
 #include "yl_internal.h"
 
 namespace {
