@@ -69,8 +69,13 @@ constexpr int kWaveSumSeq = 2560;
 // pt row stride: positions up to max_seq rounded to 64 (the serial sum
 // reads zero padding to that length), + 4 floats to spread banks
 __host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq + 63) & ~63) / 8 + 4; }
+// contexts longer than this take the scores kernel + the decode kernel
+constexpr int kAttnSplitSeq = 4096;
+// + for contexts up to kAttnSplitSeq, the exponentials in position order for
+// the serial sum (max_seq rounded up to 64); longer ones sum from pt
 __host__ __device__ inline size_t attn_fixed_lds_floats(int max_seq) {
-    return 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16;
+    const size_t el = max_seq <= kAttnSplitSeq ? (size_t)((max_seq + 63) & ~63) : 0;
+    return 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16 + el;
 }
 // V tile buffers that fit beside the fixed part (0: fewer than 2 fit)
 __host__ __device__ inline int attn_v_tiles(int max_seq) {
@@ -121,8 +126,9 @@ __device__ __forceinline__ void wait_v_tiles(int later) {
     }
 }
 
-template <int NV>
-__device__ __forceinline__ void exp_row(float* pt, int PCS, int b0, int seq, int pad, float mx) {
+// e = exp(score - max) into pt and, with EL, in position order into el
+template <int NV, bool EL>
+__device__ __forceinline__ void exp_row(float* pt, float* el, int PCS, int b0, int seq, int pad, float mx) {
     float ev[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -133,8 +139,59 @@ __device__ __forceinline__ void exp_row(float* pt, int PCS, int b0, int seq, int
     for (int i = 0; i < NV; i++) {
         const int t2 = b0 + (int)threadIdx.x + i * kDecThreads;
         const float e = t2 < seq ? expf_rn(ev[i] - mx) : 0.0f;
-        if (t2 < pad) pt[(t2 & 7) * PCS + (t2 >> 3)] = e;
+        if (t2 < pad) {
+            pt[(t2 & 7) * PCS + (t2 >> 3)] = e;
+            if constexpr (EL) el[t2] = e;
+        }
     }
+}
+
+// s_waitcnt lgkmcnt(N) tied to the 8 registers of one block of the serial
+// sum (see lgkm_wait_tie)
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tie8(vf4 (&r)[8]) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+                 : "n"(N)
+                 : "memory");
+}
+// The reads of one block (32 consecutive floats at LDS offset a), untracked
+__device__ __forceinline__ void sum_block_reads(vf4 (&r)[8], unsigned a) {
+    r[0] = lds_read_b128<0>(a);
+    r[1] = lds_read_b128<16>(a);
+    r[2] = lds_read_b128<32>(a);
+    r[3] = lds_read_b128<48>(a);
+    r[4] = lds_read_b128<64>(a);
+    r[5] = lds_read_b128<80>(a);
+    r[6] = lds_read_b128<96>(a);
+    r[7] = lds_read_b128<112>(a);
+}
+__device__ __forceinline__ float sum_block_adds(float sum, const vf4 (&r)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) sum = fadd(sum, r[k][c]);
+    return sum;
+}
+// ((0 + e[0]) + e[1]) + ... over nblk blocks of 32 (nblk even; one lane):
+// the next block's reads are in flight while the current one is added.
+__device__ __forceinline__ float lds_serial_sum_blocks(const float* e, int nblk) {
+    const unsigned a0 = lds_addr(e);
+    vf4 ra[8], rb[8];
+    float sum = 0.0f;
+    sum_block_reads(ra, a0);
+    for (int b = 0; b < nblk; b += 2) {
+        sum_block_reads(rb, a0 + 128u * (unsigned)(b + 1));
+        lgkm_wait_tie8<8>(ra);
+        sum = sum_block_adds(sum, ra);
+        // (past the last block: a re-read of block 0, never used)
+        sum_block_reads(ra, a0 + (b + 2 < nblk ? 128u * (unsigned)(b + 2) : 0u));
+        lgkm_wait_tie8<8>(rb);
+        sum = sum_block_adds(sum, rb);
+    }
+    lgkm_wait_tie8<0>(ra);
+    return sum;
 }
 
 constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decode kernel)
@@ -253,6 +310,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     float* part = vt + n_vt * kVTileFloats;
     float* outl = part + kDecChains;
     float* red = outl + kDecDims;
+    float* el = red + 16;   // exponentials in position order (!LONG)
     const float* __restrict__ qh = sq + (size_t)h * HD;
     const int col0 = kvh * HD + ds * kDecDims;
     // keys of this kv head through a buffer descriptor: a per-lane 32-bit
@@ -369,11 +427,11 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         // up to 8 independent exponentials per thread and round (the
         // polynomial is a chain of dependent double-precision steps)
         const int nv = (pad + kDecThreads - 1) / kDecThreads;
-        if (nv <= 1) exp_row<1>(pt, PCS, 0, seq, pad, mx);
-        else if (nv == 2) exp_row<2>(pt, PCS, 0, seq, pad, mx);
-        else if (nv <= 4) exp_row<4>(pt, PCS, 0, seq, pad, mx);
+        if (nv <= 1) exp_row<1, !LONG>(pt, el, PCS, 0, seq, pad, mx);
+        else if (nv == 2) exp_row<2, !LONG>(pt, el, PCS, 0, seq, pad, mx);
+        else if (nv <= 4) exp_row<4, !LONG>(pt, el, PCS, 0, seq, pad, mx);
         else
-            for (int b0 = 0; b0 < pad; b0 += 8 * kDecThreads) exp_row<8>(pt, PCS, b0, seq, pad, mx);
+            for (int b0 = 0; b0 < pad; b0 += 8 * kDecThreads) exp_row<8, !LONG>(pt, el, PCS, b0, seq, pad, mx);
     }
     lds_barrier();
     // the first V tiles start now, issued by the DMA wavefronts while
@@ -381,44 +439,19 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     if (dma_wave)
         for (int t = 0; t < n_tiles && t < n_vt; t++)
             v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
-    const bool wave_sum = seq > kWaveSumSeq;
-    if (wave_sum && tid < 64) {
-        // one wavefront, rows of 64 positions (see wave_serial_sum)
+    const bool wave_sum = LONG || seq > kWaveSumSeq;
+    if (LONG && tid < 64) {
+        // one wavefront, from the transposed row
         const float sum = wave_serial_sum_at([pt, PCS](int i) { return pt[(i & 7) * PCS + (i >> 3)]; }, seq);
         if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    } else if (!LONG && wave_sum && tid < 64) {
+        // one wavefront, rows of 64 positions (see wave_serial_sum)
+        const float sum = wave_serial_sum(el, seq);
+        if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     } else if (!wave_sum && tid == 0) {
-        // blocks of 32 positions = 4 columns of the 8 rows, read as 8 vf4s.
-        // Per block: 7 of the next block's reads, the block's first column
-        // (8 adds), the next block's 8th read, the other 3 columns -- so the
-        // reads land under the adds, and no more than 15 LDS reads are ever
-        // outstanding (lgkmcnt counts to 15; beyond that the compiler can
-        // only wait for all of them).  The number of blocks is even and the
-        // zero padding adds nothing.
-        const int nblk = pad / 32;
-        float sum = 0.0f;
-        vf4 va[8], vb[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) va[j] = *reinterpret_cast<const vf4*>(pt + j * PCS);
-        // the first block lands before the loop (reads pending at the loop
-        // head would make the compiler wait for all of them there)
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
-        auto block = [&](vf4 (&cur)[8], vf4 (&nxt)[8], int bn) {
-#pragma unroll
-            for (int j = 0; j < 7; j++) nxt[j] = *reinterpret_cast<const vf4*>(pt + j * PCS + 4 * bn);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < 8; j++) sum = fadd(sum, cur[j][0]);
-            nxt[7] = *reinterpret_cast<const vf4*>(pt + 7 * PCS + 4 * bn);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int c = 1; c < 4; c++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) sum = fadd(sum, cur[j][c]);
-        };
-        for (int b = 0; b < nblk; b += 2) {
-            block(va, vb, b + 1);
-            block(vb, va, b + 2 < nblk ? b + 2 : b);
-        }
+        // the exponentials in position order, blocks of 32 (pad / 32 is even;
+        // the zero padding adds nothing)
+        const float sum = lds_serial_sum_blocks(el, pad / 32);
         red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     lds_barrier();
@@ -854,9 +887,6 @@ hipError_t launch_attention(const float* sq, const float* kc, const float* vc, c
 
 size_t attn_decode_lds_bytes(int max_seq) { return attn_decode_lds_floats(max_seq) * sizeof(float); }
 
-
-// contexts longer than this take the scores kernel + the decode kernel
-constexpr int kAttnSplitSeq = 4096;
 bool attn_decode_split(int max_seq) { return max_seq > kAttnSplitSeq; }
 // Head size 64 or 128 with 2, 4 or 8 query heads per kv head runs the
 // four-kernel path, whose softmax streams rows of any length; every other

@@ -66,7 +66,7 @@ struct StepState {
     int32_t pos;               // position of the first token of this call
     uint32_t token;            // decode input token (next greedy token after a step)
     uint32_t n_out;            // tokens written to the output ring so far
-    uint32_t pad;
+    uint32_t logits_done;      // logits workgroups done in this step (zero between steps)
     unsigned long long argmax; // packed argmax key of the current step
 };
 
@@ -143,10 +143,9 @@ hipError_t launch_rope(const float* cos_t, const float* sin_t, const StepState* 
 hipError_t launch_swiglu_quant(int qfmt, const float* gate, const float* up, int hidden, int batch,
                                float* h_f32, int8_t* hq, float* hs, hipStream_t s);
 size_t logits_lds_bytes(int dim);
-int logits_blocks(const EmbQ8& e);
 // logits pass (keys: logits_blocks() per-workgroup argmax keys) + finalize
 hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, float eps, float* logits,
-                         unsigned long long* keys, StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
+                         StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
                          hipStream_t s);
 hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
                                 float* div_out, float* f16_out, hipStream_t s);

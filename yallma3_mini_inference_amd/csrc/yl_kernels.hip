@@ -178,7 +178,7 @@ __global__ void k_set_state(StepState* st, int32_t pos, uint32_t token) {
         st->pos = pos;
         st->token = token;
         st->n_out = 0;
-        st->pad = 0;
+        st->logits_done = 0;
         st->argmax = 0ull;
     }
 }

@@ -9,9 +9,9 @@
 // in the reference's order.  The embedding value is the exact f32 product
 // q * scale of the Q8_0 table (transformer_llama_gguf.rs:465-470).
 // Each workgroup writes the maximum of its rows as a packed 64-bit key
-// (larger value, then smaller index); k_finalize reduces the keys, turns the
-// winner into the next token, appends it to the output ring and advances
-// the position.
+// (larger value, then smaller index) into a device-scope atomic max and
+// counts itself done; the last workgroup to finish turns the winner into
+// the next token, appends it to the output ring and advances the position.
 #include <hip/hip_runtime.h>
 
 #include "yl_blocks.h"
@@ -35,7 +35,8 @@ constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each)
 __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* __restrict__ x,
                                                           const float* __restrict__ norm_w, float eps,
                                                           float* __restrict__ logits,
-                                                          unsigned long long* __restrict__ keys) {
+                                                          StepState* st, uint32_t* __restrict__ ring,
+                                                          uint32_t ring_cap, int advance) {
     extern __shared__ __align__(16) float lds[];
     __shared__ unsigned long long wkey[kLogitThreads / 64];
     constexpr int MP = 8192 / 8 / kLogitThreads;   // dim <= 8192
@@ -131,30 +132,23 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     }
     if (lane == 0) wkey[wave] = kk;
     __syncthreads();
-    if (tid == 0) {
-        unsigned long long m = wkey[0];
-        for (int w = 1; w < kLogitThreads / 64; w++) m = wkey[w] > m ? wkey[w] : m;
-        keys[blockIdx.x] = m;
-    }
-}
-
-// Greedy step end: maximum of the per-workgroup keys -> next token, appended
-// to the output ring, position advanced.
-__global__ __launch_bounds__(512) void k_finalize(const unsigned long long* __restrict__ keys, int n, StepState* st,
-                                                  uint32_t* __restrict__ ring, uint32_t ring_cap, int advance) {
-    __shared__ unsigned long long wk[8];
-    unsigned long long m = 0ull;
-    for (int i = threadIdx.x; i < n; i += 512) m = keys[i] > m ? keys[i] : m;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o2 = __shfl_xor(m, off, 64);
-        m = o2 > m ? o2 : m;
-    }
-    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x != 0) return;
-    m = wk[0];
-    for (int w = 1; w < 8; w++) m = wk[w] > m ? wk[w] : m;
+    if (tid != 0) return;
+    unsigned long long m = wkey[0];
+    for (int w = 1; w < kLogitThreads / 64; w++) m = wkey[w] > m ? wkey[w] : m;
+    // The step's key is the maximum over the workgroups' keys, kept by a
+    // device-scope atomic max in the step state; then this workgroup counts
+    // itself done.  The count's increment depends on the value the max
+    // returned, so it is performed after the max; the workgroup that
+    // counts last sees every workgroup's max.
+    unsigned long long prev = __hip_atomic_fetch_max(&st->argmax, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t one = 1u;
+    asm volatile("" : "+v"(one) : "v"(prev));
+    const uint32_t done = __hip_atomic_fetch_add(&st->logits_done, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done != gridDim.x - 1) return;
+    // Greedy step end: the winner -> next token, appended to the output ring,
+    // position advanced; the key and the count return to zero for the next
+    // step.
+    m = __hip_atomic_load(&st->argmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // (every key is nonzero: a row's key is zero only for a NaN past row 0,
     // and row 0's key is never zero)
     const uint32_t tok = m ? 0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull) : 0u;
@@ -162,13 +156,15 @@ __global__ __launch_bounds__(512) void k_finalize(const unsigned long long* __re
     if (ring && st->n_out < ring_cap) ring[st->n_out] = tok;
     st->n_out += 1;
     st->pos += advance;
+    __hip_atomic_store(&st->argmax, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&st->logits_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 size_t logits_lds_bytes(int dim) { return ((size_t)((dim + 63) & ~63) + rowq_lds_floats(dim)) * sizeof(float); }
-int logits_blocks(const EmbQ8& e) { return (e.tiles + kLogitThreads / 64 - 1) / (kLogitThreads / 64); }
+static int logits_blocks(const EmbQ8& e) { return (e.tiles + kLogitThreads / 64 - 1) / (kLogitThreads / 64); }
 
 hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, float eps, float* logits,
-                         unsigned long long* keys, StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
+                         StepState* st, uint32_t* ring, uint32_t ring_cap, int advance,
                          hipStream_t s) {
     const int nblk = logits_blocks(e);
     if (e.dim % 32 || e.dim > 8192) return hipErrorInvalidValue;
@@ -179,10 +175,7 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
         if (err != hipSuccess) return err;
     }
     hipLaunchKernelGGL(k_logits, dim3(nblk), dim3(kLogitThreads), logits_lds_bytes(e.dim), s, e, x, norm_w, eps,
-                       logits, keys);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_finalize, dim3(1), dim3(512), 0, s, keys, nblk, st, ring, ring_cap, advance);
+                       logits, st, ring, ring_cap, advance);
     return hipGetLastError();
 }
 

@@ -278,7 +278,6 @@ struct yl_session {
     float *x = nullptr, *sq = nullptr, *logits = nullptr;
     int8_t *aq = nullptr, *hq = nullptr, *nq = nullptr;   // nq/ns: normalized, quantized rows (prompt)
     float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
-    unsigned long long* keys = nullptr;  // per-workgroup argmax keys of the logits pass
     float* sc = nullptr;                 // attention scores of long contexts [n_heads][ctx]
     float* psc = nullptr;                // prompt attention scratch (batches of 64+ tokens)
     size_t psc_bytes = 0;
@@ -639,7 +638,7 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     if (cls == kOpLogits) {
         // final RMSNorm + logits of the last token + argmax + step bookkeeping
         if (bytes) *bytes = (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4;
-        return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->keys,
+        return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits,
                              s->st, s->ring, s->ring_cap, advance, st);
     }
     const Layer& L = m->layers[l];
@@ -769,7 +768,7 @@ yl_status put_state(yl_session* s, int32_t pos, uint32_t token) {
     s->st_host->pos = pos;
     s->st_host->token = token;
     s->st_host->n_out = 0;
-    s->st_host->pad = 0;
+    s->st_host->logits_done = 0;
     s->st_host->argmax = 0ull;
     const hipError_t e = hipMemcpyAsync(s->st, s->st_host, sizeof(StepState), hipMemcpyHostToDevice, s->stream);
     return e == hipSuccess ? YL_OK : hip_fail(e, "state upload");
@@ -1224,7 +1223,7 @@ yl_session* yl_create_session(const yl_model* m) {
               hipHostMalloc(&s->st_host, sizeof(StepState), 0) == hipSuccess &&
               hipMalloc(&s->logits, (size_t)m->vocab * 4 + 256) == hipSuccess &&
               hipMalloc(&s->ring, (size_t)s->ring_cap * 4 + 256) == hipSuccess &&
-              hipMalloc(&s->keys, (size_t)logits_blocks(m->emb) * 8 + 256) == hipSuccess && session_grow(s, 1);
+              session_grow(s, 1);
     const size_t sc_bytes = attn_scores_bytes(m->n_heads, m->ctx);
     if (ok && sc_bytes) ok = hipMalloc(&s->sc, sc_bytes) == hipSuccess;
     if (!ok) {
@@ -1240,7 +1239,7 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->nq, s->ns, s->keys, s->tokens, s->sc, s->psc};
+                   s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
