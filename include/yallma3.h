@@ -277,6 +277,12 @@ yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt
 yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, uint32_t segment,
                                  float *out);
 
+/* Probe of the timeout report: a kernel on the null stream marks the process's
+ * fault word the way a GEMV's bounded internal wait does when it gives up, so
+ * the next synchronizing call (yl_synchronize, yl_forward_x, ...) returns
+ * YL_ERR_HIP with a message, and clears the word. */
+yl_status yl_wait_fault_selftest(void);
+
 /* ----------------------------------------------------- synthetic models */
 typedef struct {
     uint32_t dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx_len;

@@ -304,3 +304,15 @@ def test_serial_sum_exact(gpu):
         got = ops.serial_sum_selftest(segs, piece)
         assert np.array_equal(np.isnan(got), nan), piece
         assert_bits(got[~nan], ref[~nan])
+
+
+def test_timed_out_wait_is_reported(gpu):
+    # A GEMV whose bounded internal wait gives up marks the fault word; the
+    # next synchronizing call must fail with a message and clear the word.
+    from yallma3_mini_inference_amd._lib import lib, last_error, YL_OK
+    L = lib()
+    assert L.yl_synchronize() == YL_OK
+    assert L.yl_wait_fault_selftest() == YL_OK
+    st = L.yl_synchronize()
+    assert st != YL_OK and "timed out" in last_error()
+    assert L.yl_synchronize() == YL_OK

@@ -27,7 +27,7 @@ EXPORTS = [
     "yl_model_free", "yl_model_name", "yl_model_shape", "yl_vocab_size", "yl_max_ctx_len", "yl_bos_token",
     "yl_eos_token", "yl_model_weight_bytes", "yl_model_embedding_bytes", "yl_get_embeddings",
     "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_pos", "yl_session_set_pos",
-    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest", "yl_serial_sum_selftest",
+    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest", "yl_serial_sum_selftest", "yl_wait_fault_selftest",
     "yl_write_synthetic_gguf", "yl_synthetic_normal",
 ]
 
@@ -125,6 +125,7 @@ def lib():
                                    C.POINTER(u32)]),
         "yl_math_selftest": (st, [vp, sz, vp, vp, vp, vp]),
         "yl_serial_sum_selftest": (st, [vp, vp, sz, u32, vp]),
+        "yl_wait_fault_selftest": (st, []),
         "yl_write_synthetic_gguf": (st, [C.c_char_p, C.POINTER(SynthConfig)]),
         "yl_synthetic_normal": (st, [u64, u64, u64, sz, f32, vp]),
     }

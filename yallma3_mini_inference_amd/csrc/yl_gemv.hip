@@ -167,15 +167,19 @@ __host__ __device__ inline GemvLds gemv_lds(int n, int nb, int R, bool norm) {
 // accesses in order, and a waiter's reads of the published data are issued
 // only after it saw the count.  The waits are bounded: the counted
 // wavefronts always arrive within microseconds, the bound only keeps a
-// defect from hanging the device.
+// defect from hanging the device; a wait that gives up sets *fault, which the
+// host reads after the call and reports as an error.
 __device__ __forceinline__ void lds_arrive(int* ctr) {
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's LDS writes done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void lds_wait_count(int* ctr, int target) {
-    for (int i = 0; __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && i < (1 << 22); i++)
+__device__ __forceinline__ void lds_wait_count(int* ctr, int target, unsigned* fault) {
+    int i = 0;
+    for (; __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && i < (1 << 22); i++)
         __builtin_amdgcn_s_sleep(1);
+    if (i == (1 << 22) && fault && (threadIdx.x & 63) == 0)
+        __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
@@ -357,12 +361,12 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             }
             // the serial sum of squares (wavefront 0, lanes 0-7) -> ss
             if (wave == 0) {
-                lds_wait_count(ctr_sq, NA);
+                lds_wait_count(ctr_sq, NA, a.fault);
                 const float ss = rowq_chain(dim, a.eps, sq);
                 if (lane == 0) *ssl = ss;
                 lds_arrive(ctr_ss);
             }
-            lds_wait_count(ctr_ss, 1);
+            lds_wait_count(ctr_ss, 1, a.fault);
             const float ss = *ssl;
             // o = w * (ss * x) and the 32-group quantization of the member's
             // slices (the 4 lanes of a quad hold one 32-group)
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         if constexpr (EPI == kEpiResid) resid = a.x[(size_t)t * o + min(my_row, o - 1)];
         __builtin_amdgcn_sched_barrier(0);
 
-        lds_wait_count(ctr_row, NA);
+        lds_wait_count(ctr_row, NA, a.fault);
         float acc = initl[min(w * RW + my_r, R - 1)];
 #pragma unroll
         for (int k = 0; k < PPL; k++) {
@@ -619,9 +623,11 @@ static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t s
     }
 }
 
-hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s) {
-    if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (a.n % 32 || a.n > 4096)) return hipErrorInvalidValue;
-    if (a.n % 32 || a.n > 16384 || a.o <= 0) return hipErrorInvalidValue;
+hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipStream_t s) {
+    if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (args.n % 32 || args.n > 4096)) return hipErrorInvalidValue;
+    if (args.n % 32 || args.n > 16384 || args.o <= 0) return hipErrorInvalidValue;
+    GemvArgs a = args;
+    a.fault = wait_fault_word(false);
     if (wfmt == kQ8) return launch_wf<kQ8>(a, epi, batch, s);
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);
     return hipErrorInvalidValue;

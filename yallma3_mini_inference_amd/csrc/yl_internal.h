@@ -95,7 +95,13 @@ struct GemvArgs {
     const StepState* state;
     // kEpiSwiglu
     int8_t* hq; float* hs; float* h_f32; int hidden; int h_fmt;
+    // set to nonzero when a bounded wait inside the kernel gives up (its
+    // results are then invalid); a word of pinned host memory, or null
+    unsigned* fault;
 };
+// The process's fault word (pinned host memory, allocated on the first call
+// with `allocate`; null before that or if the allocation failed).
+unsigned* wait_fault_word(bool allocate);
 
 // kernel launchers; all return the hipError_t of the launch
 hipError_t launch_set_state(StepState* st, int32_t pos, uint32_t token, hipStream_t s);
@@ -150,6 +156,7 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
 hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sqrt_out,
                                 float* div_out, float* f16_out, hipStream_t s);
 
+hipError_t launch_raise_fault(unsigned* fault, hipStream_t s);
 hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
                                       hipStream_t s);
 

@@ -253,6 +253,15 @@ hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sq
     return hipGetLastError();
 }
 
+// what a bounded wait that gives up does to the fault word
+__global__ void k_raise_fault(unsigned* fault) {
+    if (threadIdx.x == 0) __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+hipError_t launch_raise_fault(unsigned* fault, hipStream_t s) {
+    hipLaunchKernelGGL(k_raise_fault, dim3(1), dim3(64), 0, s, fault);
+    return hipGetLastError();
+}
+
 hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
                                       hipStream_t s) {
     if (cases <= 0) return hipSuccess;

@@ -765,16 +765,37 @@ yl_status hip_fail(hipError_t e, const char* what) {
 }
 
 yl_status put_state(yl_session* s, int32_t pos, uint32_t token) {
-    s->st_host->pos = pos;
-    s->st_host->token = token;
-    s->st_host->n_out = 0;
-    s->st_host->logits_done = 0;
-    s->st_host->argmax = 0ull;
-    const hipError_t e = hipMemcpyAsync(s->st, s->st_host, sizeof(StepState), hipMemcpyHostToDevice, s->stream);
+    const hipError_t e = launch_set_state(s->st, pos, token, s->stream);
     return e == hipSuccess ? YL_OK : hip_fail(e, "state upload");
 }
 
+// A word of pinned host memory that kernels set when one of their bounded
+// waits gives up; every synchronizing call reads and clears it.
+std::mutex g_fault_mu;
+unsigned* g_fault = nullptr;
+
+yl_status check_wait_fault(const char* what) {
+    unsigned* f = wait_fault_word(false);
+    if (f && __atomic_exchange_n(f, 0u, __ATOMIC_ACQ_REL)) {
+        set_error(std::string(what) + ": a kernel's bounded wait timed out; the results of this call are invalid");
+        return YL_ERR_HIP;
+    }
+    return YL_OK;
+}
+
 }  // namespace
+
+unsigned* yl::wait_fault_word(bool allocate) {
+    std::lock_guard<std::mutex> lk(g_fault_mu);
+    if (!g_fault && allocate) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, 64, hipHostMallocCoherent | hipHostMallocPortable) == hipSuccess) {
+            g_fault = static_cast<unsigned*>(p);
+            *g_fault = 0u;
+        }
+    }
+    return g_fault;
+}
 
 // ============================================================== C ABI ====
 
@@ -815,7 +836,7 @@ yl_status yl_memset_d(void* dst, int value, size_t bytes) {
 }
 yl_status yl_synchronize(void) {
     const hipError_t e = hipDeviceSynchronize();
-    return e == hipSuccess ? YL_OK : hip_fail(e, "hipDeviceSynchronize");
+    return e == hipSuccess ? check_wait_fault("yl_synchronize") : hip_fail(e, "hipDeviceSynchronize");
 }
 
 yl_status yl_quantize(yl_format fmt, int8_t* q, float* scale, const float* x, size_t n, uint32_t gs, void* stream) {
@@ -854,6 +875,7 @@ yl_weight* yl_weight_upload(yl_format fmt, const int8_t* qv, const float* sf, si
             h.qs[i] = (uint8_t)(lo | (hi << 4));
         }
     }
+    wait_fault_word(true);
     auto* w = new yl_weight();
     std::string err;
     if (!upload_qmat(h, &w->m, &err)) { set_error(err); free_qmat(&w->m); delete w; return nullptr; }
@@ -869,6 +891,7 @@ yl_weight* yl_weight_upload_gguf(yl_format fmt, const void* blocks, size_t o, si
     std::string err;
     const uint32_t type = fmt == YL_Q4_0 ? kGgmlQ4_0 : kGgmlQ8_0;
     if (!host_from_gguf(type, (const uint8_t*)blocks, ~0ull, o, n, &h, &err)) { set_error(err); return nullptr; }
+    wait_fault_word(true);
     auto* w = new yl_weight();
     if (!upload_qmat(h, &w->m, &err)) { set_error(err); free_qmat(&w->m); delete w; return nullptr; }
     return w;
@@ -947,6 +970,7 @@ yl_status yl_matmul_bench(const yl_weight* const* ws, size_t count, const int8_t
     if (g) hipGraphDestroy(g);
     hipStreamDestroy(st);
     if (e != hipSuccess) return hip_fail(e, "matmul_bench");
+    if (check_wait_fault("matmul_bench") != YL_OK) return YL_ERR_HIP;
     if (us_per_launch) *us_per_launch = (double)ms * 1000.0 / ((double)reps * (double)count);
     return YL_OK;
 }
@@ -1180,6 +1204,13 @@ yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) 
 
 void yl_model_free(yl_model* m) { model_release(m); }
 const char* yl_model_name(const yl_model* m) { return m ? m->name.c_str() : ""; }
+yl_status yl_wait_fault_selftest(void) {
+    unsigned* f = wait_fault_word(true);
+    if (!f) { set_error("wait_fault_selftest: no fault word (pinned allocation failed)"); return YL_ERR_HIP; }
+    const hipError_t e = launch_raise_fault(f, nullptr);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "wait_fault_selftest");
+}
+
 yl_status yl_model_shape(const yl_model* m, yl_shape* out) {
     if (!m || !out) return YL_ERR_ARG;
     *out = m->shape;
@@ -1209,6 +1240,7 @@ yl_status yl_get_embeddings(const yl_model* m, const uint32_t* tokens, size_t n,
 
 yl_session* yl_create_session(const yl_model* m) {
     if (!m) { set_error("null model"); return nullptr; }
+    wait_fault_word(true);
     auto* s = new yl_session();
     s->m = m;
     s->kv_floats = (size_t)m->n_layers * m->kv_ld * m->kv;
@@ -1298,6 +1330,7 @@ yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint
     e = hipMemcpyAsync(s->st_host, s->st, sizeof(StepState), hipMemcpyDeviceToHost, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return hip_fail(e, "forward_x");
+    if (check_wait_fault("forward_x") != YL_OK) return YL_ERR_HIP;
     if (argmax) *argmax = s->st_host->token;
     return YL_OK;
 }
@@ -1329,7 +1362,7 @@ yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, u
     hipError_t e = hipSuccess;
     if (out_tokens) e = hipMemcpyAsync(out_tokens, s->ring, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? YL_OK : hip_fail(e, "generate");
+    return e == hipSuccess ? check_wait_fault("generate") : hip_fail(e, "generate");
 }
 
 yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, uint32_t batch,
@@ -1383,6 +1416,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     if (e1) hipEventDestroy(e1);
     hipGraphExecDestroy(ge);
     if (e != hipSuccess) return hip_fail(e, "profile");
+    if (check_wait_fault("profile") != YL_OK) return YL_ERR_HIP;
     if (us_per_launch) *us_per_launch = (double)ms * 1000.0 / ((double)reps * n_launch);
     // (the replays leave the prompt buffers of the session in use)
     if (bytes_per_launch) *bytes_per_launch = nbytes / (uint64_t)n_launch;

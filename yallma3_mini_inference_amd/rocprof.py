@@ -14,6 +14,16 @@
         contains "copy" or "elementwise") scales each counter to real bytes.
         Writes the median scaled FETCH + WRITE bytes per decode dispatch (the
         class's dispatches with the smallest grid).
+
+    python -m yallma3_mini_inference_amd.rocprof mfma COUNTERS.csv KERNEL_TRACE.csv PATTERN
+        MFMA utilisation of the kernels whose name contains PATTERN, from one
+        `rocprofv3 --kernel-trace --pmc SQ_VALU_MFMA_BUSY_CYCLES
+        SQ_INSTS_VALU_MFMA_MOPS_I8 GRBM_GUI_ACTIVE` run: per kernel and grid,
+        the dispatches' MFMA-busy share of the SIMD cycles (busy cycles summed
+        over the SIMDs / (GUI-active cycles of one XCD x 1024 SIMDs),
+        rocprofv3's MfmaUtil), the int8 MFMA operations (MOPS_I8 x 512) and those
+        operations per second of dispatch time, against the 5.0 POP/s dense
+        int8 peak.
 """
 import csv
 import collections
@@ -99,11 +109,57 @@ def pmc(fetch_csv, write_csv, mib, cls, out):
     print(json.dumps(res))
 
 
+def _counters(path):
+    """{dispatch id: (kernel name, {counter: [values over dimensions]})}"""
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = r["Dispatch_Id"]
+            name, cs = out.setdefault(d, (r["Kernel_Name"], collections.defaultdict(list)))
+            cs[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return out
+
+
+SIMDS = 1024            # 256 CUs x 4 SIMDs
+XCDS = 8
+INT8_PEAK = 5.0e15      # dense int8 MFMA operations per second
+
+
+def mfma(counter_csv, trace_csv, pattern):
+    dur = {}
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            dur[r["Dispatch_Id"]] = ((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9,
+                                     r["Grid_Size_X"], r["Grid_Size_Y"])
+    by = collections.defaultdict(list)
+    for d, (name, cs) in _counters(counter_csv).items():
+        if pattern not in name or d not in dur:
+            continue
+        busy = sum(cs.get("SQ_VALU_MFMA_BUSY_CYCLES", [0.0]))
+        # rocprofv3 reports GRBM_GUI_ACTIVE summed over the XCDs
+        gui = sum(cs.get("GRBM_GUI_ACTIVE", [0.0])) / XCDS
+        ops = sum(cs.get("SQ_INSTS_VALU_MFMA_MOPS_I8", [0.0])) * 512.0
+        t, gx, gy = dur[d]
+        by[(_short(name), gx, gy)].append((busy / (gui * SIMDS) * 100.0 if gui else 0.0, ops, t))
+    print("| dispatches | kernel | grid (x, y) | MFMA busy % (median) | int8 MFMA ops / dispatch | mean us "
+          "| int8 TOP/s | % of 5.0 POP/s |")
+    print("|---|---|---|---|---|---|---|---|")
+    for k, v in sorted(by.items(), key=lambda kv: -sum(x[2] for x in kv[1])):
+        util = statistics.median(x[0] for x in v)
+        ops = statistics.median(x[1] for x in v)
+        t = statistics.mean(x[2] for x in v)
+        rate = ops / t if t else 0.0
+        print(f"| {len(v)} | `{k[0]}` | {k[1]}, {k[2]} | {util:.1f} | {ops:.4g} | {t * 1e6:.1f} | "
+              f"{rate / 1e12:.1f} | {100.0 * rate / INT8_PEAK:.2f} |")
+
+
 if __name__ == "__main__":
     if len(sys.argv) >= 3 and sys.argv[1] == "trace":
         trace(sys.argv[2])
     elif len(sys.argv) >= 7 and sys.argv[1] == "pmc":
         pmc(sys.argv[2], sys.argv[3], int(sys.argv[4]), sys.argv[5], sys.argv[6])
+    elif len(sys.argv) >= 5 and sys.argv[1] == "mfma":
+        mfma(sys.argv[2], sys.argv[3], sys.argv[4])
     else:
         print(__doc__)
         sys.exit(2)
