@@ -71,12 +71,13 @@ def sample_kv(shape, prompt_len):
     return rng.standard_normal(dims, dtype=np.float32), rng.standard_normal(dims, dtype=np.float32)
 
 
-def gpu_sample(model, kv, prompt_len):
+def gpu_sample(model, kv, prompt_len, attention):
     """The HIP path on the sample: forward_x one token at a time from token 1
     at prompt_len, greedy; returns (per-step logits, tokens)."""
     import numpy as np
     import yallma3_mini_inference_amd as Y
     sess = model.create_session()
+    sess.set_attention(attention)
     sess.upload_kv(*kv)
     tok, logits, toks = 1, [], []
     for i in range(SAMPLE_STEPS):
@@ -271,6 +272,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
     ap.add_argument("--config", default="llama32_1b", choices=sorted(DECODE),
                     help="decode workload: llama32_1b (the headline), smollm2_135m, llama3_8b_mixed")
+    ap.add_argument("--attention", choices=("exact", "split"), default="exact",
+                    help="decode attention: exact (the reference's operation order, bit-exact; the default) or "
+                         "split over the context (equal up to rounding; on these synthetic models rounding-level "
+                         "differences can move the logits by more than 1e-3 at some steps)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("decode", "prefill", "matvec"), default="decode",
@@ -324,6 +329,9 @@ def main():
     t0 = time.perf_counter()
     model = Y.Transformer(path)
     sess = model.create_session()
+    attention = args.attention
+    sess.set_attention(attention)
+    log(f"decode attention: {attention}")
     log(f"loaded to HBM in {time.perf_counter() - t0:.1f}s; GEMV weights {model.weight_bytes()} B/token, "
         f"logits embedding {model.embedding_bytes()} B/token")
     ctx = model.max_ctx_len()
@@ -396,6 +404,8 @@ def main():
             "batch": 1, "prompt_tokens": args.prompt,
             "decode_positions": f"{args.prompt + args.warmup}..{args.prompt + args.warmup + args.steps - 1}",
             "parallelism": "single GPU",
+            "attention": ("exact (the reference's operation order)" if attention == "exact" else
+                          "split over the context (f32 combine)"),
         },
         "roofline": {
             "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -412,7 +422,7 @@ def main():
     if not args.no_cpu_baseline:
         sess.close()
         kv = sample_kv(model.shape, args.prompt)
-        gpu = gpu_sample(model, kv, args.prompt)
+        gpu = gpu_sample(model, kv, args.prompt, attention)
         model.close()
         rec, cl, ct = cpu_baseline(path, args.prompt, args.cpu_seconds, kv)
         result["cpu_baseline"] = rec

@@ -162,6 +162,16 @@ yl_status yl_attention(float *out, const float *q, const float *key_cache, const
                        size_t batch, uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads,
                        uint32_t head_size, float attn_scale, void *stream);
 
+/* The split decode attention of YL_ATTN_SPLIT as an op (no counterpart in
+ * the reference: fused_attention's quantity with the context split over many
+ * workgroups, equal to it up to rounding): one query row q [n_heads*head_size]
+ * at position start_pos over a cache [start_pos+1][kv_dim] (device), out
+ * [n_heads*head_size] f32.  Head size 64 or 128 with 1, 2, 4 or 8 query heads
+ * per kv head. */
+yl_status yl_attention_split(float *out, const float *q, const float *key_cache, const float *value_cache,
+                             uint32_t start_pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_size,
+                             float attn_scale, void *stream);
+
 /* yl_attention without any allocation: no counterpart in the reference; for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
@@ -217,6 +227,19 @@ yl_status yl_get_embeddings(const yl_model *m, const uint32_t *tokens, size_t n,
 yl_session *yl_create_session(const yl_model *m);
 void yl_session_free(yl_session *s);
 yl_status yl_session_reset(yl_session *s);
+
+/* Decode attention of a session (one token per forward_x / generate step).
+ * YL_ATTN_EXACT (the default) is fused_attention (forward.rs:299-400) in the
+ * reference's operation order, bit for bit.  YL_ATTN_SPLIT has no
+ * counterpart in the reference: it computes the same softmax-weighted sum
+ * with the context split over many workgroups (running maxima and sums
+ * combined in f32, a hardware exp2), so its results differ in rounding only,
+ * for callers whose bar is a tolerance rather than identical bits; it reads
+ * contexts of any length.  Head size 64 or 128 with 1, 2, 4 or 8 query heads
+ * per kv head, else YL_ERR_UNSUPPORTED.  Prompt batches stay exact. */
+#define YL_ATTN_EXACT 0
+#define YL_ATTN_SPLIT 1
+yl_status yl_session_set_attention(yl_session *s, int32_t mode);
 /* InferenceSession.pos: kept for the caller, as in the reference (the
  * forward pass itself only reads start_pos). */
 uint32_t yl_session_pos(const yl_session *s);

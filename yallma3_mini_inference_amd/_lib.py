@@ -23,10 +23,10 @@ EXPORTS = [
     "yl_last_error", "load_transformer_ffi", "infer_ffi", "free_string", "yl_ffi_model", "yl_device_count", "yl_malloc",
     "yl_free", "yl_memcpy_h2d", "yl_memcpy_d2h", "yl_memcpy_d2d", "yl_matmul_bench", "yl_memset_d", "yl_synchronize", "yl_quantize",
     "yl_weight_upload", "yl_weight_upload_gguf", "yl_weight_free", "yl_weight_bytes", "yl_matmul",
-    "yl_rmsnorm_quantize", "yl_rope_gguf", "yl_attention", "yl_attention_noalloc", "yl_swiglu_quantize", "yl_load",
+    "yl_rmsnorm_quantize", "yl_rope_gguf", "yl_attention", "yl_attention_split", "yl_attention_noalloc", "yl_swiglu_quantize", "yl_load",
     "yl_model_free", "yl_model_name", "yl_model_shape", "yl_vocab_size", "yl_max_ctx_len", "yl_bos_token",
     "yl_eos_token", "yl_model_weight_bytes", "yl_model_embedding_bytes", "yl_get_embeddings",
-    "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_pos", "yl_session_set_pos",
+    "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_set_attention", "yl_session_pos", "yl_session_set_pos",
     "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest", "yl_serial_sum_selftest", "yl_wait_fault_selftest",
     "yl_write_synthetic_gguf", "yl_synthetic_normal",
 ]
@@ -100,6 +100,7 @@ def lib():
         "yl_rmsnorm_quantize": (st, [vp, vp, sz, f32, sz, vp, st, vp, vp, vp]),
         "yl_rope_gguf": (st, [C.POINTER(RopeParams), vp, vp, sz, u32, vp]),
         "yl_attention": (st, [vp, vp, vp, vp, sz, u32, u32, u32, u32, f32, vp]),
+        "yl_attention_split": (st, [vp, vp, vp, vp, u32, u32, u32, u32, f32, vp]),
         "yl_attention_noalloc": (st, [vp, vp, vp, vp, sz, u32, u32, u32, u32, f32, vp]),
         "yl_swiglu_quantize": (st, [vp, vp, sz, sz, vp, st, vp, vp, vp]),
         "yl_load": (vp, [C.c_char_p, u32, st]),
@@ -116,6 +117,7 @@ def lib():
         "yl_create_session": (vp, [vp]),
         "yl_session_free": (None, [vp]),
         "yl_session_reset": (st, [vp]),
+        "yl_session_set_attention": (st, [vp, C.c_int32]),
         "yl_session_pos": (u32, [vp]),
         "yl_session_set_pos": (None, [vp, u32]),
         "yl_session_kv": (st, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz)]),

@@ -157,6 +157,15 @@ hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sq
                                 float* div_out, float* f16_out, hipStream_t s);
 
 hipError_t launch_raise_fault(unsigned* fault, hipStream_t s);
+// Decode attention split over the context (tolerance mode): workgroups per
+// kv head, scratch bytes (partials + one count per kv head, the counts zero
+// before the first launch; each launch leaves them zero), and the launch.
+int attn_split_parts(int n_kv_heads);
+size_t attn_split_bytes(int n_heads, int n_kv_heads, int head_size);
+bool attn_split_supported(int n_heads, int n_kv_heads, int head_size);
+hipError_t launch_attn_split(const float* sq, const float* kc, const float* vc, const StepState* st, int kv_ld,
+                             int n_heads, int n_kv_heads, int head_size, float scale, int qfmt, int8_t* aq, float* as,
+                             float* att_f32, float* scratch, hipStream_t s);
 hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
                                       hipStream_t s);
 

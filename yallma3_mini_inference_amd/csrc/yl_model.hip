@@ -293,6 +293,8 @@ struct yl_session {
     };
     std::vector<DecodeGraph> graphs;
     int dec_seq = 0;                     // bucket of the decode step being enqueued
+    int attn_mode = YL_ATTN_EXACT;       // decode attention: exact order, or split over the context
+    float* split = nullptr;              // partials + counts of the split decode attention
     uint64_t prof_seq = 0;               // seq_len of the step yl_profile_kernel times
     uint32_t pos = 0;
 };
@@ -666,6 +668,9 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         if (bytes)
             *bytes = 2ull * s->prof_seq * (uint64_t)m->kv * 4 +
                      (uint64_t)batch * ((uint64_t)m->att * 4 + (uint64_t)m->att + (uint64_t)m->att / 8);
+        if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
+            return launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale,
+                                     L.wo.fmt, s->aq, s->as_, nullptr, s->split, st);
         if (batch == 1)
             return launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
                                       m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, s->sc, st);
@@ -750,7 +755,8 @@ hipGraphExec_t ensure_graph(const yl_model* m, yl_session* s, uint64_t seq_end) 
 }
 
 // Positions a decode step can attend over for this model's head layout.
-bool decode_in_range(const yl_model* m, uint64_t seq_end, const char* what) {
+bool decode_in_range(const yl_model* m, const yl_session* s, uint64_t seq_end, const char* what) {
+    if (s->attn_mode == YL_ATTN_SPLIT) return true;   // the split kernel reads any context length
     const int lim = attn_decode_limit(m->n_heads, m->n_kv, m->hd);
     if (seq_end <= (uint64_t)lim) return true;
     set_error(std::string(what) + ": decode attention for this head layout (head_size " + std::to_string(m->hd) +
@@ -1096,6 +1102,39 @@ yl_status yl_attention(float* out, const float* q, const float* kc, const float*
     return e == hipSuccess ? YL_OK : hip_fail(e, "attention");
 }
 
+yl_status yl_attention_split(float* out, const float* q, const float* kc, const float* vc, uint32_t start_pos,
+                             uint32_t n_heads, uint32_t n_kv_heads, uint32_t hd, float attn_scale, void* stream) {
+    if (!out || !q || !kc || !vc || !n_kv_heads || n_heads % n_kv_heads ||
+        !attn_split_supported((int)n_heads, (int)n_kv_heads, (int)hd)) {
+        set_error("attention_split: head size 64 or 128 with 1, 2, 4 or 8 query heads per kv head");
+        return YL_ERR_ARG;
+    }
+    const size_t seq = (size_t)start_pos + 1, kv_dim = (size_t)n_kv_heads * hd;
+    if (seq >= (1u << 30) || seq * kv_dim * 4 >= (1ull << 31)) {
+        set_error("attention_split: the cache must stay below 2 GiB");
+        return YL_ERR_UNSUPPORTED;
+    }
+    const int ld = ((int)seq + 3) & ~3;
+    const size_t kt_bytes = (size_t)ld * kv_dim * 4, sp_bytes = attn_split_bytes((int)n_heads, (int)n_kv_heads, (int)hd);
+    StepState* dst = nullptr;
+    float *kt = nullptr, *sp = nullptr;
+    hipStream_t strm = (hipStream_t)stream;
+    hipError_t e = hipMalloc(&dst, sizeof(StepState));
+    if (e == hipSuccess) e = hipMalloc(&kt, kt_bytes);
+    if (e == hipSuccess) e = hipMalloc(&sp, sp_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(sp, 0, sp_bytes, strm);
+    if (e == hipSuccess) e = launch_set_state(dst, (int32_t)start_pos, 0u, strm);
+    if (e == hipSuccess) e = launch_transpose(kc, kt, (int)seq, (int)kv_dim, ld, strm);
+    if (e == hipSuccess)
+        e = launch_attn_split(q, kt, vc, dst, ld, (int)n_heads, (int)n_kv_heads, (int)hd, attn_scale, -1, nullptr,
+                              nullptr, out, sp, strm);
+    if (e == hipSuccess) e = hipStreamSynchronize(strm);
+    if (dst) hipFree(dst);
+    if (kt) hipFree(kt);
+    if (sp) hipFree(sp);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "attention_split");
+}
+
 }  // extern "C"
 
 // ---------------------------------------------- allocation-free attention
@@ -1271,11 +1310,40 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc};
+                   s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc, s->split};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
     delete s;
+}
+
+yl_status yl_session_set_attention(yl_session* s, int32_t mode) {
+    if (!s || (mode != YL_ATTN_EXACT && mode != YL_ATTN_SPLIT)) { set_error("set_attention: bad arguments"); return YL_ERR_ARG; }
+    const yl_model* m = s->m;
+    if (mode == YL_ATTN_SPLIT && !attn_split_supported(m->n_heads, m->n_kv, m->hd)) {
+        set_error("set_attention: the split decode attention takes head size 64 or 128 with 1, 2, 4 or 8 query "
+                  "heads per kv head");
+        return YL_ERR_UNSUPPORTED;
+    }
+    if (mode == s->attn_mode) return YL_OK;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "set_attention");
+    if (mode == YL_ATTN_SPLIT && !s->split) {
+        // the counts must start at zero; every launch leaves them zero
+        const size_t bytes = attn_split_bytes(m->n_heads, m->n_kv, m->hd);
+        e = hipMalloc(&s->split, bytes);
+        if (e == hipSuccess) e = hipMemset(s->split, 0, bytes);
+        if (e != hipSuccess) {
+            if (s->split) hipFree(s->split);
+            s->split = nullptr;
+            return hip_fail(e, "set_attention scratch");
+        }
+    }
+    // the decode graphs captured the other attention
+    for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
+    s->graphs.clear();
+    s->attn_mode = mode;
+    return YL_OK;
 }
 
 yl_status yl_session_reset(yl_session* s) {
@@ -1307,7 +1375,7 @@ yl_status yl_forward_x(const yl_model* m, const uint32_t* tokens, size_t n, uint
         return YL_ERR_RANGE;
     }
     if (n > 65535) { set_error("forward_x: more than 65535 tokens in one call"); return YL_ERR_ARG; }
-    if (n == 1 && !decode_in_range(m, (uint64_t)start_pos + 1, "forward_x")) return YL_ERR_RANGE;
+    if (n == 1 && !decode_in_range(m, s, (uint64_t)start_pos + 1, "forward_x")) return YL_ERR_RANGE;
     yl_status rs = put_state(s, (int32_t)start_pos, tokens[0]);
     if (rs != YL_OK) return rs;
     hipError_t e;
@@ -1343,7 +1411,7 @@ yl_status yl_generate_greedy(const yl_model* m, yl_session* s, uint32_t token, u
         set_error("generate: positions beyond ctx_len " + std::to_string(m->ctx));
         return YL_ERR_RANGE;
     }
-    if (!decode_in_range(m, (uint64_t)start_pos + n_steps, "generate")) return YL_ERR_RANGE;
+    if (!decode_in_range(m, s, (uint64_t)start_pos + n_steps, "generate")) return YL_ERR_RANGE;
     yl_status rs = put_state(s, (int32_t)start_pos, token);
     if (rs != YL_OK) return rs;
     // steps of one context bucket replay that bucket's graph (the position
@@ -1374,7 +1442,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
-    if (batch == 1 && !decode_in_range(m, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
+    if (batch == 1 && !decode_in_range(m, s, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
     s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
     s->prof_seq = (uint64_t)start_pos + batch;
     if (batch > 1 && (!session_grow(s, (int)batch) || !prompt_scratch(s, (int)batch, start_pos)))

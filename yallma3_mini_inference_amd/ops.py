@@ -54,6 +54,19 @@ def attention(q: np.ndarray, key_cache: np.ndarray, value_cache: np.ndarray, bat
     return out.numpy()
 
 
+def attention_split(q: np.ndarray, key_cache: np.ndarray, value_cache: np.ndarray, start_pos: int,
+                    n_heads: int, n_kv_heads: int, head_size: int, attn_scale: float) -> np.ndarray:
+    """The split decode attention (one query row at start_pos): equal to
+    fused_attention (forward.rs:299-400) up to rounding."""
+    dq = DeviceBuffer.from_numpy(np.ascontiguousarray(q, np.float32))
+    dk = DeviceBuffer.from_numpy(np.ascontiguousarray(key_cache, np.float32))
+    dv = DeviceBuffer.from_numpy(np.ascontiguousarray(value_cache, np.float32))
+    out = DeviceBuffer.zeros(n_heads * head_size, np.float32)
+    check(lib().yl_attention_split(out.ptr, dq.ptr, dk.ptr, dv.ptr, start_pos, n_heads, n_kv_heads, head_size,
+                                   attn_scale, None))
+    return out.numpy()
+
+
 def swiglu_quantize(gate: np.ndarray, up: np.ndarray, qfmt: int = -1):
     g = np.ascontiguousarray(gate, np.float32)
     batch, hidden = (1, g.size) if g.ndim == 1 else g.shape

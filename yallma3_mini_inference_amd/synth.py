@@ -62,6 +62,10 @@ CONFIGS = {
     # ctx 8448 with 4 query heads per kv head (head size 64): decode beyond
     # 4096 positions runs the four-kernel split attention inside the graph
     "tiny_8k": ModelConfig(256, 512, 2, 4, 1, 512, 8448, seed=9),
+    # head size 128 with 8 query heads per kv head, and with 1: the split
+    # decode attention's widest and narrowest groups
+    "tiny_hd128_r8": ModelConfig(1024, 512, 2, 8, 1, 512, 2048, seed=13),
+    "tiny_hd128_r1": ModelConfig(256, 512, 2, 2, 2, 512, 2048, seed=14),
     # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
     "smollm2_135m": ModelConfig(576, 1536, 30, 9, 3, 49152, 2048),
     # Llama-3.2-1B shape: dim 2048, FFN 8192, 16 layers, 32/8 heads, vocab 128256

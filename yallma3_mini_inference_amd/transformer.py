@@ -42,6 +42,16 @@ class InferenceSession:
         """InferenceSession::reset (base_transformer.rs:100-104)."""
         check(lib().yl_session_reset(self._h))
 
+    def set_attention(self, mode: str) -> None:
+        """Decode attention of this session: "exact" (fused_attention,
+        forward.rs:299-400, in the reference's operation order) or "split"
+        (the same quantity with the context split over many workgroups;
+        differs in rounding only, for a tolerance bar)."""
+        modes = {"exact": 0, "split": 1}
+        if mode not in modes:
+            raise ValueError(f"attention mode must be one of {sorted(modes)}")
+        check(lib().yl_session_set_attention(self._h, modes[mode]))
+
     def _kv(self):
         k, v, n = C.c_void_p(), C.c_void_p(), C.c_size_t()
         check(lib().yl_session_kv(self._h, C.byref(k), C.byref(v), C.byref(n)))
