@@ -73,12 +73,27 @@ typedef struct yl_session yl_session;
  * transformer, replacing the previous one.  false on NULL, unknown
  * extension or any load error. */
 bool load_transformer_ffi(const char *model_path);
-/* README.md:81-92: generate a reply to `prompt` with the current model.
- * Returns a library-owned NUL-terminated string (release with free_string)
- * or NULL on error / no model. */
+/* README.md:81-92 (documented by the reference, which leaves it
+ * unimplemented): one chat turn with the current model, as the reference's
+ * CLI runs a turn (main.rs:161-219).  The prompt (UTF-8) is trimmed and
+ * wrapped by the GGUF's chat template (tokenizer.rs:496-543; the first turn
+ * of a conversation opens with the system template, or the BOS token when a
+ * chat template exists), prefilled, and tokens are sampled with
+ * Sampler(vocab, temperature 0.7, top-p 0.9, seed 42) (sampler.rs) until
+ * EOS, the end of the context or the yl_infer_set_max_tokens limit.  The
+ * conversation continues across calls in one KV cache, as the CLI's does;
+ * yl_infer_reset() starts a new one.  Returns the decoded pieces as a
+ * library-owned NUL-terminated string (release with free_string), or NULL on
+ * error (no model, empty or non-UTF-8 prompt, template error, context full). */
 char *infer_ffi(const char *prompt);
-/* Releases a string returned by infer_ffi; NULL is ignored. */
+/* Releases a string returned by infer_ffi or yl_generate_text; NULL is ignored. */
 void free_string(char *s);
+/* Limit of generated tokens per infer_ffi call (0, the default: none, as the
+ * CLI's --max-tokens 0, main.rs:131-136). */
+void yl_infer_set_max_tokens(uint32_t max_tokens);
+/* Ends infer_ffi's conversation: the next call starts a fresh KV cache and
+ * sampler.  Loading a model through load_transformer_ffi does the same. */
+void yl_infer_reset(void);
 /* The model load_transformer_ffi installed (the reference's `static mut`
  * current transformer, lib.rs:135-152), or NULL before the first successful
  * load; owned by the library and freed by the next successful load.  Lets a
@@ -306,6 +321,54 @@ yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t
  * YL_ERR_HIP with a message, and clears the word. */
 yl_status yl_wait_fault_selftest(void);
 
+/* ----------------------------------------------------- tokenizer, sampler */
+/* The GGUF tokenizer (tokenizer.ggml.* and tokenizer.chat_template metadata,
+ * transformer_llama_gguf.rs:584-641; Tokenizer, tokenizer.rs).  Host only.
+ * Id outputs: `out` holds `cap` ids; *n receives the result's length;
+ * YL_ERR_RANGE (nothing written) when cap is smaller.  Where the reference
+ * panics, YL_ERR_ARG. */
+typedef struct yl_tokenizer yl_tokenizer;
+/* From a GGUF file's metadata alone (no weights, no GPU). */
+yl_tokenizer *yl_tokenizer_load(const char *gguf_path);
+void yl_tokenizer_free(yl_tokenizer *t);
+/* The tokenizer of a loaded model (owned by the model). */
+const yl_tokenizer *yl_model_tokenizer(const yl_model *m);
+size_t yl_tokenizer_vocab_size(const yl_tokenizer *t);
+/* Tokenizer::encode(text, bos, eos), tokenizer.rs:325-380 (text non-empty UTF-8) */
+yl_status yl_tokenize(const yl_tokenizer *t, const char *text, int32_t bos, int32_t eos, uint32_t *out, size_t cap,
+                      size_t *n);
+/* Tokenizer::decode, tokenizer.rs:545-568: UTF-8 (invalid bytes replaced by
+ * U+FFFD), NUL-terminated into out[cap]; *len receives its byte length. */
+yl_status yl_detokenize(const yl_tokenizer *t, const uint32_t *ids, size_t n, char *out, size_t cap, size_t *len);
+/* which = 0: apply_system_template(text) (tokenizer.rs:496-514);
+ *         1: apply_turn_template(text, flag) (tokenizer.rs:516-543);
+ *         2: encode_wrap_n_header(text, "", flag) (tokenizer.rs:243-286). */
+yl_status yl_chat_template(const yl_tokenizer *t, int32_t which, const char *text, int32_t flag, uint32_t *out,
+                           size_t cap, size_t *n);
+/* The first turn's prompt ids as the CLI builds them (main.rs:148-152,183):
+ * conversation prefix + apply_turn_template(trim(user), true). */
+yl_status yl_chat_prompt(const yl_tokenizer *t, const char *user, uint32_t *out, size_t cap, size_t *n);
+/* The GPT-2 pre-tokenizer split (tokenizer.rs:29-31) of UTF-8 text: byte
+ * offsets [begin, end) of each piece, 2 per piece, into bounds[cap]. */
+yl_status yl_pretokenize(const char *text, uint32_t *bounds, size_t cap, size_t *n);
+
+/* Sampler::new / Sampler::sample (sampler.rs:40-180).  sample() rescales and
+ * normalizes `logits` (host, vocab floats) in place as the reference does;
+ * the draw uses the seed unchanged every call (sampler.rs:170). */
+typedef struct yl_sampler yl_sampler;
+yl_sampler *yl_sampler_new(size_t vocab, float temperature, float top_p, uint64_t seed);
+yl_status yl_sampler_sample(yl_sampler *s, float *logits, uint32_t *token);
+void yl_sampler_free(yl_sampler *s);
+
+/* One turn of generation (main.rs:186-216) on session `s` from its current
+ * position: prefill `prompt`, then sample and feed tokens until EOS, the end
+ * of the context or `max_tokens` (0: no limit).  *text receives the decoded
+ * pieces (release with free_string); out_ids (nullable, out_cap ids) the
+ * generated ids; *n_generated their count.  The session's position advances. */
+yl_status yl_generate_text(const yl_model *m, yl_session *s, yl_sampler *smp, const uint32_t *prompt,
+                           size_t n_prompt, uint32_t max_tokens, char **text, uint32_t *out_ids, size_t out_cap,
+                           size_t *n_generated);
+
 /* ----------------------------------------------------- synthetic models */
 typedef struct {
     uint32_t dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx_len;
@@ -324,6 +387,25 @@ typedef struct {
  * nibble of byte j and j+16 in the high nibble), norms = 1.0, and a vocabulary
  * of placeholder token strings.  Host only (no GPU needed). */
 yl_status yl_write_synthetic_gguf(const char *path, const yl_synth_config *cfg);
+
+/* Tokenizer metadata for yl_write_synthetic_gguf_tok: `tokens` (n_tokens =
+ * cfg->vocab strings) and `merges` ("left right" strings) become
+ * tokenizer.ggml.tokens/merges; pre and chat_template (nullable: omitted)
+ * tokenizer.ggml.pre and tokenizer.chat_template; add_bos_token and
+ * add_space_prefix (-1: omitted, else 0/1) the boolean keys. */
+typedef struct {
+    const char *const *tokens;
+    size_t n_tokens;
+    const char *const *merges;
+    size_t n_merges;
+    uint32_t bos, eos;
+    const char *pre;
+    const char *chat_template;
+    int32_t add_bos_token, add_space_prefix;
+} yl_synth_tokenizer;
+/* yl_write_synthetic_gguf with this tokenizer instead of the placeholder
+ * vocabulary. */
+yl_status yl_write_synthetic_gguf_tok(const char *path, const yl_synth_config *cfg, const yl_synth_tokenizer *tok);
 
 /* Fills `out` (host, count floats) with the generator's N(0, std) stream
  * `stream` starting at element `first` (same values the writer uses). */

@@ -8,17 +8,20 @@ reference's API over it:
   Transformer (TransformerLlamaGguf), InferenceSession transformer.rs,
                                                        base_transformer.rs
   load_transformer, load_transformer_ffi, infer_ffi    lib.rs, README.md
+  Tokenizer, Sampler                                   tokenizer.rs, sampler.rs
   ops.*                                                util.rs, forward.rs
   synth                                                seeded GGUF models
 """
 from ._lib import LIB_PATH, YlError, check, lib
 from .device import DeviceBuffer, device_count
-from .transformer import (InferenceSession, Transformer, TransformerLlamaGguf, infer_ffi, load_transformer,
-                          load_transformer_ffi)
+from .tokenizer import Sampler, Tokenizer, pretokenize
+from .transformer import (InferenceSession, Transformer, TransformerLlamaGguf, infer_ffi, infer_reset,
+                          infer_set_max_tokens, load_transformer, load_transformer_ffi)
 from .weight_type import QuantizedWeight, WeightFormat, matmul, matmul_device, quantize, quantize_device
 
 __all__ = [
     "LIB_PATH", "YlError", "check", "lib", "DeviceBuffer", "device_count", "InferenceSession", "Transformer",
     "TransformerLlamaGguf", "infer_ffi", "load_transformer", "load_transformer_ffi", "QuantizedWeight",
-    "WeightFormat", "matmul", "matmul_device", "quantize", "quantize_device",
+    "WeightFormat", "matmul", "matmul_device", "quantize", "quantize_device", "Sampler", "Tokenizer", "pretokenize",
+    "infer_reset", "infer_set_max_tokens",
 ]

@@ -28,7 +28,10 @@ EXPORTS = [
     "yl_eos_token", "yl_model_weight_bytes", "yl_model_embedding_bytes", "yl_get_embeddings",
     "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_set_attention", "yl_session_pos", "yl_session_set_pos",
     "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest", "yl_serial_sum_selftest", "yl_wait_fault_selftest",
-    "yl_write_synthetic_gguf", "yl_synthetic_normal",
+    "yl_write_synthetic_gguf", "yl_synthetic_normal", "yl_write_synthetic_gguf_tok", "yl_infer_set_max_tokens",
+    "yl_infer_reset", "yl_tokenizer_load", "yl_tokenizer_free", "yl_model_tokenizer", "yl_tokenizer_vocab_size",
+    "yl_tokenize", "yl_detokenize", "yl_chat_template", "yl_chat_prompt", "yl_pretokenize", "yl_sampler_new",
+    "yl_sampler_sample", "yl_sampler_free", "yl_generate_text",
 ]
 
 
@@ -61,6 +64,12 @@ class SynthConfig(C.Structure):
                 ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("weight_std", C.c_float),
                 ("attn_format", C.c_int32), ("ffn_format", C.c_int32), ("embd_format", C.c_int32),
                 ("file_type", C.c_int32), ("seed", C.c_uint64)]
+
+
+class SynthTokenizer(C.Structure):
+    _fields_ = [("tokens", C.POINTER(C.c_char_p)), ("n_tokens", C.c_size_t), ("merges", C.POINTER(C.c_char_p)),
+                ("n_merges", C.c_size_t), ("bos", C.c_uint32), ("eos", C.c_uint32), ("pre", C.c_char_p),
+                ("chat_template", C.c_char_p), ("add_bos_token", C.c_int32), ("add_space_prefix", C.c_int32)]
 
 
 _lib = None
@@ -130,6 +139,22 @@ def lib():
         "yl_wait_fault_selftest": (st, []),
         "yl_write_synthetic_gguf": (st, [C.c_char_p, C.POINTER(SynthConfig)]),
         "yl_synthetic_normal": (st, [u64, u64, u64, sz, f32, vp]),
+        "yl_write_synthetic_gguf_tok": (st, [C.c_char_p, C.POINTER(SynthConfig), C.POINTER(SynthTokenizer)]),
+        "yl_infer_set_max_tokens": (None, [u32]),
+        "yl_infer_reset": (None, []),
+        "yl_tokenizer_load": (vp, [C.c_char_p]),
+        "yl_tokenizer_free": (None, [vp]),
+        "yl_model_tokenizer": (vp, [vp]),
+        "yl_tokenizer_vocab_size": (sz, [vp]),
+        "yl_tokenize": (st, [vp, C.c_char_p, st, st, vp, sz, C.POINTER(sz)]),
+        "yl_detokenize": (st, [vp, vp, sz, vp, sz, C.POINTER(sz)]),
+        "yl_chat_template": (st, [vp, st, C.c_char_p, st, vp, sz, C.POINTER(sz)]),
+        "yl_chat_prompt": (st, [vp, C.c_char_p, vp, sz, C.POINTER(sz)]),
+        "yl_pretokenize": (st, [C.c_char_p, vp, sz, C.POINTER(sz)]),
+        "yl_sampler_new": (vp, [sz, f32, f32, u64]),
+        "yl_sampler_sample": (st, [vp, vp, C.POINTER(u32)]),
+        "yl_sampler_free": (None, [vp]),
+        "yl_generate_text": (st, [vp, vp, vp, vp, sz, u32, C.POINTER(vp), vp, sz, C.POINTER(sz)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -21,7 +21,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libyallma3_amd.so")
 
 SOURCES = ["yl_kernels.hip", "yl_gemv.hip", "yl_gemm.hip", "yl_attn.hip", "yl_attn_split.hip", "yl_pattn.hip", "yl_logits.hip", "yl_model.hip",
-           "yl_gguf.cpp", "yl_synth.cpp"]
+           "yl_gguf.cpp", "yl_synth.cpp", "yl_tokenizer.cpp", "yl_jinja.cpp"]
 ARCH = os.environ.get("YL_OFFLOAD_ARCH", "gfx950")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",

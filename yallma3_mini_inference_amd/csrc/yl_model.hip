@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -30,6 +31,7 @@
 
 #include "yallma3.h"
 #include "yl_gguf.h"
+#include "yl_tokenizer.h"
 #include "yl_internal.h"
 
 namespace yl {
@@ -262,6 +264,7 @@ struct yl_model {
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
     std::vector<std::string> vocab_str;
+    std::unique_ptr<yl_tokenizer> tok;   // tokenizer.ggml.* and tokenizer.chat_template
     size_t weight_bytes = 0, emb_bytes = 0;
     int device = 0;
 };
@@ -429,8 +432,13 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     else if (file_type == 2) wfmt = YL_Q4_0;
     else if (file_type == 7) wfmt = YL_Q8_0;
     else { set_error("Unsupported GGUF file_type: " + std::to_string(file_type) + " -- supported: F16=1, Q4_0=2, Q8_0=7"); return nullptr; }
-    if (const GgufValue* b = g.get("tokenizer.ggml.bos_token_id")) m->bos = (uint32_t)(b->type == 5 || b->type == 11 ? (uint64_t)b->i : b->u);
-    if (const GgufValue* e = g.get("tokenizer.ggml.eos_token_id")) m->eos = (uint32_t)(e->type == 5 || e->type == 11 ? (uint64_t)e->i : e->u);
+    {
+        std::string terr;
+        m->tok.reset(tokenizer_from_gguf(g, &terr));
+        if (!m->tok) { set_error(terr); return nullptr; }
+        m->bos = m->tok->t.bos();
+        m->eos = m->tok->t.eos();
+    }
 
     m->att = m->n_heads * m->hd;
     m->kv = m->n_kv * m->hd;
@@ -1492,10 +1500,92 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     return YL_OK;
 }
 
+// ------------------------------------------------ tokenizer and sampler
+
+namespace {
+
+// The opening of a conversation as the CLI builds it (main.rs:148-152):
+// the system template when the GGUF has no chat template, else the BOS
+// token when add_bos_token is set.
+bool conversation_prefix(const Tokenizer& t, std::vector<uint32_t>* out, std::string* err) {
+    if (!t.has_chat_template()) return t.apply_system_template("", out, err);
+    if (t.add_bos_token()) out->push_back(t.bos());
+    return true;
+}
+
+// One chat turn's generation (main.rs:186-216): prefill the prompt at the
+// session's position, then sample, print and feed tokens until EOS, the end
+// of the context or max_tokens (0: no limit).
+yl_status run_turn(const yl_model* m, yl_session* s, Sampler& smp, const std::vector<uint32_t>& prompt,
+                   uint32_t max_tokens, std::string* text, std::vector<uint32_t>* ids) {
+    if (prompt.empty()) { set_error("generate: empty prompt"); return YL_ERR_ARG; }
+    if ((uint64_t)s->pos + prompt.size() > (uint64_t)m->ctx) {
+        set_error("generate: the prompt does not fit the context (" + std::to_string(m->ctx) + " positions)");
+        return YL_ERR_RANGE;
+    }
+    std::vector<float> logits((size_t)m->vocab);
+    yl_status st = yl_forward_x(m, prompt.data(), prompt.size(), s->pos, s, logits.data(), nullptr);
+    if (st != YL_OK) return st;
+    s->pos += (uint32_t)prompt.size();
+    uint32_t next = 0;
+    if (!smp.sample(logits.data(), &next)) { set_error("sampler: no token above the top-p cutoff"); return YL_ERR_ARG; }
+    const uint64_t max_gen = max_tokens ? max_tokens : 0xFFFFFFFFull;
+    uint64_t gen = 0;
+    while (next != m->eos && s->pos < (uint32_t)m->ctx && gen < max_gen) {
+        *text += m->tok->t.decode({next});
+        if (ids) ids->push_back(next);
+        st = yl_forward_x(m, &next, 1, s->pos, s, logits.data(), nullptr);
+        if (st != YL_OK) return st;
+        s->pos += 1;
+        gen++;
+        if (!smp.sample(logits.data(), &next)) { set_error("sampler: no token above the top-p cutoff"); return YL_ERR_ARG; }
+    }
+    return YL_OK;
+}
+
+char* dup_string(const std::string& t) {
+    char* r = (char*)malloc(t.size() + 1);
+    if (r) memcpy(r, t.c_str(), t.size() + 1);
+    return r;
+}
+
+}  // namespace
+
+const yl_tokenizer* yl_model_tokenizer(const yl_model* m) { return m ? m->tok.get() : nullptr; }
+
+yl_status yl_generate_text(const yl_model* m, yl_session* s, yl_sampler* smp, const uint32_t* prompt, size_t n_prompt,
+                           uint32_t max_tokens, char** text, uint32_t* out_ids, size_t out_cap, size_t* n_generated) {
+    if (!m || !s || s->m != m || !smp || !prompt || !text) { set_error("generate_text: null argument"); return YL_ERR_ARG; }
+    *text = nullptr;
+    std::string out;
+    std::vector<uint32_t> ids;
+    const yl_status st = run_turn(m, s, sampler_of(smp), std::vector<uint32_t>(prompt, prompt + n_prompt), max_tokens, &out, &ids);
+    if (n_generated) *n_generated = ids.size();
+    if (out_ids) memcpy(out_ids, ids.data(), std::min(ids.size(), out_cap) * 4);
+    if (st != YL_OK) return st;
+    *text = dup_string(out);
+    return *text ? YL_OK : YL_ERR_NOMEM;
+}
+
 // ------------------------------------------------------- product FFI
 
 static std::mutex g_ffi_mu;
 static yl_model* g_current = nullptr;
+// The conversation infer_ffi continues, as the CLI's loop does over its turns
+// (main.rs:161-219: one session and one Sampler(vocab, 0.7, 0.9, 42) for the
+// life of the model; the first turn opens with the conversation prefix).
+static yl_session* g_chat = nullptr;
+static Sampler* g_chat_sampler = nullptr;
+static bool g_chat_started = false;
+static uint32_t g_infer_max_tokens = 0;
+
+static void chat_close() {
+    if (g_chat) yl_session_free(g_chat);
+    g_chat = nullptr;
+    delete g_chat_sampler;
+    g_chat_sampler = nullptr;
+    g_chat_started = false;
+}
 
 bool load_transformer_ffi(const char* model_path) {
     if (!model_path) return false;
@@ -1511,6 +1601,7 @@ bool load_transformer_ffi(const char* model_path) {
     yl_model* m = yl_load(model_path, 0xFFFFFFFFu, -1);
     if (!m) return false;
     std::lock_guard<std::mutex> lk(g_ffi_mu);
+    chat_close();
     if (g_current) model_release(g_current);
     g_current = m;
     return true;
@@ -1521,11 +1612,41 @@ const yl_model* yl_ffi_model(void) {
     return g_current;
 }
 
+void yl_infer_set_max_tokens(uint32_t max_tokens) {
+    std::lock_guard<std::mutex> lk(g_ffi_mu);
+    g_infer_max_tokens = max_tokens;
+}
+
+void yl_infer_reset(void) {
+    std::lock_guard<std::mutex> lk(g_ffi_mu);
+    chat_close();
+}
+
 char* infer_ffi(const char* prompt) {
     std::lock_guard<std::mutex> lk(g_ffi_mu);
     if (!prompt || !g_current) { set_error("infer_ffi: no prompt or no model loaded"); return nullptr; }
-    set_error("infer_ffi: text generation needs the tokenizer, which is not built yet");
-    return nullptr;
+    if (!valid_utf8(prompt)) { set_error("infer_ffi: prompt is not UTF-8"); return nullptr; }
+    const std::string user = trim_unicode(prompt);
+    if (user.empty()) { set_error("infer_ffi: empty prompt"); return nullptr; }
+    if (!g_chat) {
+        g_chat = yl_create_session(g_current);
+        if (!g_chat) return nullptr;
+        g_chat_sampler = new Sampler((size_t)g_current->vocab, 0.7f, 0.9f, 42);
+        g_chat_started = false;
+    }
+    const Tokenizer& t = g_current->tok->t;
+    std::vector<uint32_t> ids;
+    std::string err;
+    if ((!g_chat_started && !conversation_prefix(t, &ids, &err)) || !t.apply_turn_template(user, true, &ids, &err)) {
+        set_error("infer_ffi: " + err);
+        return nullptr;
+    }
+    g_chat_started = true;
+    std::string out;
+    if (run_turn(g_current, g_chat, *g_chat_sampler, ids, g_infer_max_tokens, &out, nullptr) != YL_OK) return nullptr;
+    char* r = dup_string(out);
+    if (!r) set_error("infer_ffi: out of memory");
+    return r;
 }
 
 void free_string(char* s) { free(s); }

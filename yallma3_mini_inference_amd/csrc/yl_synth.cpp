@@ -211,7 +211,26 @@ extern "C" yl_status yl_synthetic_normal(uint64_t seed, uint64_t stream, uint64_
     return YL_OK;
 }
 
+static yl_status write_gguf(const char* path, const yl_synth_config* c, const yl_synth_tokenizer* tk);
+
 extern "C" yl_status yl_write_synthetic_gguf(const char* path, const yl_synth_config* c) {
+    return write_gguf(path, c, nullptr);
+}
+
+extern "C" yl_status yl_write_synthetic_gguf_tok(const char* path, const yl_synth_config* c,
+                                                 const yl_synth_tokenizer* tk) {
+    if (!tk || !tk->tokens || (tk->n_merges && !tk->merges)) {
+        yl::set_error("yl_write_synthetic_gguf_tok: null tokenizer arrays");
+        return YL_ERR_ARG;
+    }
+    if (!c || tk->n_tokens != c->vocab) {
+        yl::set_error("yl_write_synthetic_gguf_tok: the token list must hold cfg->vocab strings");
+        return YL_ERR_ARG;
+    }
+    return write_gguf(path, c, tk);
+}
+
+static yl_status write_gguf(const char* path, const yl_synth_config* c, const yl_synth_tokenizer* tk) {
     if (!path || !c || !c->dim || !c->n_heads || c->dim % c->n_heads || !c->n_layers || !c->vocab ||
         c->dim % 32 || c->hidden % 32 || !c->n_kv_heads || c->n_heads % c->n_kv_heads) {
         yl::set_error("yl_write_synthetic_gguf: invalid config");
@@ -249,7 +268,9 @@ extern "C" yl_status yl_write_synthetic_gguf(const char* path, const yl_synth_co
     Writer w;
     w.f = fopen(path, "wb");
     if (!w.f) { yl::set_error(std::string("cannot create ") + path); return YL_ERR_IO; }
-    const uint32_t n_kv = 15;
+    const uint32_t n_kv = 15 + (tk ? (tk->n_merges ? 1 : 0) + (tk->pre ? 1 : 0) + (tk->chat_template ? 1 : 0) +
+                                         (tk->add_bos_token >= 0 ? 1 : 0) + (tk->add_space_prefix >= 0 ? 1 : 0)
+                                    : 0);
     w.u32(0x46554747u);
     w.u32(3);
     w.u64(ts.size());
@@ -266,13 +287,27 @@ extern "C" yl_status yl_write_synthetic_gguf(const char* path, const yl_synth_co
     w.kv_u32("llama.attention.head_count_kv", c->n_kv_heads);
     w.kv_f32("llama.attention.layer_norm_rms_epsilon", c->rms_eps);
     w.kv_f32("llama.rope.freq_base", c->rope_theta);
-    w.kv_u32("tokenizer.ggml.bos_token_id", 1);
-    w.kv_u32("tokenizer.ggml.eos_token_id", 2);
+    w.kv_u32("tokenizer.ggml.bos_token_id", tk ? tk->bos : 1);
+    w.kv_u32("tokenizer.ggml.eos_token_id", tk ? tk->eos : 2);
     w.str("tokenizer.ggml.tokens");
     w.u32(9);
     w.u32(8);
     w.u64(c->vocab);
-    for (uint32_t i = 0; i < c->vocab; i++) w.str("<t" + std::to_string(i) + ">");
+    for (uint32_t i = 0; i < c->vocab; i++) w.str(tk ? std::string(tk->tokens[i]) : "<t" + std::to_string(i) + ">");
+    if (tk) {
+        if (tk->n_merges) {
+            w.str("tokenizer.ggml.merges");
+            w.u32(9);
+            w.u32(8);
+            w.u64(tk->n_merges);
+            for (size_t i = 0; i < tk->n_merges; i++) w.str(tk->merges[i]);
+        }
+        if (tk->pre) w.kv_str("tokenizer.ggml.pre", tk->pre);
+        if (tk->chat_template) w.kv_str("tokenizer.chat_template", tk->chat_template);
+        auto kv_bool = [&](const char* k, int v) { w.str(k); w.u32(7); const uint8_t b = v ? 1 : 0; w.bytes(&b, 1); };
+        if (tk->add_bos_token >= 0) kv_bool("tokenizer.ggml.add_bos_token", tk->add_bos_token);
+        if (tk->add_space_prefix >= 0) kv_bool("tokenizer.ggml.add_space_prefix", tk->add_space_prefix);
+    }
     for (const auto& t : ts) {
         w.str(t.name);
         const bool vec = t.ne1 == 1;

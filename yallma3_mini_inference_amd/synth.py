@@ -13,7 +13,7 @@ import dataclasses
 import os
 import sys
 
-from ._lib import SynthConfig, check, lib
+from ._lib import SynthConfig, SynthTokenizer, check, lib
 from .weight_type import WeightFormat
 
 Q8, Q4 = WeightFormat.Q8_0, WeightFormat.Q4_0
@@ -77,9 +77,32 @@ CONFIGS = {
 }
 
 
-def write(path: str, cfg: ModelConfig) -> str:
+@dataclasses.dataclass(frozen=True)
+class TokenizerSpec:
+    """GGUF tokenizer metadata for a synthetic model (len(tokens) = vocab)."""
+    tokens: tuple
+    merges: tuple = ()
+    bos: int = 1
+    eos: int = 2
+    pre: str | None = None
+    chat_template: str | None = None
+    add_bos_token: bool | None = None
+    add_space_prefix: bool | None = None
+
+
+def write(path: str, cfg: ModelConfig, tokenizer: TokenizerSpec | None = None) -> str:
     c = cfg.to_c()
-    check(lib().yl_write_synthetic_gguf(os.fsencode(path), C.byref(c)))
+    if tokenizer is None:
+        check(lib().yl_write_synthetic_gguf(os.fsencode(path), C.byref(c)))
+        return path
+    toks = (C.c_char_p * len(tokenizer.tokens))(*[t.encode() for t in tokenizer.tokens])
+    merges = (C.c_char_p * max(1, len(tokenizer.merges)))(*[m.encode() for m in tokenizer.merges])
+    tri = lambda v: -1 if v is None else int(v)
+    spec = SynthTokenizer(toks, len(tokenizer.tokens), merges, len(tokenizer.merges), tokenizer.bos, tokenizer.eos,
+                          None if tokenizer.pre is None else tokenizer.pre.encode(),
+                          None if tokenizer.chat_template is None else tokenizer.chat_template.encode(),
+                          tri(tokenizer.add_bos_token), tri(tokenizer.add_space_prefix))
+    check(lib().yl_write_synthetic_gguf_tok(os.fsencode(path), C.byref(c), C.byref(spec)))
     return path
 
 

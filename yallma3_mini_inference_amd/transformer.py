@@ -18,6 +18,7 @@ import os
 import numpy as np
 
 from ._lib import Shape, YlError, check, last_error, lib
+from .tokenizer import Sampler, Tokenizer
 from .weight_type import WeightFormat
 
 
@@ -183,6 +184,25 @@ class Transformer:
     def create_session(self) -> InferenceSession:
         return InferenceSession(self)
 
+    def tokenizer(self) -> Tokenizer:
+        """Transformer::tokenizer (transformer.rs): the GGUF's tokenizer."""
+        return Tokenizer(lib().yl_model_tokenizer(self._h), owner=self)
+
+    def generate_text(self, session: InferenceSession, sampler: Sampler, prompt_ids, max_tokens: int = 0):
+        """One chat turn's generation (main.rs:186-216) from session.pos:
+        returns (text, generated ids); session.pos advances."""
+        t = np.ascontiguousarray(prompt_ids, np.uint32)
+        cap = max_tokens if max_tokens else self.max_ctx_len()
+        ids = np.zeros(max(cap, 1), np.uint32)
+        text, n = C.c_void_p(), C.c_size_t()
+        check(lib().yl_generate_text(self._h, session._h, sampler._h, t.ctypes.data, t.size, int(max_tokens),
+                                     C.byref(text), ids.ctypes.data, ids.size, C.byref(n)))
+        try:
+            out = C.string_at(text.value).decode()
+        finally:
+            lib().free_string(text)
+        return out, [int(x) for x in ids[:min(n.value, ids.size)]]
+
     def max_ctx_len(self) -> int:
         return int(lib().yl_max_ctx_len(self._h))
 
@@ -224,6 +244,14 @@ def load_transformer(model_path: str, sequential: bool = False, max_ctx_len: int
 
 def load_transformer_ffi(model_path: str | None) -> bool:
     return bool(lib().load_transformer_ffi(None if model_path is None else os.fsencode(model_path)))
+
+
+def infer_set_max_tokens(n: int) -> None:
+    lib().yl_infer_set_max_tokens(int(n))
+
+
+def infer_reset() -> None:
+    lib().yl_infer_reset()
 
 
 def infer_ffi(prompt: str) -> str | None:
