@@ -129,6 +129,9 @@ yl_weight *yl_weight_upload(yl_format fmt, const int8_t *quant_vals, const float
 /* From raw GGUF blocks (host): Q8_0 34-byte / Q4_0 18-byte blocks of a
  * row-major [o][n] tensor (transformer_llama_gguf.rs:345-410). */
 yl_weight *yl_weight_upload_gguf(yl_format fmt, const void *blocks, size_t o, size_t n);
+/* An F16 matrix (QuantizedTensor::F16) from binary16 bits [o][n] (host); the
+ * values are exactly the reference's widened f32 weights. */
+yl_weight *yl_weight_upload_f16(const uint16_t *bits, size_t o, size_t n);
 void yl_weight_free(yl_weight *w);
 /* Bytes the matrix occupies on the device (quantized values + f16 scales). */
 size_t yl_weight_bytes(const yl_weight *w);
@@ -140,6 +143,12 @@ size_t yl_weight_bytes(const yl_weight *w);
  * in block order.  gs must be 32.  YL_ERR_FORMAT if fmt differs from w's. */
 yl_status yl_matmul(float *out, yl_format fmt, const int8_t *xq, const float *xs, size_t batch,
                     const yl_weight *w, size_t n, size_t o, uint32_t gs, void *stream);
+/* weight_type::matmul's F16 branch, matmul_f32 (weight_type.rs:228-270):
+ * out[r][c] = sum over i in order of x[r][i] * w[c][i] (f32 products and adds,
+ * one accumulator per column), assigned for every column.  out: batch*o f32,
+ * x: batch*n f32 (device); w: an F16 matrix. */
+yl_status yl_matmul_f32(float *out, const float *x, size_t batch, const yl_weight *w, size_t n, size_t o,
+                        void *stream);
 
 /* Timing of yl_matmul (`=` into out, no accumulation): the count weights
  * (same format and shape, device-resident) are multiplied by the same

@@ -20,6 +20,31 @@ def test_matmul_reference_kat(oracle):
     assert np.all(np.abs(out - n) < 1e-5)
 
 
+def test_matmul_f32_pins(oracle):
+    """weight_type.rs:228-270: every column assigned (no `+=`); sums of exactly
+    representable terms are exact; the column order of the f32 chain matters
+    (1 + 2^-24 ... does not round the same as the reversed order)."""
+    n, o = 64, 5
+    out = np.full(o, 7.0, np.float32)
+    oracle.matmul_f32(out, np.ones(n, np.float32), np.full(o * n, 0.5, np.float32), n, o)
+    assert np.all(out == 32.0)                        # assigned, not accumulated
+    # order-sensitive chain: x = [1, 2^-24 x 63]: left to right each tiny term
+    # rounds away (ties to even), so the sum stays 1
+    x = np.array([1.0] + [2.0 ** -24] * 63, np.float32)
+    out = np.zeros(1, np.float32)
+    oracle.matmul_f32(out, x, np.ones(64, np.float32), 64, 1)
+    assert out[0] == 1.0
+    out2 = np.zeros(1, np.float32)
+    oracle.matmul_f32(out2, x[::-1].copy(), np.ones(64, np.float32), 64, 1)
+    assert out2[0] > 1.0                              # the reversed order keeps them
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((3, 96)).astype(np.float32)
+    w = rng.standard_normal((7, 96)).astype(np.float16).astype(np.float32)
+    out = np.zeros((3, 7), np.float32)
+    oracle.matmul_f32(out, x, w, 96, 7)
+    np.testing.assert_allclose(out, x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-5, atol=1e-5)
+
+
 def test_f16_all_patterns(oracle):
     bits = np.arange(65536, dtype=np.uint16)
     ref = bits.view(np.float16).astype(np.float32)

@@ -31,7 +31,7 @@ EXPORTS = [
     "yl_write_synthetic_gguf", "yl_synthetic_normal", "yl_write_synthetic_gguf_tok", "yl_infer_set_max_tokens",
     "yl_infer_reset", "yl_tokenizer_load", "yl_tokenizer_free", "yl_model_tokenizer", "yl_tokenizer_vocab_size",
     "yl_tokenize", "yl_detokenize", "yl_chat_template", "yl_chat_prompt", "yl_pretokenize", "yl_sampler_new",
-    "yl_sampler_sample", "yl_sampler_free", "yl_generate_text",
+    "yl_sampler_sample", "yl_sampler_free", "yl_generate_text", "yl_weight_upload_f16", "yl_matmul_f32",
 ]
 
 
@@ -155,6 +155,8 @@ def lib():
         "yl_sampler_sample": (st, [vp, vp, C.POINTER(u32)]),
         "yl_sampler_free": (None, [vp]),
         "yl_generate_text": (st, [vp, vp, vp, vp, sz, u32, C.POINTER(vp), vp, sz, C.POINTER(sz)]),
+        "yl_weight_upload_f16": (vp, [vp, sz, sz]),
+        "yl_matmul_f32": (st, [vp, vp, sz, vp, sz, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -38,12 +38,15 @@ struct QMat {          // device-resident quantized matrix
     int o = 0, n = 0, nb = 0;
     uint8_t* qs = nullptr;
     uint16_t* d = nullptr;
-    size_t bytes() const { return (size_t)o * (fmt == 1 ? n / 2 : n) + (size_t)o * nb * 2; }
+    size_t bytes() const {
+        return fmt == kF16 ? (size_t)o * n * 2 : (size_t)o * (fmt == kQ4 ? n / 2 : n) + (size_t)o * nb * 2;
+    }
 };
 
-struct EmbQ8 {         // interleaved Q8_0 token embedding
+struct EmbQ8 {         // interleaved token embedding
     int vocab = 0, dim = 0, tiles = 0;
-    int dimp = 0;      // dim rounded up to 64: the padding has scale 0
+    int dimp = 0;      // dim rounded up to 64: the padding has scale 0 (Q8) or value 0 (F16)
+    int fmt = 0;       // 0: Q8_0 (q = u8 values, d = f16 scales); 1: F16 (q = f16 values, d unused)
     int8_t* q = nullptr;
     uint16_t* d = nullptr;
 };
@@ -157,6 +160,13 @@ hipError_t launch_math_selftest(const float* x, int n, float* exp_out, float* sq
                                 float* div_out, float* f16_out, hipStream_t s);
 
 hipError_t launch_raise_fault(unsigned* fault, hipStream_t s);
+// F16 weights (matmul_f32): out[t * out_ld + r] (= or +=, epi 0/1) of f16 w [o][n]
+// and f32 x [batch][n]; the QKV step (RoPE, `=` into the caches)
+hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, int batch, float* out, int out_ld,
+                             int epi, hipStream_t s);
+hipError_t launch_qkv_f16(const float* raw, const float* cos_t, const float* sin_t, const StepState* st, int batch,
+                          float* sq, float* kc, float* vc, int att, int kv, int hd, int kv_ld, int hf_pairs,
+                          hipStream_t s);
 // Decode attention split over the context (tolerance mode): workgroups per
 // kv head, scratch bytes (partials + one count per kv head, the counts zero
 // before the first launch; each launch leaves them zero), and the launch.

@@ -48,8 +48,13 @@ __global__ __launch_bounds__(kThreads) void k_embed(EmbQ8 e, const uint32_t* __r
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         float v = 0.0f;
         if (tok < (uint32_t)e.vocab) {
-            const int q = (int)(uint8_t)e.q[emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15)] - 128;
-            v = fmul((float)q, f16_to_f32(e.d[emb_d_idx(e.tiles, tile, i >> 5, lane)]));
+            const size_t off = emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15);
+            if (e.fmt == 1) {
+                v = f16_to_f32(reinterpret_cast<const uint16_t*>(e.q)[off]);
+            } else {
+                const int q = (int)(uint8_t)e.q[off] - 128;
+                v = fmul((float)q, f16_to_f32(e.d[emb_d_idx(e.tiles, tile, i >> 5, lane)]));
+            }
         }
         x[(size_t)t * dim + i] = v;
     }

@@ -32,6 +32,10 @@ __device__ __forceinline__ uint32_t load_stream(const uint32_t* p) { return __bu
 constexpr int kLogitThreads = 256;
 constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each) in flight
 
+// EF = 0: Q8_0 table (u8 chunks of 16 + f16 scale pairs); EF = 1: f16 table
+// (32-byte chunks of 16 values), whose values are exactly the reference's f32
+// table (load_f16_tensor, transformer_llama_gguf.rs:412-421,487).
+template <int EF>
 __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* __restrict__ x,
                                                           const float* __restrict__ norm_w, float eps,
                                                           float* __restrict__ logits,
@@ -50,7 +54,8 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     const int ng = e.dimp / 64;   // groups: 4 chunks, one block pair
     // chunk k of this row at qp[k * cs], the scales of block pair g at dp[g * cs]
     const size_t cs = (size_t)e.tiles * 64;
-    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 + lane;
+    // (F16: each chunk is two int4, chunk k of this row at qp[2 * k * cs], qp[2 * k * cs + 1])
+    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 * (EF + 1) + lane * (EF + 1);
     const uint32_t* dp = reinterpret_cast<const uint32_t*>(e.d) + (size_t)(live ? tile : 0) * 64 + lane;
     for (int i = dim + tid; i < e.dimp; i += kLogitThreads) xn[i] = 0.0f;
 
@@ -64,15 +69,23 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     rowq_load_f32<MP>(tm, wv, norm_w, dim, passes);
     __syncthreads();
     // a ring of NG groups: each group's scale word, then its 4 chunks
-    int4 qv[NG][4];
+    int4 qv[NG][4 * (EF + 1)];
     uint32_t sv[NG];
+    auto load_group = [&](int gg, int g) {
+        if constexpr (EF == 0) {
+            sv[gg] = load_stream(dp + (size_t)g * cs);
 #pragma unroll
-    for (int gg = 0; gg < NG; gg++) {
-        const int g = min(gg, ng - 1);
-        sv[gg] = load_stream(dp + (size_t)g * cs);
+            for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
+        } else {
 #pragma unroll
-        for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
-    }
+            for (int c = 0; c < 4; c++) {
+                qv[gg][2 * c] = load_stream(qp + (size_t)(4 * g + c) * cs * 2);
+                qv[gg][2 * c + 1] = load_stream(qp + (size_t)(4 * g + c) * cs * 2 + 1);
+            }
+        }
+    };
+#pragma unroll
+    for (int gg = 0; gg < NG; gg++) load_group(gg, min(gg, ng - 1));
     rowq_stage<MP>(tm, xv, wv, dim, passes, sq);
     rowq_norm_quant<-1, false>(dim, eps, sq, nullptr, nullptr, xn);
 
@@ -84,17 +97,30 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
             for (int gg = 0; gg < NG; gg++) {
                 const int g = g0 + gg;
                 if (NG > 1 && g >= ng) break;
-                const uint32_t sw = sv[gg];
-                int4 q4[4];
+                const uint32_t sw = EF == 0 ? sv[gg] : 0u;
+                int4 q4[4 * (EF + 1)];
 #pragma unroll
-                for (int c = 0; c < 4; c++) q4[c] = qv[gg][c];
+                for (int c = 0; c < 4 * (EF + 1); c++) q4[c] = qv[gg][c];
                 // refill with group g + NG (clamped re-reads past the row are
                 // never used)
-                const int gn = min(g + NG, ng - 1);
-                sv[gg] = load_stream(dp + (size_t)gn * cs);
-#pragma unroll
-                for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * gn + c) * cs);
+                load_group(gg, min(g + NG, ng - 1));
                 __builtin_amdgcn_sched_barrier(0);
+                if constexpr (EF == 1) {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float* xk = xn + (4 * g + c) * 16;
+                        const uint32_t w[8] = {(uint32_t)q4[2 * c].x, (uint32_t)q4[2 * c].y, (uint32_t)q4[2 * c].z,
+                                               (uint32_t)q4[2 * c].w, (uint32_t)q4[2 * c + 1].x,
+                                               (uint32_t)q4[2 * c + 1].y, (uint32_t)q4[2 * c + 1].z,
+                                               (uint32_t)q4[2 * c + 1].w};
+#pragma unroll
+                        for (int ei = 0; ei < 16; ei++) {
+                            const float ev = f16_to_f32((uint16_t)(w[ei >> 1] >> (16 * (ei & 1))));
+                            l[ei & 7] = fadd(l[ei & 7], fmul(xk[ei], ev));
+                        }
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const float scv = f16_to_f32((uint16_t)(c < 2 ? sw & 0xffffu : sw >> 16));
@@ -168,13 +194,14 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
                          hipStream_t s) {
     const int nblk = logits_blocks(e);
     if (e.dim % 32 || e.dim > 8192) return hipErrorInvalidValue;
+    auto kern = e.fmt == 1 ? k_logits<1> : k_logits<0>;
     if (logits_lds_bytes(e.dim) > 65536) {
-        const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(k_logits),
+        const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)logits_lds_bytes(e.dim));
         if (err != hipSuccess) return err;
     }
-    hipLaunchKernelGGL(k_logits, dim3(nblk), dim3(kLogitThreads), logits_lds_bytes(e.dim), s, e, x, norm_w, eps,
+    hipLaunchKernelGGL(kern, dim3(nblk), dim3(kLogitThreads), logits_lds_bytes(e.dim), s, e, x, norm_w, eps,
                        logits, st, ring, ring_cap, advance);
     return hipGetLastError();
 }

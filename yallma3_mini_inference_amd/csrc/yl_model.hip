@@ -94,7 +94,7 @@ struct HostQMat {
     size_t o = 0, n = 0, nb = 0;
     std::vector<uint8_t> qs;
     std::vector<uint16_t> d;
-    size_t row_bytes() const { return fmt == kQ4 ? n / 2 : n; }
+    size_t row_bytes() const { return fmt == kQ4 ? n / 2 : fmt == kF16 ? n * 2 : n; }
 };
 
 // GGUF blocks -> repacked planes (transformer_llama_gguf.rs:345-410).
@@ -127,8 +127,14 @@ static bool host_from_gguf(uint32_t type, const uint8_t* src, uint64_t avail, si
         }
         return true;
     }
-    *err = "unsupported tensor type " + std::to_string(type) +
-           " for a quantized matmul (Q8_0 and Q4_0 are built; F16 is not)";
+    if (type == kGgmlF16) {   // load_f16_tensor (transformer_llama_gguf.rs:412-421): kept as f16 bits
+        if (o * n * 2 > avail) { *err = "F16 tensor exceeds the file"; return false; }
+        h->fmt = kF16;
+        h->nb = 0;
+        h->qs.assign(src, src + o * n * 2);
+        return true;
+    }
+    *err = "unsupported tensor type " + std::to_string(type) + " (Q8_0, Q4_0 and F16 are built)";
     return false;
 }
 
@@ -245,6 +251,7 @@ struct yl_weight {
 
 struct Layer {
     QMat qkv, wo, w13, w2;
+    QMat w1, w3;                // F16 models: gate and up apart (w13 unused)
     float* rms_att = nullptr;
     float* rms_ffn = nullptr;
 };
@@ -261,6 +268,8 @@ struct yl_model {
     EmbQ8 emb;
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
+    bool f16 = false;           // WeightFormat::F16: matmul_f32 on f16 weights (no activation quantization)
+    int hf_rope = 0;            // 1: util::rope pairs (j, j + head/2); 0: rope_gguf pairs (2j, 2j + 1)
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
     std::vector<std::string> vocab_str;
@@ -281,6 +290,8 @@ struct yl_session {
     float *x = nullptr, *sq = nullptr, *logits = nullptr;
     int8_t *aq = nullptr, *hq = nullptr, *nq = nullptr;   // nq/ns: normalized, quantized rows (prompt)
     float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
+    // F16 models: normalized rows, raw QKV outputs, attention output, gate/up/h (f32)
+    float *xn = nullptr, *qkv_raw = nullptr, *attf = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
     float* sc = nullptr;                 // attention scores of long contexts [n_heads][ctx]
     float* psc = nullptr;                // prompt attention scratch (batches of 64+ tokens)
     size_t psc_bytes = 0;
@@ -307,7 +318,7 @@ namespace {
 void model_release(yl_model* m) {
     if (!m) return;
     for (auto& L : m->layers) {
-        free_qmat(&L.qkv); free_qmat(&L.wo); free_qmat(&L.w13); free_qmat(&L.w2);
+        free_qmat(&L.qkv); free_qmat(&L.wo); free_qmat(&L.w13); free_qmat(&L.w2); free_qmat(&L.w1); free_qmat(&L.w3);
         if (L.rms_att) hipFree(L.rms_att);
         if (L.rms_ffn) hipFree(L.rms_ffn);
     }
@@ -331,12 +342,29 @@ bool upload_embedding(const GgufTensor* t, int dim, int vocab, EmbQ8* e, std::st
     std::vector<int8_t> q((size_t)tiles * 64 * dimp, 0);
     std::vector<uint16_t> d((size_t)tiles * 64 * (dimp / 32), 0);
     const size_t blocks = (size_t)vocab * nbE;
+    if (t->type == kGgmlF16) {
+        // f16 values in the same chunk-major order (16 per chunk, 32 bytes);
+        // the padding columns are +0
+        if ((uint64_t)vocab * dim * 2 > t->avail) { *err = "token_embd exceeds the file"; return false; }
+        std::vector<uint16_t> h((size_t)tiles * 64 * dimp, 0);
+        for (int v = 0; v < vocab; v++)
+            for (int i = 0; i < dim; i++)
+                h[emb_q_off(tiles, v / 64, i >> 4, v % 64) + (i & 15)] =
+                    (uint16_t)(t->data[((size_t)v * dim + i) * 2] | (t->data[((size_t)v * dim + i) * 2 + 1] << 8));
+        e->vocab = vocab; e->dim = dim; e->tiles = tiles; e->dimp = dimp; e->fmt = 1;
+        if (hipMalloc(&e->q, h.size() * 2 + 256) != hipSuccess || hipMalloc(&e->d, 256) != hipSuccess ||
+            hipMemcpy(e->q, h.data(), h.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
+            *err = "upload of the token embedding failed";
+            return false;
+        }
+        return true;
+    }
     if (t->type == kGgmlQ8_0) {
         if (blocks * 34 > t->avail) { *err = "token_embd exceeds the file"; return false; }
     } else if (t->type == kGgmlQ4_0) {
         if (blocks * 18 > t->avail) { *err = "token_embd exceeds the file"; return false; }
     } else {
-        *err = "token_embd.weight type " + std::to_string(t->type) + " is not built (Q8_0 and Q4_0 are)";
+        *err = "token_embd.weight type " + std::to_string(t->type) + " is not built (Q8_0, Q4_0 and F16 are)";
         return false;
     }
     for (int v = 0; v < vocab; v++) {
@@ -466,7 +494,8 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     const GgufTensor* te = g.tensor("token_embd.weight");
     if (!te) { set_error("token_embd.weight not found"); return nullptr; }
     if (!upload_embedding(te, m->dim, m->vocab, &m->emb, &err)) { set_error(err); *st = YL_ERR_UNSUPPORTED; return nullptr; }
-    m->emb_bytes = (size_t)m->vocab * m->dim + (size_t)m->vocab * (m->dim / 32) * 2;
+    m->emb_bytes = m->emb.fmt == 1 ? (size_t)m->vocab * m->dim * 2
+                                   : (size_t)m->vocab * m->dim + (size_t)m->vocab * (m->dim / 32) * 2;
 
     auto load_f32 = [&](const std::string& nm, size_t n, float** dst) {
         const GgufTensor* t = g.tensor(nm);
@@ -502,14 +531,25 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
                 return nullptr;
             }
         }
+        int n_f16 = 0;
+        for (int k = 0; k < 7; k++) n_f16 += h[k].fmt == kF16;
+        if (n_f16 != 0 && n_f16 != 7) {
+            set_error(p + "*: F16 projections beside quantized ones are not built (the F16 path needs all seven)");
+            *st = YL_ERR_UNSUPPORTED;
+            return nullptr;
+        }
+        if (l == 0) m->f16 = n_f16 == 7;
+        else if (m->f16 != (n_f16 == 7)) { set_error("layers mix F16 and quantized weights"); *st = YL_ERR_UNSUPPORTED; return nullptr; }
         HostQMat qkv, w13;
-        if (!host_concat_rows({&h[0], &h[1], &h[2]}, &qkv, &err) || !host_interleave_gate_up(h[4], h[6], &w13, &err) ||
-            !upload_qmat(qkv, &L.qkv, &err) || !upload_qmat(h[3], &L.wo, &err) || !upload_qmat(w13, &L.w13, &err) ||
-            !upload_qmat(h[5], &L.w2, &err)) {
+        bool ok = host_concat_rows({&h[0], &h[1], &h[2]}, &qkv, &err) && upload_qmat(qkv, &L.qkv, &err) &&
+                  upload_qmat(h[3], &L.wo, &err) && upload_qmat(h[5], &L.w2, &err);
+        if (ok && m->f16) ok = upload_qmat(h[4], &L.w1, &err) && upload_qmat(h[6], &L.w3, &err);
+        else if (ok) ok = host_interleave_gate_up(h[4], h[6], &w13, &err) && upload_qmat(w13, &L.w13, &err);
+        if (!ok) {
             set_error(p + err);
             return nullptr;
         }
-        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w13.bytes() + L.w2.bytes();
+        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w13.bytes() + L.w2.bytes() + L.w1.bytes() + L.w3.bytes();
     }
     // RoPE angle table for every position of the context
     {
@@ -561,7 +601,17 @@ bool session_grow(yl_session* s, int batch) {
     s->graphs.clear();
     auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
     rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens); rel(s->nq); rel(s->ns);
+    rel(s->xn); rel(s->qkv_raw); rel(s->attf); rel(s->gate); rel(s->up); rel(s->hf);
     const size_t B = (size_t)batch;
+    if (m->f16) {
+        const bool okf = hipMalloc(&s->xn, B * m->dim * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->qkv_raw, B * (m->att + 2 * m->kv) * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->attf, B * m->att * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->gate, B * m->hidden * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->up, B * m->hidden * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->hf, B * m->hidden * 4 + 256) == hipSuccess;
+        if (!okf) { set_error("hipMalloc failed for session buffers"); s->cap_b = 0; return false; }
+    }
     bool ok = hipMalloc(&s->x, B * m->dim * 4 + 256) == hipSuccess &&
               hipMalloc(&s->sq, B * m->att * 4 + 256) == hipSuccess &&
               hipMalloc(&s->aq, B * m->att + 256) == hipSuccess &&
@@ -664,7 +714,11 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         // RMSNorm + quantize (prologue) -> Q,K,V -> K/V += into the cache -> RoPE
         a.qs = L.qkv.qs; a.d = L.qkv.d; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
         a.x = s->x; a.norm_w = L.rms_att; a.eps = m->eps;
-        if (l == 0) { a.emb = m->emb; a.tokens = tok; }
+        if (l == 0 && m->emb.fmt == 0) { a.emb = m->emb; a.tokens = tok; }
+        if (l == 0 && m->emb.fmt != 0) {   // an f16 table: the lookup runs first
+            const hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
+            if (e != hipSuccess) return e;
+        }
         a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
         a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
         a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
@@ -713,7 +767,56 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
 
 // One forward pass over `batch` tokens whose ids are at `tok` (device) and
 // whose first position is st->pos (device).  Enqueued on s->stream only.
+// The forward pass of an F16 model (forward.rs:120-297 with F16Kernel:
+// activations stay f32, every matmul is matmul_f32 and assigns its columns,
+// so K and V overwrite their cache entries).
+hipError_t enqueue_forward_f16(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+    hipStream_t st = s->stream;
+    const size_t lay_kv = (size_t)m->kv_ld * m->kv;
+    const int qkv_n = m->att + 2 * m->kv;
+    hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
+    for (int l = 0; l < m->n_layers && e == hipSuccess; l++) {
+        const Layer& L = m->layers[l];
+        float* kc = s->kc + (size_t)l * lay_kv;
+        float* vc = s->vc + (size_t)l * lay_kv;
+        e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        if (e == hipSuccess)
+            e = launch_matmul_f16((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->xn, batch, s->qkv_raw, qkv_n, 0, st);
+        if (e == hipSuccess)
+            e = launch_qkv_f16(s->qkv_raw, m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, vc, m->att, m->kv, m->hd,
+                               m->kv_ld, m->hf_rope, st);
+        if (e == hipSuccess) {
+            if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
+                e = launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale, -1,
+                                      nullptr, nullptr, s->attf, s->split, st);
+            else if (batch == 1)
+                e = launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                       m->attn_scale, -1, nullptr, nullptr, s->attf, s->sc, st);
+            else if (prompt_attn_applies(batch, s->pseq, m->hd))
+                e = launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv,
+                                            m->hd, m->attn_scale, -1, nullptr, nullptr, s->attf, s->psc, st);
+            else
+                e = launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                     m->attn_scale, -1, nullptr, nullptr, s->attf, st);
+        }
+        if (e == hipSuccess)
+            e = launch_matmul_f16((const uint16_t*)L.wo.qs, m->att, m->dim, s->attf, batch, s->x, m->dim, 1, st);
+        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        if (e == hipSuccess)
+            e = launch_matmul_f16((const uint16_t*)L.w1.qs, m->dim, m->hidden, s->xn, batch, s->gate, m->hidden, 0, st);
+        if (e == hipSuccess)
+            e = launch_matmul_f16((const uint16_t*)L.w3.qs, m->dim, m->hidden, s->xn, batch, s->up, m->hidden, 0, st);
+        if (e == hipSuccess) e = launch_swiglu_quant(-1, s->gate, s->up, m->hidden, batch, s->hf, nullptr, nullptr, st);
+        if (e == hipSuccess)
+            e = launch_matmul_f16((const uint16_t*)L.w2.qs, m->hidden, m->dim, s->hf, batch, s->x, m->dim, 1, st);
+    }
+    if (e != hipSuccess) return e;
+    return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st, s->ring,
+                         s->ring_cap, advance, st);
+}
+
 hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+    if (m->f16) return enqueue_forward_f16(m, s, batch, tok, advance);
     for (int l = 0; l < m->n_layers; l++)
         for (int c = kOpQkv; c <= kOpW2; c++) {
             const hipError_t e = enqueue_op(m, s, c, l, batch, tok, advance, nullptr);
@@ -918,6 +1021,32 @@ void yl_weight_free(yl_weight* w) {
 }
 
 size_t yl_weight_bytes(const yl_weight* w) { return w ? w->m.bytes() : 0; }
+
+yl_weight* yl_weight_upload_f16(const uint16_t* bits, size_t o, size_t n) {
+    if (!bits || !o || n % 32) {
+        set_error("yl_weight_upload_f16: binary16 [o][n] with n a multiple of 32");
+        return nullptr;
+    }
+    HostQMat h;
+    h.fmt = kF16;
+    h.o = o; h.n = n; h.nb = 0;
+    h.qs.assign((const uint8_t*)bits, (const uint8_t*)bits + o * n * 2);
+    auto* w = new yl_weight();
+    std::string err;
+    if (!upload_qmat(h, &w->m, &err)) { set_error(err); free_qmat(&w->m); delete w; return nullptr; }
+    return w;
+}
+
+yl_status yl_matmul_f32(float* out, const float* x, size_t batch, const yl_weight* w, size_t n, size_t o, void* stream) {
+    if (!w || !out || !x) { set_error("yl_matmul_f32: null argument"); return YL_ERR_ARG; }
+    if (w->m.fmt != kF16) { set_error("matmul: format/variant mismatch or mixed formats"); return YL_ERR_FORMAT; }
+    if ((int)n != w->m.n || (int)o != w->m.o) { set_error("yl_matmul_f32: n/o do not match the weight"); return YL_ERR_ARG; }
+    if (batch == 0) return YL_OK;
+    if (batch > 65535) { set_error("yl_matmul_f32: batch > 65535"); return YL_ERR_ARG; }
+    const hipError_t e = launch_matmul_f16((const uint16_t*)w->m.qs, (int)n, (int)o, x, (int)batch, out, (int)o, 0,
+                                           (hipStream_t)stream);
+    return e == hipSuccess ? YL_OK : hip_fail(e, "matmul_f32 launch");
+}
 
 yl_status yl_matmul(float* out, yl_format fmt, const int8_t* xq, const float* xs, size_t batch, const yl_weight* w,
                     size_t n, size_t o, uint32_t gs, void* stream) {
@@ -1318,7 +1447,8 @@ void yl_session_free(yl_session* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
-                   s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc, s->split};
+                   s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc, s->split,
+                   s->xn, s->qkv_raw, s->attf, s->gate, s->up, s->hf};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
@@ -1450,6 +1580,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
+    if (m->f16) { set_error("profile: the kernel classes are those of the quantized path"); return YL_ERR_UNSUPPORTED; }
     if (batch == 1 && !decode_in_range(m, s, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
     s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
     s->prof_seq = (uint64_t)start_pos + batch;

@@ -16,7 +16,7 @@ import sys
 from ._lib import SynthConfig, SynthTokenizer, check, lib
 from .weight_type import WeightFormat
 
-Q8, Q4 = WeightFormat.Q8_0, WeightFormat.Q4_0
+Q8, Q4, F16 = WeightFormat.Q8_0, WeightFormat.Q4_0, WeightFormat.F16
 
 
 @dataclasses.dataclass(frozen=True)
@@ -66,6 +66,13 @@ CONFIGS = {
     # decode attention's widest and narrowest groups
     "tiny_hd128_r8": ModelConfig(1024, 512, 2, 8, 1, 512, 2048, seed=13),
     "tiny_hd128_r1": ModelConfig(256, 512, 2, 2, 2, 512, 2048, seed=14),
+    # F16 weights and embedding (general.file_type 1), and a Q8_0 model whose
+    # token embedding is F16
+    "tiny_f16": ModelConfig(128, 256, 2, 4, 2, 512, 256, attn_format=F16, ffn_format=F16, embd_format=F16,
+                            file_type=1, seed=21),
+    "tiny_q8_f16emb": ModelConfig(128, 256, 2, 4, 2, 512, 256, embd_format=F16, seed=22),
+    "small_f16": ModelConfig(576, 1536, 3, 9, 3, 2048, 1024, attn_format=F16, ffn_format=F16, embd_format=F16,
+                             file_type=1, seed=23),
     # SmolLM2-135M shape: dim 576, FFN 1536, 30 layers, 9/3 heads, vocab 49152
     "smollm2_135m": ModelConfig(576, 1536, 30, 9, 3, 49152, 2048),
     # Llama-3.2-1B shape: dim 2048, FFN 8192, 16 layers, 32/8 heads, vocab 128256

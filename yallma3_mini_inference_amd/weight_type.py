@@ -58,6 +58,18 @@ class QuantizedWeight:
             raise YlError(-1, last_error())
         return cls(h, fmt, o, n)
 
+    @classmethod
+    def upload_f16(cls, values: np.ndarray, o: int, n: int):
+        """QuantizedTensor::F16 from float16 values (or their bits as uint16)."""
+        v = np.ascontiguousarray(values)
+        bits = v.view(np.uint16) if v.dtype == np.float16 else np.ascontiguousarray(v, np.uint16)
+        if bits.size != o * n:
+            raise ValueError("values must hold o*n elements")
+        h = lib().yl_weight_upload_f16(bits.ctypes.data, o, n)
+        if not h:
+            raise YlError(-1, last_error())
+        return cls(h, WeightFormat.F16, o, n)
+
     @property
     def nbytes(self) -> int:
         return int(lib().yl_weight_bytes(self._h))
@@ -105,3 +117,14 @@ def matmul(out: np.ndarray, x_q: np.ndarray, x_scale: np.ndarray, w: QuantizedWe
     matmul_device(dout, w.fmt if fmt is None else fmt, dq, ds, batch, w, n, o, gs)
     out[...] = dout.numpy().reshape(out.shape)
     return out
+
+
+def matmul_f32(x: np.ndarray, w: QuantizedWeight, n: int, o: int) -> np.ndarray:
+    """matmul_f32 (weight_type.rs:228-270) on an F16 weight: x [batch][n] f32 ->
+    [batch][o], every column assigned."""
+    x = np.ascontiguousarray(x, np.float32)
+    batch = x.size // n
+    dx = DeviceBuffer.from_numpy(x.ravel())
+    dout = DeviceBuffer.zeros(batch * o, np.float32)
+    check(lib().yl_matmul_f32(dout.ptr, dx.ptr, batch, w._h, n, o, None))
+    return dout.numpy().reshape(batch, o)
