@@ -9,8 +9,10 @@
  *   load_transformer_ffi   src_llm/lib.rs:135-152
  *   infer_ffi, free_string README.md:81-92, PoC_Bun_load.js:12-38 (documented,
  *                          not implemented by the reference)
- *   yl_load                lib.rs:107-133 load_transformer (".gguf" branch) ->
- *                          transformer_llama_gguf.rs:179-655
+ *   yl_load                lib.rs:107-133 load_transformer: ".gguf" ->
+ *                          transformer_llama_gguf.rs:179-655; ".lmrs" ->
+ *                          transformer_llama_lmrs.rs:60-434; ".safetensors" ->
+ *                          transformer_llama_st.rs:36-300
  *   yl_forward_x           Transformer::forward_x, transformer.rs:53 ->
  *                          forward.rs:282-297 llama_forward_x
  *   yl_create_session      Transformer::create_session, transformer.rs:56;
@@ -228,9 +230,16 @@ typedef struct {                 /* TransformerShape, base_transformer.rs:25-44 
     int32_t weight_format;       /* yl_format the file declares (general.file_type) */
 } yl_shape;
 
-/* Load a GGUF v3 llama model onto the current device.  max_ctx_len caps
- * llama.context_length (gguf.rs:233); fmt_override -1 = none.  Tensors keep
- * their own stored format (a Q4_0 FFN beside Q8_0 attention works). */
+/* Load a model onto the current device; the extension picks the loader.
+ *   .gguf: GGUF v3 llama.  max_ctx_len caps llama.context_length
+ *     (gguf.rs:233); fmt_override -1 = none.  Tensors keep their own stored
+ *     format (a Q4_0 FFN beside Q8_0 attention works).
+ *   .lmrs: the lm.rs format (Q8 with f32 group scales, the file's group
+ *     size; tokenizer.bin beside it), HF-layout RoPE (util.rs:589-635).
+ *   .safetensors: config.json + tokenizer.json (or tokenizer.bin) beside it;
+ *     F16 weights, or MLX 8-bit affine groups requantized symmetric on load
+ *     (util.rs:452-503); HF-layout RoPE.  Q4_0 here is refused (the
+ *     reference loads such tensors as Q8 and runs its Q4_0 kernel on them). */
 yl_model *yl_load(const char *path, uint32_t max_ctx_len, int32_t fmt_override);
 void yl_model_free(yl_model *m);
 const char *yl_model_name(const yl_model *m);
@@ -337,8 +346,11 @@ yl_status yl_wait_fault_selftest(void);
  * YL_ERR_RANGE (nothing written) when cap is smaller.  Where the reference
  * panics, YL_ERR_ARG. */
 typedef struct yl_tokenizer yl_tokenizer;
-/* From a GGUF file's metadata alone (no weights, no GPU). */
-yl_tokenizer *yl_tokenizer_load(const char *gguf_path);
+/* From a file alone (no weights, no GPU): a Hugging Face tokenizer.json
+ * (Tokenizer::from_json, tokenizer.rs:134-224), a llama2.c tokenizer.bin
+ * (Tokenizer::new, tokenizer.rs:226-268), else a GGUF file's metadata
+ * (Tokenizer::from_gguf_parts, tokenizer.rs:77-132). */
+yl_tokenizer *yl_tokenizer_load(const char *path);
 void yl_tokenizer_free(yl_tokenizer *t);
 /* The tokenizer of a loaded model (owned by the model). */
 const yl_tokenizer *yl_model_tokenizer(const yl_model *m);

@@ -92,6 +92,12 @@ def lib():
     L.yo_forward_x.argtypes = [C.c_void_p, _u32p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_void_p]
     L.yo_forward_x.restype = C.c_int
     L.yo_num_threads.restype = C.c_int
+    L.yo_rope_hf.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32, _f32p, _f32p, C.c_uint32]
+    L.yo_model_new.argtypes = [_u32p, C.c_float, C.c_float, C.c_uint32, C.c_int, C.c_int, _f32p, _f32p]
+    L.yo_model_new.restype = C.c_void_p
+    L.yo_model_set_norms.argtypes = [C.c_void_p, C.c_uint32, _f32p, _f32p]
+    L.yo_model_set_weight.argtypes = [C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_size_t]
     _lib = L
     return L
 
@@ -194,6 +200,11 @@ def argmax(p) -> int:
     return int(lib().yo_argmax(np.ascontiguousarray(p, np.float32), len(p)))
 
 
+def rope_hf(sq, k, head_size, n_heads, n_kv_heads, rope_theta, ctx_len, pos):
+    """util::rope (util.rs:589-635) on one token's q and k, in place."""
+    lib().yo_rope_hf(head_size, n_heads, n_kv_heads, rope_theta, ctx_len, sq, k, pos)
+
+
 def num_threads() -> int:
     return int(lib().yo_num_threads())
 
@@ -201,8 +212,8 @@ def num_threads() -> int:
 class Model:
     """TransformerLlamaGguf restated (transformer_llama_gguf.rs:183-729)."""
 
-    def __init__(self, path: str, max_ctx_len: int = 0xFFFFFFFF, fmt_override: int = -1):
-        self._h = lib().yo_model_load(path.encode(), max_ctx_len, fmt_override)
+    def __init__(self, path: str | None = None, max_ctx_len: int = 0xFFFFFFFF, fmt_override: int = -1, handle=None):
+        self._h = handle if handle is not None else lib().yo_model_load(path.encode(), max_ctx_len, fmt_override)
         if not self._h:
             raise RuntimeError("oracle load failed: " + lib().yo_last_error().decode())
         shp = np.zeros(8, np.uint32)
@@ -210,6 +221,27 @@ class Model:
         (self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.head_size,
          self.vocab, self.ctx_len) = (int(v) for v in shp)
         self.kv_dim = self.n_kv_heads * self.head_size
+
+    @classmethod
+    def from_arrays(cls, shape, eps, rope_theta, gs, hf_rope, fmt, embedding, rms_final, rms_att, rms_ffn, layers):
+        """A model from loader output (oracle/loaders.py): shape = (dim, hidden,
+        n_layers, n_heads, n_kv_heads, head_size, vocab, ctx_len); layers[l] =
+        7 projections (q, k, v, o, gate, down, up), each (q int8, s f32) for
+        Q8_0 or an f32 array for F16."""
+        h = lib().yo_model_new(np.array(shape, np.uint32), eps, rope_theta, gs, int(hf_rope), fmt,
+                               np.ascontiguousarray(embedding, np.float32), np.ascontiguousarray(rms_final, np.float32))
+        for l, projs in enumerate(layers):
+            lib().yo_model_set_norms(h, l, np.ascontiguousarray(rms_att[l], np.float32),
+                                     np.ascontiguousarray(rms_ffn[l], np.float32))
+            for k, w in enumerate(projs):
+                if fmt == F16:
+                    f = np.ascontiguousarray(w, np.float32)
+                    lib().yo_model_set_weight(h, l, k, F16, None, None, f.ctypes.data, f.size)
+                else:
+                    q = np.ascontiguousarray(w[0], np.int8)
+                    sc = np.ascontiguousarray(w[1], np.float32)
+                    lib().yo_model_set_weight(h, l, k, fmt, q.ctypes.data, sc.ctypes.data, None, q.size)
+        return cls(handle=h)
 
     def close(self):
         if self._h:

@@ -18,6 +18,8 @@ crossings worked by hand, the stale-entry quirk).
 from __future__ import annotations
 
 import ctypes
+import json
+import struct
 
 import jinja2
 import numpy as np
@@ -54,21 +56,29 @@ class OracleTokenizer:
     """Tokenizer::from_gguf_parts (tokenizer.rs:77-137) and its methods."""
 
     def __init__(self, vocab, merges, bos, eos, pre="default", add_bos_token=True, add_space_prefix=False,
-                 chat_template=None):
+                 chat_template=None, byte_level=True, scores=None):
         self.vocab = list(vocab)
         self.bos, self.eos, self.pre = bos, eos, pre
         self.add_bos_token, self.add_space_prefix = add_bos_token, add_space_prefix
         self.chat_template = chat_template
+        self.byte_level = byte_level
         # HashMap collect: the last id of equal texts; binary_search on the
         # stable-sorted vocabulary lands on the same (last) entry
         self.index = {t: i for i, t in enumerate(self.vocab)}
-        self.scores = [0.0] * len(self.vocab)
-        for i, m in enumerate(merges):
-            parts = m.split(" ", 1)
-            if len(parts) == 2:
-                j = self.index.get(parts[0] + parts[1])
-                if j is not None:
-                    self.scores[j] = float(np.float32(len(merges) - i))
+        if scores is not None:
+            self.scores = [float(np.float32(x)) for x in scores]
+        else:
+            self.scores = [0.0] * len(self.vocab)
+            for i, m in enumerate(merges):
+                parts = m.split(" ", 1)
+                if len(parts) == 2:
+                    j = self.index.get(parts[0] + parts[1])
+                    if j is not None:
+                        self.scores[j] = float(np.float32(len(merges) - i))
+        if not byte_level:   # Tokenizer::new: byte b is token b + 3 (tokenizer.rs:259)
+            self.char_to_byte, self.token_to_byte = {}, {}
+            self.byte_to_token = [b + 3 for b in range(256)]
+            return
         table = gpt2_byte_table()
         self.char_to_byte = {c: b for b, c in enumerate(table)}
         self.byte_to_token = [0] * 256
@@ -78,6 +88,42 @@ class OracleTokenizer:
             if j is not None:
                 self.byte_to_token[b] = j
                 self.token_to_byte[j] = b
+
+    @classmethod
+    def from_hf_json(cls, path):
+        """Tokenizer::from_json (tokenizer.rs:134-224): ids 0..=max id, gaps
+        empty, added tokens over the vocabulary, string merges, bos/eos from
+        the added tokens' names (defaults 128000 / 128009)."""
+        with open(path, encoding="utf-8") as f:
+            root = json.load(f)
+        vocab_obj, added = root["model"]["vocab"], root["added_tokens"]
+        max_id = max([v for v in vocab_obj.values()] + [t["id"] for t in added] + [0])
+        vocab = [""] * (max_id + 1)
+        for text, i in vocab_obj.items():
+            vocab[i] = text
+        for t in added:
+            vocab[t["id"]] = t["content"]
+        bos, eos = 128000, 128009
+        for t in added:
+            if t["content"] == "<|begin_of_text|>":
+                bos = t["id"]
+            if t["content"] in ("<|end_of_text|>", "<|eot_id|>"):
+                eos = t["id"]
+        return cls(vocab, root["model"]["merges"], bos, eos)
+
+    @classmethod
+    def from_llama2c(cls, path):
+        """Tokenizer::new (tokenizer.rs:226-268): the llama2.c tokenizer.bin."""
+        raw = open(path, "rb").read()
+        n, _, bos, eos = struct.unpack_from("<4I", raw, 0)
+        vocab, scores, o = [], [], 16
+        for _ in range(n):
+            sc, ln = struct.unpack_from("<fI", raw, o)
+            o += 8
+            vocab.append(raw[o:o + ln].decode("utf-8"))
+            scores.append(sc)
+            o += ln
+        return cls(vocab, [], bos, eos, byte_level=False, scores=scores)
 
     def has_llama_tokens(self):
         return len(self.vocab) > 128009
@@ -105,15 +151,23 @@ class OracleTokenizer:
                 text = " " + text
             for seg in gpt2_split(text):
                 tokens += self.bpe_merge([self.byte_to_token[b] for b in seg.encode()])
-        else:
+        elif self.byte_level:
             tokens += [self.byte_to_token[b] for b in text.encode()]
+            tokens = self.bpe_merge(tokens)
+        else:
+            for c in text:   # tokenizer.rs:356-370
+                j = self.index.get(c)
+                tokens += [j] if j is not None else [b + 3 for b in c.encode()]
             tokens = self.bpe_merge(tokens)
         if eos:
             tokens.append(self.eos)
         return tokens
 
     def decode(self, ids):
-        """tokenizer.rs:545-568 (byte-level) with String::from_utf8_lossy."""
+        """tokenizer.rs:540-568: byte-level ids through String::from_utf8_lossy,
+        else the vocabulary texts concatenated."""
+        if not self.byte_level:
+            return "".join(self.vocab[t] for t in ids if t < len(self.vocab))
         out = bytearray()
         for t in ids:
             if t in self.token_to_byte:

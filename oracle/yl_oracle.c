@@ -303,6 +303,43 @@ void yo_rope_gguf(const yo_rope_params *p, float *sq, float *k, uint32_t pos) {
 }
 
 /* forward.rs:299-400 */
+/* util::rope (util.rs:589-635): HF layout, element j of a head rotates with
+ * element j + head_size/2; llama3 frequency scaling with the model's ctx_len
+ * as the original context length. */
+void yo_rope_hf(uint32_t head_size, uint32_t n_heads, uint32_t n_kv_heads, float rope_theta, uint32_t ctx_len,
+                float *sq, float *k, uint32_t pos) {
+    const float rope_factor = 32.0f, low_freq_factor = 1.0f, high_freq_factor = 4.0f;
+    const float old_context_len = (float)ctx_len;
+    const float low_freq_wavelen = old_context_len / low_freq_factor;
+    const float high_freq_wavelen = old_context_len / high_freq_factor;
+    const uint32_t half = head_size / 2;
+    for (uint32_t j = 0; j < half; j++) {
+        const uint32_t head_dim = j * 2;
+        float freq = powf(rope_theta, -(float)head_dim / (float)head_size);
+        const float wavelen = (2.0f * (float)M_PI) / freq;
+        if (wavelen > low_freq_wavelen) {
+            freq /= rope_factor;
+        } else if (wavelen <= low_freq_wavelen && wavelen >= high_freq_wavelen) {
+            const float smooth = (old_context_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor);
+            freq = (1.0f - smooth) * freq / rope_factor + smooth * freq;
+        }
+        const float val = (float)pos * freq;
+        const float fcr = cosf(val), fci = sinf(val);
+        for (uint32_t h = 0; h < n_heads; h++) {
+            float *v = sq + h * head_size + j;
+            const float v0 = v[0], v1 = v[half];
+            v[0] = v0 * fcr - v1 * fci;
+            v[half] = v0 * fci + v1 * fcr;
+        }
+        for (uint32_t h = 0; h < n_kv_heads; h++) {
+            float *v = k + h * head_size + j;
+            const float v0 = v[0], v1 = v[half];
+            v[0] = v0 * fcr - v1 * fci;
+            v[half] = v0 * fci + v1 * fcr;
+        }
+    }
+}
+
 void yo_fused_attention(float *output, float *scores, const float *sq,
                         const float *key_cache, const float *value_cache,
                         size_t seq_len, size_t batch, size_t n_heads, size_t n_kv_heads,
@@ -417,6 +454,8 @@ struct yo_model {
     float eps, attention_scale;
     yo_rope_params rope;
     int weight_format;
+    uint32_t gs;         /* shape.group_size: 32 for GGUF, from the file for lm.rs / safetensors */
+    int hf_rope;         /* 1: util::rope (lm.rs, safetensors); 0: rope_gguf */
     float *token_embedding;            /* vocab*dim f32 */
     float *w_rms_final;
     float **w_rms_att, **w_rms_ffn;
@@ -630,6 +669,8 @@ yo_model *yo_model_load(const char *path, uint32_t max_ctx_len, int fmt_override
     m->rope.original_ctx_len = meta_u64(&kv[KW_RS_ORIG], &u) ? (uint32_t)u : seq_len;
     m->attention_scale = meta_f32(&kv[KW_ATT_SCALE], &f) ? f : 0.0f;
     m->rope.rope_theta = rope_theta;
+    m->gs = 32;
+    m->hf_rope = 0;
     m->rope.head_size = m->head_size;
     m->rope.n_heads = m->n_heads;
     m->rope.n_kv_heads = m->n_kv_heads;
@@ -721,6 +762,68 @@ fail:
     return NULL;
 }
 
+/* A model built from arrays: the lm.rs and safetensors loaders are restated
+ * in Python (oracle/loaders.py), which hands the weights over here.
+ * shape: dim, hidden, n_layers, n_heads, n_kv_heads, head_size, vocab, ctx_len. */
+yo_model *yo_model_new(const uint32_t shape[8], float eps, float rope_theta, uint32_t gs, int hf_rope,
+                       int weight_format, const float *embedding, const float *rms_final) {
+    yo_model *m = (yo_model *)calloc(1, sizeof *m);
+    m->dim = shape[0]; m->hidden = shape[1]; m->n_layers = shape[2]; m->n_heads = shape[3];
+    m->n_kv_heads = shape[4]; m->head_size = shape[5]; m->vocab = shape[6]; m->ctx_len = shape[7];
+    m->eps = eps;
+    m->attention_scale = 0.0f;
+    memset(&m->rope, 0, sizeof m->rope);
+    m->rope.rope_theta = rope_theta;
+    m->rope.head_size = m->head_size;
+    m->rope.n_heads = m->n_heads;
+    m->rope.n_kv_heads = m->n_kv_heads;
+    m->rope.freq_scale = 1.0f;
+    m->rope.attn_factor = 1.0f;
+    m->rope.original_ctx_len = m->ctx_len;
+    m->gs = gs;
+    m->hf_rope = hf_rope;
+    m->weight_format = weight_format;
+    const size_t ne = (size_t)m->vocab * m->dim, L = m->n_layers;
+    m->token_embedding = (float *)malloc(ne * sizeof(float) + 4);
+    memcpy(m->token_embedding, embedding, ne * sizeof(float));
+    m->w_rms_final = (float *)malloc(m->dim * sizeof(float) + 4);
+    memcpy(m->w_rms_final, rms_final, m->dim * sizeof(float));
+    m->w_rms_att = (float **)calloc(L, sizeof(float *));
+    m->w_rms_ffn = (float **)calloc(L, sizeof(float *));
+    m->wq = (yo_qt *)calloc(L, sizeof(yo_qt)); m->wk = (yo_qt *)calloc(L, sizeof(yo_qt));
+    m->wv = (yo_qt *)calloc(L, sizeof(yo_qt)); m->wo = (yo_qt *)calloc(L, sizeof(yo_qt));
+    m->w1 = (yo_qt *)calloc(L, sizeof(yo_qt)); m->w2 = (yo_qt *)calloc(L, sizeof(yo_qt));
+    m->w3 = (yo_qt *)calloc(L, sizeof(yo_qt));
+    return m;
+}
+
+void yo_model_set_norms(yo_model *m, uint32_t layer, const float *rms_att, const float *rms_ffn) {
+    m->w_rms_att[layer] = (float *)malloc(m->dim * sizeof(float) + 4);
+    m->w_rms_ffn[layer] = (float *)malloc(m->dim * sizeof(float) + 4);
+    memcpy(m->w_rms_att[layer], rms_att, m->dim * sizeof(float));
+    memcpy(m->w_rms_ffn[layer], rms_ffn, m->dim * sizeof(float));
+}
+
+/* which: 0 q, 1 k, 2 v, 3 o, 4 gate (w1), 5 down (w2), 6 up (w3); Q8_0 values q
+ * with f32 scales s (n / gs of them), or F16 values f as f32 */
+void yo_model_set_weight(yo_model *m, uint32_t layer, int which, int fmt, const int8_t *q, const float *s,
+                         const float *f, size_t n) {
+    yo_qt *all[7] = {m->wq, m->wk, m->wv, m->wo, m->w1, m->w2, m->w3};
+    yo_qt *t = &all[which][layer];
+    memset(t, 0, sizeof *t);
+    t->fmt = fmt;
+    t->n = n;
+    if (fmt == YO_F16) {
+        t->f = (float *)malloc(n * sizeof(float) + 4);
+        memcpy(t->f, f, n * sizeof(float));
+    } else {
+        t->q = (int8_t *)malloc(n + 4);
+        t->s = (float *)malloc(n / m->gs * sizeof(float) + 4);
+        memcpy(t->q, q, n);
+        memcpy(t->s, s, n / m->gs * sizeof(float));
+    }
+}
+
 void yo_model_shape(const yo_model *m, uint32_t out[8]) {
     out[0] = m->dim; out[1] = m->hidden; out[2] = m->n_layers; out[3] = m->n_heads;
     out[4] = m->n_kv_heads; out[5] = m->head_size; out[6] = m->vocab; out[7] = m->ctx_len;
@@ -752,14 +855,14 @@ float *yo_session_value_cache(yo_session *s) { return s->value_cache; }
 /* workspace for one activation quantization in a weight's format */
 typedef struct { int8_t *q; float *s; float *f; } xq_t;
 
-static void quant_for(const yo_qt *w, xq_t *xq, const float *x, size_t n) {
-    yo_quantize(w->fmt, xq->q, xq->s, xq->f, x, n, 32);
+static void quant_for(const yo_qt *w, xq_t *xq, const float *x, size_t n, uint32_t gs) {
+    yo_quantize(w->fmt, xq->q, xq->s, xq->f, x, n, gs);
 }
 
 /* ForwardKernel::matmul for the weight's format (forward.rs:39-43,61-65,83-87) */
-static void matmul_for(float *out, const xq_t *xq, const yo_qt *w, size_t n, size_t o, size_t batch) {
+static void matmul_for(float *out, const xq_t *xq, const yo_qt *w, size_t n, size_t o, size_t batch, uint32_t gs) {
     if (w->fmt == YO_F16) yo_matmul_f32(out, xq->f, w->f, n, o, batch);
-    else yo_matmul_q8_slices(out, xq->q, xq->s, w->q, w->s, n, o, 32, batch);
+    else yo_matmul_q8_slices(out, xq->q, xq->s, w->q, w->s, n, o, gs, batch);
 }
 
 /* forward.rs:120-280 */
@@ -772,7 +875,7 @@ int yo_forward_x(const yo_model *m, const uint32_t *tokens, size_t n_tokens,
     const size_t kv_dim = (size_t)m->n_kv_heads * m->head_size;
     const size_t seq_len = (size_t)start_pos + batch;
     if (seq_len > m->ctx_len) { set_err("position beyond ctx_len"); return -1; }
-    const size_t gs = 32;
+    const size_t gs = m->gs;
 
     /* embeddings (base_transformer.rs:143-161): out-of-range ids -> zeros */
     float *x = (float *)calloc(batch * dim, sizeof(float));
@@ -799,31 +902,37 @@ int yo_forward_x(const yo_model *m, const uint32_t *tokens, size_t n_tokens,
         const size_t cache_off = (size_t)layer * m->ctx_len * kv_dim;
         const size_t write_off = (size_t)start_pos * kv_dim;
         for (size_t t = 0; t < batch; t++) yo_rmsnorm(xn + t * dim, x + t * dim, m->w_rms_att[layer], dim, m->eps);
-        quant_for(&m->wq[layer], &xq, xn, batch * dim);
+        quant_for(&m->wq[layer], &xq, xn, batch * dim, m->gs);
         memset(sq, 0, batch * att_dim * sizeof(float));
-        matmul_for(sq, &xq, &m->wq[layer], dim, att_dim, batch);
+        matmul_for(sq, &xq, &m->wq[layer], dim, att_dim, batch, m->gs);
         float *k = s->key_cache + cache_off + write_off;
         float *v = s->value_cache + cache_off + write_off;
-        matmul_for(k, &xq, &m->wk[layer], dim, kv_dim, batch);
-        matmul_for(v, &xq, &m->wv[layer], dim, kv_dim, batch);
-        for (size_t t = 0; t < batch; t++) yo_rope_gguf(&m->rope, sq + t * att_dim, k + t * kv_dim, start_pos + (uint32_t)t);
+        matmul_for(k, &xq, &m->wk[layer], dim, kv_dim, batch, m->gs);
+        matmul_for(v, &xq, &m->wv[layer], dim, kv_dim, batch, m->gs);
+        for (size_t t = 0; t < batch; t++) {
+            if (m->hf_rope)
+                yo_rope_hf(m->head_size, m->n_heads, m->n_kv_heads, m->rope.rope_theta, m->ctx_len, sq + t * att_dim,
+                           k + t * kv_dim, start_pos + (uint32_t)t);
+            else
+                yo_rope_gguf(&m->rope, sq + t * att_dim, k + t * kv_dim, start_pos + (uint32_t)t);
+        }
         yo_fused_attention(att, scores, sq, s->key_cache + cache_off, s->value_cache + cache_off,
                            seq_len, batch, m->n_heads, m->n_kv_heads, m->head_size, start_pos, kv_dim, attn_scale);
-        quant_for(&m->wo[layer], &xq, att, batch * att_dim);
+        quant_for(&m->wo[layer], &xq, att, batch * att_dim, m->gs);
         memset(ffn, 0, batch * dim * sizeof(float));
-        matmul_for(ffn, &xq, &m->wo[layer], att_dim, dim, batch);
+        matmul_for(ffn, &xq, &m->wo[layer], att_dim, dim, batch, m->gs);
         for (size_t i = 0; i < total; i++) x[i] = x[i] + ffn[i];          /* :196-204 */
         for (size_t t = 0; t < batch; t++) yo_rmsnorm(xn + t * dim, x + t * dim, m->w_rms_ffn[layer], dim, m->eps);
-        quant_for(&m->w1[layer], &xq, xn, batch * dim);
+        quant_for(&m->w1[layer], &xq, xn, batch * dim, m->gs);
         memset(hg, 0, batch * hidden * sizeof(float));
         memset(hu, 0, batch * hidden * sizeof(float));
-        matmul_for(hg, &xq, &m->w1[layer], dim, hidden, batch);
-        matmul_for(hu, &xq, &m->w3[layer], dim, hidden, batch);
+        matmul_for(hg, &xq, &m->w1[layer], dim, hidden, batch, m->gs);
+        matmul_for(hu, &xq, &m->w3[layer], dim, hidden, batch, m->gs);
 #pragma omp parallel for schedule(static)
         for (size_t t = 0; t < batch; t++) yo_swiglu(hg + t * hidden, hu + t * hidden, hidden);
-        quant_for(&m->w2[layer], &xq, hg, batch * hidden);
+        quant_for(&m->w2[layer], &xq, hg, batch * hidden, m->gs);
         memset(ffn, 0, batch * dim * sizeof(float));
-        matmul_for(ffn, &xq, &m->w2[layer], hidden, dim, batch);
+        matmul_for(ffn, &xq, &m->w2[layer], hidden, dim, batch, m->gs);
         for (size_t i = 0; i < total; i++) x[i] = x[i] + ffn[i];          /* :245-253 */
     }
     for (size_t t = 0; t < batch; t++) yo_rmsnorm(xn + t * dim, x + t * dim, m->w_rms_final, dim, m->eps);

@@ -66,6 +66,9 @@ typedef struct {
 } yo_rope_params;
 /* util::rope_gguf, util.rs:653-718 (+ rope_yarn_ramp :720-724) */
 void yo_rope_gguf(const yo_rope_params *p, float *sq, float *k, uint32_t pos);
+/* util::rope (util.rs:589-635), HF layout with llama3 scaling */
+void yo_rope_hf(uint32_t head_size, uint32_t n_heads, uint32_t n_kv_heads, float rope_theta, uint32_t ctx_len,
+                float *sq, float *k, uint32_t pos);
 /* cos/sin of every pair at `pos`, exactly as rope_gguf derives them */
 void yo_rope_cos_sin(const yo_rope_params *p, uint32_t pos, float *cos_out, float *sin_out);
 
@@ -93,6 +96,12 @@ typedef struct yo_session yo_session;
  * fmt_override: -1 = none, else YO_Q8_0/YO_Q4_0/YO_F16.  Per-tensor formats
  * are kept as stored (the mixed-format extension); NULL on error. */
 yo_model *yo_model_load(const char *path, uint32_t max_ctx_len, int fmt_override);
+/* a model from arrays (lm.rs / safetensors loaders restated in oracle/loaders.py) */
+yo_model *yo_model_new(const uint32_t shape[8], float eps, float rope_theta, uint32_t gs, int hf_rope,
+                       int weight_format, const float *embedding, const float *rms_final);
+void yo_model_set_norms(yo_model *m, uint32_t layer, const float *rms_att, const float *rms_ffn);
+void yo_model_set_weight(yo_model *m, uint32_t layer, int which, int fmt, const int8_t *q, const float *s,
+                         const float *f, size_t n);
 void yo_model_free(yo_model *m);
 const char *yo_last_error(void);
 /* shape query: dim, hidden, n_layers, n_heads, n_kv_heads, head_size, vocab, ctx_len */

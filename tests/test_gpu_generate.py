@@ -28,9 +28,10 @@ def chat_model(tmp_path_factory):
     return path, otok
 
 
-def oracle_conversation(path, otok, prompts, max_tokens, temperature=0.7, top_p=0.9, seed=42):
-    """The CLI loop (main.rs:148-216) on the oracle: one session and sampler."""
-    m = O.Model(path)
+def oracle_conversation(model, otok, prompts, max_tokens, temperature=0.7, top_p=0.9, seed=42):
+    """The CLI loop (main.rs:148-216) on the oracle: one session and sampler.
+    `model` is a GGUF path or an oracle Model."""
+    m = O.Model(model) if isinstance(model, str) else model
     s = m.create_session()
     smp = OT.OracleSampler(len(otok.vocab), temperature, top_p, seed)
     pos, texts, ids_all = 0, [], []

@@ -20,8 +20,8 @@ OBJ = os.path.join(PKG, "_build")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libyallma3_amd.so")
 
-SOURCES = ["yl_kernels.hip", "yl_gemv.hip", "yl_gemm.hip", "yl_attn.hip", "yl_attn_split.hip", "yl_pattn.hip", "yl_logits.hip", "yl_f16.hip", "yl_model.hip",
-           "yl_gguf.cpp", "yl_synth.cpp", "yl_tokenizer.cpp", "yl_jinja.cpp"]
+SOURCES = ["yl_kernels.hip", "yl_gemv.hip", "yl_gemm.hip", "yl_attn.hip", "yl_attn_split.hip", "yl_pattn.hip", "yl_logits.hip", "yl_f16.hip", "yl_q8g.hip", "yl_model.hip",
+           "yl_gguf.cpp", "yl_synth.cpp", "yl_tokenizer.cpp", "yl_jinja.cpp", "yl_loaders.cpp"]
 ARCH = os.environ.get("YL_OFFLOAD_ARCH", "gfx950")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",

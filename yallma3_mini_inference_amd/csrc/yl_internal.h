@@ -34,11 +34,14 @@ namespace yl {
 enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs:17-22
 
 struct QMat {          // device-resident quantized matrix
-    int fmt = 0;       // kQ8 / kQ4
+    int fmt = 0;       // kQ8 / kQ4 / kF16
     int o = 0, n = 0, nb = 0;
     uint8_t* qs = nullptr;
     uint16_t* d = nullptr;
+    float* sf = nullptr;   // Q8 with f32 scales [o][n/gs] (lm.rs, safetensors); d unused then
+    int gs = 32;
     size_t bytes() const {
+        if (sf) return (size_t)o * n + (size_t)o * (n / gs) * 4;
         return fmt == kF16 ? (size_t)o * n * 2 : (size_t)o * (fmt == kQ4 ? n / 2 : n) + (size_t)o * nb * 2;
     }
 };
@@ -46,7 +49,7 @@ struct QMat {          // device-resident quantized matrix
 struct EmbQ8 {         // interleaved token embedding
     int vocab = 0, dim = 0, tiles = 0;
     int dimp = 0;      // dim rounded up to 64: the padding has scale 0 (Q8) or value 0 (F16)
-    int fmt = 0;       // 0: Q8_0 (q = u8 values, d = f16 scales); 1: F16 (q = f16 values, d unused)
+    int fmt = 0;       // 0: Q8_0 (q = u8 values, d = f16 scales); 1: F16 (q = f16 values); 2: F32 (q = f32 values)
     int8_t* q = nullptr;
     uint16_t* d = nullptr;
 };
@@ -164,6 +167,13 @@ hipError_t launch_raise_fault(unsigned* fault, hipStream_t s);
 // and f32 x [batch][n]; the QKV step (RoPE, `=` into the caches)
 hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, int batch, float* out, int out_ld,
                              int epi, hipStream_t s);
+// Q8 with f32 scales and group size gs (see yl_q8g.hip)
+hipError_t launch_matmul_q8g(const int8_t* w, const float* wsc, int n, int o, int gs, const int8_t* xq,
+                             const float* xs, int batch, float* out, const StepState* st, long pos_stride,
+                             long stride_row, long stride_tok, int acc_cols, int epi, hipStream_t s);
+hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size_t n, hipStream_t s);
+hipError_t launch_rope_cache(const float* cos_t, const float* sin_t, const StepState* st, int batch, float* q,
+                             float* kc, int att, int kv, int hd, int kv_ld, int hf_pairs, hipStream_t s);
 hipError_t launch_qkv_f16(const float* raw, const float* cos_t, const float* sin_t, const StepState* st, int batch,
                           float* sq, float* kc, float* vc, int att, int kv, int hd, int kv_ld, int hf_pairs,
                           hipStream_t s);

@@ -34,7 +34,9 @@ constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each)
 
 // EF = 0: Q8_0 table (u8 chunks of 16 + f16 scale pairs); EF = 1: f16 table
 // (32-byte chunks of 16 values), whose values are exactly the reference's f32
-// table (load_f16_tensor, transformer_llama_gguf.rs:412-421,487).
+// table (load_f16_tensor, transformer_llama_gguf.rs:412-421,487); EF = 2: the
+// f32 table itself (64-byte chunks), for tables dequantized with f32 scales
+// (lm.rs and safetensors Q8 embeddings, transformer_llama_lmrs.rs:176-181).
 template <int EF>
 __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* __restrict__ x,
                                                           const float* __restrict__ norm_w, float eps,
@@ -44,7 +46,8 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     extern __shared__ __align__(16) float lds[];
     __shared__ unsigned long long wkey[kLogitThreads / 64];
     constexpr int MP = 8192 / 8 / kLogitThreads;   // dim <= 8192
-    constexpr int NG = kLogitGroups;
+    constexpr int NG = EF == 2 ? 1 : kLogitGroups;
+    constexpr int CI = EF == 0 ? 1 : (EF == 1 ? 2 : 4);   // int4 loads per 16-value chunk
     const int dim = e.dim, tid = threadIdx.x;
     float* xn = lds;             // the normalized row, zero over the padding
     float* sq = lds + e.dimp;
@@ -54,8 +57,8 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     const int ng = e.dimp / 64;   // groups: 4 chunks, one block pair
     // chunk k of this row at qp[k * cs], the scales of block pair g at dp[g * cs]
     const size_t cs = (size_t)e.tiles * 64;
-    // (F16: each chunk is two int4, chunk k of this row at qp[2 * k * cs], qp[2 * k * cs + 1])
-    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 * (EF + 1) + lane * (EF + 1);
+    // (F16 and F32: each chunk is CI int4, chunk k of this row at qp[CI * k * cs + i])
+    const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 * CI + lane * CI;
     const uint32_t* dp = reinterpret_cast<const uint32_t*>(e.d) + (size_t)(live ? tile : 0) * 64 + lane;
     for (int i = dim + tid; i < e.dimp; i += kLogitThreads) xn[i] = 0.0f;
 
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     rowq_load_f32<MP>(tm, wv, norm_w, dim, passes);
     __syncthreads();
     // a ring of NG groups: each group's scale word, then its 4 chunks
-    int4 qv[NG][4 * (EF + 1)];
+    int4 qv[NG][4 * CI];
     uint32_t sv[NG];
     auto load_group = [&](int gg, int g) {
         if constexpr (EF == 0) {
@@ -78,10 +81,9 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
             for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
         } else {
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                qv[gg][2 * c] = load_stream(qp + (size_t)(4 * g + c) * cs * 2);
-                qv[gg][2 * c + 1] = load_stream(qp + (size_t)(4 * g + c) * cs * 2 + 1);
-            }
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int i = 0; i < CI; i++) qv[gg][CI * c + i] = load_stream(qp + (size_t)(4 * g + c) * cs * CI + i);
         }
     };
 #pragma unroll
@@ -98,13 +100,26 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                 const int g = g0 + gg;
                 if (NG > 1 && g >= ng) break;
                 const uint32_t sw = EF == 0 ? sv[gg] : 0u;
-                int4 q4[4 * (EF + 1)];
+                int4 q4[4 * CI];
 #pragma unroll
-                for (int c = 0; c < 4 * (EF + 1); c++) q4[c] = qv[gg][c];
+                for (int c = 0; c < 4 * CI; c++) q4[c] = qv[gg][c];
                 // refill with group g + NG (clamped re-reads past the row are
                 // never used)
                 load_group(gg, min(g + NG, ng - 1));
                 __builtin_amdgcn_sched_barrier(0);
+                if constexpr (EF == 2) {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float* xk = xn + (4 * g + c) * 16;
+#pragma unroll
+                        for (int ei = 0; ei < 16; ei++) {
+                            const int4 v4 = q4[4 * c + (ei >> 2)];
+                            const int bits = (ei & 3) == 0 ? v4.x : (ei & 3) == 1 ? v4.y : (ei & 3) == 2 ? v4.z : v4.w;
+                            l[ei & 7] = fadd(l[ei & 7], fmul(xk[ei], __builtin_bit_cast(float, bits)));
+                        }
+                    }
+                    continue;
+                }
                 if constexpr (EF == 1) {
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
@@ -194,7 +209,7 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
                          hipStream_t s) {
     const int nblk = logits_blocks(e);
     if (e.dim % 32 || e.dim > 8192) return hipErrorInvalidValue;
-    auto kern = e.fmt == 1 ? k_logits<1> : k_logits<0>;
+    auto kern = e.fmt == 2 ? k_logits<2> : (e.fmt == 1 ? k_logits<1> : k_logits<0>);
     if (logits_lds_bytes(e.dim) > 65536) {
         const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,

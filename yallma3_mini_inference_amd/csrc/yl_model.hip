@@ -31,6 +31,7 @@
 
 #include "yallma3.h"
 #include "yl_gguf.h"
+#include "yl_host_model.h"
 #include "yl_tokenizer.h"
 #include "yl_internal.h"
 
@@ -193,7 +194,8 @@ static bool upload_qmat(const HostQMat& h, QMat* m, std::string* err) {
 static void free_qmat(QMat* m) {
     if (m->qs) hipFree(m->qs);
     if (m->d) hipFree(m->d);
-    m->qs = nullptr; m->d = nullptr;
+    if (m->sf) hipFree(m->sf);
+    m->qs = nullptr; m->d = nullptr; m->sf = nullptr;
 }
 
 static float* upload_f32(const float* src, size_t n, std::string* err) {
@@ -207,6 +209,37 @@ static float* upload_f32(const float* src, size_t n, std::string* err) {
 
 // The (cos, sin) per pair and position of rope_gguf (util.rs:653-718), with
 // the C library's powf/cosf/sinf/logf as Rust's std calls them.
+// util::rope (util.rs:589-635): per pair j of a head, freq = theta^(-2j/hd)
+// with the llama3 frequency scaling (factor 32, low 1, high 4, the model's
+// ctx_len standing for the original context), angle = pos * freq; f32 steps
+// and the C library's powf/cosf/sinf as Rust's std calls them.
+static void rope_table_hf(float rope_theta, int head_size, uint32_t ctx_len, uint32_t count, float* cos_t, float* sin_t) {
+    const float rope_factor = 32.0f, low_freq_factor = 1.0f, high_freq_factor = 4.0f;
+    const float old_context_len = (float)ctx_len;
+    const float low_freq_wavelen = old_context_len / low_freq_factor;
+    const float high_freq_wavelen = old_context_len / high_freq_factor;
+    const int half = head_size / 2;
+    std::vector<float> freqs(half);
+    for (int j = 0; j < half; j++) {
+        const int head_dim = j * 2;
+        float freq = powf(rope_theta, -(float)head_dim / (float)head_size);
+        const float wavelen = (2.0f * 3.14159265358979323846f) / freq;
+        if (wavelen > low_freq_wavelen) {
+            freq = freq / rope_factor;
+        } else if (wavelen <= low_freq_wavelen && wavelen >= high_freq_wavelen) {
+            const float smooth = (old_context_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor);
+            freq = (1.0f - smooth) * freq / rope_factor + smooth * freq;
+        }
+        freqs[j] = freq;
+    }
+    for (uint32_t pos = 0; pos < count; pos++)
+        for (int j = 0; j < half; j++) {
+            const float val = (float)pos * freqs[j];
+            cos_t[(size_t)pos * half + j] = cosf(val);
+            sin_t[(size_t)pos * half + j] = sinf(val);
+        }
+}
+
 static void rope_table(const yl_rope_params& p, uint32_t pos_begin, uint32_t count, float* cos_t, float* sin_t) {
     const float beta_fast = 32.0f, beta_slow = 1.0f;
     const float two_pi = 2.0f * 3.14159265358979323846f;
@@ -251,7 +284,8 @@ struct yl_weight {
 
 struct Layer {
     QMat qkv, wo, w13, w2;
-    QMat w1, w3;                // F16 models: gate and up apart (w13 unused)
+    QMat w1, w3;                // F16 and f32-scaled Q8 models: gate and up apart (w13 unused)
+    QMat wq, wk, wv;            // f32-scaled Q8 models: q, k, v apart (qkv unused)
     float* rms_att = nullptr;
     float* rms_ffn = nullptr;
 };
@@ -269,6 +303,8 @@ struct yl_model {
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
     bool f16 = false;           // WeightFormat::F16: matmul_f32 on f16 weights (no activation quantization)
+    bool q8g = false;           // Q8 with f32 scales and group size gs (lm.rs, safetensors)
+    int gs = 32;
     int hf_rope = 0;            // 1: util::rope pairs (j, j + head/2); 0: rope_gguf pairs (2j, 2j + 1)
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
@@ -292,6 +328,8 @@ struct yl_session {
     float *as_ = nullptr, *hs = nullptr, *ns = nullptr;
     // F16 models: normalized rows, raw QKV outputs, attention output, gate/up/h (f32)
     float *xn = nullptr, *qkv_raw = nullptr, *attf = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
+    int8_t* gq = nullptr;                // f32-scaled Q8 models: quantized activation row and its scales
+    float* gsc = nullptr;
     float* sc = nullptr;                 // attention scores of long contexts [n_heads][ctx]
     float* psc = nullptr;                // prompt attention scratch (batches of 64+ tokens)
     size_t psc_bytes = 0;
@@ -319,6 +357,7 @@ void model_release(yl_model* m) {
     if (!m) return;
     for (auto& L : m->layers) {
         free_qmat(&L.qkv); free_qmat(&L.wo); free_qmat(&L.w13); free_qmat(&L.w2); free_qmat(&L.w1); free_qmat(&L.w3);
+        free_qmat(&L.wq); free_qmat(&L.wk); free_qmat(&L.wv);
         if (L.rms_att) hipFree(L.rms_att);
         if (L.rms_ffn) hipFree(L.rms_ffn);
     }
@@ -571,6 +610,126 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
     return m.release();
 }
 
+// A safetensors or lm.rs model (HostModel) onto the device.
+static bool upload_embedding_table(const HostModel& h, EmbQ8* e, std::string* err) {
+    const int dim = h.dim, vocab = h.vocab;
+    const int tiles = (vocab + 63) / 64, dimp = (dim + 63) & ~63;
+    const bool f16 = !h.emb_f16.empty();
+    const size_t elem = f16 ? 2 : 4, n = (size_t)tiles * 64 * dimp;
+    std::vector<uint8_t> buf(n * elem, 0);
+    for (int v = 0; v < vocab; v++)
+        for (int i = 0; i < dim; i++) {
+            const size_t at = emb_q_off(tiles, v / 64, i >> 4, v % 64) + (i & 15);
+            if (f16) memcpy(&buf[at * 2], &h.emb_f16[(size_t)v * dim + i], 2);
+            else memcpy(&buf[at * 4], &h.emb_f32[(size_t)v * dim + i], 4);
+        }
+    e->vocab = vocab; e->dim = dim; e->tiles = tiles; e->dimp = dimp; e->fmt = f16 ? 1 : 2;
+    if (hipMalloc(&e->q, buf.size() + 256) != hipSuccess || hipMalloc(&e->d, 256) != hipSuccess ||
+        hipMemcpy(e->q, buf.data(), buf.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "upload of the token embedding failed";
+        return false;
+    }
+    return true;
+}
+
+static bool upload_hostmat(const HostMat& h, QMat* m, std::string* err) {
+    m->o = (int)h.o; m->n = (int)h.n;
+    if (h.f16) {
+        m->fmt = kF16; m->nb = 0;
+        if (hipMalloc(&m->qs, h.h.size() * 2 + 256) != hipSuccess ||
+            hipMemcpy(m->qs, h.h.data(), h.h.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
+            *err = "weight upload failed";
+            return false;
+        }
+        return true;
+    }
+    m->fmt = kQ8; m->nb = 0; m->gs = h.gs;
+    if (hipMalloc(&m->qs, h.q.size() + 256) != hipSuccess || hipMalloc(&m->sf, h.s.size() * 4 + 256) != hipSuccess ||
+        hipMemcpy(m->qs, h.q.data(), h.q.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sf, h.s.data(), h.s.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        *err = "weight upload failed";
+        return false;
+    }
+    return true;
+}
+
+yl_model* model_from_host(HostModel& h, yl_status* st) {
+    *st = YL_ERR_UNSUPPORTED;
+    std::unique_ptr<yl_model, void (*)(yl_model*)> m(new yl_model(), model_release);
+    m->name = h.name;
+    m->dim = h.dim; m->hidden = h.hidden; m->n_layers = h.n_layers; m->n_heads = h.n_heads; m->n_kv = h.n_kv;
+    m->hd = h.hd; m->vocab = h.vocab; m->ctx = h.ctx; m->eps = h.eps;
+    m->kv_ld = (m->ctx + 3) & ~3;
+    m->att = m->n_heads * m->hd;
+    m->kv = m->n_kv * m->hd;
+    m->attn_scale = 1.0f / sqrtf((float)m->hd);
+    m->hf_rope = 1;
+    m->f16 = h.f16;
+    m->q8g = !h.f16;
+    m->gs = h.gs;
+    if (m->n_kv <= 0 || m->n_heads % m->n_kv || (m->hd != 32 && m->hd != 64 && m->hd != 128) || m->dim % 32 ||
+        m->hidden % 32 || m->att % 32 || m->kv % 32 || m->ctx <= 0 || m->dim > 8192 ||
+        (m->q8g && (m->dim % m->gs || m->att % m->gs || m->hidden % m->gs))) {
+        set_error("unsupported shape: head_size 32/64/128, dimensions multiples of 32 (and of the group size)");
+        return nullptr;
+    }
+    if ((uint64_t)m->kv_ld * (uint64_t)m->kv * 4 >= (1ull << 31)) {
+        set_error("context_length " + std::to_string(m->ctx) + " too long: cap it with max_ctx_len");
+        return nullptr;
+    }
+    hipGetDevice(&m->device);
+    std::string err;
+    if (!upload_embedding_table(h, &m->emb, &err)) { set_error(err); return nullptr; }
+    m->emb_bytes = (size_t)m->vocab * m->dim * (m->emb.fmt == 1 ? 2 : 4);
+    m->rms_final = upload_f32(h.rms_final.data(), m->dim, &err);
+    if (!m->rms_final) { set_error(err); return nullptr; }
+    m->layers.resize(m->n_layers);
+    for (int l = 0; l < m->n_layers; l++) {
+        Layer& L = m->layers[l];
+        const auto& H = h.layers[l];
+        L.rms_att = upload_f32(h.rms_att[l].data(), m->dim, &err);
+        L.rms_ffn = upload_f32(h.rms_ffn[l].data(), m->dim, &err);
+        if (!L.rms_att || !L.rms_ffn) { set_error(err); return nullptr; }
+        bool ok;
+        if (m->f16) {
+            HostQMat qkv;
+            qkv.fmt = kF16; qkv.n = H[0].n; qkv.o = H[0].o + H[1].o + H[2].o;
+            for (int k = 0; k < 3; k++)
+                qkv.qs.insert(qkv.qs.end(), (const uint8_t*)H[k].h.data(), (const uint8_t*)H[k].h.data() + H[k].h.size() * 2);
+            ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
+                 upload_hostmat(H[4], &L.w1, &err) && upload_hostmat(H[5], &L.w2, &err) && upload_hostmat(H[6], &L.w3, &err);
+        } else {
+            ok = upload_hostmat(H[0], &L.wq, &err) && upload_hostmat(H[1], &L.wk, &err) &&
+                 upload_hostmat(H[2], &L.wv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
+                 upload_hostmat(H[4], &L.w1, &err) && upload_hostmat(H[5], &L.w2, &err) && upload_hostmat(H[6], &L.w3, &err);
+        }
+        if (!ok) { set_error(err); return nullptr; }
+        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w1.bytes() + L.w2.bytes() + L.w3.bytes() + L.wq.bytes() +
+                           L.wk.bytes() + L.wv.bytes();
+    }
+    {
+        const size_t half = m->hd / 2;
+        std::vector<float> c((size_t)m->ctx * half), sn((size_t)m->ctx * half);
+        rope_table_hf(h.rope_theta, m->hd, (uint32_t)m->ctx, (uint32_t)m->ctx, c.data(), sn.data());
+        m->rope_cos = upload_f32(c.data(), c.size(), &err);
+        m->rope_sin = upload_f32(sn.data(), sn.size(), &err);
+        if (!m->rope_cos || !m->rope_sin) { set_error(err); return nullptr; }
+    }
+    m->tok.reset(h.tok);
+    h.tok = nullptr;
+    m->bos = m->tok->t.bos();
+    m->eos = m->tok->t.eos();
+    m->vocab_str.clear();
+    yl_shape& S = m->shape;
+    S.dimension = m->dim; S.hidden_dimension = m->hidden; S.n_heads = m->n_heads; S.head_size = m->hd;
+    S.n_kv_heads = m->n_kv; S.vocab_size = m->vocab; S.n_layers = m->n_layers; S.ctx_len = m->ctx;
+    S.rms_norm_eps = m->eps; S.rope_theta = h.rope_theta; S.group_size = m->gs;
+    S.rope_freq_scale = 1.0f; S.rope_ext_factor = 0.0f; S.rope_attn_factor = 1.0f;
+    S.rope_original_ctx_len = (uint32_t)m->ctx; S.attention_scale = 0.0f; S.weight_format = m->f16 ? YL_F16 : YL_Q8_0;
+    *st = YL_OK;
+    return m.release();
+}
+
 // The prompt attention scratch for `batch` tokens from `start_pos` (kept at
 // the largest size used; prompts below 64 tokens need none).
 bool prompt_scratch(yl_session* s, int batch, uint32_t start_pos) {
@@ -601,9 +760,17 @@ bool session_grow(yl_session* s, int batch) {
     s->graphs.clear();
     auto rel = [](auto*& p) { if (p) hipFree(p); p = nullptr; };
     rel(s->x); rel(s->sq); rel(s->aq); rel(s->hq); rel(s->as_); rel(s->hs); rel(s->tokens); rel(s->nq); rel(s->ns);
-    rel(s->xn); rel(s->qkv_raw); rel(s->attf); rel(s->gate); rel(s->up); rel(s->hf);
+    rel(s->xn); rel(s->qkv_raw); rel(s->attf); rel(s->gate); rel(s->up); rel(s->hf); rel(s->gq); rel(s->gsc);
     const size_t B = (size_t)batch;
-    if (m->f16) {
+    if (m->q8g) {
+        const size_t mx = std::max({(size_t)m->dim, (size_t)m->att, (size_t)m->hidden});
+        if (hipMalloc(&s->gq, B * mx + 256) != hipSuccess || hipMalloc(&s->gsc, B * mx / m->gs * 4 + 256) != hipSuccess) {
+            set_error("hipMalloc failed for session buffers");
+            s->cap_b = 0;
+            return false;
+        }
+    }
+    if (m->f16 || m->q8g) {
         const bool okf = hipMalloc(&s->xn, B * m->dim * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->qkv_raw, B * (m->att + 2 * m->kv) * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->attf, B * m->att * 4 + 256) == hipSuccess &&
@@ -815,8 +982,65 @@ hipError_t enqueue_forward_f16(const yl_model* m, yl_session* s, int batch, cons
                          s->ring_cap, advance, st);
 }
 
+// The forward pass of a Q8 model with f32 scales and group size gs
+// (forward.rs:120-297 with Q8Kernel; lm.rs and safetensors models): every
+// activation row quantized in gs groups, q/gate/up/FFN outputs from zero, K
+// and V accumulated onto the cache entries (`+=`), RoPE in place afterwards.
+hipError_t enqueue_forward_q8g(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+    hipStream_t st = s->stream;
+    const size_t lay_kv = (size_t)m->kv_ld * m->kv;
+    const int gs = m->gs;
+    auto mm = [&](const QMat& w, float* out, const StepState* stp, long pos_stride, long stride_row, long stride_tok,
+                  int acc_cols, int epi) {
+        return launch_matmul_q8g((const int8_t*)w.qs, w.sf, w.n, w.o, gs, s->gq, s->gsc, batch, out, stp, pos_stride,
+                                 stride_row, stride_tok, acc_cols, epi, st);
+    };
+    hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
+    for (int l = 0; l < m->n_layers && e == hipSuccess; l++) {
+        const Layer& L = m->layers[l];
+        float* kc = s->kc + (size_t)l * lay_kv;
+        float* vc = s->vc + (size_t)l * lay_kv;
+        e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        if (e == hipSuccess) e = launch_quantize_gs(s->xn, s->gq, s->gsc, gs, (size_t)batch * m->dim, st);
+        if (e == hipSuccess) e = mm(L.wq, s->sq, nullptr, 0, 1, m->att, 0, 0);
+        // K: [kv][kv_ld] from position pos; V: [pos][kv]
+        if (e == hipSuccess) e = mm(L.wk, kc, s->st, 1, m->kv_ld, 1, m->kv / 4 * 4, 0);
+        if (e == hipSuccess) e = mm(L.wv, vc, s->st, m->kv, 1, m->kv, m->kv / 4 * 4, 0);
+        if (e == hipSuccess)
+            e = launch_rope_cache(m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, m->att, m->kv, m->hd, m->kv_ld,
+                                  m->hf_rope, st);
+        if (e == hipSuccess) {
+            if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
+                e = launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale, -1,
+                                      nullptr, nullptr, s->attf, s->split, st);
+            else if (batch == 1)
+                e = launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                       m->attn_scale, -1, nullptr, nullptr, s->attf, s->sc, st);
+            else if (prompt_attn_applies(batch, s->pseq, m->hd))
+                e = launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv,
+                                            m->hd, m->attn_scale, -1, nullptr, nullptr, s->attf, s->psc, st);
+            else
+                e = launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                     m->attn_scale, -1, nullptr, nullptr, s->attf, st);
+        }
+        if (e == hipSuccess) e = launch_quantize_gs(s->attf, s->gq, s->gsc, gs, (size_t)batch * m->att, st);
+        if (e == hipSuccess) e = mm(L.wo, s->x, nullptr, 0, 1, m->dim, 0, 1);
+        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        if (e == hipSuccess) e = launch_quantize_gs(s->xn, s->gq, s->gsc, gs, (size_t)batch * m->dim, st);
+        if (e == hipSuccess) e = mm(L.w1, s->gate, nullptr, 0, 1, m->hidden, 0, 0);
+        if (e == hipSuccess) e = mm(L.w3, s->up, nullptr, 0, 1, m->hidden, 0, 0);
+        if (e == hipSuccess) e = launch_swiglu_quant(-1, s->gate, s->up, m->hidden, batch, s->hf, nullptr, nullptr, st);
+        if (e == hipSuccess) e = launch_quantize_gs(s->hf, s->gq, s->gsc, gs, (size_t)batch * m->hidden, st);
+        if (e == hipSuccess) e = mm(L.w2, s->x, nullptr, 0, 1, m->dim, 0, 1);
+    }
+    if (e != hipSuccess) return e;
+    return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st, s->ring,
+                         s->ring_cap, advance, st);
+}
+
 hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
     if (m->f16) return enqueue_forward_f16(m, s, batch, tok, advance);
+    if (m->q8g) return enqueue_forward_q8g(m, s, batch, tok, advance);
     for (int l = 0; l < m->n_layers; l++)
         for (int c = kOpQkv; c <= kOpW2; c++) {
             const hipError_t e = enqueue_op(m, s, c, l, batch, tok, advance, nullptr);
@@ -1375,6 +1599,18 @@ yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) 
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) { set_error("no HIP device"); return nullptr; }
     yl_status st;
+    // lib.rs:107-133: the loader by file extension
+    const std::string p(path);
+    const size_t dot = p.rfind('.');
+    const std::string ext = dot == std::string::npos ? "" : p.substr(dot + 1);
+    if (ext == "safetensors" || ext == "lmrs") {
+        HostModel h;
+        std::string err;
+        const bool ok = ext == "lmrs" ? load_lmrs(p, max_ctx_len, fmt_override, &h, &err)
+                                      : load_safetensors(p, max_ctx_len, fmt_override, &h, &err);
+        if (!ok) { set_error(err); return nullptr; }
+        return model_from_host(h, &st);
+    }
     return load_model(path, max_ctx_len, fmt_override, &st);
 }
 
@@ -1448,7 +1684,7 @@ void yl_session_free(yl_session* s) {
     for (auto& g : s->graphs) hipGraphExecDestroy(g.exec);
     void* dev[] = {s->kc, s->vc, s->st, s->logits, s->ring, s->x, s->sq, s->aq, s->hq,
                    s->as_, s->hs, s->nq, s->ns, s->tokens, s->sc, s->psc, s->split,
-                   s->xn, s->qkv_raw, s->attf, s->gate, s->up, s->hf};
+                   s->xn, s->qkv_raw, s->attf, s->gate, s->up, s->hf, s->gq, s->gsc};
     for (void* p : dev) if (p) hipFree(p);
     if (s->st_host) hipHostFree(s->st_host);
     if (s->stream) hipStreamDestroy(s->stream);
@@ -1580,7 +1816,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
-    if (m->f16) { set_error("profile: the kernel classes are those of the quantized path"); return YL_ERR_UNSUPPORTED; }
+    if (m->f16 || m->q8g) { set_error("profile: the kernel classes are those of the GGUF quantized path"); return YL_ERR_UNSUPPORTED; }
     if (batch == 1 && !decode_in_range(m, s, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
     s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
     s->prof_seq = (uint64_t)start_pos + batch;
@@ -1723,10 +1959,8 @@ bool load_transformer_ffi(const char* model_path) {
     const std::string p(model_path);
     const size_t dot = p.rfind('.');
     const std::string ext = dot == std::string::npos ? "" : p.substr(dot + 1);
-    if (ext != "gguf") {
-        set_error(ext == "lmrs" || ext == "safetensors"
-                      ? "Unsupported model extension here: ." + ext + " loaders are not built (GGUF is)"
-                      : "Unsupported model extension for path: " + p);
+    if (ext != "gguf" && ext != "lmrs" && ext != "safetensors") {
+        set_error("Unsupported model extension for path: " + p);
         return false;
     }
     yl_model* m = yl_load(model_path, 0xFFFFFFFFu, -1);

@@ -2,6 +2,7 @@
 #include "yl_tokenizer.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
@@ -9,7 +10,9 @@
 #include "yallma3.h"
 #include "yl_gguf.h"
 #include "yl_internal.h"
+#include "yl_host_model.h"
 #include "yl_jinja.h"
+#include "yl_json.h"
 #include "yl_unicode_tables.h"
 
 namespace yl {
@@ -156,20 +159,29 @@ std::string trim_unicode(const std::string& s) {
 Tokenizer::Tokenizer(TokenizerSpec spec)
     : vocab_(std::move(spec.vocab)), bos_(spec.bos), eos_(spec.eos), pre_(std::move(spec.pre)),
       add_bos_token_(spec.add_bos_token), add_space_prefix_(spec.add_space_prefix), has_template_(spec.has_template),
-      template_(std::move(spec.chat_template)) {
+      template_(std::move(spec.chat_template)), byte_level_(spec.byte_level) {
     const size_t V = vocab_.size();
     index_.reserve(V * 2);
     for (size_t i = 0; i < V; i++) index_[vocab_[i]] = (uint32_t)i;   // equal texts: the last id
-    // merge rank -> score of the merged token (from_gguf_parts, tokenizer.rs:80-90)
-    scores_.assign(V, 0.0f);
-    const size_t M = spec.merges.size();
-    for (size_t i = 0; i < M; i++) {
-        const std::string& mg = spec.merges[i];
-        const size_t sp = mg.find(' ');
-        if (sp == std::string::npos) continue;
-        const std::string merged = mg.substr(0, sp) + mg.substr(sp + 1);
-        auto it = index_.find(merged);
-        if (it != index_.end()) scores_[it->second] = (float)(M - i);
+    if (spec.has_scores) {
+        scores_ = spec.scores;
+        scores_.resize(V, 0.0f);
+    } else {
+        // merge rank -> score of the merged token (from_gguf_parts, tokenizer.rs:80-90)
+        scores_.assign(V, 0.0f);
+        const size_t M = spec.merges.size();
+        for (size_t i = 0; i < M; i++) {
+            const std::string& mg = spec.merges[i];
+            const size_t sp = mg.find(' ');
+            if (sp == std::string::npos) continue;
+            const std::string merged = mg.substr(0, sp) + mg.substr(sp + 1);
+            auto it = index_.find(merged);
+            if (it != index_.end()) scores_[it->second] = (float)(M - i);
+        }
+    }
+    if (!byte_level_) {   // Tokenizer::new: bytes map to ids 3..258, no byte characters
+        for (int b = 0; b < 256; b++) byte_to_token_[b] = (uint32_t)b + 3;
+        return;
     }
     uint32_t table[256];
     gpt2_byte_table(table);
@@ -219,11 +231,26 @@ bool Tokenizer::encode(const std::string& text, bool bos, bool eos, std::vector<
             bpe_merge(&seg);
             tokens.insert(tokens.end(), seg.begin(), seg.end());
         }
-    } else {
+    } else if (byte_level_) {
         for (unsigned char c : text) tokens.push_back(byte_to_token_[c]);
         for (uint32_t id : tokens)
             if (id >= vocab_.size()) { *err = "token id " + std::to_string(id) + " outside the vocabulary"; return false; }
         bpe_merge(&tokens);   // the BOS token takes part in the merges (tokenizer.rs:372)
+    } else {
+        // each character by its vocabulary entry, else its UTF-8 bytes as ids b + 3 (tokenizer.rs:356-370)
+        std::vector<uint32_t> cp;
+        std::vector<size_t> off;
+        decode_utf8(text, &cp, &off);
+        for (size_t k = 0; k < cp.size(); k++) {
+            const std::string ch = text.substr(off[k], off[k + 1] - off[k]);
+            auto it = index_.find(ch);
+            if (it != index_.end()) tokens.push_back(it->second);
+            else
+                for (unsigned char b : ch) tokens.push_back((uint32_t)b + 3);
+        }
+        for (uint32_t id : tokens)
+            if (id >= vocab_.size()) { *err = "token id " + std::to_string(id) + " outside the vocabulary"; return false; }
+        bpe_merge(&tokens);
     }
     if (eos) tokens.push_back(eos_);
     out->insert(out->end(), tokens.begin(), tokens.end());
@@ -231,6 +258,12 @@ bool Tokenizer::encode(const std::string& text, bool bos, bool eos, std::vector<
 }
 
 std::string Tokenizer::decode(const std::vector<uint32_t>& ids) const {
+    if (!byte_level_) {   // the vocabulary texts concatenated (tokenizer.rs:560-566)
+        std::string text;
+        for (uint32_t tid : ids)
+            if (tid < vocab_.size()) text += vocab_[tid];
+        return text;
+    }
     std::string bytes;
     for (uint32_t tid : ids) {
         if (tid < token_to_byte_.size() && token_to_byte_[tid] >= 0) {
@@ -477,6 +510,100 @@ yl_tokenizer* tokenizer_from_gguf(const GgufFile& g, std::string* err) {
     return new yl_tokenizer{Tokenizer(std::move(ts))};
 }
 
+yl_tokenizer* tokenizer_from_hf_json(const std::string& path, std::string* err) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) { *err = "cannot open " + path; return nullptr; }
+    std::string text;
+    char buf[1 << 16];
+    size_t k;
+    while ((k = fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, k);
+    fclose(f);
+    json::Value root;
+    if (!json::parse(text, &root, err)) return nullptr;
+    const json::Value* model = root.get("model");
+    const json::Value* vocab = model ? model->get("vocab") : nullptr;
+    const json::Value* added = root.get("added_tokens");
+    const json::Value* merges = model ? model->get("merges") : nullptr;
+    if (!vocab || vocab->kind != json::Value::kObj || !added || added->kind != json::Value::kArr || !merges ||
+        merges->kind != json::Value::kArr) {
+        *err = "tokenizer.json: model.vocab, model.merges and added_tokens are required";
+        return nullptr;
+    }
+    uint64_t max_id = 0, id = 0;
+    for (const auto& kv : vocab->obj) {
+        if (!kv.second.as_u64(&id)) { *err = "tokenizer.json: vocabulary ids must be integers"; return nullptr; }
+        max_id = std::max(max_id, id);
+    }
+    for (const auto& t : added->arr) {
+        const json::Value* v = t.get("id");
+        if (!v || !v->as_u64(&id) || !t.get("content") || !t.get("content")->as_str()) {
+            *err = "tokenizer.json: added_tokens need id and content";
+            return nullptr;
+        }
+        max_id = std::max(max_id, id);
+    }
+    if (max_id > 10000000) { *err = "tokenizer.json: vocabulary id out of range"; return nullptr; }
+    TokenizerSpec ts;
+    ts.vocab.assign(max_id + 1, std::string());
+    for (const auto& kv : vocab->obj) {
+        kv.second.as_u64(&id);
+        ts.vocab[id] = kv.first;
+    }
+    for (const auto& t : added->arr) {
+        t.get("id")->as_u64(&id);
+        ts.vocab[id] = *t.get("content")->as_str();
+    }
+    for (const auto& m : merges->arr) {
+        if (!m.as_str()) { *err = "tokenizer.json: merges must be strings"; return nullptr; }
+        ts.merges.push_back(*m.as_str());
+    }
+    ts.bos = 128000u;
+    ts.eos = 128009u;
+    for (const auto& t : added->arr) {
+        const std::string& c = *t.get("content")->as_str();
+        t.get("id")->as_u64(&id);
+        if (c == "<|begin_of_text|>") ts.bos = (uint32_t)id;
+        if (c == "<|end_of_text|>" || c == "<|eot_id|>") ts.eos = (uint32_t)id;
+    }
+    return new yl_tokenizer{Tokenizer(std::move(ts))};
+}
+
+yl_tokenizer* tokenizer_from_llama2c(const std::string& path, std::string* err) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) { *err = "cannot open " + path; return nullptr; }
+    std::string d;
+    char buf[1 << 16];
+    size_t k;
+    while ((k = fread(buf, 1, sizeof buf, f)) > 0) d.append(buf, k);
+    fclose(f);
+    auto u32 = [&](size_t o) { uint32_t v; memcpy(&v, d.data() + o, 4); return v; };
+    if (d.size() < 16) { *err = "tokenizer.bin: too short"; return nullptr; }
+    TokenizerSpec ts;
+    const uint32_t n = u32(0);
+    ts.bos = u32(8);
+    ts.eos = u32(12);
+    ts.byte_level = false;
+    ts.has_scores = true;
+    size_t o = 16;
+    for (uint32_t i = 0; i < n; i++) {
+        if (o + 8 > d.size()) { *err = "tokenizer.bin: truncated"; return nullptr; }
+        float sc;
+        memcpy(&sc, d.data() + o, 4);
+        const uint32_t len = u32(o + 4);
+        o += 8;
+        if (o + len > d.size()) { *err = "tokenizer.bin: truncated"; return nullptr; }
+        std::string t = d.substr(o, len);
+        if (!valid_utf8(t.c_str()) || t.find('\0') != std::string::npos) {
+            *err = "tokenizer.bin: a token is not UTF-8";
+            return nullptr;
+        }
+        ts.vocab.push_back(std::move(t));
+        ts.scores.push_back(sc);
+        o += len;
+    }
+    return new yl_tokenizer{Tokenizer(std::move(ts))};
+}
+
 }  // namespace yl
 
 using namespace yl;
@@ -499,10 +626,20 @@ extern "C" {
 
 yl_tokenizer* yl_tokenizer_load(const char* path) {
     if (!path) { set_error("tokenizer_load: null path"); return nullptr; }
-    GgufFile g;
+    const std::string p = path;
+    auto ends = [&](const char* x) {
+        const size_t n = strlen(x);
+        return p.size() >= n && p.compare(p.size() - n, n, x) == 0;
+    };
     std::string err;
-    if (!g.open(path, &err)) { set_error(err); return nullptr; }
-    yl_tokenizer* t = tokenizer_from_gguf(g, &err);
+    yl_tokenizer* t = nullptr;
+    if (ends(".json")) t = tokenizer_from_hf_json(p, &err);
+    else if (ends(".bin")) t = tokenizer_from_llama2c(p, &err);
+    else {
+        GgufFile g;
+        if (!g.open(path, &err)) { set_error(err); return nullptr; }
+        t = tokenizer_from_gguf(g, &err);
+    }
     if (!t) set_error(err);
     return t;
 }

@@ -20,6 +20,9 @@ namespace yl {
 struct TokenizerSpec {
     std::vector<std::string> vocab;
     std::vector<std::string> merges;
+    bool byte_level = true;         // GPT-2 byte characters (GGUF, tokenizer.json); false: llama2.c tokenizer.bin
+    bool has_scores = false;        // scores given (tokenizer.bin) instead of derived from merges
+    std::vector<float> scores;
     uint32_t bos = 0, eos = 0;
     std::string pre = "default";
     bool add_bos_token = true, add_space_prefix = false;
@@ -60,6 +63,7 @@ private:
     bool add_bos_token_, add_space_prefix_;
     bool has_template_;
     std::string template_;
+    bool byte_level_ = true;
     uint32_t byte_to_token_[256];
     std::vector<int> token_to_byte_;                    // -1: none
     std::unordered_map<uint32_t, uint8_t> char_to_byte_;   // GPT-2 byte table, code point -> byte

@@ -42,11 +42,17 @@ class Tokenizer:
         self._owner = owner   # the model that owns the handle, or None (owned here)
 
     @classmethod
-    def from_gguf(cls, path: str) -> "Tokenizer":
+    def from_file(cls, path: str) -> "Tokenizer":
+        """tokenizer.json (Tokenizer::from_json), tokenizer.bin
+        (Tokenizer::new) or a GGUF file (Tokenizer::from_gguf_parts), by the
+        file's extension."""
         h = lib().yl_tokenizer_load(os.fsencode(path))
         if not h:
             raise YlError(-4, last_error())
         return cls(h)
+
+    from_gguf = from_file
+    from_json = from_file
 
     @property
     def vocab_size(self) -> int:

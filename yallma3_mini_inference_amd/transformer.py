@@ -1,7 +1,7 @@
 """The Transformer trait and InferenceSession over the HIP forward path.
 
 Python mirror of the reference's model API:
-  load_transformer(path, ...)     lib.rs:107-133 (".gguf" models)
+  load_transformer(path, ...)     lib.rs:107-133 (.gguf, .lmrs, .safetensors)
   Transformer                     trait Transformer, transformer.rs:19-69,
                                   implemented as TransformerLlamaGguf
                                   (transformer_llama_gguf.rs:658-729)
@@ -114,7 +114,8 @@ class InferenceSession:
 
 
 class Transformer:
-    """TransformerLlamaGguf on one MI355X."""
+    """TransformerLlamaGguf / TransformerLlamaLmrs / TransformerLlamaSt on one
+    MI355X (the file's extension picks the loader; name() says which)."""
 
     def __init__(self, path: str, max_ctx_len: int = 0xFFFFFFFF, fmt_override: WeightFormat | None = None):
         ov = -1 if fmt_override is None else int(fmt_override)
@@ -235,10 +236,16 @@ TransformerLlamaGguf = Transformer
 
 def load_transformer(model_path: str, sequential: bool = False, max_ctx_len: int = 0xFFFFFFFF,
                      fmt_override: WeightFormat | None = None) -> Transformer:
-    """lib.rs:107-133.  Only the ".gguf" branch is built; others raise."""
+    """lib.rs:107-133: ".gguf" (TransformerLlamaGguf), ".lmrs"
+    (TransformerLlamaLmrs) and ".safetensors" (TransformerLlamaSt) files.
+    sequential=True with a safetensors file asks for the reference's scalar
+    teaching forward (TransformerLlamaStSeq), which is not built here."""
     ext = os.path.splitext(model_path)[1].lstrip(".")
-    if ext != "gguf":
-        raise YlError(-6, f"Unsupported model extension for path: {model_path} (GGUF is built)")
+    if ext not in ("gguf", "lmrs", "safetensors"):
+        raise YlError(-6, f"Unsupported model extension for path: {model_path}")
+    if ext == "safetensors" and sequential:
+        raise YlError(-6, "TransformerLlamaStSeq (the sequential scalar forward) is not built; "
+                          "load with sequential=False")
     return Transformer(model_path, max_ctx_len, fmt_override)
 
 
