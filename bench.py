@@ -96,7 +96,7 @@ def cpu_baseline(path, prompt_len, seconds, kv):
     import numpy as np
     from oracle import oracle as O
     t0 = time.perf_counter()
-    m = O.Model(path)
+    m = oracle_model(path)
     s = m.create_session()
     s.key_cache()[:, :prompt_len] = kv[0]
     s.value_cache()[:, :prompt_len] = kv[1]
@@ -145,7 +145,36 @@ DECODE = {
     "smollm2_135m": (256, 128, "SmolLM2-135M-shaped Q8_0 greedy decode, batch 1, 256-token prompt then 128 steps"),
     "llama3_8b_mixed": (8192, 256, "Llama-3-8B-shaped decode (Q4_0 FFN, Q8_0 attention/output), batch 1, KV cache "
                                    "prefilled to 8192 positions, then 256 steps"),
+    "lmrs_1b": (512, 256, "Llama-3.2-1B-shaped lm.rs model (Q8, f32 scales per group of 32, HF-layout RoPE) greedy "
+                          "decode, batch 1, 512-token prompt then 256 steps, KV f32 ctx 4096"),
+    "st_f16_1b": (512, 256, "Llama-3.2-1B-shaped safetensors F16 model (matmul_f32, HF-layout RoPE) greedy decode, "
+                            "batch 1, 512-token prompt then 256 steps, KV f32 ctx 4096"),
 }
+
+# Models of the lm.rs and safetensors formats (synth_files), and the kernel
+# that runs each GEMV class of theirs.
+FILE_CONFIGS = {"lmrs_1b", "st_f16_1b"}
+FILE_KERNELS = {
+    "lmrs_1b": {"qkv": "k_matmul_q8g (q, k, v; RMSNorm and group quantize before)",
+                "wo": "k_matmul_q8g (output projection, residual add)",
+                "w13": "k_matmul_q8g (gate and up; SwiGLU after)", "w2": "k_matmul_q8g (down, residual add)"},
+    "st_f16_1b": {"qkv": "k_matmul_f16_tok1 (fused q/k/v rows)", "wo": "k_matmul_f16_tok1 (output, residual add)",
+                  "w13": "k_matmul_f16_tok1 (gate and up)", "w2": "k_matmul_f16_tok1 (down, residual add)"},
+}
+
+
+def model_path(config):
+    from yallma3_mini_inference_amd import synth, synth_files
+    return synth_files.ensure(config) if config in FILE_CONFIGS else synth.ensure(config)
+
+
+def oracle_model(path):
+    """The oracle's model of a GGUF, lm.rs or safetensors file."""
+    from oracle import oracle as O
+    if path.endswith(".gguf"):
+        return O.Model(path)
+    from oracle import loaders
+    return (loaders.load_lmrs if path.endswith(".lmrs") else loaders.load_safetensors)(path)[0]
 
 
 def run_prefill(args):
@@ -271,7 +300,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
     ap.add_argument("--config", default="llama32_1b", choices=sorted(DECODE),
-                    help="decode workload: llama32_1b (the headline), smollm2_135m, llama3_8b_mixed")
+                    help="decode workload: llama32_1b (the headline), smollm2_135m, llama3_8b_mixed, lmrs_1b "
+                         "(lm.rs Q8 with f32 group scales), st_f16_1b (safetensors F16)")
     ap.add_argument("--attention", choices=("exact", "split"), default="exact",
                     help="decode attention: exact (the reference's operation order, bit-exact; the default) or "
                          "split over the context (equal up to rounding; on these synthetic models rounding-level "
@@ -324,7 +354,7 @@ def main():
     if args.steps is None:
         args.steps = d_steps - args.warmup
     t0 = time.perf_counter()
-    path = synth.ensure(args.config)
+    path = model_path(args.config)
     log(f"model {path} ready in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     model = Y.Transformer(path)
@@ -397,8 +427,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights, GGUF blocks; random prompt ids)",
+        "dtype": "f16 weights, f32 activations" if args.config == "st_f16_1b" else "int8",
+        "data": ("synthetic (seeded N(0,0.02) weights, GGUF blocks; random prompt ids)" if args.config not in
+                 FILE_CONFIGS else "synthetic (seeded random weights, lm.rs / safetensors file; random prompt ids)"),
         "config": {
             "workload": d_desc,
             "batch": 1, "prompt_tokens": args.prompt,
@@ -410,7 +441,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": KERNEL_NAMES[dom], "class": dom,
+            "kernel": FILE_KERNELS.get(args.config, KERNEL_NAMES)[dom], "class": dom,
             "avg_launch_us": kern[dom]["us"], "bytes_per_launch": kern[dom]["bytes"],
         },
         "gemv_all": {"us_per_token": round(gemv_us, 2), "bytes_per_token": gemv_bytes,

@@ -18,6 +18,15 @@ from . import oracle as O
 from . import tokenizer as OT
 
 
+# binary16 -> float32 for every bit pattern (numpy's IEEE conversion), used as
+# a lookup table: numpy converts half floats one element at a time.
+_F16_TO_F32 = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+
+
+def _f16(raw: bytes, count: int, offset: int) -> np.ndarray:
+    return _F16_TO_F32[np.frombuffer(raw, np.uint16, count, offset)]
+
+
 def _round_away(x: np.ndarray) -> np.ndarray:
     """Rust f32::round (half away from zero), exactly (in float64)."""
     x = x.astype(np.float64)
@@ -31,8 +40,8 @@ def load_q8_tensor_st(raw: bytes, rows: int, cols: int, gs: int, w_off: int, s_o
     n = rows * cols
     groups = n // gs
     vals = np.frombuffer(raw, np.uint8, n, w_off).astype(np.float32)
-    scale = np.frombuffer(raw, np.float16, groups, s_off).astype(np.float32)
-    bias = np.frombuffer(raw, np.float16, groups, b_off).astype(np.float32)
+    scale = _f16(raw, groups, s_off)
+    bias = _f16(raw, groups, b_off)
     deq = (vals.reshape(groups, gs) * scale[:, None]).astype(np.float32) + bias[:, None]
     deq = deq.astype(np.float32)
     max_abs = np.max(np.abs(deq), axis=1)
@@ -68,7 +77,7 @@ def read_safetensors(path: str, max_ctx_len: int = 0xFFFFFFFF) -> dict:
     hdr = json.loads(raw[8:8 + hlen])
     start = 8 + hlen
     off = {k: start + v["data_offsets"][0] for k, v in hdr.items() if k != "__metadata__"}
-    f16v = lambda name, n: np.frombuffer(raw, np.float16, n, off[name]).astype(np.float32)
+    f16v = lambda name, n: _f16(raw, n, off[name])
     out = {"shape": (dim, hidden, nl, nh, nkv, hd, vocab, ctx), "eps": eps, "rope_theta": theta, "gs": gs,
            "fmt": O.F16 if f16 else O.Q8_0}
     out["rms_final"] = f16v("model.norm.weight", dim)

@@ -28,8 +28,9 @@ struct HostModel {
     float eps = 0.0f, rope_theta = 0.0f;
     bool f16 = false;             // WeightFormat::F16, else Q8_0 with f32 scales
     int gs = 32;
-    std::vector<float> emb_f32;   // token embedding [vocab][dim] as the reference holds it (Q8 models)
-    std::vector<uint16_t> emb_f16;   // F16 models: the same values as binary16
+    HostMat emb_q8;               // Q8 models: token embedding [vocab][dim] int8 + f32 scales per gs group;
+                                  // the reference's f32 table is exactly q * scale (transformer_llama_lmrs.rs:176-181)
+    std::vector<uint16_t> emb_f16;   // F16 models: the table's values as binary16
     std::vector<std::vector<float>> rms_att, rms_ffn;
     std::vector<float> rms_final;
     // per layer: attn q, k, v, output, ffn gate, down, up

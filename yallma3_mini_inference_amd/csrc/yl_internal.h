@@ -49,9 +49,12 @@ struct QMat {          // device-resident quantized matrix
 struct EmbQ8 {         // interleaved token embedding
     int vocab = 0, dim = 0, tiles = 0;
     int dimp = 0;      // dim rounded up to 64: the padding has scale 0 (Q8) or value 0 (F16)
-    int fmt = 0;       // 0: Q8_0 (q = u8 values, d = f16 scales); 1: F16 (q = f16 values); 2: F32 (q = f32 values)
+    int fmt = 0;       // 0: Q8_0 (q = u8 values, d = f16 scales); 1: F16 (q = f16 values);
+                       // 3: Q8 with f32 scales per gs group (q = int8 values, d32 = scales)
     int8_t* q = nullptr;
     uint16_t* d = nullptr;
+    float* d32 = nullptr;   // fmt 3: scale of group g of row (tile, lane) at d32[(g * tiles + tile) * 64 + lane]
+    int gs = 32;
 };
 // Layout: vocabulary rows in tiles of 64 (lane = row % 64).  Chunk k (16
 // values, bytes u = q + 128) of every row of every tile lies together,
@@ -167,10 +170,32 @@ hipError_t launch_raise_fault(unsigned* fault, hipStream_t s);
 // and f32 x [batch][n]; the QKV step (RoPE, `=` into the caches)
 hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, int batch, float* out, int out_ld,
                              int epi, hipStream_t s);
-// Q8 with f32 scales and group size gs (see yl_q8g.hip)
-hipError_t launch_matmul_q8g(const int8_t* w, const float* wsc, int n, int o, int gs, const int8_t* xq,
-                             const float* xs, int batch, float* out, const StepState* st, long pos_stride,
-                             long stride_row, long stride_tok, int acc_cols, int epi, hipStream_t s);
+// Q8 with f32 scales and group size gs (see yl_q8g.hip).  Output rows
+// [seg[i-1].row_end, seg[i].row_end) go to segment i: element (token t,
+// column c) at out[pos * pos_stride + t * stride_tok + c * stride_row], pos =
+// st->pos (0 without st); columns below acc_cols start from the output's value.
+struct Q8gSegArgs {
+    float* out = nullptr;
+    long pos_stride = 0, stride_row = 1, stride_tok = 0;
+    int row_end = 0, acc_cols = 0;
+};
+struct Q8gArgs {
+    const int8_t* w = nullptr;    // [o][n]
+    const float* wsc = nullptr;   // [o][n/gs]
+    int n = 0, o = 0, gs = 32;
+    int pro = 0;   // 0: quantized rows xq/xs; 1: quantize the f32 rows x; 2: RMSNorm(x, norm_w, eps), then quantize
+    int epi = 0;   // 0: store (segments); 1: add to the output (segment 0); 2: SwiGLU of gate/up tile pairs -> seg 0
+    const int8_t* xq = nullptr;
+    const float* xs = nullptr;
+    const float* x = nullptr;
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+    int batch = 1;
+    const StepState* st = nullptr;
+    int nseg = 1;
+    Q8gSegArgs seg[3];
+};
+hipError_t launch_matmul_q8g(const Q8gArgs& a, hipStream_t s);
 hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size_t n, hipStream_t s);
 hipError_t launch_rope_cache(const float* cos_t, const float* sin_t, const StepState* st, int batch, float* q,
                              float* kc, int att, int kv, int hd, int kv_ld, int hf_pairs, hipStream_t s);

@@ -49,8 +49,8 @@ __global__ __launch_bounds__(kThreads) void k_embed(EmbQ8 e, const uint32_t* __r
         float v = 0.0f;
         if (tok < (uint32_t)e.vocab) {
             const size_t off = emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15);
-            if (e.fmt == 2) {
-                v = reinterpret_cast<const float*>(e.q)[off];
+            if (e.fmt == 3) {
+                v = fmul((float)e.q[off], e.d32[((size_t)(i / e.gs) * e.tiles + tile) * 64 + lane]);
             } else if (e.fmt == 1) {
                 v = f16_to_f32(reinterpret_cast<const uint16_t*>(e.q)[off]);
             } else {

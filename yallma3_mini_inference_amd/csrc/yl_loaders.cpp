@@ -243,10 +243,8 @@ bool load_safetensors(const std::string& path, uint32_t max_ctx_len, int fmt_ove
         const StTensor* s = w ? find("model.embed_tokens.scales") : nullptr;
         const StTensor* b = s ? find("model.embed_tokens.biases") : nullptr;
         if (!b) return false;
-        HostMat e;
-        if (!load_q8_st(data, file.size(), V, dim, m->gs, w->offset, s->offset, b->offset, &e, err)) return false;
-        m->emb_f32.resize(V * dim);
-        for (size_t i = 0; i < V * dim; i++) m->emb_f32[i] = (float)e.q[i] * e.s[i / m->gs];
+        if (dim % (size_t)m->gs) { *err = "token embedding: hidden_size must be a multiple of the group size"; return false; }
+        if (!load_q8_st(data, file.size(), V, dim, m->gs, w->offset, s->offset, b->offset, &m->emb_q8, err)) return false;
     }
     // projections
     const size_t qr = (size_t)m->n_heads * m->hd, kr = (size_t)m->n_kv * m->hd, H = m->hidden;
@@ -339,10 +337,8 @@ bool load_lmrs(const std::string& path, uint32_t max_ctx_len, int fmt_override, 
         off += n * 4;
         return true;
     };
-    HostMat e;
-    if (!take_q8(vocab, dim, &e)) return false;
-    m->emb_f32.resize((size_t)vocab * dim);
-    for (size_t i = 0; i < m->emb_f32.size(); i++) m->emb_f32[i] = (float)e.q[i] * e.s[i / gs];
+    if (dim % gs) { *err = "lm.rs: dim must be a multiple of the group size"; return false; }
+    if (!take_q8(vocab, dim, &m->emb_q8)) return false;
     m->rms_att.resize(n_layers);
     m->rms_ffn.resize(n_layers);
     m->layers.resize(n_layers);

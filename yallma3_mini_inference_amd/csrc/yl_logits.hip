@@ -34,9 +34,11 @@ constexpr int kLogitGroups = 2;   // groups of 4 chunks (16 bytes per lane each)
 
 // EF = 0: Q8_0 table (u8 chunks of 16 + f16 scale pairs); EF = 1: f16 table
 // (32-byte chunks of 16 values), whose values are exactly the reference's f32
-// table (load_f16_tensor, transformer_llama_gguf.rs:412-421,487); EF = 2: the
-// f32 table itself (64-byte chunks), for tables dequantized with f32 scales
-// (lm.rs and safetensors Q8 embeddings, transformer_llama_lmrs.rs:176-181).
+// table (load_f16_tensor, transformer_llama_gguf.rs:412-421,487); EF = 3:
+// int8 chunks of 16 with an f32 scale per group of gs (lm.rs and safetensors
+// Q8 embeddings): the reference dequantizes these into an f32 table
+// (transformer_llama_lmrs.rs:176-181, transformer_llama_st.rs:236-250) whose
+// values are exactly q * scale, recomputed here for a quarter of the bytes.
 template <int EF>
 __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* __restrict__ x,
                                                           const float* __restrict__ norm_w, float eps,
@@ -46,8 +48,8 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     extern __shared__ __align__(16) float lds[];
     __shared__ unsigned long long wkey[kLogitThreads / 64];
     constexpr int MP = 8192 / 8 / kLogitThreads;   // dim <= 8192
-    constexpr int NG = EF == 2 ? 1 : kLogitGroups;
-    constexpr int CI = EF == 0 ? 1 : (EF == 1 ? 2 : 4);   // int4 loads per 16-value chunk
+    constexpr int NG = kLogitGroups;
+    constexpr int CI = EF == 1 ? 2 : 1;   // int4 loads per 16-value chunk
     const int dim = e.dim, tid = threadIdx.x;
     float* xn = lds;             // the normalized row, zero over the padding
     float* sq = lds + e.dimp;
@@ -60,6 +62,8 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     // (F16 and F32: each chunk is CI int4, chunk k of this row at qp[CI * k * cs + i])
     const int4* qp = reinterpret_cast<const int4*>(e.q) + (size_t)(live ? tile : 0) * 64 * CI + lane * CI;
     const uint32_t* dp = reinterpret_cast<const uint32_t*>(e.d) + (size_t)(live ? tile : 0) * 64 + lane;
+    // (EF 3: the scale of chunk k's group at sp[(16 * k / gs) * cs])
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(e.d32) + (size_t)(live ? tile : 0) * 64 + lane;
     for (int i = dim + tid; i < e.dimp; i += kLogitThreads) xn[i] = 0.0f;
 
     // the residual row and norm weights first (every wavefront's loads issued
@@ -74,11 +78,18 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
     // a ring of NG groups: each group's scale word, then its 4 chunks
     int4 qv[NG][4 * CI];
     uint32_t sv[NG];
+    uint32_t s4[NG][4];
     auto load_group = [&](int gg, int g) {
         if constexpr (EF == 0) {
             sv[gg] = load_stream(dp + (size_t)g * cs);
 #pragma unroll
             for (int c = 0; c < 4; c++) qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
+        } else if constexpr (EF == 3) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                s4[gg][c] = load_stream(sp + (size_t)((16 * (4 * g + c)) / e.gs) * cs);
+                qv[gg][c] = load_stream(qp + (size_t)(4 * g + c) * cs);
+            }
         } else {
 #pragma unroll
             for (int c = 0; c < 4; c++)
@@ -100,6 +111,9 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                 const int g = g0 + gg;
                 if (NG > 1 && g >= ng) break;
                 const uint32_t sw = EF == 0 ? sv[gg] : 0u;
+                uint32_t sc4[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) sc4[c] = EF == 3 ? s4[gg][c] : 0u;
                 int4 q4[4 * CI];
 #pragma unroll
                 for (int c = 0; c < 4 * CI; c++) q4[c] = qv[gg][c];
@@ -107,15 +121,17 @@ __global__ __launch_bounds__(kLogitThreads) void k_logits(EmbQ8 e, const float* 
                 // never used)
                 load_group(gg, min(g + NG, ng - 1));
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (EF == 2) {
+                if constexpr (EF == 3) {
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
+                        const float scv = __builtin_bit_cast(float, sc4[c]);
                         const float* xk = xn + (4 * g + c) * 16;
+                        const uint32_t w[4] = {(uint32_t)q4[c].x, (uint32_t)q4[c].y, (uint32_t)q4[c].z,
+                                               (uint32_t)q4[c].w};
 #pragma unroll
                         for (int ei = 0; ei < 16; ei++) {
-                            const int4 v4 = q4[4 * c + (ei >> 2)];
-                            const int bits = (ei & 3) == 0 ? v4.x : (ei & 3) == 1 ? v4.y : (ei & 3) == 2 ? v4.z : v4.w;
-                            l[ei & 7] = fadd(l[ei & 7], fmul(xk[ei], __builtin_bit_cast(float, bits)));
+                            const int qv8 = (int)(int8_t)((w[ei >> 2] >> (8 * (ei & 3))) & 0xffu);
+                            l[ei & 7] = fadd(l[ei & 7], fmul(xk[ei], fmul((float)qv8, scv)));
                         }
                     }
                     continue;
@@ -209,7 +225,8 @@ hipError_t launch_logits(const EmbQ8& e, const float* x, const float* norm_w, fl
                          hipStream_t s) {
     const int nblk = logits_blocks(e);
     if (e.dim % 32 || e.dim > 8192) return hipErrorInvalidValue;
-    auto kern = e.fmt == 2 ? k_logits<2> : (e.fmt == 1 ? k_logits<1> : k_logits<0>);
+    if (e.fmt == 3 && (e.gs <= 0 || e.gs % 16)) return hipErrorInvalidValue;
+    auto kern = e.fmt == 3 ? k_logits<3> : (e.fmt == 1 ? k_logits<1> : k_logits<0>);
     if (logits_lds_bytes(e.dim) > 65536) {
         const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,

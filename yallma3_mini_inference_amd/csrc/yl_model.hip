@@ -364,6 +364,7 @@ void model_release(yl_model* m) {
     if (m->rms_final) hipFree(m->rms_final);
     if (m->emb.q) hipFree(m->emb.q);
     if (m->emb.d) hipFree(m->emb.d);
+    if (m->emb.d32) hipFree(m->emb.d32);
     if (m->rope_cos) hipFree(m->rope_cos);
     if (m->rope_sin) hipFree(m->rope_sin);
     delete m;
@@ -614,18 +615,34 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
 static bool upload_embedding_table(const HostModel& h, EmbQ8* e, std::string* err) {
     const int dim = h.dim, vocab = h.vocab;
     const int tiles = (vocab + 63) / 64, dimp = (dim + 63) & ~63;
-    const bool f16 = !h.emb_f16.empty();
-    const size_t elem = f16 ? 2 : 4, n = (size_t)tiles * 64 * dimp;
-    std::vector<uint8_t> buf(n * elem, 0);
-    for (int v = 0; v < vocab; v++)
-        for (int i = 0; i < dim; i++) {
-            const size_t at = emb_q_off(tiles, v / 64, i >> 4, v % 64) + (i & 15);
-            if (f16) memcpy(&buf[at * 2], &h.emb_f16[(size_t)v * dim + i], 2);
-            else memcpy(&buf[at * 4], &h.emb_f32[(size_t)v * dim + i], 4);
+    e->vocab = vocab; e->dim = dim; e->tiles = tiles; e->dimp = dimp;
+    if (h.emb_f16.empty()) {
+        // int8 values chunk-major as the Q8_0 table's bytes, f32 group scales
+        // [group][tile][lane]; the padding columns hold value 0, scale 0
+        const HostMat& q = h.emb_q8;
+        const int gs = q.gs, ngs = (dimp + gs - 1) / gs, G = dim / gs;
+        std::vector<int8_t> vb((size_t)tiles * 64 * dimp, 0);
+        std::vector<float> sb((size_t)ngs * tiles * 64, 0.0f);
+        for (int v = 0; v < vocab; v++) {
+            for (int i = 0; i < dim; i++) vb[emb_q_off(tiles, v / 64, i >> 4, v % 64) + (i & 15)] = q.q[(size_t)v * dim + i];
+            for (int g = 0; g < G; g++) sb[((size_t)g * tiles + v / 64) * 64 + v % 64] = q.s[(size_t)v * G + g];
         }
-    e->vocab = vocab; e->dim = dim; e->tiles = tiles; e->dimp = dimp; e->fmt = f16 ? 1 : 2;
-    if (hipMalloc(&e->q, buf.size() + 256) != hipSuccess || hipMalloc(&e->d, 256) != hipSuccess ||
-        hipMemcpy(e->q, buf.data(), buf.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        e->fmt = 3;
+        e->gs = gs;
+        if (hipMalloc(&e->q, vb.size() + 256) != hipSuccess || hipMalloc(&e->d32, sb.size() * 4 + 256) != hipSuccess ||
+            hipMalloc(&e->d, 256) != hipSuccess || hipMemcpy(e->q, vb.data(), vb.size(), hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(e->d32, sb.data(), sb.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            *err = "upload of the token embedding failed";
+            return false;
+        }
+        return true;
+    }
+    std::vector<uint16_t> buf((size_t)tiles * 64 * dimp, 0);
+    for (int v = 0; v < vocab; v++)
+        for (int i = 0; i < dim; i++) buf[emb_q_off(tiles, v / 64, i >> 4, v % 64) + (i & 15)] = h.emb_f16[(size_t)v * dim + i];
+    e->fmt = 1;
+    if (hipMalloc(&e->q, buf.size() * 2 + 256) != hipSuccess || hipMalloc(&e->d, 256) != hipSuccess ||
+        hipMemcpy(e->q, buf.data(), buf.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
         *err = "upload of the token embedding failed";
         return false;
     }
@@ -680,7 +697,8 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
     hipGetDevice(&m->device);
     std::string err;
     if (!upload_embedding_table(h, &m->emb, &err)) { set_error(err); return nullptr; }
-    m->emb_bytes = (size_t)m->vocab * m->dim * (m->emb.fmt == 1 ? 2 : 4);
+    m->emb_bytes = m->emb.fmt == 1 ? (size_t)m->vocab * m->dim * 2
+                                    : (size_t)m->vocab * m->dim + (size_t)m->vocab * (m->dim / m->emb.gs) * 4;
     m->rms_final = upload_f32(h.rms_final.data(), m->dim, &err);
     if (!m->rms_final) { set_error(err); return nullptr; }
     m->layers.resize(m->n_layers);
@@ -699,13 +717,26 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
             ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
                  upload_hostmat(H[4], &L.w1, &err) && upload_hostmat(H[5], &L.w2, &err) && upload_hostmat(H[6], &L.w3, &err);
         } else {
-            ok = upload_hostmat(H[0], &L.wq, &err) && upload_hostmat(H[1], &L.wk, &err) &&
-                 upload_hostmat(H[2], &L.wv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
-                 upload_hostmat(H[4], &L.w1, &err) && upload_hostmat(H[5], &L.w2, &err) && upload_hostmat(H[6], &L.w3, &err);
+            // q, k and v rows in one matrix; gate and up rows interleaved in
+            // blocks of 16 (the SwiGLU tiles of the f32-scaled Q8 GEMV)
+            HostMat qkv, w13;
+            qkv.o = H[0].o + H[1].o + H[2].o; qkv.n = H[0].n; qkv.gs = H[0].gs;
+            for (int k = 0; k < 3; k++) {
+                qkv.q.insert(qkv.q.end(), H[k].q.begin(), H[k].q.end());
+                qkv.s.insert(qkv.s.end(), H[k].s.begin(), H[k].s.end());
+            }
+            w13.o = 2 * H[4].o; w13.n = H[4].n; w13.gs = H[4].gs;
+            const size_t G = H[4].n / H[4].gs;
+            for (size_t r0 = 0; r0 < H[4].o; r0 += 16)
+                for (int k : {4, 6}) {
+                    w13.q.insert(w13.q.end(), H[k].q.begin() + r0 * H[k].n, H[k].q.begin() + (r0 + 16) * H[k].n);
+                    w13.s.insert(w13.s.end(), H[k].s.begin() + r0 * G, H[k].s.begin() + (r0 + 16) * G);
+                }
+            ok = upload_hostmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
+                 upload_hostmat(w13, &L.w13, &err) && upload_hostmat(H[5], &L.w2, &err);
         }
         if (!ok) { set_error(err); return nullptr; }
-        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w1.bytes() + L.w2.bytes() + L.w3.bytes() + L.wq.bytes() +
-                           L.wk.bytes() + L.wv.bytes();
+        m->weight_bytes += L.qkv.bytes() + L.wo.bytes() + L.w13.bytes() + L.w1.bytes() + L.w2.bytes() + L.w3.bytes();
     }
     {
         const size_t half = m->hd / 2;
@@ -932,121 +963,197 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     }
 }
 
-// One forward pass over `batch` tokens whose ids are at `tok` (device) and
-// whose first position is st->pos (device).  Enqueued on s->stream only.
-// The forward pass of an F16 model (forward.rs:120-297 with F16Kernel:
-// activations stay f32, every matmul is matmul_f32 and assigns its columns,
-// so K and V overwrite their cache entries).
-hipError_t enqueue_forward_f16(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+// Attention of layer l into s->attf (f32), for the F16 and f32-scaled Q8
+// models (the same kernels as the GGUF path, with an f32 output).
+static hipError_t enqueue_attn_f32(const yl_model* m, yl_session* s, int batch, float* kc, float* vc) {
     hipStream_t st = s->stream;
+    if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
+        return launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale, -1,
+                                 nullptr, nullptr, s->attf, s->split, st);
+    if (batch == 1)
+        return launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                  m->attn_scale, -1, nullptr, nullptr, s->attf, s->sc, st);
+    if (prompt_attn_applies(batch, s->pseq, m->hd))
+        return launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                                       m->attn_scale, -1, nullptr, nullptr, s->attf, s->psc, st);
+    return launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
+                            m->attn_scale, -1, nullptr, nullptr, s->attf, st);
+}
+
+static uint64_t attn_bytes(const yl_model* m, const yl_session* s, int batch) {
+    return 2ull * s->prof_seq * (uint64_t)m->kv * 4 + (uint64_t)batch * (uint64_t)m->att * 8;
+}
+
+// One op class of layer l of an F16 model's forward pass (forward.rs:120-297
+// with F16Kernel: activations stay f32, every matmul is matmul_f32 and
+// assigns its columns, so K and V overwrite their cache entries).  `bytes`
+// (nullable): the algorithmic bytes of the class -- f16 weights, f32
+// activations read, f32 outputs written.
+hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
+                          int advance, uint64_t* bytes) {
+    hipStream_t st = s->stream;
+    const uint64_t B = (uint64_t)batch;
+    if (cls == kOpLogits) {
+        if (bytes) *bytes = (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4;
+        return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st,
+                             s->ring, s->ring_cap, advance, st);
+    }
     const size_t lay_kv = (size_t)m->kv_ld * m->kv;
-    const int qkv_n = m->att + 2 * m->kv;
-    hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
-    for (int l = 0; l < m->n_layers && e == hipSuccess; l++) {
-        const Layer& L = m->layers[l];
-        float* kc = s->kc + (size_t)l * lay_kv;
-        float* vc = s->vc + (size_t)l * lay_kv;
-        e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+    const Layer& L = m->layers[l];
+    float* kc = s->kc + (size_t)l * lay_kv;
+    float* vc = s->vc + (size_t)l * lay_kv;
+    hipError_t e = hipSuccess;
+    switch (cls) {
+    case kOpQkv: {
+        const int qkv_n = m->att + 2 * m->kv;
+        if (bytes) *bytes = (uint64_t)qkv_n * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)qkv_n * 4);
+        if (l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
+        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
         if (e == hipSuccess)
             e = launch_matmul_f16((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->xn, batch, s->qkv_raw, qkv_n, 0, st);
         if (e == hipSuccess)
             e = launch_qkv_f16(s->qkv_raw, m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, vc, m->att, m->kv, m->hd,
                                m->kv_ld, m->hf_rope, st);
-        if (e == hipSuccess) {
-            if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
-                e = launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale, -1,
-                                      nullptr, nullptr, s->attf, s->split, st);
-            else if (batch == 1)
-                e = launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                       m->attn_scale, -1, nullptr, nullptr, s->attf, s->sc, st);
-            else if (prompt_attn_applies(batch, s->pseq, m->hd))
-                e = launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv,
-                                            m->hd, m->attn_scale, -1, nullptr, nullptr, s->attf, s->psc, st);
-            else
-                e = launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                     m->attn_scale, -1, nullptr, nullptr, s->attf, st);
-        }
-        if (e == hipSuccess)
-            e = launch_matmul_f16((const uint16_t*)L.wo.qs, m->att, m->dim, s->attf, batch, s->x, m->dim, 1, st);
-        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        return e;
+    }
+    case kOpAttn:
+        if (bytes) *bytes = attn_bytes(m, s, batch);
+        return enqueue_attn_f32(m, s, batch, kc, vc);
+    case kOpWo:
+        if (bytes) *bytes = (uint64_t)m->att * m->dim * 2 + B * ((uint64_t)m->att * 4 + (uint64_t)m->dim * 8);
+        return launch_matmul_f16((const uint16_t*)L.wo.qs, m->att, m->dim, s->attf, batch, s->x, m->dim, 1, st);
+    case kOpW13:
+        if (bytes) *bytes = 2ull * m->hidden * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)m->hidden * 4);
+        e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
         if (e == hipSuccess)
             e = launch_matmul_f16((const uint16_t*)L.w1.qs, m->dim, m->hidden, s->xn, batch, s->gate, m->hidden, 0, st);
         if (e == hipSuccess)
             e = launch_matmul_f16((const uint16_t*)L.w3.qs, m->dim, m->hidden, s->xn, batch, s->up, m->hidden, 0, st);
         if (e == hipSuccess) e = launch_swiglu_quant(-1, s->gate, s->up, m->hidden, batch, s->hf, nullptr, nullptr, st);
-        if (e == hipSuccess)
-            e = launch_matmul_f16((const uint16_t*)L.w2.qs, m->hidden, m->dim, s->hf, batch, s->x, m->dim, 1, st);
+        return e;
+    case kOpW2:
+        if (bytes) *bytes = (uint64_t)m->hidden * m->dim * 2 + B * ((uint64_t)m->hidden * 4 + (uint64_t)m->dim * 8);
+        return launch_matmul_f16((const uint16_t*)L.w2.qs, m->hidden, m->dim, s->hf, batch, s->x, m->dim, 1, st);
+    default:
+        return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
-    return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st, s->ring,
-                         s->ring_cap, advance, st);
 }
 
-// The forward pass of a Q8 model with f32 scales and group size gs
+// One op class of layer l of a Q8 model with f32 scales and group size gs
 // (forward.rs:120-297 with Q8Kernel; lm.rs and safetensors models): every
 // activation row quantized in gs groups, q/gate/up/FFN outputs from zero, K
 // and V accumulated onto the cache entries (`+=`), RoPE in place afterwards.
-hipError_t enqueue_forward_q8g(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
+// One token: RMSNorm and quantization run inside the GEMV workgroups, and
+// SwiGLU in the gate/up GEMV's epilogue (five kernels per layer and RoPE).
+// Prompts: the rows are normalized and quantized once by their own kernels
+// first.  `bytes`: int8 weights + f32 scales, the activations read, the
+// outputs written.
+hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
+                          int advance, uint64_t* bytes) {
     hipStream_t st = s->stream;
-    const size_t lay_kv = (size_t)m->kv_ld * m->kv;
+    const uint64_t B = (uint64_t)batch;
     const int gs = m->gs;
-    auto mm = [&](const QMat& w, float* out, const StepState* stp, long pos_stride, long stride_row, long stride_tok,
-                  int acc_cols, int epi) {
-        return launch_matmul_q8g((const int8_t*)w.qs, w.sf, w.n, w.o, gs, s->gq, s->gsc, batch, out, stp, pos_stride,
-                                 stride_row, stride_tok, acc_cols, epi, st);
+    if (cls == kOpLogits) {
+        if (bytes) *bytes = (uint64_t)m->emb_bytes + (uint64_t)m->dim * 8 + (uint64_t)m->vocab * 4;
+        return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st,
+                             s->ring, s->ring_cap, advance, st);
+    }
+    const size_t lay_kv = (size_t)m->kv_ld * m->kv;
+    const Layer& L = m->layers[l];
+    float* kc = s->kc + (size_t)l * lay_kv;
+    float* vc = s->vc + (size_t)l * lay_kv;
+    const bool one = batch == 1;
+    auto args = [&](const QMat& w, int epi) {
+        Q8gArgs a;
+        a.w = (const int8_t*)w.qs; a.wsc = w.sf; a.n = w.n; a.o = w.o; a.gs = gs;
+        a.epi = epi; a.batch = batch; a.xq = s->gq; a.xs = s->gsc; a.eps = m->eps;
+        a.seg[0].row_end = w.o;
+        return a;
     };
-    hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
-    for (int l = 0; l < m->n_layers && e == hipSuccess; l++) {
-        const Layer& L = m->layers[l];
-        float* kc = s->kc + (size_t)l * lay_kv;
-        float* vc = s->vc + (size_t)l * lay_kv;
-        e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
-        if (e == hipSuccess) e = launch_quantize_gs(s->xn, s->gq, s->gsc, gs, (size_t)batch * m->dim, st);
-        if (e == hipSuccess) e = mm(L.wq, s->sq, nullptr, 0, 1, m->att, 0, 0);
-        // K: [kv][kv_ld] from position pos; V: [pos][kv]
-        if (e == hipSuccess) e = mm(L.wk, kc, s->st, 1, m->kv_ld, 1, m->kv / 4 * 4, 0);
-        if (e == hipSuccess) e = mm(L.wv, vc, s->st, m->kv, 1, m->kv, m->kv / 4 * 4, 0);
+    // one token: the GEMV makes its input row; prompts: a kernel does, once
+    auto input = [&](Q8gArgs& a, const float* x, const float* norm_w, int n) -> hipError_t {
+        if (one) {
+            a.pro = norm_w ? 2 : 1;
+            a.x = x;
+            a.norm_w = norm_w;
+            return hipSuccess;
+        }
+        hipError_t e = hipSuccess;
+        if (norm_w) {
+            e = launch_rmsnorm(-1, x, norm_w, n, m->eps, batch, s->xn, nullptr, nullptr, st);
+            x = s->xn;
+        }
+        if (e == hipSuccess) e = launch_quantize_gs(x, s->gq, s->gsc, gs, (size_t)batch * n, st);
+        return e;
+    };
+    auto xbytes = [&](int n) { return B * (one ? (uint64_t)n * 4 : (uint64_t)n + (uint64_t)(n / gs) * 4); };
+    hipError_t e = hipSuccess;
+    switch (cls) {
+    case kOpQkv: {
+        if (bytes) *bytes = L.qkv.bytes() + xbytes(m->dim) + B * ((uint64_t)m->att + 2ull * m->kv) * 4;
+        if (l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
+        Q8gArgs a = args(L.qkv, 0);
+        if (e == hipSuccess) e = input(a, s->x, L.rms_att, m->dim);
+        // q [t][att] from 0; K [kv][kv_ld] and V [pos][kv] from position pos, `+=`
+        a.nseg = 3;
+        a.st = s->st;
+        a.seg[0] = Q8gSegArgs{s->sq, 0, 1, m->att, m->att, 0};
+        a.seg[1] = Q8gSegArgs{kc, 1, m->kv_ld, 1, m->att + m->kv, m->kv / 4 * 4};
+        a.seg[2] = Q8gSegArgs{vc, m->kv, 1, m->kv, m->att + 2 * m->kv, m->kv / 4 * 4};
+        if (e == hipSuccess) e = launch_matmul_q8g(a, st);
         if (e == hipSuccess)
             e = launch_rope_cache(m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, m->att, m->kv, m->hd, m->kv_ld,
                                   m->hf_rope, st);
-        if (e == hipSuccess) {
-            if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
-                e = launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale, -1,
-                                      nullptr, nullptr, s->attf, s->split, st);
-            else if (batch == 1)
-                e = launch_attn_decode(s->sq, kc, vc, s->st, s->dec_seq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                       m->attn_scale, -1, nullptr, nullptr, s->attf, s->sc, st);
-            else if (prompt_attn_applies(batch, s->pseq, m->hd))
-                e = launch_prompt_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv,
-                                            m->hd, m->attn_scale, -1, nullptr, nullptr, s->attf, s->psc, st);
-            else
-                e = launch_attention(s->sq, kc, vc, s->st, batch, s->pseq, m->kv_ld, m->n_heads, m->n_kv, m->hd,
-                                     m->attn_scale, -1, nullptr, nullptr, s->attf, st);
-        }
-        if (e == hipSuccess) e = launch_quantize_gs(s->attf, s->gq, s->gsc, gs, (size_t)batch * m->att, st);
-        if (e == hipSuccess) e = mm(L.wo, s->x, nullptr, 0, 1, m->dim, 0, 1);
-        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
-        if (e == hipSuccess) e = launch_quantize_gs(s->xn, s->gq, s->gsc, gs, (size_t)batch * m->dim, st);
-        if (e == hipSuccess) e = mm(L.w1, s->gate, nullptr, 0, 1, m->hidden, 0, 0);
-        if (e == hipSuccess) e = mm(L.w3, s->up, nullptr, 0, 1, m->hidden, 0, 0);
-        if (e == hipSuccess) e = launch_swiglu_quant(-1, s->gate, s->up, m->hidden, batch, s->hf, nullptr, nullptr, st);
-        if (e == hipSuccess) e = launch_quantize_gs(s->hf, s->gq, s->gsc, gs, (size_t)batch * m->hidden, st);
-        if (e == hipSuccess) e = mm(L.w2, s->x, nullptr, 0, 1, m->dim, 0, 1);
+        return e;
     }
-    if (e != hipSuccess) return e;
-    return launch_logits(m->emb, s->x + (size_t)(batch - 1) * m->dim, m->rms_final, m->eps, s->logits, s->st, s->ring,
-                         s->ring_cap, advance, st);
+    case kOpAttn:
+        if (bytes) *bytes = attn_bytes(m, s, batch);
+        return enqueue_attn_f32(m, s, batch, kc, vc);
+    case kOpWo: {
+        if (bytes) *bytes = L.wo.bytes() + xbytes(m->att) + B * (uint64_t)m->dim * 8;
+        Q8gArgs a = args(L.wo, 1);
+        e = input(a, s->attf, nullptr, m->att);
+        a.seg[0] = Q8gSegArgs{s->x, 0, 1, m->dim, m->dim, 0};
+        if (e == hipSuccess) e = launch_matmul_q8g(a, st);
+        return e;
+    }
+    case kOpW13: {
+        if (bytes) *bytes = L.w13.bytes() + xbytes(m->dim) + B * (uint64_t)m->hidden * 4;
+        Q8gArgs a = args(L.w13, 2);
+        e = input(a, s->x, L.rms_ffn, m->dim);
+        a.seg[0] = Q8gSegArgs{s->hf, 0, 1, m->hidden, L.w13.o, 0};
+        if (e == hipSuccess) e = launch_matmul_q8g(a, st);
+        return e;
+    }
+    case kOpW2: {
+        if (bytes) *bytes = L.w2.bytes() + xbytes(m->hidden) + B * (uint64_t)m->dim * 8;
+        Q8gArgs a = args(L.w2, 1);
+        e = input(a, s->hf, nullptr, m->hidden);
+        a.seg[0] = Q8gSegArgs{s->x, 0, 1, m->dim, m->dim, 0};
+        if (e == hipSuccess) e = launch_matmul_q8g(a, st);
+        return e;
+    }
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+// One op class of any model's forward pass (the GGUF quantized path, F16,
+// or Q8 with f32 group scales).
+hipError_t enqueue_class(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
+                         int advance, uint64_t* bytes, bool prologue = true) {
+    if (m->f16) return enqueue_op_f16(m, s, cls, l, batch, tok, advance, bytes);
+    if (m->q8g) return enqueue_op_q8g(m, s, cls, l, batch, tok, advance, bytes);
+    return enqueue_op(m, s, cls, l, batch, tok, advance, bytes, prologue);
 }
 
 hipError_t enqueue_forward(const yl_model* m, yl_session* s, int batch, const uint32_t* tok, int advance) {
-    if (m->f16) return enqueue_forward_f16(m, s, batch, tok, advance);
-    if (m->q8g) return enqueue_forward_q8g(m, s, batch, tok, advance);
     for (int l = 0; l < m->n_layers; l++)
         for (int c = kOpQkv; c <= kOpW2; c++) {
-            const hipError_t e = enqueue_op(m, s, c, l, batch, tok, advance, nullptr);
+            const hipError_t e = enqueue_class(m, s, c, l, batch, tok, advance, nullptr);
             if (e != hipSuccess) return e;
         }
-    return enqueue_op(m, s, kOpLogits, 0, batch, tok, advance, nullptr);
+    return enqueue_class(m, s, kOpLogits, 0, batch, tok, advance, nullptr);
 }
 
 // Decode attention is sized for a context bucket: 4096 positions (the one
@@ -1816,7 +1923,6 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
         return YL_ERR_ARG;
     }
     if ((uint64_t)start_pos + batch > (uint64_t)m->ctx) { set_error("profile: position beyond ctx_len"); return YL_ERR_RANGE; }
-    if (m->f16 || m->q8g) { set_error("profile: the kernel classes are those of the GGUF quantized path"); return YL_ERR_UNSUPPORTED; }
     if (batch == 1 && !decode_in_range(m, s, (uint64_t)start_pos + 1, "profile")) return YL_ERR_RANGE;
     s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
     s->prof_seq = (uint64_t)start_pos + batch;
@@ -1834,7 +1940,7 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     hipError_t ec = hipSuccess;
     for (int l = 0; l < n_launch && ec == hipSuccess; l++) {
         uint64_t b = 0;
-        ec = enqueue_op(m, s, kernel_class, l, (int)batch, batch == 1 ? &s->st->token : s->tokens, 0, &b, false);
+        ec = enqueue_class(m, s, kernel_class, l, (int)batch, batch == 1 ? &s->st->token : s->tokens, 0, &b, false);
         nbytes += b;
     }
     e = hipStreamEndCapture(s->stream, &g);

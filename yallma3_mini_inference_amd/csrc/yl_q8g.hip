@@ -8,50 +8,293 @@
 // x_scale in group order.  The accumulator starts from the output's old
 // value for the first 4*floor(o/4) columns (`+=`) and from 0 for the rest
 // (`=`); callers that zero the output first (forward.rs fills q, gate, up and
-// the FFN output with 0) pass acc_cols = 0.  One lane per (column, token).
+// the FFN output with 0) pass acc_cols = 0.
 #include <hip/hip_runtime.h>
 
+#include "yl_blocks.h"
 #include "yl_device.h"
 #include "yl_internal.h"
 
 namespace yl {
 
-// EPI 0: out = chain; EPI 1: out = out + chain-from-0 (the residual add of
-// forward.rs:196-204 after a zeroed FFN output).
-// Output element (token t, column c) at out[pos * pos_stride + t * stride_tok
-// + c * stride_row], pos = st->pos (0 without a step state).
-template <int EPI>
-__global__ __launch_bounds__(64) void k_matmul_q8g(const int8_t* __restrict__ w, const float* __restrict__ wsc, int n,
-                                                   int o, int gs, const int8_t* __restrict__ xq,
-                                                   const float* __restrict__ xs, float* __restrict__ out,
-                                                   const StepState* __restrict__ st, long pos_stride, long stride_row,
-                                                   long stride_tok, int acc_cols) {
-    extern __shared__ __align__(16) int xl[];
-    const int t = blockIdx.y, lane = threadIdx.x;
-    const int c = blockIdx.x * 64 + lane;
-    const int* xr = reinterpret_cast<const int*>(xq + (size_t)t * n);
-    for (int i = lane; i < n / 4; i += 64) xl[i] = xr[i];
-    __syncthreads();
-    if (c >= o) return;
-    const int G = n / gs;
-    const float* xsr = xs + (size_t)t * G;
-    const int8_t* wr = w + (size_t)c * n;
-    const float* wsr = wsc + (size_t)c * G;
-    const size_t at = (st ? (size_t)st->pos * pos_stride : 0) + (size_t)t * stride_tok + (size_t)c * stride_row;
-    float acc = (EPI == 0 && c < acc_cols) ? out[at] : 0.0f;
-    for (int g = 0; g < G; g++) {
-        int isum = 0;
-        for (int k = 0; k < gs; k += 16) {
-            const int4 wv = *reinterpret_cast<const int4*>(wr + (size_t)g * gs + k);
-            const int* xv = xl + (g * gs + k) / 4;
-            isum = __builtin_amdgcn_sdot4(wv.x, xv[0], isum, false);
-            isum = __builtin_amdgcn_sdot4(wv.y, xv[1], isum, false);
-            isum = __builtin_amdgcn_sdot4(wv.z, xv[2], isum, false);
-            isum = __builtin_amdgcn_sdot4(wv.w, xv[3], isum, false);
-        }
-        acc = fadd(acc, fmul(fmul((float)isum, wsr[g]), xsr[g]));
+// Tile kernel: a workgroup of 256 threads owns R consecutive output rows
+// (their weights are R*n contiguous bytes) and TB consecutive tokens.
+//   0. The tokens' quantized rows and scales and the tile's weight scales go
+//      to LDS.  With a prologue (one token per workgroup) the row is made
+//      here from f32: RMSNorm (util.rs:389-426: the 8 lane chains of squares
+//      in element order, o = w * (ss * x)) when PRO == 2, then quantization
+//      in groups of gs (quantization.rs:29-52).  The first weight loads are
+//      issued before the prologue.
+//   1. Threads walk the tile in 16-byte chunks (consecutive threads,
+//      consecutive chunks: each wavefront load is 1 KB of contiguous
+//      weights).  A chunk's exact int32 dot with the activation (v_dot4) is
+//      combined with the other chunks of its group -- integer sums, so in any
+//      order -- by cross-lane xor shuffles when gs/16 is a power of two up to
+//      64 (the group's chunks sit in consecutive lanes of one wavefront),
+//      else by LDS atomic adds.
+//   2. One thread per (token, row) forms the row's terms
+//      ((float)isum * w_scale) * x_scale in group order and adds them onto
+//      the accumulator one at a time: the reference's serial `xout += term`.
+// Epilogues: EPI 0 stores to up to three row segments (q, k, v of a fused
+// projection), each with its own addressing and `+=` columns; EPI 1 adds the
+// chain (from 0) to the output (the residual adds of forward.rs:196-204,
+// 244-253); EPI 2 takes tiles of 32 rows holding 16 gate rows then the 16 up
+// rows of the same columns (the upload interleaves w1 and w3 so) and writes
+// h = silu(gate) * up (forward.rs:220-237).
+constexpr int kQ8gThreads = 256;
+constexpr int kQ8gUnroll = 8;    // 16-byte weight loads per thread per batch (two batches in flight)
+constexpr int kPairRows = 16;   // EPI 2: gate rows then up rows per 32-row tile
+
+// rows [previous row_end, row_end) of the matrix go to `out`: element
+// (token t, column c) at out[pos * pos_stride + t * stride_tok + c * stride_row]
+// (pos = st->pos, 0 without a step state); columns below acc_cols start
+// their chain from the output's value
+struct Q8gSeg {
+    float* out;
+    long pos_stride, stride_row, stride_tok;
+    int row_end, acc_cols;
+};
+struct Q8gOut {
+    Q8gSeg seg[3];
+    int nseg;
+};
+
+// squares row of one RMSNorm chain: n/8 values + zero padding to a multiple
+// of 32 (whole read batches of lds_serial_sum; +0 added to a sum of squares
+// changes nothing), + 4 floats so the 8 chains start on distinct bank quads
+__host__ __device__ inline int q8g_norm_len(int n) { return (n / 8 + 31) & ~31; }
+__host__ __device__ inline int q8g_norm_stride(int n) { return q8g_norm_len(n) + 4; }
+// per-row stride of the scale and term arrays: G rounded up to 32, + 4
+// (the chain lanes' 16-byte reads then start on distinct bank quads)
+__host__ __device__ inline int q8g_gpad(int G) { return ((G + 31) & ~31) + 4; }
+
+// activation scales: TB*G floats rounded up to 4 (keeps the term rows 16-byte aligned)
+__host__ __device__ inline int q8g_xs_len(int tb, int G) { return (tb * G + 3) & ~3; }
+
+// LDS bytes: xl TB*n | xsl q8g_xs_len*4 | wsl R*GP*4 | terms TB*R*GP*4 | res TB*R*4
+// | prologue: xf n*4 | (PRO 2) xt 8*S*4 + red 64 + norm weights n*4
+__host__ __device__ inline size_t q8g_lds_bytes(int tb, int pro, int n, int G, int R) {
+    const size_t GP = (size_t)q8g_gpad(G);
+    size_t b = (size_t)tb * n + (size_t)q8g_xs_len(tb, G) * 4 + (size_t)R * GP * 4 + (size_t)tb * R * GP * 4 +
+               (size_t)((tb * R + 3) & ~3) * 4;
+    if (pro >= 1) b += (size_t)n * 4;
+    if (pro == 2) b += (size_t)8 * q8g_norm_stride(n) * 4 + 64 + (size_t)n * 4;
+    return b;
+}
+
+template <int TB, int PRO, int EPI>
+__global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
+    const int8_t* __restrict__ w, const float* __restrict__ wsc, int n, int o, int gs, int R, int lg,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, const float* __restrict__ x,
+    const float* __restrict__ norm_w, float eps, int batch, Q8gOut dst, const StepState* __restrict__ st) {
+    static_assert(PRO == 0 || TB == 1, "a prologue makes one token's row");
+    extern __shared__ __align__(16) int lds[];
+    const int tid = threadIdx.x;
+    const int G = n / gs, GP = q8g_gpad(G), cpr = n / 16;
+    const int row0 = blockIdx.x * R;
+    const int rows = min(R, o - row0);
+    const int t0 = blockIdx.y * TB;
+    int* xl = lds;                                              // [TB][n/4] quantized rows
+    float* xsl = reinterpret_cast<float*>(xl + TB * (n / 4));   // [TB][G]
+    float* wsl = xsl + q8g_xs_len(TB, G);                       // [R][GP] weight scales
+    float* trm = wsl + R * GP;                                  // [TB][R][GP] terms (int sums first when lg < 0)
+    float* res = trm + TB * R * GP;                             // [TB][R]
+    float* xf = res + ((TB * R + 3) & ~3);                      // [n] (prologue)
+    float* xt = xf + n;                                         // [8][S] squares (PRO 2)
+    float* red = xt + 8 * q8g_norm_stride(n);                   // [16] (PRO 2)
+
+    const int nch = rows * cpr;
+    const int4* wt = reinterpret_cast<const int4*>(w + (size_t)row0 * n);
+    const int span = kQ8gThreads * kQ8gUnroll;
+    int4 cur[kQ8gUnroll];
+#pragma unroll
+    for (int u = 0; u < kQ8gUnroll; u++) {   // the first weight loads go out before the staging
+        const int c = u * kQ8gThreads + tid;
+        cur[u] = c < nch ? wt[c] : make_int4(0, 0, 0, 0);
     }
-    out[at] = EPI == 0 ? acc : fadd(out[at], acc);
+
+    if constexpr (PRO == 0) {
+        for (int tb = 0; tb < TB; tb++) {
+            const bool live = t0 + tb < batch;
+            const int* xr = reinterpret_cast<const int*>(xq + (size_t)(t0 + tb) * n);
+            for (int i = tid; i < n / 4; i += kQ8gThreads) xl[tb * (n / 4) + i] = live ? xr[i] : 0;
+            for (int i = tid; i < G; i += kQ8gThreads) xsl[tb * G + i] = live ? xs[(size_t)(t0 + tb) * G + i] : 0.0f;
+        }
+    } else {
+        // the row (and the norm weights) in 16-byte loads, eight per thread
+        // in flight: n/4 vf4 over 256 threads
+        const vf4* xr4 = reinterpret_cast<const vf4*>(x + (size_t)t0 * n);
+        const vf4* nw4 = reinterpret_cast<const vf4*>(norm_w);
+        vf4* xf4 = reinterpret_cast<vf4*>(xf);
+        vf4* wn4 = reinterpret_cast<vf4*>(xt + 8 * q8g_norm_stride(n) + 16);   // (PRO 2) norm weights
+        const int S = q8g_norm_stride(n), L8 = q8g_norm_len(n), n8 = n / 8;
+        for (int b = 0; b < n / 4; b += 8 * kQ8gThreads) {
+            vf4 v[8], wv8[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i4 = b + k * kQ8gThreads + tid;
+                if (i4 < n / 4) {
+                    v[k] = xr4[i4];
+                    if constexpr (PRO == 2) wv8[k] = nw4[i4];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i4 = b + k * kQ8gThreads + tid;
+                if (i4 < n / 4) {
+                    xf4[i4] = v[k];
+                    if constexpr (PRO == 2) {
+                        wn4[i4] = wv8[k];
+                        const int e = i4 * 4;   // elements e..e+3: chains e&7 .. (e&7)+3, index e>>3
+                        xt[((e + 0) & 7) * S + (e >> 3)] = fmul(v[k].x, v[k].x);
+                        xt[((e + 1) & 7) * S + (e >> 3)] = fmul(v[k].y, v[k].y);
+                        xt[((e + 2) & 7) * S + (e >> 3)] = fmul(v[k].z, v[k].z);
+                        xt[((e + 3) & 7) * S + (e >> 3)] = fmul(v[k].w, v[k].w);
+                    }
+                }
+            }
+        }
+        if constexpr (PRO == 2) {
+            for (int i = tid; i < 8 * (L8 - n8); i += kQ8gThreads) xt[(i / (L8 - n8)) * S + n8 + i % (L8 - n8)] = 0.0f;
+            __syncthreads();
+            if (tid < 8)   // chain tid: x[8i + tid]^2 for i = 0, 1, ... in order
+                red[tid] = lds_serial_sum(reinterpret_cast<const vf4*>(xt + tid * S), L8 / 32, 0.0f);
+            __syncthreads();
+            float part[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) part[j] = red[j];
+            float ss = reduce_add8(part);
+            ss = ss / (float)n;
+            ss = fadd(ss, eps);
+            ss = 1.0f / sqrtf(ss);
+            const float* wn = reinterpret_cast<const float*>(wn4);
+            for (int i = tid; i < n; i += kQ8gThreads) xf[i] = fmul(wn[i], fmul(ss, xf[i]));
+        }
+        __syncthreads();
+        // group absmax, one thread per group (order-free; fmaxf ignores NaN
+        // as the reference's f32::max does)
+        for (int g = tid; g < G; g += kQ8gThreads) {
+            const vf4* v4 = reinterpret_cast<const vf4*>(xf + g * gs);
+            float am = 0.0f;
+            for (int k = 0; k < gs / 4; k++) {
+                const vf4 v = v4[k];
+                am = fmaxf(am, fabsf(v.x));
+                am = fmaxf(am, fabsf(v.y));
+                am = fmaxf(am, fabsf(v.z));
+                am = fmaxf(am, fabsf(v.w));
+            }
+            xsl[g] = group_scale<kQ8>(am);
+        }
+        __syncthreads();
+        // quantize 8 values at a time (x * 1/scale with the exact division
+        // where rounding could differ)
+        uint2* xb8 = reinterpret_cast<uint2*>(xl);
+        for (int j = tid; j < n / 8; j += kQ8gThreads) {
+            const vf4 a = xf4[2 * j], b = xf4[2 * j + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            int q[8];
+            quant8<kQ8>(v, xsl[(j * 8) / gs], q);
+            xb8[j] = make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
+        }
+    }
+    const float* wsr = wsc + (size_t)row0 * G;
+    for (int i = tid; i < rows * G; i += kQ8gThreads) {
+        const int r = i / G;
+        wsl[r * GP + (i - r * G)] = wsr[i];
+    }
+    if (lg < 0)
+        for (int i = tid; i < TB * R * GP; i += kQ8gThreads) trm[i] = 0.0f;   // int 0
+    __syncthreads();
+
+    // chunk c = c0 + u * 256 + tid lies in tile row r at chunk kc of the row;
+    // (r, kc) advance by 256 chunks per step without a division
+    const int dr = kQ8gThreads / cpr, dk = kQ8gThreads % cpr;
+    int r_c = tid / cpr, k_c = tid - r_c * cpr;
+    const int gmask = lg >= 0 ? (1 << lg) - 1 : 0;
+    for (int c0 = 0; c0 < nch; c0 += span) {   // uniform trip count: shuffles see every lane
+        int4 nxt[kQ8gUnroll];
+#pragma unroll
+        for (int u = 0; u < kQ8gUnroll; u++) {
+            const int c = c0 + span + u * kQ8gThreads + tid;
+            nxt[u] = c < nch ? wt[c] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kQ8gUnroll; u++) {
+            const int c = c0 + u * kQ8gThreads + tid;
+            const bool live = c < nch;
+            const int r = r_c, kc = k_c;
+            k_c += dk;
+            r_c += dr;
+            if (k_c >= cpr) { k_c -= cpr; r_c++; }
+            const int g = lg >= 0 ? kc >> lg : (kc * 16) / gs;
+#pragma unroll
+            for (int tb = 0; tb < TB; tb++) {
+                const int4 xv = *reinterpret_cast<const int4*>(xl + tb * (n / 4) + kc * 4);
+                int p = __builtin_amdgcn_sdot4(cur[u].x, xv.x, 0, false);
+                p = __builtin_amdgcn_sdot4(cur[u].y, xv.y, p, false);
+                p = __builtin_amdgcn_sdot4(cur[u].z, xv.z, p, false);
+                p = __builtin_amdgcn_sdot4(cur[u].w, xv.w, p, false);
+                float* d = trm + (tb * R + r) * GP + g;
+                if (lg >= 0) {
+                    for (int sh = 0; sh < lg; sh++) p += __shfl_xor(p, 1 << sh, 64);
+                    // the group's first lane writes its term ((float)isum * w_scale) * x_scale
+                    if (live && (kc & gmask) == 0) *d = fmul(fmul((float)p, wsl[r * GP + g]), xsl[tb * G + g]);
+                } else if (live) {
+                    atomicAdd(reinterpret_cast<int*>(d), p);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kQ8gUnroll; u++) cur[u] = nxt[u];
+    }
+    if (lg < 0) {   // integer sums -> terms
+        __syncthreads();
+        for (int i = tid; i < TB * R * GP; i += kQ8gThreads) {
+            const int tb = i / (R * GP), rem = i - tb * R * GP, r = rem / GP, g = rem - r * GP;
+            if (g < G)
+                trm[i] = fmul(fmul((float)reinterpret_cast<const int*>(trm)[i], wsl[r * GP + g]), xsl[tb * G + g]);
+        }
+    }
+    __syncthreads();
+
+    for (int j = tid; j < TB * rows; j += kQ8gThreads) {
+        const int tb = j / rows, r = j - tb * rows;
+        const int t = t0 + tb;
+        if (t >= batch) continue;
+        const int c = row0 + r;
+        int sg = 0;
+        if constexpr (EPI == 0)
+            while (sg + 1 < dst.nseg && c >= dst.seg[sg].row_end) sg++;
+        const Q8gSeg& q = dst.seg[sg];
+        const int col = c - (sg ? dst.seg[sg - 1].row_end : 0);
+        const size_t at = (st ? (size_t)st->pos * q.pos_stride : 0) + (size_t)t * q.stride_tok + (size_t)col * q.stride_row;
+        float acc = (EPI == 0 && col < q.acc_cols) ? q.out[at] : 0.0f;
+        const float* tr = trm + (tb * R + r) * GP;
+        int g = 0;
+        for (; g + 4 <= G; g += 4) {   // terms in group order, four per 16-byte read
+            const vf4 v = *reinterpret_cast<const vf4*>(tr + g);
+            acc = fadd(acc, v.x);
+            acc = fadd(acc, v.y);
+            acc = fadd(acc, v.z);
+            acc = fadd(acc, v.w);
+        }
+        for (; g < G; g++) acc = fadd(acc, tr[g]);
+        if constexpr (EPI == 0) q.out[at] = acc;
+        else if constexpr (EPI == 1) q.out[at] = fadd(q.out[at], acc);
+        else res[tb * R + r] = acc;
+    }
+    if constexpr (EPI == 2) {
+        __syncthreads();
+        const Q8gSeg& q = dst.seg[0];
+        for (int j = tid; j < TB * kPairRows; j += kQ8gThreads) {
+            const int tb = j / kPairRows, cc = j - tb * kPairRows;
+            const int t = t0 + tb;
+            if (t >= batch || cc >= rows / 2) continue;
+            const float g = res[tb * R + cc], u = res[tb * R + kPairRows + cc];
+            const float den = fadd(1.0f, expf_rn(-g));
+            q.out[(size_t)t * q.stride_tok + (size_t)(blockIdx.x * kPairRows + cc) * q.stride_row] = fmul(g / den, u);
+        }
+    }
 }
 
 // quantization::quantize (quantization.rs:29-52) over `groups` groups of gs.
@@ -90,20 +333,62 @@ __global__ void k_rope_cache(const float* __restrict__ cos_t, const float* __res
     *a1 = fadd(fmul(v0, s), fmul(v1, c));
 }
 
-hipError_t launch_matmul_q8g(const int8_t* w, const float* wsc, int n, int o, int gs, const int8_t* xq,
-                             const float* xs, int batch, float* out, const StepState* st, long pos_stride,
-                             long stride_row, long stride_tok, int acc_cols, int epi, hipStream_t s) {
-    if (gs <= 0 || gs % 32 || n % gs || batch <= 0 || batch > 65535) return hipErrorInvalidValue;
-    const size_t lds = (size_t)n;
-    auto k = epi == 0 ? k_matmul_q8g<0> : k_matmul_q8g<1>;
-    if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+template <int TB, int PRO, int EPI>
+static hipError_t launch_q8g_t(const Q8gArgs& a, int R, int lg, size_t lds, hipStream_t s) {
+    auto k = k_matmul_q8g<TB, PRO, EPI>;
+    static bool raised = false;
+    if (lds > 65536 && !raised) {
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
+        raised = true;
     }
-    hipLaunchKernelGGL(k, dim3((o + 63) / 64, batch), dim3(64), lds, s, w, wsc, n, o, gs, xq, xs, out, st, pos_stride,
-                       stride_row, stride_tok, acc_cols);
+    Q8gOut d{};
+    d.nseg = a.nseg;
+    for (int i = 0; i < a.nseg; i++)
+        d.seg[i] = Q8gSeg{a.seg[i].out, a.seg[i].pos_stride, a.seg[i].stride_row, a.seg[i].stride_tok,
+                          a.seg[i].row_end, a.seg[i].acc_cols};
+    const int gy = (a.batch + TB - 1) / TB;
+    hipLaunchKernelGGL(k, dim3((a.o + R - 1) / R, gy), dim3(kQ8gThreads), lds, s, a.w, a.wsc, a.n, a.o, a.gs, R, lg,
+                       a.xq, a.xs, a.x, a.norm_w, a.eps, a.batch, d, a.st);
     return hipGetLastError();
+}
+
+hipError_t launch_matmul_q8g(const Q8gArgs& a, hipStream_t s) {
+    const int n = a.n, o = a.o, gs = a.gs;
+    if (gs <= 0 || gs % 32 || n <= 0 || n % gs || o <= 0 || a.batch <= 0 || a.nseg < 1 || a.nseg > 3 ||
+        a.pro < 0 || a.pro > 2 || a.epi < 0 || a.epi > 2 || (a.pro > 0 && a.batch > 65535) ||
+        (long)a.batch > 65535L * 4 || a.seg[a.nseg - 1].row_end != o)
+        return hipErrorInvalidValue;
+    if (a.epi == 2 && o % (2 * kPairRows)) return hipErrorInvalidValue;
+    const int G = n / gs;
+    const int tb = a.pro > 0 || a.batch == 1 ? 1 : 4;
+    const int gy = (a.batch + tb - 1) / tb;
+    // rows per workgroup: about 1024 workgroups over the chip (256 when each
+    // workgroup makes its own input row), dividing every segment boundary,
+    // within 64 KB of LDS (EPI 2: one gate/up tile pair)
+    int R = 64;
+    if (a.epi == 2) {
+        R = 2 * kPairRows;
+    } else {
+        const long want = a.pro > 0 ? 256 : 1024;
+        while (R > 1 && (long)((o + R - 1) / R) * gy < want) R /= 2;
+        for (int i = 0; i < a.nseg; i++)
+            while (R > 1 && a.seg[i].row_end % R) R /= 2;
+        while (R > 1 && q8g_lds_bytes(tb, a.pro, n, G, R) > 65536) R /= 2;
+    }
+    const size_t lds = q8g_lds_bytes(tb, a.pro, n, G, R);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    const int cpg = gs / 16;
+    const int lg = (cpg <= 64 && (cpg & (cpg - 1)) == 0) ? __builtin_ctz(cpg) : -1;
+#define YL_Q8G(TB_, PRO_, EPI_) \
+    if (tb == TB_ && a.pro == PRO_ && a.epi == EPI_) return launch_q8g_t<TB_, PRO_, EPI_>(a, R, lg, lds, s);
+    YL_Q8G(1, 0, 0) YL_Q8G(1, 0, 1) YL_Q8G(1, 0, 2)
+    YL_Q8G(4, 0, 0) YL_Q8G(4, 0, 1) YL_Q8G(4, 0, 2)
+    YL_Q8G(1, 1, 0) YL_Q8G(1, 1, 1) YL_Q8G(1, 1, 2)
+    YL_Q8G(1, 2, 0) YL_Q8G(1, 2, 1) YL_Q8G(1, 2, 2)
+#undef YL_Q8G
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size_t n, hipStream_t s) {
