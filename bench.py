@@ -28,7 +28,10 @@ Also reported (same JSON line):
                 time per token (the 60%-of-8-TB/s target's figure).
   cpu_baseline  the oracle (C restatement of the reference's Rayon CPU path,
                 OpenMP) decoding a bounded sample of the same workload on this
-                host's cores.
+                host's cores; `variants` times the same sample at the
+                reference's default thread count (ceil(50% of cores)) and as an
+                SSE2-only build (the reference's Cargo.toml sets no
+                target-cpu), in child processes.
   parity        outside the timed region: the HIP path decodes the same
                 sample (same random-filled KV cache, same first token) one
                 forward_x at a time, and every step's logits and greedy token
@@ -118,6 +121,67 @@ def cpu_baseline(path, prompt_len, seconds, kv):
            "sample": f"{n} greedy decode steps at positions {prompt_len}..{prompt_len + n - 1} of the same "
                      f"model, KV cache below {prompt_len} random-filled (N(0,1), seed 0), {el:.1f}s"}
     return rec, logits, toks
+
+
+def cpu_variant_child(path, prompt_len, seconds):
+    """Child process of one CPU-baseline variant: the oracle build and thread
+    count come from YL_ORACLE_ISA / OMP_NUM_THREADS; prints one JSON line."""
+    from oracle import oracle as O
+
+    class _Shape:
+        pass
+    m = oracle_model(path)
+    sh = _Shape()
+    sh.n_kv_heads, sh.head_size, sh.n_layers = m.n_kv_heads, m.head_size, m.n_layers
+    kv = sample_kv(sh, prompt_len)
+    s = m.create_session()
+    s.key_cache()[:, :prompt_len] = kv[0]
+    s.value_cache()[:, :prompt_len] = kv[1]
+    tok, pos, n, toks = 1, prompt_len, 0, []
+    t0 = time.perf_counter()
+    while True:
+        tok = O.argmax(m.forward_x([tok], pos, s))
+        toks.append(tok)
+        pos += 1
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= SAMPLE_STEPS:
+            break
+    print(json.dumps({"value": n / el, "steps": n, "seconds": el, "cores": O.num_threads(), "tokens": toks}))
+
+
+def cpu_variants(path, prompt_len, seconds, ref_tokens):
+    """The reference's own defaults beside the all-cores native-ISA baseline:
+    ceil(50% of the cores) threads (parallelism.rs:59-71) and the SSE2-only
+    build that its Cargo.toml produces (no target-cpu), each in a child
+    process on the same sample; its tokens must equal the main baseline's."""
+    import math
+    import subprocess
+    # the cores this process may use: OpenMP's thread count when set (the
+    # host's share), else every core the OS reports
+    cores = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
+    half = math.ceil(cores / 2)
+    out = []
+    for isa, threads, what in (("native", half, "reference default threads ceil(50% of cores), native ISA"),
+                               ("sse2", cores, "SSE2-only build (the reference's Cargo.toml), all cores"),
+                               ("sse2", half, "SSE2-only build, ceil(50% of cores): the reference's defaults")):
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+        if isa != "native":
+            env["YL_ORACLE_ISA"] = isa
+        else:
+            env.pop("YL_ORACLE_ISA", None)
+        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-variant-child", path, "--prompt", str(prompt_len),
+               "--cpu-seconds", str(seconds)]
+        res = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+        if res.returncode != 0:
+            log(f"cpu variant {what}: failed: {res.stderr[-400:]}")
+            continue
+        r = json.loads(res.stdout.strip().splitlines()[-1])
+        n = r["steps"]
+        out.append({"value": round(r["value"], 3), "unit": "tok/s", "cores": r["cores"], "isa": isa,
+                    "what": what, "steps": n, "tokens_match": r["tokens"] == list(ref_tokens[:n])})
+        log(f"cpu variant {what}: {r['value']:.3f} tok/s on {r['cores']} threads")
+    return out
 
 
 def parity_record(gpu, cpu):
@@ -313,10 +377,15 @@ def main():
                          "prompt of --prefill-tokens on the int8-MFMA GEMM, then greedy decode; matvec: the "
                          "isolated 8192x2048 Q8_0 matvec")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--cpu-variants", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the oracle at the reference's default thread count and as an SSE2-only build")
+    ap.add_argument("--cpu-variant-child", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.cpu_variant_child:   # oracle only: no GPU in this process
+        return cpu_variant_child(args.cpu_variant_child, args.prompt, args.cpu_seconds)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (the decode path is "
               f"single-GPU, see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -459,6 +528,8 @@ def main():
         result["cpu_baseline"] = rec
         result["parity"] = parity_record(gpu, (cl, ct))
         log(f"cpu baseline {rec['value']:.3f} tok/s; parity {result['parity']}")
+        if args.cpu_variants:
+            rec["variants"] = cpu_variants(path, args.prompt, min(args.cpu_seconds, 10.0), ct)
     print(json.dumps(result), flush=True)
 
 

@@ -38,8 +38,13 @@ def build() -> None:
 
 
 def lib_path() -> str:
-    name = "liboracle_v4.so" if _host_has_avx512() else "liboracle_v3.so"
-    return os.path.join(_BUILD, name)
+    """The build for this host (v4 with AVX-512, else v3), or the one the
+    environment names: YL_ORACLE_ISA = v4 | v3 | sse2 (the thread count is
+    OpenMP's OMP_NUM_THREADS)."""
+    isa = os.environ.get("YL_ORACLE_ISA") or ("v4" if _host_has_avx512() else "v3")
+    if isa not in ("v4", "v3", "sse2"):
+        raise ValueError(f"YL_ORACLE_ISA={isa}: expected v4, v3 or sse2")
+    return os.path.join(_BUILD, f"liboracle_{isa}.so")
 
 
 _lib = None

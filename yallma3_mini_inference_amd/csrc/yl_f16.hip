@@ -9,15 +9,21 @@
 // in the reference's memory, so the device keeps them as f16 (half the
 // bytes) and widens them exactly.  Each output is one lane's serial chain;
 // the kernels keep that chain fed:
-//   decode (one token): four product wavefronts multiply a 64-row x 64-column
-//   weight tile by the activations into LDS while a fifth wavefront adds the
-//   previous tile's products into its 64 row accumulators, so the chain wave
-//   issues one LDS read per four adds;
+//   decode (one token): a workgroup owns 16 output rows.  Three product
+//   wavefronts multiply a 16-row x 256-column weight tile by the activations
+//   into LDS while the fourth wavefront's 16 lanes add the previous tile's
+//   products onto their row accumulators, reading 16 bytes per four adds and
+//   keeping two read batches in flight.  A chain of n dependent adds is the
+//   kernel's floor (~n x 5.8 cycles), so the weight loads run four tiles
+//   ahead in registers and many small workgroups share the chip.  The
+//   prologue can apply RMSNorm (util.rs:389-426) to the input row, and the
+//   epilogue add the residual or form SwiGLU from gate/up row pairs;
 //   batches: a workgroup takes 64 rows x 4 tokens, one wavefront per token,
 //   each lane multiplying and adding its own (token, row) chain, the weight
 //   tile shared through LDS.
 #include <hip/hip_runtime.h>
 
+#include "yl_blocks.h"
 #include "yl_device.h"
 #include "yl_internal.h"
 
@@ -38,81 +44,170 @@ __device__ __forceinline__ void widen8(const uint4& v, float w[8]) {
 }
 
 // ------------------------------------------------------------- one token
-// 320 threads: waves 0-3 make products, wave 4 holds the accumulators.
-// LDS: x [n] f32, then two product buffers P[16][64] of float4 (column group
-// c4 of row r at P[c4][r]: the chain lane reads 16 contiguous bytes, the 64
-// lanes 1 KiB).
-template <int EPI>
-__global__ __launch_bounds__(320) void k_matmul_f16_tok1(const uint16_t* __restrict__ w, int n, int o,
-                                                         const float* __restrict__ x, float* __restrict__ out) {
+constexpr int kFgThreads = 256;       // all wavefronts: products; wavefront 0 also the chains
+constexpr int kFgRows = 16;           // output rows per workgroup (EPI 2: 8 gate rows, then their 8 up rows)
+constexpr int kFgKT = 256;            // columns per tile
+constexpr int kFgStride = kFgKT + 4;  // product row stride (floats)
+constexpr int kFgDepth = 4;           // tiles of weight loads in flight
+constexpr int kFgChunks = kFgRows * kFgKT / 8;                    // 16-byte weight chunks per tile
+constexpr int kFgPer = kFgChunks / kFgThreads;                      // chunks per thread and tile
+constexpr int kFgPairRows = kFgRows / 2;
+static_assert(kFgChunks % kFgThreads == 0, "every thread takes whole chunks");
+
+__host__ __device__ inline int fg_norm_len(int n) { return (n / 8 + 31) & ~31; }
+__host__ __device__ inline int fg_norm_stride(int n) { return fg_norm_len(n) + 4; }
+// LDS floats: x [n] | products 2 x [16][260] | (PRO 1) squares 8 x S, reduction 16, norm weights [n]
+__host__ __device__ inline size_t fg_lds_floats(int n, int pro) {
+    size_t f = (size_t)n + 2 * kFgRows * kFgStride;
+    if (pro) f += (size_t)8 * fg_norm_stride(n) + 16 + n;
+    return f;
+}
+
+// PRO 1: x <- RMSNorm(x) * norm_w first.  EPI 0: out[r] = sum; EPI 1: out[r]
+// += sum (the residual add); EPI 2: out[8 * blockIdx.x + c] = silu(g) * u of
+// rows (c, c + 8) of the tile (forward.rs:220-237).
+template <int PRO, int EPI>
+__global__ __launch_bounds__(kFgThreads) void k_f16_gemv(const uint16_t* __restrict__ w, int n, int o,
+                                                         const float* __restrict__ x, const float* __restrict__ norm_w,
+                                                         float eps, float* __restrict__ out) {
     extern __shared__ __align__(16) float lds[];
-    float* xl = lds;
-    vf4* P = reinterpret_cast<vf4*>(lds + ((n + 3) & ~3));
+    float* xl = lds;                                   // [n]
+    float* P = lds + n;                                // [2][16][260]
+    float* sq = P + 2 * kFgRows * kFgStride;           // (PRO) squares, then reduction, then norm weights
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int row0 = blockIdx.x * kF16Rows;
-    for (int i = tid; i < n; i += 320) xl[i] = x[i];
-    __syncthreads();
-    const int ntile = (n + kF16Cols - 1) / kF16Cols;
-    // product thread t: row r = t / 4, columns (t % 4) * 16 .. + 16 of the tile
-    const int pr = tid >> 2, pq = tid & 3;
-    const int prow = min(row0 + pr, o - 1);
-    const uint16_t* wrow = w + (size_t)prow * n;
-    float acc = 0.0f;
-    uint4 wv[2];
-    auto load = [&](int t) {
-        const int k = t * kF16Cols + pq * 16;
-        const int kc = min(k, n - 16 < 0 ? 0 : n - 16);   // a partial tile re-reads in range
-        const uint4* src = reinterpret_cast<const uint4*>(wrow + (k < n ? k : kc));
-        wv[0] = src[0];
-        wv[1] = src[1];
-    };
-    auto products = [&](int t, vf4* buf) {
-        const int k0 = t * kF16Cols + pq * 16;
+    const int row0 = blockIdx.x * kFgRows;
+    const int ntile = (n + kFgKT - 1) / kFgKT;
+    uint4 wr[kFgDepth][kFgPer];
+    // chunk j = tid + 256 i of a tile: row j / 32, 8 columns from 8 * (j % 32).
+    // Every load is issued unconditionally (tiles past the last and columns
+    // past n re-read in range, unused), so the compiler's wait counts stay
+    // exact: a consumer waits only for its own tile, not the ones behind it.
+    auto load_tile = [&](uint4 (&dst)[kFgPer], int t) {
+        const int k0 = min(t, ntile - 1) * kFgKT;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            float wf[8];
-            widen8(wv[h], wf);
-#pragma unroll
-            for (int g = 0; g < 2; g++) {
-                const int k = k0 + h * 8 + g * 4;
-                vf4 p;
-                p.x = k + 0 < n ? fmul(xl[k + 0], wf[g * 4 + 0]) : 0.0f;
-                p.y = k + 1 < n ? fmul(xl[k + 1], wf[g * 4 + 1]) : 0.0f;
-                p.z = k + 2 < n ? fmul(xl[k + 2], wf[g * 4 + 2]) : 0.0f;
-                p.w = k + 3 < n ? fmul(xl[k + 3], wf[g * 4 + 3]) : 0.0f;
-                buf[(pq * 4 + h * 2 + g) * kF16Rows + pr] = p;
-            }
+        for (int i = 0; i < kFgPer; i++) {
+            const int j = tid + kFgThreads * i;
+            const int k = min(k0 + 8 * (j & 31), n - 8);
+            dst[i] = *reinterpret_cast<const uint4*>(w + (size_t)(row0 + (j >> 5)) * n + k);
         }
     };
-    if (wave < 4) {
-        load(0);
-        products(0, P);
-    }
-    __syncthreads();
-    for (int t = 0; t < ntile; t++) {
-        vf4* cur = P + (t & 1) * 16 * kF16Rows;
-        vf4* nxt = P + ((t + 1) & 1) * 16 * kF16Rows;
-        if (wave < 4) {
-            if (t + 1 < ntile) {
-                load(t + 1);
-                products(t + 1, nxt);
+#pragma unroll
+    for (int d = 0; d < kFgDepth; d++) load_tile(wr[d], d);
+    // the input row (RMSNorm first when PRO): 16-byte loads, 8 per thread in flight
+    {
+        const vf4* x4 = reinterpret_cast<const vf4*>(x);
+        const vf4* w4 = reinterpret_cast<const vf4*>(norm_w);
+        vf4* xl4 = reinterpret_cast<vf4*>(xl);
+        const int S = fg_norm_stride(n), L8 = fg_norm_len(n), n8 = n / 8;
+        float* red = sq + 8 * S;
+        vf4* wn4 = reinterpret_cast<vf4*>(red + 16);
+        for (int b = 0; b < n / 4; b += 8 * kFgThreads) {
+            vf4 v[8], nv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i4 = b + k * kFgThreads + tid;
+                if (i4 < n / 4) {
+                    v[k] = x4[i4];
+                    if constexpr (PRO) nv[k] = w4[i4];
+                }
             }
-        } else {
-            const int kn = min(kF16Cols, n - t * kF16Cols);   // columns in this tile (a multiple of 4)
-            for (int c4 = 0; c4 < kn / 4; c4++) {
-                const vf4 p = cur[c4 * kF16Rows + lane];
-                acc = fadd(acc, p.x);
-                acc = fadd(acc, p.y);
-                acc = fadd(acc, p.z);
-                acc = fadd(acc, p.w);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i4 = b + k * kFgThreads + tid;
+                if (i4 < n / 4) {
+                    xl4[i4] = v[k];
+                    if constexpr (PRO) {
+                        wn4[i4] = nv[k];
+                        const int e = i4 * 4;
+                        sq[((e + 0) & 7) * S + (e >> 3)] = fmul(v[k].x, v[k].x);
+                        sq[((e + 1) & 7) * S + (e >> 3)] = fmul(v[k].y, v[k].y);
+                        sq[((e + 2) & 7) * S + (e >> 3)] = fmul(v[k].z, v[k].z);
+                        sq[((e + 3) & 7) * S + (e >> 3)] = fmul(v[k].w, v[k].w);
+                    }
+                }
             }
+        }
+        if constexpr (PRO) {
+            for (int i = tid; i < 8 * (L8 - n8); i += kFgThreads) sq[(i / (L8 - n8)) * S + n8 + i % (L8 - n8)] = 0.0f;
+            __syncthreads();
+            if (tid < 8) red[tid] = lds_serial_sum(reinterpret_cast<const vf4*>(sq + tid * S), L8 / 32, 0.0f);
+            __syncthreads();
+            float part[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) part[j] = red[j];
+            float ss = reduce_add8(part);
+            ss = ss / (float)n;
+            ss = fadd(ss, eps);
+            ss = 1.0f / sqrtf(ss);
+            const float* wn = red + 16;
+            for (int i = tid; i < n; i += kFgThreads) xl[i] = fmul(wn[i], fmul(ss, xl[i]));
         }
         __syncthreads();
     }
-    if (wave == 4 && row0 + lane < o) {
-        float* dst = out + row0 + lane;
-        *dst = EPI == 0 ? acc : fadd(*dst, acc);
+
+    float acc = 0.0f;
+    // iteration t: products of tile t -> P[t & 1], then the loads of tile
+    // t + depth into the freed registers; wavefront 0's first 16 lanes add
+    // tile t - 1.  The trip count is padded to whole rings of `depth`.
+    const int nit = (ntile + 1 + kFgDepth - 1) / kFgDepth * kFgDepth;
+    for (int t0 = 0; t0 < nit; t0 += kFgDepth) {
+#pragma unroll
+        for (int d = 0; d < kFgDepth; d++) {
+            const int t = t0 + d;
+            if (t < ntile) {
+                float* buf = P + (t & 1) * kFgRows * kFgStride;
+                const int k0 = t * kFgKT;
+#pragma unroll
+                for (int i = 0; i < kFgPer; i++) {
+                    const int j = tid + kFgThreads * i;
+                    const int kk = 8 * (j & 31);
+                    if (k0 + kk < n) {
+                        float wf[8];
+                        widen8(wr[d][i], wf);
+                        const vf4 xa = *reinterpret_cast<const vf4*>(xl + k0 + kk);
+                        const vf4 xb = *reinterpret_cast<const vf4*>(xl + k0 + kk + 4);
+                        float* dst = buf + (j >> 5) * kFgStride + kk;
+                        *reinterpret_cast<vf4*>(dst) =
+                            vf4{fmul(xa.x, wf[0]), fmul(xa.y, wf[1]), fmul(xa.z, wf[2]), fmul(xa.w, wf[3])};
+                        *reinterpret_cast<vf4*>(dst + 4) =
+                            vf4{fmul(xb.x, wf[4]), fmul(xb.y, wf[5]), fmul(xb.z, wf[6]), fmul(xb.w, wf[7])};
+                    }
+                }
+            }
+            load_tile(wr[d], t + kFgDepth);
+            if (wave == 0 && lane < kFgRows && t >= 1 && t <= ntile) {
+                const int tp = t - 1;
+                const int kn = min(kFgKT, n - tp * kFgKT);   // a multiple of 32
+                acc = lds_serial_sum(reinterpret_cast<const vf4*>(P + (tp & 1) * kFgRows * kFgStride + lane * kFgStride),
+                                     kn / 32, acc);
+            }
+            __syncthreads();
+        }
     }
+    if (wave == 0) {
+        if constexpr (EPI == 2) {
+            const float u = __shfl_down(acc, kFgPairRows, 64);
+            if (lane < kFgPairRows) {
+                const float den = fadd(1.0f, expf_rn(-acc));
+                out[blockIdx.x * kFgPairRows + lane] = fmul(acc / den, u);
+            }
+        } else if (lane < kFgRows) {
+            float* dst = out + row0 + lane;
+            *dst = EPI == 0 ? acc : fadd(*dst, acc);
+        }
+    }
+}
+
+// SwiGLU of a batched gate/up product in the pair layout (rows c, c + 8 of
+// each 16-row block): raw [batch][2 * hidden] -> h [batch][hidden].
+__global__ void k_swiglu_pairs(const float* __restrict__ raw, int hidden, float* __restrict__ h) {
+    const int t = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= hidden) return;
+    const float* r = raw + (size_t)t * 2 * hidden + (size_t)(c / kFgPairRows) * kFgRows + c % kFgPairRows;
+    const float g = r[0], u = r[kFgPairRows];
+    const float den = fadd(1.0f, expf_rn(-g));
+    h[(size_t)t * hidden + c] = fmul(g / den, u);
 }
 
 // --------------------------------------------------------------- batches
@@ -212,26 +307,49 @@ __global__ void k_qkv_f16(const float* __restrict__ raw, const float* __restrict
     }
 }
 
-size_t matmul_f16_lds_bytes(int n) { return ((size_t)((n + 3) & ~3) + 2 * 16 * kF16Rows * 4) * sizeof(float); }
-
 hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, int batch, float* out, int out_ld,
                              int epi, hipStream_t s) {
-    if (n % 32 || n <= 0 || o <= 0 || batch <= 0) return hipErrorInvalidValue;
+    if (n % 32 || n <= 0 || o <= 0 || batch <= 0 || epi < 0 || epi > 1) return hipErrorInvalidValue;
+    if (batch == 1 && o % kFgRows == 0) return launch_f16_gemv(w, n, o, x, nullptr, 0.0f, epi, out, s);
     const int rb = (o + kF16Rows - 1) / kF16Rows;
-    if (batch == 1) {
-        const size_t lds = matmul_f16_lds_bytes(n);
-        auto k = epi == 0 ? k_matmul_f16_tok1<0> : k_matmul_f16_tok1<1>;
-        if (lds > 65536) {
-            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL(k, dim3(rb), dim3(320), lds, s, w, n, o, x, out);
-    } else {
-        auto k = epi == 0 ? k_matmul_f16_batch<0> : k_matmul_f16_batch<1>;
-        hipLaunchKernelGGL(k, dim3(rb, (batch + kF16Tok - 1) / kF16Tok), dim3(256), 0, s, w, n, o, x, batch, out,
-                           out_ld);
+    auto k = epi == 0 ? k_matmul_f16_batch<0> : k_matmul_f16_batch<1>;
+    hipLaunchKernelGGL(k, dim3(rb, (batch + kF16Tok - 1) / kF16Tok), dim3(256), 0, s, w, n, o, x, batch, out, out_ld);
+    return hipGetLastError();
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps,
+                            float* out, hipStream_t s) {
+    const size_t lds = fg_lds_floats(n, PRO) * sizeof(float);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    auto k = k_f16_gemv<PRO, EPI>;
+    static bool raised = false;
+    if (lds > 65536 && !raised) {
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        raised = true;
     }
+    hipLaunchKernelGGL(k, dim3(o / kFgRows), dim3(kFgThreads), lds, s, w, n, o, x, norm_w, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_f16_gemv(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps, int epi,
+                           float* out, hipStream_t s) {
+    if (n % 32 || n <= 0 || o <= 0 || o % kFgRows || epi < 0 || epi > 2) return hipErrorInvalidValue;
+    if (norm_w) {
+        if (epi == 0) return launch_fg<1, 0>(w, n, o, x, norm_w, eps, out, s);
+        if (epi == 2) return launch_fg<1, 2>(w, n, o, x, norm_w, eps, out, s);
+        return hipErrorInvalidValue;
+    }
+    if (epi == 0) return launch_fg<0, 0>(w, n, o, x, norm_w, eps, out, s);
+    if (epi == 1) return launch_fg<0, 1>(w, n, o, x, norm_w, eps, out, s);
+    return launch_fg<0, 2>(w, n, o, x, norm_w, eps, out, s);
+}
+
+hipError_t launch_swiglu_pairs(const float* raw, int hidden, int batch, float* h, hipStream_t s) {
+    if (hidden % kFgPairRows || batch <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_swiglu_pairs, dim3((hidden + 255) / 256, batch), dim3(256), 0, s, raw, hidden, h);
     return hipGetLastError();
 }
 

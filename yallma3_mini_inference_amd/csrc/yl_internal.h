@@ -199,6 +199,13 @@ hipError_t launch_matmul_q8g(const Q8gArgs& a, hipStream_t s);
 hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size_t n, hipStream_t s);
 hipError_t launch_rope_cache(const float* cos_t, const float* sin_t, const StepState* st, int batch, float* q,
                              float* kc, int att, int kv, int hd, int kv_ld, int hf_pairs, hipStream_t s);
+// One token through f16 weights with the chain fed from LDS (o % 16 == 0):
+// norm_w non-null applies RMSNorm to x first; epi 0 store, 1 add, 2 SwiGLU
+// of the 8-row gate/up pairs of each 16-row block -> out[o / 2].
+hipError_t launch_f16_gemv(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps, int epi,
+                           float* out, hipStream_t s);
+// raw [batch][2 * hidden] in that pair layout -> h [batch][hidden]
+hipError_t launch_swiglu_pairs(const float* raw, int hidden, int batch, float* h, hipStream_t s);
 hipError_t launch_qkv_f16(const float* raw, const float* cos_t, const float* sin_t, const StepState* st, int batch,
                           float* sq, float* kc, float* vc, int att, int kv, int hd, int kv_ld, int hf_pairs,
                           hipStream_t s);

@@ -98,6 +98,22 @@ struct HostQMat {
     size_t row_bytes() const { return fmt == kQ4 ? n / 2 : fmt == kF16 ? n * 2 : n; }
 };
 
+// F16 gate and up rows in the pairs the one-token F16 GEMV's SwiGLU epilogue
+// reads: blocks of 16 rows, 8 gate rows then the same 8 up rows.
+static void f16_pair_rows(const uint16_t* gate, const uint16_t* up, size_t o, size_t n, HostQMat* out) {
+    out->fmt = kF16;
+    out->o = 2 * o;
+    out->n = n;
+    out->qs.resize(2 * o * n * 2);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(out->qs.data());
+    for (size_t r0 = 0; r0 < o; r0 += 8)
+        for (int k = 0; k < 2; k++) {
+            const uint16_t* src = (k == 0 ? gate : up) + r0 * n;
+            memcpy(dst, src, 8 * n * 2);
+            dst += 8 * n;
+        }
+}
+
 // GGUF blocks -> repacked planes (transformer_llama_gguf.rs:345-410).
 static bool host_from_gguf(uint32_t type, const uint8_t* src, uint64_t avail, size_t o, size_t n,
                            HostQMat* h, std::string* err) {
@@ -583,8 +599,13 @@ yl_model* load_model(const char* path, uint32_t max_ctx_len, int32_t fmt_overrid
         HostQMat qkv, w13;
         bool ok = host_concat_rows({&h[0], &h[1], &h[2]}, &qkv, &err) && upload_qmat(qkv, &L.qkv, &err) &&
                   upload_qmat(h[3], &L.wo, &err) && upload_qmat(h[5], &L.w2, &err);
-        if (ok && m->f16) ok = upload_qmat(h[4], &L.w1, &err) && upload_qmat(h[6], &L.w3, &err);
-        else if (ok) ok = host_interleave_gate_up(h[4], h[6], &w13, &err) && upload_qmat(w13, &L.w13, &err);
+        if (ok && m->f16) {
+            f16_pair_rows(reinterpret_cast<const uint16_t*>(h[4].qs.data()),
+                          reinterpret_cast<const uint16_t*>(h[6].qs.data()), h[4].o, h[4].n, &w13);
+            ok = upload_qmat(w13, &L.w13, &err);
+        } else if (ok) {
+            ok = host_interleave_gate_up(h[4], h[6], &w13, &err) && upload_qmat(w13, &L.w13, &err);
+        }
         if (!ok) {
             set_error(p + err);
             return nullptr;
@@ -714,8 +735,10 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
             qkv.fmt = kF16; qkv.n = H[0].n; qkv.o = H[0].o + H[1].o + H[2].o;
             for (int k = 0; k < 3; k++)
                 qkv.qs.insert(qkv.qs.end(), (const uint8_t*)H[k].h.data(), (const uint8_t*)H[k].h.data() + H[k].h.size() * 2);
-            ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
-                 upload_hostmat(H[4], &L.w1, &err) && upload_hostmat(H[5], &L.w2, &err) && upload_hostmat(H[6], &L.w3, &err);
+            HostQMat w13;
+            f16_pair_rows(H[4].h.data(), H[6].h.data(), H[4].o, H[4].n, &w13);
+            ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) && upload_qmat(w13, &L.w13, &err) &&
+                 upload_hostmat(H[5], &L.w2, &err);
         } else {
             // q, k and v rows in one matrix; gate and up rows interleaved in
             // blocks of 16 (the SwiGLU tiles of the f32-scaled Q8 GEMV)
@@ -805,7 +828,7 @@ bool session_grow(yl_session* s, int batch) {
         const bool okf = hipMalloc(&s->xn, B * m->dim * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->qkv_raw, B * (m->att + 2 * m->kv) * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->attf, B * m->att * 4 + 256) == hipSuccess &&
-                         hipMalloc(&s->gate, B * m->hidden * 4 + 256) == hipSuccess &&
+                         hipMalloc(&s->gate, B * 2 * m->hidden * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->up, B * m->hidden * 4 + 256) == hipSuccess &&
                          hipMalloc(&s->hf, B * m->hidden * 4 + 256) == hipSuccess;
         if (!okf) { set_error("hipMalloc failed for session buffers"); s->cap_b = 0; return false; }
@@ -1003,14 +1026,22 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
     hipError_t e = hipSuccess;
+    const bool one = batch == 1;
     switch (cls) {
     case kOpQkv: {
         const int qkv_n = m->att + 2 * m->kv;
         if (bytes) *bytes = (uint64_t)qkv_n * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)qkv_n * 4);
         if (l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
-        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
-        if (e == hipSuccess)
-            e = launch_matmul_f16((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->xn, batch, s->qkv_raw, qkv_n, 0, st);
+        if (one) {   // RMSNorm inside the GEMV
+            if (e == hipSuccess)
+                e = launch_f16_gemv((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->x, L.rms_att, m->eps, 0, s->qkv_raw,
+                                    st);
+        } else {
+            if (e == hipSuccess)
+                e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+            if (e == hipSuccess)
+                e = launch_matmul_f16((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->xn, batch, s->qkv_raw, qkv_n, 0, st);
+        }
         if (e == hipSuccess)
             e = launch_qkv_f16(s->qkv_raw, m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, vc, m->att, m->kv, m->hd,
                                m->kv_ld, m->hf_rope, st);
@@ -1023,13 +1054,16 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
         if (bytes) *bytes = (uint64_t)m->att * m->dim * 2 + B * ((uint64_t)m->att * 4 + (uint64_t)m->dim * 8);
         return launch_matmul_f16((const uint16_t*)L.wo.qs, m->att, m->dim, s->attf, batch, s->x, m->dim, 1, st);
     case kOpW13:
+        // gate and up rows in pairs (8 + 8 per 16-row block), SwiGLU after
         if (bytes) *bytes = 2ull * m->hidden * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)m->hidden * 4);
+        if (one)
+            return launch_f16_gemv((const uint16_t*)L.w13.qs, m->dim, 2 * m->hidden, s->x, L.rms_ffn, m->eps, 2, s->hf,
+                                   st);
         e = launch_rmsnorm(-1, s->x, L.rms_ffn, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
         if (e == hipSuccess)
-            e = launch_matmul_f16((const uint16_t*)L.w1.qs, m->dim, m->hidden, s->xn, batch, s->gate, m->hidden, 0, st);
-        if (e == hipSuccess)
-            e = launch_matmul_f16((const uint16_t*)L.w3.qs, m->dim, m->hidden, s->xn, batch, s->up, m->hidden, 0, st);
-        if (e == hipSuccess) e = launch_swiglu_quant(-1, s->gate, s->up, m->hidden, batch, s->hf, nullptr, nullptr, st);
+            e = launch_matmul_f16((const uint16_t*)L.w13.qs, m->dim, 2 * m->hidden, s->xn, batch, s->gate,
+                                  2 * m->hidden, 0, st);
+        if (e == hipSuccess) e = launch_swiglu_pairs(s->gate, m->hidden, batch, s->hf, st);
         return e;
     case kOpW2:
         if (bytes) *bytes = (uint64_t)m->hidden * m->dim * 2 + B * ((uint64_t)m->hidden * 4 + (uint64_t)m->dim * 8);

@@ -106,12 +106,16 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
     const int nch = rows * cpr;
     const int4* wt = reinterpret_cast<const int4*>(w + (size_t)row0 * n);
     const int span = kQ8gThreads * kQ8gUnroll;
-    int4 cur[kQ8gUnroll];
+    // two register batches of weight chunks (A: even batches, B: odd), loaded
+    // unconditionally (chunks past the tile re-read its last one, unused) so
+    // that each consumer waits only for its own batch
+    int4 wa[kQ8gUnroll], wb[kQ8gUnroll];
+    auto load_batch = [&](int4 (&dst)[kQ8gUnroll], int c0) {
 #pragma unroll
-    for (int u = 0; u < kQ8gUnroll; u++) {   // the first weight loads go out before the staging
-        const int c = u * kQ8gThreads + tid;
-        cur[u] = c < nch ? wt[c] : make_int4(0, 0, 0, 0);
-    }
+        for (int u = 0; u < kQ8gUnroll; u++) dst[u] = wt[min(c0 + u * kQ8gThreads + tid, nch - 1)];
+    };
+    load_batch(wa, 0);   // the first weight loads go out before the staging
+    load_batch(wb, span);
 
     if constexpr (PRO == 0) {
         for (int tb = 0; tb < TB; tb++) {
@@ -211,13 +215,8 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
     const int dr = kQ8gThreads / cpr, dk = kQ8gThreads % cpr;
     int r_c = tid / cpr, k_c = tid - r_c * cpr;
     const int gmask = lg >= 0 ? (1 << lg) - 1 : 0;
-    for (int c0 = 0; c0 < nch; c0 += span) {   // uniform trip count: shuffles see every lane
-        int4 nxt[kQ8gUnroll];
-#pragma unroll
-        for (int u = 0; u < kQ8gUnroll; u++) {
-            const int c = c0 + span + u * kQ8gThreads + tid;
-            nxt[u] = c < nch ? wt[c] : make_int4(0, 0, 0, 0);
-        }
+    // one batch: U chunks per thread (uniform trip counts: the shuffles see every lane)
+    auto consume = [&](const int4 (&wv)[kQ8gUnroll], int c0) {
 #pragma unroll
         for (int u = 0; u < kQ8gUnroll; u++) {
             const int c = c0 + u * kQ8gThreads + tid;
@@ -230,10 +229,10 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
 #pragma unroll
             for (int tb = 0; tb < TB; tb++) {
                 const int4 xv = *reinterpret_cast<const int4*>(xl + tb * (n / 4) + kc * 4);
-                int p = __builtin_amdgcn_sdot4(cur[u].x, xv.x, 0, false);
-                p = __builtin_amdgcn_sdot4(cur[u].y, xv.y, p, false);
-                p = __builtin_amdgcn_sdot4(cur[u].z, xv.z, p, false);
-                p = __builtin_amdgcn_sdot4(cur[u].w, xv.w, p, false);
+                int p = __builtin_amdgcn_sdot4(wv[u].x, xv.x, 0, false);
+                p = __builtin_amdgcn_sdot4(wv[u].y, xv.y, p, false);
+                p = __builtin_amdgcn_sdot4(wv[u].z, xv.z, p, false);
+                p = __builtin_amdgcn_sdot4(wv[u].w, xv.w, p, false);
                 float* d = trm + (tb * R + r) * GP + g;
                 if (lg >= 0) {
                     for (int sh = 0; sh < lg; sh++) p += __shfl_xor(p, 1 << sh, 64);
@@ -244,8 +243,12 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
                 }
             }
         }
-#pragma unroll
-        for (int u = 0; u < kQ8gUnroll; u++) cur[u] = nxt[u];
+    };
+    for (int c0 = 0; c0 < nch; c0 += 2 * span) {
+        consume(wa, c0);
+        load_batch(wa, c0 + 2 * span);
+        if (c0 + span < nch) consume(wb, c0 + span);
+        load_batch(wb, c0 + 3 * span);
     }
     if (lg < 0) {   // integer sums -> terms
         __syncthreads();
