@@ -330,11 +330,33 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // the scores of positions past seq are never used.
     constexpr int NCH = kScoreLoads / (HD / 8);   // chunks of 256 positions per round
     constexpr int RP = NCH * 256;
+    // Chunk 0 (positions 0-255, always scored) goes out first; the chunks
+    // of round 0 that hold positions follow once the position is read, the
+    // others are not fetched (zero registers, their partials never read).
     vf4 k0[LONG ? 1 : NCH][HD / 8];
-    if constexpr (!LONG)
-        score_loads<HD, NCH>(krs, 0, (min(max_seq, RP) + 3) / 4, lane, wave, kv_ld * 4, k0);
+    const int q0 = (min(max_seq, RP) + 3) / 4;
+    if constexpr (!LONG) {
+#pragma unroll
+        for (int s8 = 0; s8 < HD / 8; s8++)
+            k0[0][s8] = buf_load_f32x4(krs, min(lane, q0 - 1) * 16, (8 * s8 + wave) * kv_ld * 4);
+    }
     const int seq = st->pos + 1;
     const int n_chunks = seq / 8;
+    if constexpr (!LONG) {
+        const int live0 = min(NCH, (seq + 255) / 256);
+#pragma unroll
+        for (int ch = 1; ch < NCH; ch++) {
+            const int quad = min(ch * 64 + lane, q0 - 1);
+            if (ch < live0) {   // (uniform)
+#pragma unroll
+                for (int s8 = 0; s8 < HD / 8; s8++)
+                    k0[ch][s8] = buf_load_f32x4(krs, quad * 16, (8 * s8 + wave) * kv_ld * 4);
+            } else {
+#pragma unroll
+                for (int s8 = 0; s8 < HD / 8; s8++) k0[ch][s8] = vf4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    }
 
     // the seq % 8 tail rows of V, for the output threads (tid < 32)
     float vtail[7];
