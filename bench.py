@@ -222,8 +222,9 @@ FILE_KERNELS = {
     "lmrs_1b": {"qkv": "k_matmul_q8g (q, k, v; RMSNorm and group quantize before)",
                 "wo": "k_matmul_q8g (output projection, residual add)",
                 "w13": "k_matmul_q8g (gate and up; SwiGLU after)", "w2": "k_matmul_q8g (down, residual add)"},
-    "st_f16_1b": {"qkv": "k_matmul_f16_tok1 (fused q/k/v rows)", "wo": "k_matmul_f16_tok1 (output, residual add)",
-                  "w13": "k_matmul_f16_tok1 (gate and up)", "w2": "k_matmul_f16_tok1 (down, residual add)"},
+    "st_f16_1b": {"qkv": "k_f16_gemv (fused q/k/v rows, RMSNorm prologue)", "wo": "k_f16_gemv (output, residual add)",
+                  "w13": "k_f16_gemv (gate/up row pairs, RMSNorm prologue, SwiGLU epilogue)",
+                  "w2": "k_f16_gemv (down, residual add)"},
 }
 
 

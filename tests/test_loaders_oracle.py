@@ -239,3 +239,40 @@ def test_library_tokenizer_bin_matches_oracle(tmp_path):
         assert ids == ot.encode(s, bos=True), s
         assert lt.decode(ids) == ot.decode(ids)
     assert lt.chat_prompt("Hello world") == ot.chat_prompt("Hello world")
+
+
+# ------------------------------------------------- forward composition
+@pytest.mark.parametrize("kind", ["lmrs_gs64", "st_q8_gs32", "st_f16"])
+def test_forward_matches_float64(tmp_path, kind):
+    """The oracle's forward on lm.rs / safetensors models (HF RoPE with the
+    llama3 scaling, the file's group size, F16 chains) against an
+    independent float64 forward: within 1e-5 of the logits' scale, while
+    plausible mistakes computed the same way differ by more than 1e-4."""
+    import formats_np as FN
+    s = MF.Shape(dim=64, hidden=128, n_layers=2, n_heads=4, n_kv=2, head_dim=16, ctx=48, rope_theta=10000.0)
+    d = str(tmp_path / kind)
+    if kind == "lmrs_gs64":
+        p = MF.write_lmrs(d, s, gs=64, seed=11)
+        arrays, loader = L.read_lmrs(p), L.load_lmrs
+    elif kind == "st_q8_gs32":
+        p = MF.write_safetensors(d, s, q8_gs=32, seed=12, tokenizer="bin")
+        arrays, loader = L.read_safetensors(p), L.load_safetensors
+    else:
+        p = MF.write_safetensors(d, s, seed=13, tokenizer="bin")
+        arrays, loader = L.read_safetensors(p), L.load_safetensors
+    m, _ = loader(p)
+    sess = m.create_session()
+    toks = [3, 17, 250, 5, 99, 42, 7, 300, 11, 64]
+    variants = ["reference", "rope_gguf_pairs", "no_llama3_scaling", "gate_up_swapped"]
+    if kind == "lmrs_gs64":
+        variants.append("group_32")
+    refs = {v: FN.Float64Model(arrays, v) for v in variants}
+    worst = {v: 0.0 for v in variants}
+    for pos, t in enumerate(toks):
+        lo = m.forward_x(np.array([t], np.uint32), pos, sess).astype(np.float64)
+        scale = np.max(np.abs(lo))
+        for v, f in refs.items():
+            worst[v] = max(worst[v], float(np.max(np.abs(f.step(t) - lo)) / scale))
+    assert worst["reference"] < 1e-5, worst
+    for v in variants[1:]:
+        assert worst[v] > 1e-4, (v, worst)
