@@ -219,9 +219,11 @@ DECODE = {
 # that runs each GEMV class of theirs.
 FILE_CONFIGS = {"lmrs_1b", "st_f16_1b"}
 FILE_KERNELS = {
-    "lmrs_1b": {"qkv": "k_matmul_q8g (q, k, v; RMSNorm and group quantize before)",
-                "wo": "k_matmul_q8g (output projection, residual add)",
-                "w13": "k_matmul_q8g (gate and up; SwiGLU after)", "w2": "k_matmul_q8g (down, residual add)"},
+    "lmrs_1b": {"qkv": "k_gemv<kQ8S> (q|k|v rows with f32 block scales, q/k heads in RoPE pair order; RMSNorm "
+                       "prologue, RoPE + KV-cache epilogue)",
+                "wo": "k_gemv<kQ8S> (output projection, residual add)",
+                "w13": "k_gemv<kQ8S> (32 gate + 32 up rows per workgroup, RMSNorm prologue, SwiGLU + quantize "
+                       "epilogue)", "w2": "k_gemv<kQ8S> (down, residual add)"},
     "st_f16_1b": {"qkv": "k_f16_gemv (fused q/k/v rows, RMSNorm prologue)", "wo": "k_f16_gemv (output, residual add)",
                   "w13": "k_f16_gemv (gate/up row pairs, RMSNorm prologue, SwiGLU epilogue)",
                   "w2": "k_f16_gemv (down, residual add)"},

@@ -60,6 +60,19 @@ template <>
 struct WBlock<kQ8> { uint4 a, b; };
 template <>
 struct WBlock<kQ4> { uint4 a; };
+template <>
+struct WBlock<kQ8S> { uint4 a, b; };
+
+// The activation format of a weight format (Q8 rows with f32 block scales
+// dot against the same 32-groups as Q8_0).
+template <int WF>
+constexpr int act_fmt() { return WF == kQ4 ? kQ4 : kQ8; }
+
+// Block scales: f16 words (Q8_0, Q4_0) or f32 (kQ8S).
+template <int WF>
+struct ScaleWord { using type = uint16_t; };
+template <>
+struct ScaleWord<kQ8S> { using type = float; };
 
 constexpr int kBufRaw = 0x00020000;   // buffer descriptor word 3: raw 32-bit data
 
@@ -87,7 +100,7 @@ __device__ __forceinline__ uint4 buf_u4(__amdgpu_buffer_rsrc_t r, int voff, int 
 
 template <int WF>
 __device__ __forceinline__ void load_block(WBlock<WF>& w, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    if constexpr (WF == kQ8) {
+    if constexpr (WF != kQ4) {
         w.a = buf_u4(r, voff, soff);
         w.b = buf_u4(r, voff + 16, soff);
     } else {
@@ -100,7 +113,7 @@ __device__ __forceinline__ void load_block(WBlock<WF>& w, __amdgpu_buffer_rsrc_t
 template <int WF>
 __device__ __forceinline__ int block_dot(const WBlock<WF>& w, const int32_t* xw) {
     int a0 = 0, a1 = 0;
-    if constexpr (WF == kQ8) {
+    if constexpr (WF != kQ4) {
         a0 = __builtin_amdgcn_sdot4((int)w.a.x, xw[0], a0, false);
         a1 = __builtin_amdgcn_sdot4((int)w.b.x, xw[4], a1, false);
         a0 = __builtin_amdgcn_sdot4((int)w.a.y, xw[1], a0, false);
@@ -352,7 +365,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                         const int row = min(row0 + i, o - 1);
                         const int att = a.att_dim, kv = a.kv_dim;
                         const bool is_k = row >= att && row < att + kv, is_v = row >= att + kv;
-                        const int c = is_v ? row - att - kv : (is_k ? row - att : 0);
+                        const int c = is_v ? row - att - kv : (is_k ? qk_column(row - att, a.head_size, a.hf_rows) : 0);
                         if ((is_k || is_v) && c < (kv / 4) * 4)
                             v = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
                     }
@@ -385,9 +398,9 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                     }
                     am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
                     am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
-                    const float sc = group_scale<WF>(am);
+                    const float sc = group_scale<act_fmt<WF>()>(am);
                     int q[8];
-                    quant8<WF>(v, sc, q);
+                    quant8<act_fmt<WF>()>(v, sc, q);
                     *reinterpret_cast<uint2*>(xl + e) =
                         WF == kQ4 ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
                                   : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
@@ -423,14 +436,18 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         const int wrow0 = row0 + w * RW;                    // this wavefront's first row
         const int r = lane / LPR, j = lane - (lane / LPR) * LPR;
         const int rows_here = max(0, min(RW, o - wrow0));
-        const size_t row_bytes = WF == kQ8 ? (size_t)n : (size_t)n / 2;
-        constexpr int kBlockBytes = WF == kQ8 ? 32 : 16;
+        const size_t row_bytes = WF != kQ4 ? (size_t)n : (size_t)n / 2;
+        constexpr int kBlockBytes = WF != kQ4 ? 32 : 16;
+        using SW = typename ScaleWord<WF>::type;
+        constexpr int kScaleBytes = (int)sizeof(SW);
         // descriptors over this wavefront's rows: rows past the matrix read 0
         const __amdgpu_buffer_rsrc_t qr =
             uniform_rsrc(a.qs + (size_t)min(wrow0, o - 1) * row_bytes, (int)(rows_here * row_bytes));
-        const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(a.d + (size_t)min(wrow0, o - 1) * nb, rows_here * nb * 2);
+        const void* scale_rows = WF == kQ8S ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nb)
+                                            : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
+        const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(scale_rows, rows_here * nb * kScaleBytes);
         const int qv = (int)(r * row_bytes) + j * kBlockBytes;
-        const int dv_off = (r * nb + j) * 2;
+        const int dv_off = (r * nb + j) * kScaleBytes;
         // Slot by slot (loads complete in issue order, so slot k's wait
         // leaves the later slots in flight; the scheduling barriers keep the
         // compiler from regrouping them).  LA slots go out first, then slot
@@ -440,10 +457,14 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         // slot only when most data had arrived.
         constexpr int LA = PPL <= 4 ? PPL : (PPL / 2 < 8 ? PPL / 2 : 8);
         WBlock<WF> wv[LA];
-        uint16_t dv[LA];
+        SW dv[LA];
         auto issue = [&](int k) {
             load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
-            dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, kPolStream);
+            if constexpr (WF == kQ8S)
+                dv[k % LA] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(dr, dv_off, k * LPR * kScaleBytes, kPolStream));
+            else
+                dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, kPolStream);
             __builtin_amdgcn_sched_barrier(0);
         };
 #pragma unroll
@@ -465,7 +486,10 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             const int b = k * LPR + j;
             const int bb = b < nb ? b : nb - 1;
             const int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
-            const float term = fmul(fmul((float)isum, f16_to_f32(dv[k % LA])), xsl[bb]);
+            float ws;
+            if constexpr (WF == kQ8S) ws = dv[k % LA];
+            else ws = f16_to_f32(dv[k % LA]);
+            const float term = fmul(fmul((float)isum, ws), xsl[bb]);
             acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
             if (k + LA < PPL) issue(k + LA);
         }
@@ -480,7 +504,10 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         } else if constexpr (EPI == kEpiQkvRope) {
             // rope_gguf (util.rs:653-718): pair (2i, 2i+1) of a head rotated
             // by the angle table row `pos`; v rows are stored as summed.
-            // The rows of a pair are in this wavefront (RW even).
+            // The rows of a pair are in this wavefront (RW even).  With
+            // hf_rows the stored pair (2j, 2j+1) is util::rope's pair
+            // (j, j + head/2) (util.rs:589-635), the same rotation, written
+            // to those columns.
             const float other = __shfl_xor(acc, LPR, 64);
             if (live) {
                 const float* ropel = reinterpret_cast<const float*>(smem + L.rope);
@@ -490,7 +517,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                 if (my_row >= att + kv) {
                     a.v_cache[(size_t)pos * kv + (my_row - att - kv)] = acc;
                 } else {
-                    const int col = my_row < att ? my_row : my_row - att;
+                    const int col = qk_column(my_row < att ? my_row : my_row - att, a.head_size, a.hf_rows);
                     const int li = w * RW + my_r;
                     const float c = ropel[2 * li];
                     const float s = ropel[2 * li + 1];
@@ -630,6 +657,7 @@ hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipSt
     a.fault = wait_fault_word(false);
     if (wfmt == kQ8) return launch_wf<kQ8>(a, epi, batch, s);
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);
+    if (wfmt == kQ8S) return launch_wf<kQ8S>(a, epi, batch, s);
     return hipErrorInvalidValue;
 }
 

@@ -32,6 +32,20 @@
 namespace yl {
 
 enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs:17-22
+// The GEMV's weight format for Q8 rows whose 32-blocks carry f32 scales
+// (QMat::sf: lm.rs and safetensors Q8 with group size 32); activations and
+// results as for kQ8.
+constexpr int kQ8S = 3;
+
+// The column of stored row c of a q or k projection whose heads (hd a
+// power of two) hold their rows in the order 0, h, 1, h+1, ..., h-1, 2h-1
+// (h = hd/2), so that util::rope's pairs (j, j + h) are adjacent rows: row
+// 2j+e of a head holds column j + e*h.  c itself when `hf` is 0.
+__host__ __device__ __forceinline__ int qk_column(int c, int hd, int hf) {
+    if (!hf) return c;
+    const int within = c & (hd - 1);
+    return c - within + (within >> 1) + (within & 1) * (hd >> 1);
+}
 
 struct QMat {          // device-resident quantized matrix
     int fmt = 0;       // kQ8 / kQ4 / kF16
@@ -91,6 +105,7 @@ enum Epi : int {
 struct GemvArgs {
     // weights and activations
     const uint8_t* qs; const uint16_t* d; int n, o, nb;
+    const float* sf;                           // kQ8S: f32 block scales [o][nb] (d unused)
     const int8_t* xq; const float* xs;        // [batch][n], [batch][nb] (staged prologue)
     // kEpiQkvRope / kEpiSwiglu prologue: RMSNorm + quantize of x [batch][n]
     float* x; const float* norm_w; float eps;
@@ -102,6 +117,11 @@ struct GemvArgs {
     int att_dim, kv_dim, head_size, kv_ld;
     const float* rope_cos; const float* rope_sin;  // [ctx][head_size/2]
     const StepState* state;
+    // nonzero: util::rope pairs (j, j + head_size/2), with the q and k rows
+    // of each head stored in the order 0, h, 1, h+1, ..., h-1, 2h-1
+    // (h = head_size/2) so a pair's rows are adjacent; row 2j+e of a head
+    // holds column j + e*h, where its result is written
+    int hf_rows;
     // kEpiSwiglu
     int8_t* hq; float* hs; float* h_f32; int hidden; int h_fmt;
     // set to nonzero when a bounded wait inside the kernel gives up (its
@@ -194,6 +214,8 @@ struct Q8gArgs {
     const StepState* st = nullptr;
     int nseg = 1;
     Q8gSegArgs seg[3];
+    int pair_rows = 16;   // epi 2: gate rows then up rows per block (16 or 32; the upload's interleave)
+    int perm_hd = 0;      // epi 0: 0, or the head size of segments 0 and 1 stored in pair order (qk_column)
 };
 hipError_t launch_matmul_q8g(const Q8gArgs& a, hipStream_t s);
 hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size_t n, hipStream_t s);

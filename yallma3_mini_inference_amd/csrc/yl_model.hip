@@ -322,6 +322,8 @@ struct yl_model {
     bool q8g = false;           // Q8 with f32 scales and group size gs (lm.rs, safetensors)
     int gs = 32;
     int hf_rope = 0;            // 1: util::rope pairs (j, j + head/2); 0: rope_gguf pairs (2j, 2j + 1)
+    int pair_rows = 16;         // q8g: gate/up rows per interleaved block of w13 (16, or 32 with q8_gemv)
+    bool q8_gemv = false;       // q8g with group size 32: one-token steps on the GGUF path's GEMVs (kQ8S)
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
     std::vector<std::string> vocab_str;
@@ -681,7 +683,7 @@ static bool upload_hostmat(const HostMat& h, QMat* m, std::string* err) {
         }
         return true;
     }
-    m->fmt = kQ8; m->nb = 0; m->gs = h.gs;
+    m->fmt = kQ8; m->nb = (int)(h.n / h.gs); m->gs = h.gs;
     if (hipMalloc(&m->qs, h.q.size() + 256) != hipSuccess || hipMalloc(&m->sf, h.s.size() * 4 + 256) != hipSuccess ||
         hipMemcpy(m->qs, h.q.data(), h.q.size(), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(m->sf, h.s.data(), h.s.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
@@ -705,9 +707,13 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
     m->f16 = h.f16;
     m->q8g = !h.f16;
     m->gs = h.gs;
+    // group size 32 (rows up to the GEMV's limits): one-token steps run the
+    // 32-block GEMV (kQ8S), whose SwiGLU tiles are 32 gate + 32 up rows
+    m->q8_gemv = m->q8g && m->gs == 32 && m->dim <= 4096 && m->att <= 16384 && m->hidden <= 16384;
+    m->pair_rows = m->q8_gemv ? 32 : 16;
     if (m->n_kv <= 0 || m->n_heads % m->n_kv || (m->hd != 32 && m->hd != 64 && m->hd != 128) || m->dim % 32 ||
         m->hidden % 32 || m->att % 32 || m->kv % 32 || m->ctx <= 0 || m->dim > 8192 ||
-        (m->q8g && (m->dim % m->gs || m->att % m->gs || m->hidden % m->gs))) {
+        (m->q8g && (m->dim % m->gs || m->att % m->gs || m->hidden % m->gs || m->hidden % m->pair_rows))) {
         set_error("unsupported shape: head_size 32/64/128, dimensions multiples of 32 (and of the group size)");
         return nullptr;
     }
@@ -740,20 +746,26 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
             ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) && upload_qmat(w13, &L.w13, &err) &&
                  upload_hostmat(H[5], &L.w2, &err);
         } else {
-            // q, k and v rows in one matrix; gate and up rows interleaved in
-            // blocks of 16 (the SwiGLU tiles of the f32-scaled Q8 GEMV)
+            // q, k and v rows in one matrix, the q and k rows of each head in
+            // util::rope's pair order (stored row p holds qk_column(p), so a
+            // rotated pair is two adjacent rows); gate and up rows interleaved
+            // in blocks of m->pair_rows (the SwiGLU tiles of the GEMVs)
             HostMat qkv, w13;
             qkv.o = H[0].o + H[1].o + H[2].o; qkv.n = H[0].n; qkv.gs = H[0].gs;
             for (int k = 0; k < 3; k++) {
-                qkv.q.insert(qkv.q.end(), H[k].q.begin(), H[k].q.end());
-                qkv.s.insert(qkv.s.end(), H[k].s.begin(), H[k].s.end());
+                const size_t G = H[k].n / H[k].gs;
+                for (size_t p = 0; p < H[k].o; p++) {
+                    const size_t r = k < 2 ? (size_t)qk_column((int)p, m->hd, 1) : p;
+                    qkv.q.insert(qkv.q.end(), H[k].q.begin() + r * H[k].n, H[k].q.begin() + (r + 1) * H[k].n);
+                    qkv.s.insert(qkv.s.end(), H[k].s.begin() + r * G, H[k].s.begin() + (r + 1) * G);
+                }
             }
             w13.o = 2 * H[4].o; w13.n = H[4].n; w13.gs = H[4].gs;
-            const size_t G = H[4].n / H[4].gs;
-            for (size_t r0 = 0; r0 < H[4].o; r0 += 16)
+            const size_t G = H[4].n / H[4].gs, P = (size_t)m->pair_rows;
+            for (size_t r0 = 0; r0 < H[4].o; r0 += P)
                 for (int k : {4, 6}) {
-                    w13.q.insert(w13.q.end(), H[k].q.begin() + r0 * H[k].n, H[k].q.begin() + (r0 + 16) * H[k].n);
-                    w13.s.insert(w13.s.end(), H[k].s.begin() + r0 * G, H[k].s.begin() + (r0 + 16) * G);
+                    w13.q.insert(w13.q.end(), H[k].q.begin() + r0 * H[k].n, H[k].q.begin() + (r0 + P) * H[k].n);
+                    w13.s.insert(w13.s.end(), H[k].s.begin() + r0 * G, H[k].s.begin() + (r0 + P) * G);
                 }
             ok = upload_hostmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) &&
                  upload_hostmat(w13, &L.w13, &err) && upload_hostmat(H[5], &L.w2, &err);
@@ -847,6 +859,10 @@ bool session_grow(yl_session* s, int batch) {
     return true;
 }
 
+// The GEMV weight format of a matrix: its own, or kQ8S for Q8 rows with f32
+// scales (which reach the GEMV with group size 32 only: yl_model::q8_gemv).
+static int gemv_fmt(const QMat& w) { return w.sf ? kQ8S : w.fmt; }
+
 uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
     return (uint64_t)w.bytes() + (uint64_t)batch * ((uint64_t)w.n + (uint64_t)w.nb * 4 + (uint64_t)out_elems * 4);
 }
@@ -933,8 +949,9 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     switch (cls) {
     case kOpQkv:
         // RMSNorm + quantize (prologue) -> Q,K,V -> K/V += into the cache -> RoPE
-        a.qs = L.qkv.qs; a.d = L.qkv.d; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
+        a.qs = L.qkv.qs; a.d = L.qkv.d; a.sf = L.qkv.sf; a.n = L.qkv.n; a.o = L.qkv.o; a.nb = L.qkv.nb;
         a.x = s->x; a.norm_w = L.rms_att; a.eps = m->eps;
+        a.hf_rows = m->hf_rope;
         if (l == 0 && m->emb.fmt == 0) { a.emb = m->emb; a.tokens = tok; }
         if (l == 0 && m->emb.fmt != 0) {   // an f16 table: the lookup runs first
             const hipError_t e = launch_embed(m->emb, tok, batch, s->x, st);
@@ -944,7 +961,7 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
         a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st;
         if (bytes) *bytes = gemv_bytes(L.qkv, L.qkv.o, batch);
-        return launch_gemv(a, L.qkv.fmt, kEpiQkvRope, batch, st);
+        return launch_gemv(a, gemv_fmt(L.qkv), kEpiQkvRope, batch, st);
     case kOpAttn:
         // attention (+ quantize of its output).  Algorithmic bytes: the keys
         // and values of every position, the queries, the quantized output.
@@ -964,23 +981,23 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
                                 m->attn_scale, L.wo.fmt, s->aq, s->as_, nullptr, st);
     case kOpWo:
         // WO -> residual add
-        a.qs = L.wo.qs; a.d = L.wo.d; a.n = L.wo.n; a.o = L.wo.o; a.nb = L.wo.nb;
+        a.qs = L.wo.qs; a.d = L.wo.d; a.sf = L.wo.sf; a.n = L.wo.n; a.o = L.wo.o; a.nb = L.wo.nb;
         a.xq = s->aq; a.xs = s->as_; a.x = s->x;
         if (bytes) *bytes = gemv_bytes(L.wo, L.wo.o, batch);
-        return launch_gemv(a, L.wo.fmt, kEpiResid, batch, st);
+        return launch_gemv(a, gemv_fmt(L.wo), kEpiResid, batch, st);
     case kOpW13:
         // RMSNorm + quantize (prologue) -> W1, W3 -> SwiGLU -> quantize
-        a.qs = L.w13.qs; a.d = L.w13.d; a.n = L.w13.n; a.o = L.w13.o; a.nb = L.w13.nb;
+        a.qs = L.w13.qs; a.d = L.w13.d; a.sf = L.w13.sf; a.n = L.w13.n; a.o = L.w13.o; a.nb = L.w13.nb;
         a.x = s->x; a.norm_w = L.rms_ffn; a.eps = m->eps;
         a.hq = s->hq; a.hs = s->hs; a.h_f32 = nullptr; a.hidden = m->hidden; a.h_fmt = L.w2.fmt;
         if (bytes) *bytes = gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch);
-        return launch_gemv(a, L.w13.fmt, kEpiSwiglu, batch, st);
+        return launch_gemv(a, gemv_fmt(L.w13), kEpiSwiglu, batch, st);
     case kOpW2:
         // W2 -> residual add
-        a.qs = L.w2.qs; a.d = L.w2.d; a.n = L.w2.n; a.o = L.w2.o; a.nb = L.w2.nb;
+        a.qs = L.w2.qs; a.d = L.w2.d; a.sf = L.w2.sf; a.n = L.w2.n; a.o = L.w2.o; a.nb = L.w2.nb;
         a.xq = s->hq; a.xs = s->hs; a.x = s->x;
         if (bytes) *bytes = gemv_bytes(L.w2, L.w2.o, batch);
-        return launch_gemv(a, L.w2.fmt, kEpiResid, batch, st);
+        return launch_gemv(a, gemv_fmt(L.w2), kEpiResid, batch, st);
     default:
         return hipErrorInvalidValue;
     }
@@ -1130,6 +1147,7 @@ hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int 
         if (e == hipSuccess) e = input(a, s->x, L.rms_att, m->dim);
         // q [t][att] from 0; K [kv][kv_ld] and V [pos][kv] from position pos, `+=`
         a.nseg = 3;
+        a.perm_hd = m->hd;
         a.st = s->st;
         a.seg[0] = Q8gSegArgs{s->sq, 0, 1, m->att, m->att, 0};
         a.seg[1] = Q8gSegArgs{kc, 1, m->kv_ld, 1, m->att + m->kv, m->kv / 4 * 4};
@@ -1154,6 +1172,7 @@ hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int 
     case kOpW13: {
         if (bytes) *bytes = L.w13.bytes() + xbytes(m->dim) + B * (uint64_t)m->hidden * 4;
         Q8gArgs a = args(L.w13, 2);
+        a.pair_rows = m->pair_rows;
         e = input(a, s->x, L.rms_ffn, m->dim);
         a.seg[0] = Q8gSegArgs{s->hf, 0, 1, m->hidden, L.w13.o, 0};
         if (e == hipSuccess) e = launch_matmul_q8g(a, st);
@@ -1177,7 +1196,9 @@ hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int 
 hipError_t enqueue_class(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
                          int advance, uint64_t* bytes, bool prologue = true) {
     if (m->f16) return enqueue_op_f16(m, s, cls, l, batch, tok, advance, bytes);
-    if (m->q8g) return enqueue_op_q8g(m, s, cls, l, batch, tok, advance, bytes);
+    // f32-scaled Q8 with group size 32: one token takes the GGUF path's
+    // GEMVs (32-blocks, f32 scales), prompts the tile kernel
+    if (m->q8g && (batch > 1 || !m->q8_gemv)) return enqueue_op_q8g(m, s, cls, l, batch, tok, advance, bytes);
     return enqueue_op(m, s, cls, l, batch, tok, advance, bytes, prologue);
 }
 

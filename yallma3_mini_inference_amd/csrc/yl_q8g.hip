@@ -38,12 +38,14 @@ namespace yl {
 // Epilogues: EPI 0 stores to up to three row segments (q, k, v of a fused
 // projection), each with its own addressing and `+=` columns; EPI 1 adds the
 // chain (from 0) to the output (the residual adds of forward.rs:196-204,
-// 244-253); EPI 2 takes tiles of 32 rows holding 16 gate rows then the 16 up
-// rows of the same columns (the upload interleaves w1 and w3 so) and writes
-// h = silu(gate) * up (forward.rs:220-237).
+// 244-253); EPI 2 takes tiles of R rows holding R/2 gate rows then the R/2
+// up rows of the same columns (the upload interleaves w1 and w3 so, in
+// blocks of 16 or 32 rows) and writes h = silu(gate) * up
+// (forward.rs:220-237).  With perm_hd, segments 0 and 1 (q and k) hold
+// each head's rows in util::rope's pair order (qk_column), and results go
+// to the rows' own columns.
 constexpr int kQ8gThreads = 256;
 constexpr int kQ8gUnroll = 8;    // 16-byte weight loads per thread per batch (two batches in flight)
-constexpr int kPairRows = 16;   // EPI 2: gate rows then up rows per 32-row tile
 
 // rows [previous row_end, row_end) of the matrix go to `out`: element
 // (token t, column c) at out[pos * pos_stride + t * stride_tok + c * stride_row]
@@ -57,6 +59,7 @@ struct Q8gSeg {
 struct Q8gOut {
     Q8gSeg seg[3];
     int nseg;
+    int perm_hd;   // 0, or the head size of segments 0 and 1 stored in pair order
 };
 
 // squares row of one RMSNorm chain: n/8 values + zero padding to a multiple
@@ -269,7 +272,9 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
         if constexpr (EPI == 0)
             while (sg + 1 < dst.nseg && c >= dst.seg[sg].row_end) sg++;
         const Q8gSeg& q = dst.seg[sg];
-        const int col = c - (sg ? dst.seg[sg - 1].row_end : 0);
+        int col = c - (sg ? dst.seg[sg - 1].row_end : 0);
+        if constexpr (EPI == 0)
+            if (sg < 2) col = qk_column(col, dst.perm_hd, dst.perm_hd);
         const size_t at = (st ? (size_t)st->pos * q.pos_stride : 0) + (size_t)t * q.stride_tok + (size_t)col * q.stride_row;
         float acc = (EPI == 0 && col < q.acc_cols) ? q.out[at] : 0.0f;
         const float* tr = trm + (tb * R + r) * GP;
@@ -289,13 +294,14 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
     if constexpr (EPI == 2) {
         __syncthreads();
         const Q8gSeg& q = dst.seg[0];
-        for (int j = tid; j < TB * kPairRows; j += kQ8gThreads) {
-            const int tb = j / kPairRows, cc = j - tb * kPairRows;
+        const int PR = R / 2;   // gate rows, then as many up rows
+        for (int j = tid; j < TB * PR; j += kQ8gThreads) {
+            const int tb = j / PR, cc = j - tb * PR;
             const int t = t0 + tb;
             if (t >= batch || cc >= rows / 2) continue;
-            const float g = res[tb * R + cc], u = res[tb * R + kPairRows + cc];
+            const float g = res[tb * R + cc], u = res[tb * R + PR + cc];
             const float den = fadd(1.0f, expf_rn(-g));
-            q.out[(size_t)t * q.stride_tok + (size_t)(blockIdx.x * kPairRows + cc) * q.stride_row] = fmul(g / den, u);
+            q.out[(size_t)t * q.stride_tok + (size_t)(blockIdx.x * PR + cc) * q.stride_row] = fmul(g / den, u);
         }
     }
 }
@@ -348,6 +354,7 @@ static hipError_t launch_q8g_t(const Q8gArgs& a, int R, int lg, size_t lds, hipS
     }
     Q8gOut d{};
     d.nseg = a.nseg;
+    d.perm_hd = a.perm_hd;
     for (int i = 0; i < a.nseg; i++)
         d.seg[i] = Q8gSeg{a.seg[i].out, a.seg[i].pos_stride, a.seg[i].stride_row, a.seg[i].stride_tok,
                           a.seg[i].row_end, a.seg[i].acc_cols};
@@ -363,16 +370,22 @@ hipError_t launch_matmul_q8g(const Q8gArgs& a, hipStream_t s) {
         a.pro < 0 || a.pro > 2 || a.epi < 0 || a.epi > 2 || (a.pro > 0 && a.batch > 65535) ||
         (long)a.batch > 65535L * 4 || a.seg[a.nseg - 1].row_end != o)
         return hipErrorInvalidValue;
-    if (a.epi == 2 && o % (2 * kPairRows)) return hipErrorInvalidValue;
+    if (a.epi == 2 && ((a.pair_rows != 16 && a.pair_rows != 32) || o % (2 * a.pair_rows))) return hipErrorInvalidValue;
+    if (a.perm_hd && ((a.perm_hd & (a.perm_hd - 1)) || a.perm_hd < 2 || a.nseg < 2 || a.seg[0].row_end % a.perm_hd ||
+                      (a.seg[1].row_end - a.seg[0].row_end) % a.perm_hd))
+        return hipErrorInvalidValue;
     const int G = n / gs;
-    const int tb = a.pro > 0 || a.batch == 1 ? 1 : 4;
+    int tb = a.pro > 0 || a.batch == 1 ? 1 : 4;
+    // a SwiGLU tile of 32 + 32 rows over a long row takes one token per
+    // workgroup when four do not fit in LDS
+    if (a.epi == 2 && q8g_lds_bytes(tb, a.pro, n, G, 2 * a.pair_rows) > 160 * 1024) tb = 1;
     const int gy = (a.batch + tb - 1) / tb;
     // rows per workgroup: about 1024 workgroups over the chip (256 when each
     // workgroup makes its own input row), dividing every segment boundary,
     // within 64 KB of LDS (EPI 2: one gate/up tile pair)
     int R = 64;
     if (a.epi == 2) {
-        R = 2 * kPairRows;
+        R = 2 * a.pair_rows;
     } else {
         const long want = a.pro > 0 ? 256 : 1024;
         while (R > 1 && (long)((o + R - 1) / R) * gy < want) R /= 2;
