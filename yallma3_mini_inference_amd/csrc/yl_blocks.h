@@ -394,4 +394,38 @@ __device__ void rowq_norm_quant(int dim, float eps, float* sq, int8_t* q_lds, fl
     __syncthreads();
 }
 
+// Hand-offs between wavefronts of one workgroup through LDS counters
+// (relaxed atomics: a volatile LDS access would make the compiler wait for
+// every outstanding global load first).  LDS serves one wavefront's
+// accesses in order, and a waiter's reads of the published data are issued
+// only after it saw the count.  The waits are bounded: the counted
+// wavefronts always arrive within microseconds, the bound only keeps a
+// defect from hanging the device; a wait that gives up sets *fault, which the
+// host reads after the call and reports as an error.
+__device__ __forceinline__ void lds_arrive(int* ctr) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's LDS writes done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// lds_arrive without the wait: LDS performs one wavefront's operations in
+// issue order, so a count added after LDS writes is seen only once those
+// writes are performed, and a waiter reads the data only after it saw the
+// count; the signal fence keeps the compiler from moving the writes past
+// the add.  No wait on the wavefront's own outstanding LDS reads either.
+__device__ __forceinline__ void lds_arrive_nowait(int* ctr) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Returns the count it saw (>= target unless the wait gave up).
+__device__ __forceinline__ int lds_wait_count(int* ctr, int target, unsigned* fault) {
+    int i = 0, c;
+    for (; (c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < target && i < (1 << 22); i++)
+        __builtin_amdgcn_s_sleep(1);
+    if (i == (1 << 22) && fault && (threadIdx.x & 63) == 0)
+        __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return c;
+}
+
 }  // namespace yl

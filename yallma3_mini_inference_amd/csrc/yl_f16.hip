@@ -9,15 +9,10 @@
 // in the reference's memory, so the device keeps them as f16 (half the
 // bytes) and widens them exactly.  Each output is one lane's serial chain;
 // the kernels keep that chain fed:
-//   decode (one token): a workgroup owns 16 output rows.  Three product
-//   wavefronts multiply a 16-row x 256-column weight tile by the activations
-//   into LDS while the fourth wavefront's 16 lanes add the previous tile's
-//   products onto their row accumulators, reading 16 bytes per four adds and
-//   keeping two read batches in flight.  A chain of n dependent adds is the
-//   kernel's floor (~n x 5.8 cycles), so the weight loads run four tiles
-//   ahead in registers and many small workgroups share the chip.  The
-//   prologue can apply RMSNorm (util.rs:389-426) to the input row, and the
-//   epilogue add the residual or form SwiGLU from gate/up row pairs;
+//   decode (one token): a workgroup owns 64 output rows, one chain lane
+//   each, fed from LDS by three product wavefronts (below).  The prologue
+//   can apply RMSNorm (util.rs:389-426) to the input row, and the epilogue
+//   add the residual or form SwiGLU from gate/up row pairs;
 //   batches: a workgroup takes 64 rows x 4 tokens, one wavefront per token,
 //   each lane multiplying and adding its own (token, row) chain, the weight
 //   tile shared through LDS.
@@ -44,167 +39,271 @@ __device__ __forceinline__ void widen8(const uint4& v, float w[8]) {
 }
 
 // ------------------------------------------------------------- one token
-constexpr int kFgThreads = 256;       // all wavefronts: products; wavefront 0 also the chains
-constexpr int kFgRows = 16;           // output rows per workgroup (EPI 2: 8 gate rows, then their 8 up rows)
-constexpr int kFgKT = 256;            // columns per tile
-constexpr int kFgStride = kFgKT + 4;  // product row stride (floats)
-constexpr int kFgDepth = 4;           // tiles of weight loads in flight
-constexpr int kFgChunks = kFgRows * kFgKT / 8;                    // 16-byte weight chunks per tile
-constexpr int kFgPer = kFgChunks / kFgThreads;                      // chunks per thread and tile
-constexpr int kFgPairRows = kFgRows / 2;
-static_assert(kFgChunks % kFgThreads == 0, "every thread takes whole chunks");
+// A workgroup owns R output rows.  Wavefront 0 is the chain wavefront: lane
+// r adds row r's products in column order, one f32 add after another
+// (matmul_f32's serial sum).  A dependent add issues every ~4-5 cycles, so
+// the wavefront needs its SIMD to itself and its operands in LDS: PW
+// product wavefronts (on the other SIMDs) widen the f16 weights, multiply
+// them by the activations and write R-row x 64-column product tiles into a
+// ring of LDS slots (8, or 4 for R = 64), their weight loads D tiles ahead
+// in registers.  Hand-offs use LDS counters, not barriers: each product
+// wavefront counts the tiles it has written, the chain wavefront counts the
+// tiles it has read (`consumed`), a tile is ready when every product
+// wavefront's count passed it, and a product wavefront refills a slot only
+// once its previous tile was consumed.  The chain wavefront reads the next
+// tile's 64 products per lane while it adds the current one's (two register
+// sets, unconditional reads), so its adds never wait for LDS, and checks
+// the counts only when it reaches the last tile it knew to be ready.
+//
+// One CU streams only ~20 GB/s of weights, so a projection needs about 256
+// workgroups to reach HBM bandwidth: R is chosen per matrix (64 rows for
+// the gate/up matrix, 8-32 for the others), and the chain, whose length n
+// is fixed, runs on every CU at once.
+constexpr int kFgThreadsMax = 256;
+constexpr int kFgKT = 64;                   // columns per tile
+constexpr int kFgStride = kFgKT + 4;        // product row stride (floats): the 16 lanes of a read hit distinct banks
+constexpr int kFgPairRows = 32;             // EPI 2: 32 gate rows, then their 32 up rows (R = 64)
+static_assert(kFgPairRows == kF16PairRows, "the upload's gate/up interleave");
 
-__host__ __device__ inline int fg_norm_len(int n) { return (n / 8 + 31) & ~31; }
-__host__ __device__ inline int fg_norm_stride(int n) { return fg_norm_len(n) + 4; }
-// LDS floats: x [n] | products 2 x [16][260] | (PRO 1) squares 8 x S, reduction 16, norm weights [n]
-__host__ __device__ inline size_t fg_lds_floats(int n, int pro) {
-    size_t f = (size_t)n + 2 * kFgRows * kFgStride;
-    if (pro) f += (size_t)8 * fg_norm_stride(n) + 16 + n;
-    return f;
+// Shape of a variant: R rows, PW product wavefronts, each product lane
+// taking CPL 16-byte chunks (8 columns of one row) per tile, D tiles of
+// loads in flight.
+template <int R>
+struct FgShape {
+    static constexpr int PW = R == 64 ? 3 : (R == 8 ? 1 : 2);
+    static constexpr int CPL = (8 * R + 64 * PW - 1) / (64 * PW);
+    static constexpr int D = R == 8 ? 24 : (R == 16 ? 16 : 8);
+    static constexpr int threads = 64 * (1 + PW);
+    static constexpr int slot_floats = R * kFgStride;
+    static constexpr int slots = R == 64 ? 4 : 8;   // tiles in the LDS ring
+};
+
+// LDS floats: counters 8 | product slots [slots][R][68] | the input row:
+// without PRO the row (rounded to whole 1 KiB DMA rows), with PRO the
+// RMSNorm staging (squares in 8 chain rows | row | norm weights)
+__host__ __device__ inline size_t fg_row_floats(int n, int pro) {
+    return pro ? rowq_lds_floats(n) : (size_t)rowq_row_len(n);
+}
+__host__ __device__ inline size_t fg_lds_floats(int n, int pro, int R) {
+    return 8 + (size_t)(R == 64 ? 4 : 8) * R * kFgStride + fg_row_floats(n, pro);
+}
+
+__device__ __forceinline__ float f16_prod(uint32_t bits16, float x) { return fmul(h2f(bits16), x); }
+
+// 16 product reads (one tile row: 64 floats) of row `row` from slot `s`
+template <int R>
+__device__ __forceinline__ void fg_read_row(vf4 (&v)[16], const float* P, int s, int row) {
+    const vf4* r = reinterpret_cast<const vf4*>(P + s * FgShape<R>::slot_floats + row * kFgStride);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = r[i];
+}
+// the serial adds of one tile row (kn = 64 or 32 columns)
+__device__ __forceinline__ float fg_add_row(float acc, const vf4 (&v)[16], int kn) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc = fadd(acc, v[i].x); acc = fadd(acc, v[i].y); acc = fadd(acc, v[i].z); acc = fadd(acc, v[i].w);
+    }
+    if (kn > 32) {
+#pragma unroll
+        for (int i = 8; i < 16; i++) {
+            acc = fadd(acc, v[i].x); acc = fadd(acc, v[i].y); acc = fadd(acc, v[i].z); acc = fadd(acc, v[i].w);
+        }
+    }
+    return acc;
 }
 
 // PRO 1: x <- RMSNorm(x) * norm_w first.  EPI 0: out[r] = sum; EPI 1: out[r]
-// += sum (the residual add); EPI 2: out[8 * blockIdx.x + c] = silu(g) * u of
-// rows (c, c + 8) of the tile (forward.rs:220-237).
-template <int PRO, int EPI>
-__global__ __launch_bounds__(kFgThreads) void k_f16_gemv(const uint16_t* __restrict__ w, int n, int o,
-                                                         const float* __restrict__ x, const float* __restrict__ norm_w,
-                                                         float eps, float* __restrict__ out) {
+// += sum (the residual add); EPI 2 (R = 64): out[32 * blockIdx.x + c] =
+// silu(g) * u of rows (c, c + 32) of the workgroup (forward.rs:220-237).
+template <int PRO, int EPI, int R>
+__global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __restrict__ w, int n, int o,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ norm_w, float eps,
+                                                            float* __restrict__ out, unsigned* fault) {
+    using Sh = FgShape<R>;
+    constexpr int PW = Sh::PW, CPL = Sh::CPL, D = Sh::D, SF = Sh::slot_floats, SL = Sh::slots;
+    static_assert(EPI != 2 || R == 2 * kFgPairRows, "SwiGLU tiles are 64 rows");
     extern __shared__ __align__(16) float lds[];
-    float* xl = lds;                                   // [n]
-    float* P = lds + n;                                // [2][16][260]
-    float* sq = P + 2 * kFgRows * kFgStride;           // (PRO) squares, then reduction, then norm weights
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int row0 = blockIdx.x * kFgRows;
+    int* ctr = reinterpret_cast<int*>(lds);   // [0..PW-1] tiles written per product wavefront, [4] tiles consumed,
+                                              // [5] input row ready
+    float* P = lds + 8;                       // [SL][R][68]
+    float* sq = P + SL * SF;
+    float* xl = PRO ? sq + 8 * rowq_stride(n) : sq;   // the input row
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = blockIdx.x * R;
     const int ntile = (n + kFgKT - 1) / kFgKT;
-    uint4 wr[kFgDepth][kFgPer];
-    // chunk j = tid + 256 i of a tile: row j / 32, 8 columns from 8 * (j % 32).
-    // Every load is issued unconditionally (tiles past the last and columns
-    // past n re-read in range, unused), so the compiler's wait counts stay
-    // exact: a consumer waits only for its own tile, not the ones behind it.
-    auto load_tile = [&](uint4 (&dst)[kFgPer], int t) {
-        const int k0 = min(t, ntile - 1) * kFgKT;
-#pragma unroll
-        for (int i = 0; i < kFgPer; i++) {
-            const int j = tid + kFgThreads * i;
-            const int k = min(k0 + 8 * (j & 31), n - 8);
-            dst[i] = *reinterpret_cast<const uint4*>(w + (size_t)(row0 + (j >> 5)) * n + k);
-        }
-    };
-#pragma unroll
-    for (int d = 0; d < kFgDepth; d++) load_tile(wr[d], d);
-    // the input row (RMSNorm first when PRO): 16-byte loads, 8 per thread in flight
-    {
-        const vf4* x4 = reinterpret_cast<const vf4*>(x);
-        const vf4* w4 = reinterpret_cast<const vf4*>(norm_w);
-        vf4* xl4 = reinterpret_cast<vf4*>(xl);
-        const int S = fg_norm_stride(n), L8 = fg_norm_len(n), n8 = n / 8;
-        float* red = sq + 8 * S;
-        vf4* wn4 = reinterpret_cast<vf4*>(red + 16);
-        for (int b = 0; b < n / 4; b += 8 * kFgThreads) {
-            vf4 v[8], nv[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i4 = b + k * kFgThreads + tid;
-                if (i4 < n / 4) {
-                    v[k] = x4[i4];
-                    if constexpr (PRO) nv[k] = w4[i4];
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i4 = b + k * kFgThreads + tid;
-                if (i4 < n / 4) {
-                    xl4[i4] = v[k];
-                    if constexpr (PRO) {
-                        wn4[i4] = nv[k];
-                        const int e = i4 * 4;
-                        sq[((e + 0) & 7) * S + (e >> 3)] = fmul(v[k].x, v[k].x);
-                        sq[((e + 1) & 7) * S + (e >> 3)] = fmul(v[k].y, v[k].y);
-                        sq[((e + 2) & 7) * S + (e >> 3)] = fmul(v[k].z, v[k].z);
-                        sq[((e + 3) & 7) * S + (e >> 3)] = fmul(v[k].w, v[k].w);
-                    }
-                }
-            }
-        }
-        if constexpr (PRO) {
-            for (int i = tid; i < 8 * (L8 - n8); i += kFgThreads) sq[(i / (L8 - n8)) * S + n8 + i % (L8 - n8)] = 0.0f;
-            __syncthreads();
-            if (tid < 8) red[tid] = lds_serial_sum(reinterpret_cast<const vf4*>(sq + tid * S), L8 / 32, 0.0f);
-            __syncthreads();
-            float part[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) part[j] = red[j];
-            float ss = reduce_add8(part);
-            ss = ss / (float)n;
-            ss = fadd(ss, eps);
-            ss = 1.0f / sqrtf(ss);
-            const float* wn = red + 16;
-            for (int i = tid; i < n; i += kFgThreads) xl[i] = fmul(wn[i], fmul(ss, xl[i]));
-        }
-        __syncthreads();
-    }
+    // the counters start at zero (LDS holds whatever the previous workgroup left)
+    if (tid < 8) ctr[tid] = 0;
+    __syncthreads();
 
-    float acc = 0.0f;
-    // iteration t: products of tile t -> P[t & 1], then the loads of tile
-    // t + depth into the freed registers; wavefront 0's first 16 lanes add
-    // tile t - 1.  The trip count is padded to whole rings of `depth`.
-    const int nit = (ntile + 1 + kFgDepth - 1) / kFgDepth * kFgDepth;
-    for (int t0 = 0; t0 < nit; t0 += kFgDepth) {
-#pragma unroll
-        for (int d = 0; d < kFgDepth; d++) {
-            const int t = t0 + d;
-            if (t < ntile) {
-                float* buf = P + (t & 1) * kFgRows * kFgStride;
-                const int k0 = t * kFgKT;
-#pragma unroll
-                for (int i = 0; i < kFgPer; i++) {
-                    const int j = tid + kFgThreads * i;
-                    const int kk = 8 * (j & 31);
-                    if (k0 + kk < n) {
-                        float wf[8];
-                        widen8(wr[d][i], wf);
-                        const vf4 xa = *reinterpret_cast<const vf4*>(xl + k0 + kk);
-                        const vf4 xb = *reinterpret_cast<const vf4*>(xl + k0 + kk + 4);
-                        float* dst = buf + (j >> 5) * kFgStride + kk;
-                        *reinterpret_cast<vf4*>(dst) =
-                            vf4{fmul(xa.x, wf[0]), fmul(xa.y, wf[1]), fmul(xa.z, wf[2]), fmul(xa.w, wf[3])};
-                        *reinterpret_cast<vf4*>(dst + 4) =
-                            vf4{fmul(xb.x, wf[4]), fmul(xb.y, wf[5]), fmul(xb.z, wf[6]), fmul(xb.w, wf[7])};
-                    }
-                }
-            }
-            load_tile(wr[d], t + kFgDepth);
-            if (wave == 0 && lane < kFgRows && t >= 1 && t <= ntile) {
-                const int tp = t - 1;
-                const int kn = min(kFgKT, n - tp * kFgKT);   // a multiple of 32
-                acc = lds_serial_sum(reinterpret_cast<const vf4*>(P + (tp & 1) * kFgRows * kFgStride + lane * kFgStride),
-                                     kn / 32, acc);
-            }
-            __syncthreads();
-        }
-    }
     if (wave == 0) {
+        // ------------------------------------------------- chain wavefront
+        // first the input row, by LDS DMA (this wavefront has no other
+        // loads in flight): with PRO, RMSNorm (util.rs:389-426: the 8 lane
+        // chains of squares, o = w * (ss * x)) in place; then the product
+        // wavefronts may start
+        rowq_dma_f32(xl, x, n);
+        if constexpr (PRO) rowq_dma_f32(xl + rowq_row_len(n), norm_w, n);
+        wait_vm_all();
+        if constexpr (PRO) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            rowq_squares_wave(n, sq);
+            const float ss = rowq_chain(n, eps, sq);
+            const float* wl = xl + rowq_row_len(n);
+            for (int e = 8 * lane; e < n; e += 512) {
+                vf4* xv = reinterpret_cast<vf4*>(xl + e);
+                const vf4* wv = reinterpret_cast<const vf4*>(wl + e);
+                const vf4 a = xv[0], b = xv[1], wa = wv[0], wb = wv[1];
+                xv[0] = vf4{fmul(wa.x, fmul(ss, a.x)), fmul(wa.y, fmul(ss, a.y)), fmul(wa.z, fmul(ss, a.z)),
+                            fmul(wa.w, fmul(ss, a.w))};
+                xv[1] = vf4{fmul(wb.x, fmul(ss, b.x)), fmul(wb.y, fmul(ss, b.y)), fmul(wb.z, fmul(ss, b.z)),
+                            fmul(wb.w, fmul(ss, b.w))};
+            }
+        }
+        lds_arrive(ctr + 5);
+
+        // tiles t < ready are known filled: the least of the product
+        // wavefronts' counts
+        auto refresh = [&](int t) {
+            for (int it = 0; it < (1 << 22); it++) {
+                int c[PW];
+#pragma unroll
+                for (int k = 0; k < PW; k++)
+                    c[k] = __builtin_amdgcn_readfirstlane(
+                        __hip_atomic_load(ctr + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                int r = c[0];
+#pragma unroll
+                for (int k = 1; k < PW; k++) r = min(r, c[k]);
+                if (r > t) return r;
+            }
+            if (fault && lane == 0) __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            return ntile;
+        };
+        // lanes past R re-read row R - 1 (unused)
+        const int myrow = lane < R ? lane : R - 1;
+        float acc = 0.0f;
+        vf4 ra[16], rb[16];
+        int ready = refresh(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        fg_read_row<R>(ra, P, 0, myrow);
+        // two tiles per trip: ra holds tile t, rb is read with tile t + 1
+        // (or tile t again past the end: every read is unconditional), and
+        // the scheduling barriers keep each tile's reads ahead of the
+        // previous tile's adds
+        for (int t = 0; t < ntile; t += 2) {
+            const int t1 = t + 1 < ntile ? t + 1 : t;
+            if (t1 >= ready) ready = refresh(t1);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            fg_read_row<R>(rb, P, t1 % SL, myrow);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = fg_add_row(acc, ra, min(kFgKT, n - t * kFgKT));
+            if (t + 1 >= ntile) {
+                lds_arrive_nowait(ctr + 4);
+                break;
+            }
+            const int t2 = t + 2 < ntile ? t + 2 : t + 1;
+            if (t2 >= ready) ready = refresh(t2);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            fg_read_row<R>(ra, P, t2 % SL, myrow);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = fg_add_row(acc, rb, min(kFgKT, n - (t + 1) * kFgKT));
+            // tiles t and t + 1 consumed (one count per two tiles)
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane == 0) __hip_atomic_fetch_add(ctr + 4, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        }
+        const int row = row0 + lane;
         if constexpr (EPI == 2) {
             const float u = __shfl_down(acc, kFgPairRows, 64);
             if (lane < kFgPairRows) {
                 const float den = fadd(1.0f, expf_rn(-acc));
                 out[blockIdx.x * kFgPairRows + lane] = fmul(acc / den, u);
             }
-        } else if (lane < kFgRows) {
-            float* dst = out + row0 + lane;
+        } else if (lane < R && row < o) {
+            float* dst = out + row;
             *dst = EPI == 0 ? acc : fadd(*dst, acc);
+        }
+    } else {
+        // ----------------------------------------------- product wavefronts
+        // product lane p (0 .. 64 PW - 1) takes chunks j = p + 64 PW i of
+        // each tile: row j / 8, columns 8 (j % 8) .. +8 of the tile.  All of
+        // a lane's chunks share its 8 columns, so one pair of x reads serves
+        // them; chunk i exists for the wavefronts with PW i + pw < R / 8 (a
+        // uniform branch), and the others' loads re-read chunk 8R - 1 (one
+        // address per wavefront).  Every load is issued unconditionally
+        // (tiles past the last and columns past n re-read in range), so the
+        // compiler's wait counts stay exact: a tile's products wait only for
+        // that tile's loads.  In a last tile of 32 columns, lanes past n
+        // compute products the chain never reads (their x reads stay inside
+        // the row's rounded LDS region).
+        const int p = tid - 64, pw = wave - 1;
+        const int kk = 8 * (p & 7);
+        const int r0 = p >> 3;   // row of chunk 0; chunk i is 8 PW i rows further
+        uint4 wr[D][CPL];
+        auto load_tile = [&](uint4 (&dst)[CPL], int t) {
+            const int k0 = min(t, ntile - 1) * kFgKT;
+#pragma unroll
+            for (int i = 0; i < CPL; i++) {
+                const int j = min(p + 64 * PW * i, 8 * R - 1);
+                const int k = min(k0 + 8 * (j & 7), n - 8);
+                dst[i] = *reinterpret_cast<const uint4*>(w + (size_t)min(row0 + (j >> 3), o - 1) * n + k);
+            }
+        };
+        // iteration t: (once slot t % SL is free) the products of tile t into
+        // it, then the loads of tile t + D into the registers tile t used.
+        // The trip count is padded to whole rings of D.
+        const int nit = (ntile + D - 1) / D * D;
+#pragma unroll
+        for (int d = 0; d < D; d++) load_tile(wr[d], d);
+        lds_wait_count(ctr + 5, 1, fault);   // the input row
+        int seen = 0;                        // tiles consumed, as last read
+        // the lane's 8 activations of tile t, read one tile ahead (two sets,
+        // alternating with d; D is even); reads past the row's last tile
+        // stay inside its rounded LDS region
+        static_assert(D % 2 == 0, "x register sets alternate");
+        vf4 xr[2][2];
+        xr[0][0] = *reinterpret_cast<const vf4*>(xl + kk);
+        xr[0][1] = *reinterpret_cast<const vf4*>(xl + kk + 4);
+        for (int t0 = 0; t0 < nit; t0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const int t = t0 + d;
+                if (t < ntile) {
+                    if (t >= SL && seen < t - SL + 1) seen = lds_wait_count(ctr + 4, t - SL + 1, fault);
+                    const int tn = min(t + 1, ntile - 1);
+                    xr[(d + 1) & 1][0] = *reinterpret_cast<const vf4*>(xl + tn * kFgKT + kk);
+                    xr[(d + 1) & 1][1] = *reinterpret_cast<const vf4*>(xl + tn * kFgKT + kk + 4);
+                    const vf4 xa = xr[d & 1][0], xb = xr[d & 1][1];
+                    float* dst = P + (t % SL) * SF + r0 * kFgStride + kk;
+#pragma unroll
+                    for (int i = 0; i < CPL; i++) {
+                        if (PW * i + pw < R / 8) {
+                            const uint4 c = wr[d][i];
+                            float* q = dst + i * 8 * PW * kFgStride;
+                            *reinterpret_cast<vf4*>(q) =
+                                vf4{f16_prod(c.x & 0xffffu, xa.x), f16_prod(c.x >> 16, xa.y),
+                                    f16_prod(c.y & 0xffffu, xa.z), f16_prod(c.y >> 16, xa.w)};
+                            *reinterpret_cast<vf4*>(q + 4) =
+                                vf4{f16_prod(c.z & 0xffffu, xb.x), f16_prod(c.z >> 16, xb.y),
+                                    f16_prod(c.w & 0xffffu, xb.z), f16_prod(c.w >> 16, xb.w)};
+                        }
+                    }
+                    lds_arrive_nowait(ctr + pw);
+                }
+                load_tile(wr[d], t + D);
+            }
         }
     }
 }
 
-// SwiGLU of a batched gate/up product in the pair layout (rows c, c + 8 of
-// each 16-row block): raw [batch][2 * hidden] -> h [batch][hidden].
+// SwiGLU of a batched gate/up product in the pair layout (rows c, c + 32 of
+// each 64-row block): raw [batch][2 * hidden] -> h [batch][hidden].
 __global__ void k_swiglu_pairs(const float* __restrict__ raw, int hidden, float* __restrict__ h) {
     const int t = blockIdx.y;
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= hidden) return;
-    const float* r = raw + (size_t)t * 2 * hidden + (size_t)(c / kFgPairRows) * kFgRows + c % kFgPairRows;
+    const float* r = raw + (size_t)t * 2 * hidden + (size_t)(c / kFgPairRows) * (2 * kFgPairRows) + c % kFgPairRows;
     const float g = r[0], u = r[kFgPairRows];
     const float den = fadd(1.0f, expf_rn(-g));
     h[(size_t)t * hidden + c] = fmul(g / den, u);
@@ -310,19 +409,19 @@ __global__ void k_qkv_f16(const float* __restrict__ raw, const float* __restrict
 hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, int batch, float* out, int out_ld,
                              int epi, hipStream_t s) {
     if (n % 32 || n <= 0 || o <= 0 || batch <= 0 || epi < 0 || epi > 1) return hipErrorInvalidValue;
-    if (batch == 1 && o % kFgRows == 0) return launch_f16_gemv(w, n, o, x, nullptr, 0.0f, epi, out, s);
+    if (batch == 1) return launch_f16_gemv(w, n, o, x, nullptr, 0.0f, epi, out, s);
     const int rb = (o + kF16Rows - 1) / kF16Rows;
     auto k = epi == 0 ? k_matmul_f16_batch<0> : k_matmul_f16_batch<1>;
     hipLaunchKernelGGL(k, dim3(rb, (batch + kF16Tok - 1) / kF16Tok), dim3(256), 0, s, w, n, o, x, batch, out, out_ld);
     return hipGetLastError();
 }
 
-template <int PRO, int EPI>
+template <int PRO, int EPI, int R>
 static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps,
                             float* out, hipStream_t s) {
-    const size_t lds = fg_lds_floats(n, PRO) * sizeof(float);
+    const size_t lds = fg_lds_floats(n, PRO, R) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    auto k = k_f16_gemv<PRO, EPI>;
+    auto k = k_f16_gemv<PRO, EPI, R>;
     static bool raised = false;
     if (lds > 65536 && !raised) {
         const hipError_t e =
@@ -330,21 +429,37 @@ static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, con
         if (e != hipSuccess) return e;
         raised = true;
     }
-    hipLaunchKernelGGL(k, dim3(o / kFgRows), dim3(kFgThreads), lds, s, w, n, o, x, norm_w, eps, out);
+    hipLaunchKernelGGL(k, dim3((o + R - 1) / R), dim3(FgShape<R>::threads), lds, s, w, n, o, x, norm_w, eps, out,
+                       wait_fault_word(false));
     return hipGetLastError();
+}
+
+// rows per workgroup: the fewest of 8, 16, 32, 64 that keep the grid within
+// one workgroup per CU (a second chain wavefront on a CU can share a SIMD
+// with the first and halve both)
+template <int PRO, int EPI>
+static hipError_t launch_fg_rows(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps,
+                                 float* out, hipStream_t s) {
+    if (o <= 256 * 8) return launch_fg<PRO, EPI, 8>(w, n, o, x, norm_w, eps, out, s);
+    if (o <= 256 * 16) return launch_fg<PRO, EPI, 16>(w, n, o, x, norm_w, eps, out, s);
+    if (o <= 256 * 32) return launch_fg<PRO, EPI, 32>(w, n, o, x, norm_w, eps, out, s);
+    return launch_fg<PRO, EPI, 64>(w, n, o, x, norm_w, eps, out, s);
 }
 
 hipError_t launch_f16_gemv(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps, int epi,
                            float* out, hipStream_t s) {
-    if (n % 32 || n <= 0 || o <= 0 || o % kFgRows || epi < 0 || epi > 2) return hipErrorInvalidValue;
+    if (n % 32 || n <= 0 || o <= 0 || epi < 0 || epi > 2 || (epi == 2 && o % (2 * kFgPairRows)))
+        return hipErrorInvalidValue;
+    if (epi == 2) {
+        if (norm_w) return launch_fg<1, 2, 64>(w, n, o, x, norm_w, eps, out, s);
+        return launch_fg<0, 2, 64>(w, n, o, x, norm_w, eps, out, s);
+    }
     if (norm_w) {
-        if (epi == 0) return launch_fg<1, 0>(w, n, o, x, norm_w, eps, out, s);
-        if (epi == 2) return launch_fg<1, 2>(w, n, o, x, norm_w, eps, out, s);
+        if (epi == 0) return launch_fg_rows<1, 0>(w, n, o, x, norm_w, eps, out, s);
         return hipErrorInvalidValue;
     }
-    if (epi == 0) return launch_fg<0, 0>(w, n, o, x, norm_w, eps, out, s);
-    if (epi == 1) return launch_fg<0, 1>(w, n, o, x, norm_w, eps, out, s);
-    return launch_fg<0, 2>(w, n, o, x, norm_w, eps, out, s);
+    if (epi == 0) return launch_fg_rows<0, 0>(w, n, o, x, norm_w, eps, out, s);
+    return launch_fg_rows<0, 1>(w, n, o, x, norm_w, eps, out, s);
 }
 
 hipError_t launch_swiglu_pairs(const float* raw, int hidden, int batch, float* h, hipStream_t s) {

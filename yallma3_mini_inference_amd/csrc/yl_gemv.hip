@@ -174,28 +174,6 @@ __host__ __device__ inline GemvLds gemv_lds(int n, int nb, int R, bool norm) {
     return l;
 }
 
-// Hand-offs between wavefronts of one workgroup through LDS counters
-// (relaxed atomics: a volatile LDS access would make the compiler wait for
-// every outstanding global load first).  LDS serves one wavefront's
-// accesses in order, and a waiter's reads of the published data are issued
-// only after it saw the count.  The waits are bounded: the counted
-// wavefronts always arrive within microseconds, the bound only keeps a
-// defect from hanging the device; a wait that gives up sets *fault, which the
-// host reads after the call and reports as an error.
-__device__ __forceinline__ void lds_arrive(int* ctr) {
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's LDS writes done
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void lds_wait_count(int* ctr, int target, unsigned* fault) {
-    int i = 0;
-    for (; __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target && i < (1 << 22); i++)
-        __builtin_amdgcn_s_sleep(1);
-    if (i == (1 << 22) && fault && (threadIdx.x & 63) == 0)
-        __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // `bytes` bytes from global memory into LDS by LDS DMA: EB bytes per lane
 // (16 or 4), 64*EB bytes per instruction.  `bytes` is a multiple of EB and
 // src is EB-aligned; lanes past the end re-read the last EB bytes into the

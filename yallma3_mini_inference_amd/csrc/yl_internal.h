@@ -36,6 +36,10 @@ enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs
 // (QMat::sf: lm.rs and safetensors Q8 with group size 32); activations and
 // results as for kQ8.
 constexpr int kQ8S = 3;
+// F16 gate/up matrices interleave blocks of this many gate rows with the
+// same up rows (the SwiGLU tiles of the F16 GEMV: 32 + 32 rows); the gate
+// and up row counts are multiples of 32.
+constexpr int kF16PairRows = 32;
 
 // The column of stored row c of a q or k projection whose heads (hd a
 // power of two) hold their rows in the order 0, h, 1, h+1, ..., h-1, 2h-1

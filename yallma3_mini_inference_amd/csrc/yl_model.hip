@@ -99,18 +99,18 @@ struct HostQMat {
 };
 
 // F16 gate and up rows in the pairs the one-token F16 GEMV's SwiGLU epilogue
-// reads: blocks of 16 rows, 8 gate rows then the same 8 up rows.
+// reads: blocks of 64 rows, 32 gate rows then the same 32 up rows.
 static void f16_pair_rows(const uint16_t* gate, const uint16_t* up, size_t o, size_t n, HostQMat* out) {
     out->fmt = kF16;
     out->o = 2 * o;
     out->n = n;
     out->qs.resize(2 * o * n * 2);
     uint16_t* dst = reinterpret_cast<uint16_t*>(out->qs.data());
-    for (size_t r0 = 0; r0 < o; r0 += 8)
+    for (size_t r0 = 0; r0 < o; r0 += kF16PairRows)
         for (int k = 0; k < 2; k++) {
             const uint16_t* src = (k == 0 ? gate : up) + r0 * n;
-            memcpy(dst, src, 8 * n * 2);
-            dst += 8 * n;
+            memcpy(dst, src, kF16PairRows * n * 2);
+            dst += kF16PairRows * n;
         }
 }
 
@@ -1071,7 +1071,7 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
         if (bytes) *bytes = (uint64_t)m->att * m->dim * 2 + B * ((uint64_t)m->att * 4 + (uint64_t)m->dim * 8);
         return launch_matmul_f16((const uint16_t*)L.wo.qs, m->att, m->dim, s->attf, batch, s->x, m->dim, 1, st);
     case kOpW13:
-        // gate and up rows in pairs (8 + 8 per 16-row block), SwiGLU after
+        // gate and up rows in pairs (32 + 32 per 64-row block), SwiGLU after
         if (bytes) *bytes = 2ull * m->hidden * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)m->hidden * 4);
         if (one)
             return launch_f16_gemv((const uint16_t*)L.w13.qs, m->dim, 2 * m->hidden, s->x, L.rms_ffn, m->eps, 2, s->hf,
