@@ -180,6 +180,8 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
             if (fault && lane == 0) __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             return ntile;
         };
+        // the chain's adds go first when a product wavefront shares the SIMD
+        __builtin_amdgcn_s_setprio(3);
         // lanes past R re-read row R - 1 (unused)
         const int myrow = lane < R ? lane : R - 1;
         float acc = 0.0f;
