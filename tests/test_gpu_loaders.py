@@ -27,6 +27,9 @@ CASES = {
     "lmrs_gs192_medium": lambda d: MF.write_lmrs(d, MEDIUM, gs=192, seed=6, n_pad=600),
     "st_q8_medium": lambda d: MF.write_safetensors(d, MEDIUM, q8_gs=64, seed=7),
     "st_f16_medium": lambda d: MF.write_safetensors(d, MEDIUM, seed=8),
+    # group size 32 at dim 576: the one-token steps run the 32-block GEMV with
+    # 18 blocks per row (a partial last slot) and q/k rows in RoPE pair order
+    "lmrs_gs32_medium": lambda d: MF.write_lmrs(d, MEDIUM, gs=32, seed=9, n_pad=600),
 }
 
 
@@ -50,7 +53,8 @@ def _oracle(path, max_ctx_len=0xFFFFFFFF):
                                                     ("st_q8_gs64", 130, 3), ("st_q8_gs32_bin", 33, 5),
                                                     ("lmrs_gs32", 20, 8), ("lmrs_gs32", 64, 4),
                                                     ("lmrs_gs64", 41, 6), ("lmrs_gs192_medium", 70, 4),
-                                                    ("st_q8_medium", 50, 4), ("st_f16_medium", 45, 3)])
+                                                    ("st_q8_medium", 50, 4), ("st_f16_medium", 45, 3),
+                                                    ("lmrs_gs32_medium", 37, 5)])
 def test_model_matches_oracle(gpu, files, name, prompt_len, steps):
     import yallma3_mini_inference_amd as Y
     path = files(name)
