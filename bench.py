@@ -211,19 +211,26 @@ DECODE = {
                                    "prefilled to 8192 positions, then 256 steps"),
     "lmrs_1b": (512, 256, "Llama-3.2-1B-shaped lm.rs model (Q8, f32 scales per group of 32, HF-layout RoPE) greedy "
                           "decode, batch 1, 512-token prompt then 256 steps, KV f32 ctx 4096"),
+    "st_q8_1b": (512, 256, "Llama-3.2-1B-shaped safetensors Q8 model (f32 scales per group of 64, HF-layout RoPE) "
+                           "greedy decode, batch 1, 512-token prompt then 256 steps, KV f32 ctx 4096"),
     "st_f16_1b": (512, 256, "Llama-3.2-1B-shaped safetensors F16 model (matmul_f32, HF-layout RoPE) greedy decode, "
                             "batch 1, 512-token prompt then 256 steps, KV f32 ctx 4096"),
 }
 
 # Models of the lm.rs and safetensors formats (synth_files), and the kernel
 # that runs each GEMV class of theirs.
-FILE_CONFIGS = {"lmrs_1b", "st_f16_1b"}
+FILE_CONFIGS = {"lmrs_1b", "st_q8_1b", "st_f16_1b"}
 FILE_KERNELS = {
     "lmrs_1b": {"qkv": "k_gemv<kQ8S> (q|k|v rows with f32 block scales, q/k heads in RoPE pair order; RMSNorm "
                        "prologue, RoPE + KV-cache epilogue)",
                 "wo": "k_gemv<kQ8S> (output projection, residual add)",
                 "w13": "k_gemv<kQ8S> (32 gate + 32 up rows per workgroup, RMSNorm prologue, SwiGLU + quantize "
                        "epilogue)", "w2": "k_gemv<kQ8S> (down, residual add)"},
+    "st_q8_1b": {"qkv": "k_gemv<kQ8S64> (q|k|v rows, f32 scales per 64-group, q/k heads in RoPE pair order; "
+                        "RMSNorm + 64-group quantize prologue, RoPE + KV-cache epilogue)",
+                 "wo": "k_gemv<kQ8S64> (output projection; f32 attention row quantized in the prologue, residual add)",
+                 "w13": "k_gemv<kQ8S64> (32 gate + 32 up rows per workgroup, RMSNorm prologue, SwiGLU epilogue, "
+                        "f32 h)", "w2": "k_gemv<kQ8S64> (down; f32 h quantized in the prologue, residual add)"},
     "st_f16_1b": {"qkv": "k_f16_gemv (fused q/k/v rows, RMSNorm prologue)", "wo": "k_f16_gemv (output, residual add)",
                   "w13": "k_f16_gemv (gate/up row pairs, RMSNorm prologue, SwiGLU epilogue)",
                   "w2": "k_f16_gemv (down, residual add)"},
@@ -368,7 +375,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
     ap.add_argument("--config", default="llama32_1b", choices=sorted(DECODE),
                     help="decode workload: llama32_1b (the headline), smollm2_135m, llama3_8b_mixed, lmrs_1b "
-                         "(lm.rs Q8 with f32 group scales), st_f16_1b (safetensors F16)")
+                         "(lm.rs Q8 with f32 scales per 32), st_q8_1b (safetensors Q8 with f32 scales per 64), "
+                         "st_f16_1b (safetensors F16)")
     ap.add_argument("--attention", choices=("exact", "split"), default="exact",
                     help="decode attention: exact (the reference's operation order, bit-exact; the default) or "
                          "split over the context (equal up to rounding; on these synthetic models rounding-level "

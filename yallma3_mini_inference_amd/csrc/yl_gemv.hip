@@ -62,6 +62,8 @@ template <>
 struct WBlock<kQ4> { uint4 a; };
 template <>
 struct WBlock<kQ8S> { uint4 a, b; };
+template <>
+struct WBlock<kQ8S64> { uint4 a, b; };
 
 // The activation format of a weight format (Q8 rows with f32 block scales
 // dot against the same 32-groups as Q8_0).
@@ -73,6 +75,8 @@ template <int WF>
 struct ScaleWord { using type = uint16_t; };
 template <>
 struct ScaleWord<kQ8S> { using type = float; };
+template <>
+struct ScaleWord<kQ8S64> { using type = float; };
 
 constexpr int kBufRaw = 0x00020000;   // buffer descriptor word 3: raw 32-bit data
 
@@ -222,6 +226,30 @@ __device__ __forceinline__ float chain_slot_dpp(float acc, float term, int first
     if (valid <= 0) return acc;
     return chain_slot_part<LPR>(acc, term, valid);
 }
+// The same for 64-element groups: a group's term sits on the even lane of
+// its two blocks, so the chain reads lanes 0, 2, 4, ... (`valid` counts
+// blocks; nb is even).
+template <int LPR, int I = 0>
+__device__ __forceinline__ float chain_slot_full2(float acc, float term) {
+    if constexpr (I < LPR) return chain_slot_full2<LPR, I + 2>(add_from_lane_plus<I>(acc, term), term);
+    else return acc;
+}
+template <int LPR, int I = 0>
+__device__ __forceinline__ float chain_slot_part2(float acc, float term, int valid) {
+    if constexpr (I < LPR) {
+        if (I >= valid) return acc;
+        return chain_slot_part2<LPR, I + 2>(add_from_lane_plus<I>(acc, term), term, valid);
+    } else {
+        return acc;
+    }
+}
+template <int LPR>
+__device__ __forceinline__ float chain_slot_dpp2(float acc, float term, int first_block, int nb) {
+    const int valid = nb - first_block;   // uniform
+    if (valid >= LPR) return chain_slot_full2<LPR>(acc, term);
+    if (valid <= 0) return acc;
+    return chain_slot_part2<LPR>(acc, term, valid);
+}
 
 // Few wavefronts per SIMD: registers go to loads in flight rather than to
 // occupancy.
@@ -231,7 +259,10 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
     static_assert(LPR == 8 || LPR == 16, "a row's lanes share one 16-lane DPP row");
     constexpr int RW = 64 / LPR;          // rows per weight wavefront
     constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
-    constexpr int NA = kNorm ? kNormWaves : 1;   // activation wavefronts
+    constexpr bool kQPro = EPI == kEpiResidQ;   // an f32 input row, quantized here (no RMSNorm)
+    constexpr bool kStage = kNorm || kQPro;     // the activation row is made by NA wavefronts
+    constexpr int NA = kStage ? kNormWaves : 1;   // activation wavefronts
+    constexpr int GSZ = WF == kQ8S64 ? 64 : 32;  // activation (and weight scale) group
     const int n = a.n, nb = a.nb, o = a.o;
     const int nww = (int)(blockDim.x >> 6) - NA;
     const int R = RW * nww;
@@ -257,15 +288,16 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
 
     if (wave < NA) {
         // ---------------------------------------------- activation wavefronts
-        if constexpr (kNorm) {
-            // RMSNorm (util.rs:389-426) + quantize of the residual row,
-            // shared by the NA wavefronts: member i of the team holds the 8
-            // elements from 8*(p*team + i) in pass p
-            constexpr int MP = 2;   // dim <= 4096 = 2 passes of 256 x 8
+        if constexpr (kStage) {
+            // RMSNorm (util.rs:389-426) + quantize of the residual row (or,
+            // kQPro, quantize of the f32 input row), shared by the NA
+            // wavefronts: member i of the team holds the 8 elements from
+            // 8*(p*team + i) in pass p
+            constexpr int MP = kQPro ? 4 : 2;   // dim <= 8192 (kQPro) or 4096: passes of 256 x 8
             const int dim = n;
             const RowTeam tm{tid, 64 * NA};
             const int passes = rowq_passes(dim, 64 * NA);
-            vf4 xv[2 * MP], wv_n[2 * MP];
+            vf4 xv[2 * MP], wv_n[kNorm ? 2 * MP : 1];
             EmbRegs<EMB ? MP : 1> er_;
             bool in_vocab = true;
             // the position of the QKV epilogue, loaded first (the RoPE angles
@@ -277,10 +309,12 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                 const uint32_t tok = a.tokens[t];
                 in_vocab = tok < (uint32_t)a.emb.vocab;
                 rowq_load_emb<MP>(tm, er_, a.emb, tok, passes);
+            } else if constexpr (kQPro) {
+                rowq_load_f32<MP>(tm, xv, a.xf + (size_t)t * dim, dim, passes);
             } else {
                 rowq_load_f32<MP>(tm, xv, a.x + (size_t)t * dim, dim, passes);
             }
-            rowq_load_f32<MP>(tm, wv_n, a.norm_w, dim, passes);
+            if constexpr (kNorm) rowq_load_f32<MP>(tm, wv_n, a.norm_w, dim, passes);
             __syncthreads();
             if constexpr (EMB) {
                 // the residual stream starts as the embedding row
@@ -299,6 +333,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             // squares -> the 8 transposed chain rows (zero padded)
             float* sq = reinterpret_cast<float*>(smem + L.norm);
             const int S = rowq_stride(dim);
+            if constexpr (kNorm) {
 #pragma unroll
             for (int p = 0; p < MP; p++)
                 if (p < passes && rowq_live(tm, p, dim)) {
@@ -319,6 +354,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             }
             // the chain may start: it waits for the squares only
             lds_arrive(ctr_sq);
+            }
             // initial values of the rows' sums: the K/V `+=` columns start
             // from the cache (forward.rs:166-169, weight_type.rs:190-201),
             // published with the activation row (ctr_row) while the chain runs
@@ -351,38 +387,45 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                 }
             }
             // the serial sum of squares (wavefront 0, lanes 0-7) -> ss
-            if (wave == 0) {
-                lds_wait_count(ctr_sq, NA, a.fault);
-                const float ss = rowq_chain(dim, a.eps, sq);
-                if (lane == 0) *ssl = ss;
-                lds_arrive(ctr_ss);
+            float ss = 1.0f;
+            if constexpr (kNorm) {
+                if (wave == 0) {
+                    lds_wait_count(ctr_sq, NA, a.fault);
+                    const float s0 = rowq_chain(dim, a.eps, sq);
+                    if (lane == 0) *ssl = s0;
+                    lds_arrive(ctr_ss);
+                }
+                lds_wait_count(ctr_ss, 1, a.fault);
+                ss = *ssl;
             }
-            lds_wait_count(ctr_ss, 1, a.fault);
-            const float ss = *ssl;
-            // o = w * (ss * x) and the 32-group quantization of the member's
-            // slices (the 4 lanes of a quad hold one 32-group)
+            // o = w * (ss * x) and the GSZ-group quantization of the
+            // member's slices (the 4 lanes of a quad hold one 32-group, 8
+            // consecutive lanes one 64-group)
 #pragma unroll
             for (int p = 0; p < MP; p++)
                 if (p < passes && rowq_live(tm, p, dim)) {
                     const int e = rowq_elem(tm, p, dim);
-                    const vf4 x0 = xv[2 * p], x1 = xv[2 * p + 1], w0 = wv_n[2 * p], w1 = wv_n[2 * p + 1];
+                    const vf4 x0 = xv[2 * p], x1 = xv[2 * p + 1];
                     float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                    const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
                     float am = 0.0f;
+                    if constexpr (kNorm) {
+                        const vf4 w0 = wv_n[2 * p], w1 = wv_n[2 * p + 1];
+                        const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        v[k] = fmul(w8[k], fmul(ss, v[k]));
-                        am = fmaxf(am, fabsf(v[k]));
+                        for (int k = 0; k < 8; k++) v[k] = fmul(w8[k], fmul(ss, v[k]));
                     }
+#pragma unroll
+                    for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(v[k]));
                     am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
                     am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
+                    if constexpr (GSZ == 64) am = fmaxf(am, __shfl_xor(am, 4, 64));
                     const float sc = group_scale<act_fmt<WF>()>(am);
                     int q[8];
                     quant8<act_fmt<WF>()>(v, sc, q);
                     *reinterpret_cast<uint2*>(xl + e) =
                         WF == kQ4 ? make_uint2(pack4(q[0], q[2], q[4], q[6]), pack4(q[1], q[3], q[5], q[7]))
                                   : make_uint2(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]));
-                    if ((tid & 3) == 0) xsl[e >> 5] = sc;
+                    if ((tid & (GSZ / 8 - 1)) == 0) xsl[e / GSZ] = sc;
                 }
             lds_arrive(ctr_row);
         } else {
@@ -421,11 +464,14 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         // descriptors over this wavefront's rows: rows past the matrix read 0
         const __amdgpu_buffer_rsrc_t qr =
             uniform_rsrc(a.qs + (size_t)min(wrow0, o - 1) * row_bytes, (int)(rows_here * row_bytes));
-        const void* scale_rows = WF == kQ8S ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nb)
-                                            : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
-        const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(scale_rows, rows_here * nb * kScaleBytes);
+        // scales per row: one per block, or one per block pair (kQ8S64)
+        constexpr int kBlocksPerScale = WF == kQ8S64 ? 2 : 1;
+        const int nsc = nb / kBlocksPerScale;
+        const void* scale_rows = WF == kQ8S || WF == kQ8S64 ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nsc)
+                                                            : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
+        const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(scale_rows, rows_here * nsc * kScaleBytes);
         const int qv = (int)(r * row_bytes) + j * kBlockBytes;
-        const int dv_off = (r * nb + j) * kScaleBytes;
+        const int dv_off = (r * nsc + j / kBlocksPerScale) * kScaleBytes;
         // Slot by slot (loads complete in issue order, so slot k's wait
         // leaves the later slots in flight; the scheduling barriers keep the
         // compiler from regrouping them).  LA slots go out first, then slot
@@ -438,9 +484,10 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         SW dv[LA];
         auto issue = [&](int k) {
             load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
-            if constexpr (WF == kQ8S)
+            if constexpr (WF == kQ8S || WF == kQ8S64)
                 dv[k % LA] = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(dr, dv_off, k * LPR * kScaleBytes, kPolStream));
+                    float, __builtin_amdgcn_raw_buffer_load_b32(dr, dv_off, k * (LPR / kBlocksPerScale) * kScaleBytes,
+                                                                kPolStream));
             else
                 dv[k % LA] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(dr, dv_off, k * LPR * 2, kPolStream);
             __builtin_amdgcn_sched_barrier(0);
@@ -453,7 +500,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         const int my_row = wrow0 + my_r;
         // epilogue operand of the residual add (needed only at the end)
         float resid = 0.0f;
-        if constexpr (EPI == kEpiResid) resid = a.x[(size_t)t * o + min(my_row, o - 1)];
+        if constexpr (EPI == kEpiResid || EPI == kEpiResidQ) resid = a.x[(size_t)t * o + min(my_row, o - 1)];
         __builtin_amdgcn_sched_barrier(0);
 
         lds_wait_count(ctr_row, NA, a.fault);
@@ -463,12 +510,21 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             // exact block dot -> f32 term
             const int b = k * LPR + j;
             const int bb = b < nb ? b : nb - 1;
-            const int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
+            int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
             float ws;
-            if constexpr (WF == kQ8S) ws = dv[k % LA];
+            if constexpr (WF == kQ8S || WF == kQ8S64) ws = dv[k % LA];
             else ws = f16_to_f32(dv[k % LA]);
-            const float term = fmul(fmul((float)isum, ws), xsl[bb]);
-            acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
+            if constexpr (WF == kQ8S64) {
+                // the group's exact int32 dot: this block's plus the next
+                // lane's (row_shl:1; read on the even lanes, which own the
+                // groups), then its one term ((float)isum * w_scale) * x_scale
+                isum += __builtin_amdgcn_update_dpp(0, isum, 0x101, 0xF, 0xF, true);
+                const float term = fmul(fmul((float)isum, ws), xsl[bb >> 1]);
+                acc = chain_slot_dpp2<LPR>(acc, term, k * LPR, nb);
+            } else {
+                const float term = fmul(fmul((float)isum, ws), xsl[bb]);
+                acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
+            }
             if (k + LA < PPL) issue(k + LA);
         }
 
@@ -476,7 +532,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         const bool live = chain_lane && my_row < o;
         if constexpr (EPI == kEpiStore) {
             if (live) a.out[(size_t)t * o + my_row] = acc;
-        } else if constexpr (EPI == kEpiResid) {
+        } else if constexpr (EPI == kEpiResid || EPI == kEpiResidQ) {
             // residual add (forward.rs:196-204 / 245-253)
             if (live) a.x[(size_t)t * o + my_row] = fadd(resid, acc);
         } else if constexpr (EPI == kEpiQkvRope) {
@@ -523,6 +579,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             const int grp = blockIdx.x;
             const size_t base = (size_t)t * a.hidden + (size_t)grp * kGroup;
             if (a.h_f32) a.h_f32[base + lane] = h;
+            if (!a.hq) return;   // f32 h only (the down projection quantizes it in 64-groups)
             float am = group_max(fabsf(h), 32);   // lanes 0-31 (rows 0 and 1) all active
             am = fmaxf(am, 0.0f);
             const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
@@ -572,7 +629,7 @@ static bool plan_gemv(int o, int nb, int epi, GemvPlan* p) {
 template <int WF, int EPI, bool EMB, int LPR, int PPL>
 static hipError_t launch_k(const GemvArgs& a, int nww, int batch, hipStream_t st) {
     constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
-    constexpr int NA = kNorm ? kNormWaves : 1;
+    constexpr int NA = kNorm || EPI == kEpiResidQ ? kNormWaves : 1;
     const int R = (64 / LPR) * nww;
     const GemvLds L = gemv_lds(a.n, a.nb, R, kNorm);
     if (L.total > 160 * 1024) return hipErrorInvalidValue;
@@ -624,18 +681,26 @@ static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t s
         return launch_plan<WF, kEpiQkvRope, false>(a, p, batch, st);
     case kEpiResid: return launch_plan<WF, kEpiResid, false>(a, p, batch, st);
     case kEpiSwiglu: return launch_plan<WF, kEpiSwiglu, false>(a, p, batch, st);
+    case kEpiResidQ:
+        if constexpr (WF == kQ8S64) return launch_plan<WF, kEpiResidQ, false>(a, p, batch, st);
+        return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipStream_t s) {
     if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (args.n % 32 || args.n > 4096)) return hipErrorInvalidValue;
+    if (epi == kEpiResidQ && (args.n > 8192 || !args.xf)) return hipErrorInvalidValue;
+    // kQ8S64 activations are quantized in 64-groups by the kernel's own prologue
+    if (wfmt == kQ8S64 && (args.n % 64 || args.nb != args.n / 32 || epi == kEpiResid || epi == kEpiStore))
+        return hipErrorInvalidValue;
     if (args.n % 32 || args.n > 16384 || args.o <= 0) return hipErrorInvalidValue;
     GemvArgs a = args;
     a.fault = wait_fault_word(false);
     if (wfmt == kQ8) return launch_wf<kQ8>(a, epi, batch, s);
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);
     if (wfmt == kQ8S) return launch_wf<kQ8S>(a, epi, batch, s);
+    if (wfmt == kQ8S64) return launch_wf<kQ8S64>(a, epi, batch, s);
     return hipErrorInvalidValue;
 }
 

@@ -36,6 +36,10 @@ enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs
 // (QMat::sf: lm.rs and safetensors Q8 with group size 32); activations and
 // results as for kQ8.
 constexpr int kQ8S = 3;
+// The same with one f32 scale per group of 64 elements (two 32-blocks):
+// activations are quantized in 64-groups, and a group's two block dots are
+// added as integers before its one f32 term.
+constexpr int kQ8S64 = 4;
 // F16 gate/up matrices interleave blocks of this many gate rows with the
 // same up rows (the SwiGLU tiles of the F16 GEMV: 32 + 32 rows); the gate
 // and up row counts are multiples of 32.
@@ -103,13 +107,15 @@ enum Epi : int {
     kEpiQkvRope = 1,  // rows [q | k | v]: q stored, k/v accumulate into the cache, RoPE on q,k
                       // (prologue: RMSNorm + quantize of the residual stream)
     kEpiResid = 2,    // x[r] += sum (residual add)
-    kEpiSwiglu = 3,   // 64-row groups [32 gate | 32 up] -> SwiGLU -> quantize one 32-block
+    kEpiSwiglu = 3,   // 64-row groups [32 gate | 32 up] -> SwiGLU -> quantize one 32-block (or f32 h only)
+    kEpiResidQ = 4,   // as kEpiResid, the input an f32 row xf that the prologue quantizes
 };
 
 struct GemvArgs {
     // weights and activations
     const uint8_t* qs; const uint16_t* d; int n, o, nb;
-    const float* sf;                           // kQ8S: f32 block scales [o][nb] (d unused)
+    const float* sf;                           // kQ8S: f32 block scales [o][nb]; kQ8S64: [o][nb / 2] (d unused)
+    const float* xf;                           // kEpiResidQ: f32 input rows [batch][n]
     const int8_t* xq; const float* xs;        // [batch][n], [batch][nb] (staged prologue)
     // kEpiQkvRope / kEpiSwiglu prologue: RMSNorm + quantize of x [batch][n]
     float* x; const float* norm_w; float eps;

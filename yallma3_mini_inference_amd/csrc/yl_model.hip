@@ -323,7 +323,7 @@ struct yl_model {
     int gs = 32;
     int hf_rope = 0;            // 1: util::rope pairs (j, j + head/2); 0: rope_gguf pairs (2j, 2j + 1)
     int pair_rows = 16;         // q8g: gate/up rows per interleaved block of w13 (16, or 32 with q8_gemv)
-    bool q8_gemv = false;       // q8g with group size 32: one-token steps on the GGUF path's GEMVs (kQ8S)
+    bool q8_gemv = false;       // q8g with group size 32 or 64: one-token steps on the GGUF path's GEMVs (kQ8S, kQ8S64)
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
     std::vector<std::string> vocab_str;
@@ -683,7 +683,7 @@ static bool upload_hostmat(const HostMat& h, QMat* m, std::string* err) {
         }
         return true;
     }
-    m->fmt = kQ8; m->nb = (int)(h.n / h.gs); m->gs = h.gs;
+    m->fmt = kQ8; m->nb = (int)(h.n / 32); m->gs = h.gs;   // nb: 32-blocks (scales: n / gs per row)
     if (hipMalloc(&m->qs, h.q.size() + 256) != hipSuccess || hipMalloc(&m->sf, h.s.size() * 4 + 256) != hipSuccess ||
         hipMemcpy(m->qs, h.q.data(), h.q.size(), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(m->sf, h.s.data(), h.s.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
@@ -707,9 +707,12 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
     m->f16 = h.f16;
     m->q8g = !h.f16;
     m->gs = h.gs;
-    // group size 32 (rows up to the GEMV's limits): one-token steps run the
-    // 32-block GEMV (kQ8S), whose SwiGLU tiles are 32 gate + 32 up rows
-    m->q8_gemv = m->q8g && m->gs == 32 && m->dim <= 4096 && m->att <= 16384 && m->hidden <= 16384;
+    // group size 32 or 64 (rows up to the GEMV's limits): one-token steps run
+    // the 32-block GEMV (kQ8S / kQ8S64), whose SwiGLU tiles are 32 gate + 32
+    // up rows
+    m->q8_gemv = m->q8g && m->dim <= 4096 &&
+                 ((m->gs == 32 && m->att <= 16384 && m->hidden <= 16384) ||
+                  (m->gs == 64 && m->att <= 8192 && m->hidden <= 8192));
     m->pair_rows = m->q8_gemv ? 32 : 16;
     if (m->n_kv <= 0 || m->n_heads % m->n_kv || (m->hd != 32 && m->hd != 64 && m->hd != 128) || m->dim % 32 ||
         m->hidden % 32 || m->att % 32 || m->kv % 32 || m->ctx <= 0 || m->dim > 8192 ||
@@ -859,9 +862,10 @@ bool session_grow(yl_session* s, int batch) {
     return true;
 }
 
-// The GEMV weight format of a matrix: its own, or kQ8S for Q8 rows with f32
-// scales (which reach the GEMV with group size 32 only: yl_model::q8_gemv).
-static int gemv_fmt(const QMat& w) { return w.sf ? kQ8S : w.fmt; }
+// The GEMV weight format of a matrix: its own, or kQ8S / kQ8S64 for Q8 rows
+// with f32 scales (which reach the GEMV with group size 32 or 64 only:
+// yl_model::q8_gemv).
+static int gemv_fmt(const QMat& w) { return w.sf ? (w.gs == 64 ? kQ8S64 : kQ8S) : w.fmt; }
 
 uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
     return (uint64_t)w.bytes() + (uint64_t)batch * ((uint64_t)w.n + (uint64_t)w.nb * 4 + (uint64_t)out_elems * 4);
@@ -928,6 +932,8 @@ hipError_t enqueue_op_gemm(const yl_model* m, yl_session* s, int cls, int l, int
 // (device) and whose first position is st->pos (device), on s->stream.
 // `bytes` (nullable) receives the algorithmic bytes the launch reads and
 // writes.
+static hipError_t enqueue_attn_f32(const yl_model* m, yl_session* s, int batch, float* kc, float* vc);
+
 hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok, int advance,
                       uint64_t* bytes, bool prologue = true) {
     hipStream_t st = s->stream;
@@ -941,6 +947,10 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     const Layer& L = m->layers[l];
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
+    // f32-scaled Q8 with 64-groups: attention and SwiGLU hand over f32 rows,
+    // which the Wo and down GEMVs quantize (a 64-group spans two of the
+    // producers' 32-wide workgroups)
+    const bool f32_act = m->q8g && m->gs == 64;
     if (batch >= kGemmMinTokens && cls != kOpAttn) {
         hipError_t e = enqueue_op_gemm(m, s, cls, l, batch, tok, kc, vc, bytes, prologue);
         if (e != hipErrorNotSupported) return e;
@@ -968,6 +978,8 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         if (bytes)
             *bytes = 2ull * s->prof_seq * (uint64_t)m->kv * 4 +
                      (uint64_t)batch * ((uint64_t)m->att * 4 + (uint64_t)m->att + (uint64_t)m->att / 8);
+        if (f32_act && batch == 1)   // f32 output: the Wo GEMV quantizes it in 64-groups
+            return enqueue_attn_f32(m, s, batch, kc, vc);
         if (batch == 1 && s->attn_mode == YL_ATTN_SPLIT)
             return launch_attn_split(s->sq, kc, vc, s->st, m->kv_ld, m->n_heads, m->n_kv, m->hd, m->attn_scale,
                                      L.wo.fmt, s->aq, s->as_, nullptr, s->split, st);
@@ -984,12 +996,19 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         a.qs = L.wo.qs; a.d = L.wo.d; a.sf = L.wo.sf; a.n = L.wo.n; a.o = L.wo.o; a.nb = L.wo.nb;
         a.xq = s->aq; a.xs = s->as_; a.x = s->x;
         if (bytes) *bytes = gemv_bytes(L.wo, L.wo.o, batch);
+        if (f32_act) {
+            a.xf = s->attf;
+            return launch_gemv(a, gemv_fmt(L.wo), kEpiResidQ, batch, st);
+        }
         return launch_gemv(a, gemv_fmt(L.wo), kEpiResid, batch, st);
     case kOpW13:
         // RMSNorm + quantize (prologue) -> W1, W3 -> SwiGLU -> quantize
         a.qs = L.w13.qs; a.d = L.w13.d; a.sf = L.w13.sf; a.n = L.w13.n; a.o = L.w13.o; a.nb = L.w13.nb;
         a.x = s->x; a.norm_w = L.rms_ffn; a.eps = m->eps;
         a.hq = s->hq; a.hs = s->hs; a.h_f32 = nullptr; a.hidden = m->hidden; a.h_fmt = L.w2.fmt;
+        if (f32_act) {   // f32 h: the down GEMV quantizes it in 64-groups
+            a.hq = nullptr; a.hs = nullptr; a.h_f32 = s->hf;
+        }
         if (bytes) *bytes = gemv_bytes(L.w13, m->hidden / 4 + m->hidden / 32, batch);
         return launch_gemv(a, gemv_fmt(L.w13), kEpiSwiglu, batch, st);
     case kOpW2:
@@ -997,6 +1016,10 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
         a.qs = L.w2.qs; a.d = L.w2.d; a.sf = L.w2.sf; a.n = L.w2.n; a.o = L.w2.o; a.nb = L.w2.nb;
         a.xq = s->hq; a.xs = s->hs; a.x = s->x;
         if (bytes) *bytes = gemv_bytes(L.w2, L.w2.o, batch);
+        if (f32_act) {
+            a.xf = s->hf;
+            return launch_gemv(a, gemv_fmt(L.w2), kEpiResidQ, batch, st);
+        }
         return launch_gemv(a, gemv_fmt(L.w2), kEpiResid, batch, st);
     default:
         return hipErrorInvalidValue;

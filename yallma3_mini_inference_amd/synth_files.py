@@ -259,13 +259,19 @@ def write_lmrs(d: str, s: Shape, gs: int = 32, seed: int = 0, n_pad: int = 0, vo
 
 def ensure(name: str, root: str | None = None) -> str:
     """A cached Llama-3.2-1B-shaped model directory: "lmrs_1b" (lm.rs, Q8,
-    group size 32) or "st_f16_1b" (safetensors, F16); returns the model path."""
+    group size 32), "st_q8_1b" (safetensors Q8, group size 64, the MLX 8-bit
+    default) or "st_f16_1b" (safetensors, F16); returns the model path."""
     from .synth import model_dir
     d = os.path.join(root or model_dir(), name)
     if name == "lmrs_1b":
         path = os.path.join(d, "model.lmrs")
         if not os.path.exists(path):
             write_lmrs(d, LLAMA32_1B, gs=32, seed=11, vocab=LLAMA32_1B_VOCAB)
+        return path
+    if name == "st_q8_1b":
+        path = os.path.join(d, "model.safetensors")
+        if not os.path.exists(path):
+            write_safetensors(d, LLAMA32_1B, vocab=LLAMA32_1B_VOCAB, q8_gs=64, seed=13)
         return path
     if name == "st_f16_1b":
         path = os.path.join(d, "model.safetensors")
