@@ -30,6 +30,12 @@ CASES = {
     # group size 32 at dim 576: the one-token steps run the 32-block GEMV with
     # 18 blocks per row (a partial last slot) and q/k rows in RoPE pair order
     "lmrs_gs32_medium": lambda d: MF.write_lmrs(d, MEDIUM, gs=32, seed=9, n_pad=600),
+    # group size 128: four blocks per group on the GEMV (and the tile kernel
+    # for prompts)
+    "lmrs_gs128": lambda d: MF.write_lmrs(d, MF.Shape(), gs=128, seed=10),
+    "st_q8_gs128_medium": lambda d: MF.write_safetensors(d, MF.Shape(dim=512, hidden=1536, n_layers=2, n_heads=8,
+                                                                     n_kv=2, head_dim=64, ctx=512),
+                                                         q8_gs=128, seed=11),
 }
 
 
@@ -54,7 +60,8 @@ def _oracle(path, max_ctx_len=0xFFFFFFFF):
                                                     ("lmrs_gs32", 20, 8), ("lmrs_gs32", 64, 4),
                                                     ("lmrs_gs64", 41, 6), ("lmrs_gs192_medium", 70, 4),
                                                     ("st_q8_medium", 50, 4), ("st_f16_medium", 45, 3),
-                                                    ("lmrs_gs32_medium", 37, 5)])
+                                                    ("lmrs_gs32_medium", 37, 5), ("lmrs_gs128", 30, 6),
+                                                    ("st_q8_gs128_medium", 45, 4)])
 def test_model_matches_oracle(gpu, files, name, prompt_len, steps):
     import yallma3_mini_inference_amd as Y
     path = files(name)

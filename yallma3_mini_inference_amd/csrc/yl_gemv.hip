@@ -64,6 +64,12 @@ template <>
 struct WBlock<kQ8S> { uint4 a, b; };
 template <>
 struct WBlock<kQ8S64> { uint4 a, b; };
+template <>
+struct WBlock<kQ8S128> { uint4 a, b; };
+
+// 32-blocks per scale group of a weight format
+template <int WF>
+constexpr int blocks_per_group() { return WF == kQ8S64 ? 2 : (WF == kQ8S128 ? 4 : 1); }
 
 // The activation format of a weight format (Q8 rows with f32 block scales
 // dot against the same 32-groups as Q8_0).
@@ -77,6 +83,8 @@ template <>
 struct ScaleWord<kQ8S> { using type = float; };
 template <>
 struct ScaleWord<kQ8S64> { using type = float; };
+template <>
+struct ScaleWord<kQ8S128> { using type = float; };
 
 constexpr int kBufRaw = 0x00020000;   // buffer descriptor word 3: raw 32-bit data
 
@@ -226,29 +234,29 @@ __device__ __forceinline__ float chain_slot_dpp(float acc, float term, int first
     if (valid <= 0) return acc;
     return chain_slot_part<LPR>(acc, term, valid);
 }
-// The same for 64-element groups: a group's term sits on the even lane of
-// its two blocks, so the chain reads lanes 0, 2, 4, ... (`valid` counts
-// blocks; nb is even).
-template <int LPR, int I = 0>
-__device__ __forceinline__ float chain_slot_full2(float acc, float term) {
-    if constexpr (I < LPR) return chain_slot_full2<LPR, I + 2>(add_from_lane_plus<I>(acc, term), term);
+// The same for groups of G blocks: a group's term sits on the first lane of
+// its blocks, so the chain reads lanes 0, G, 2G, ... (`valid` counts blocks;
+// nb is a multiple of G).
+template <int LPR, int G, int I = 0>
+__device__ __forceinline__ float chain_slot_fullg(float acc, float term) {
+    if constexpr (I < LPR) return chain_slot_fullg<LPR, G, I + G>(add_from_lane_plus<I>(acc, term), term);
     else return acc;
 }
-template <int LPR, int I = 0>
-__device__ __forceinline__ float chain_slot_part2(float acc, float term, int valid) {
+template <int LPR, int G, int I = 0>
+__device__ __forceinline__ float chain_slot_partg(float acc, float term, int valid) {
     if constexpr (I < LPR) {
         if (I >= valid) return acc;
-        return chain_slot_part2<LPR, I + 2>(add_from_lane_plus<I>(acc, term), term, valid);
+        return chain_slot_partg<LPR, G, I + G>(add_from_lane_plus<I>(acc, term), term, valid);
     } else {
         return acc;
     }
 }
-template <int LPR>
-__device__ __forceinline__ float chain_slot_dpp2(float acc, float term, int first_block, int nb) {
+template <int LPR, int G>
+__device__ __forceinline__ float chain_slot_dppg(float acc, float term, int first_block, int nb) {
     const int valid = nb - first_block;   // uniform
-    if (valid >= LPR) return chain_slot_full2<LPR>(acc, term);
+    if (valid >= LPR) return chain_slot_fullg<LPR, G>(acc, term);
     if (valid <= 0) return acc;
-    return chain_slot_part2<LPR>(acc, term, valid);
+    return chain_slot_partg<LPR, G>(acc, term, valid);
 }
 
 // Few wavefronts per SIMD: registers go to loads in flight rather than to
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
     constexpr bool kQPro = EPI == kEpiResidQ;   // an f32 input row, quantized here (no RMSNorm)
     constexpr bool kStage = kNorm || kQPro;     // the activation row is made by NA wavefronts
     constexpr int NA = kStage ? kNormWaves : 1;   // activation wavefronts
-    constexpr int GSZ = WF == kQ8S64 ? 64 : 32;  // activation (and weight scale) group
+    constexpr int GSZ = 32 * blocks_per_group<WF>();   // activation (and weight scale) group
     const int n = a.n, nb = a.nb, o = a.o;
     const int nww = (int)(blockDim.x >> 6) - NA;
     const int R = RW * nww;
@@ -418,7 +426,8 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                     for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(v[k]));
                     am = fmaxf(am, dpp_mov<0xB1>(am));   // quad_perm [1,0,3,2]
                     am = fmaxf(am, dpp_mov<0x4E>(am));   // quad_perm [2,3,0,1]
-                    if constexpr (GSZ == 64) am = fmaxf(am, __shfl_xor(am, 4, 64));
+                    if constexpr (GSZ >= 64) am = fmaxf(am, __shfl_xor(am, 4, 64));
+                    if constexpr (GSZ >= 128) am = fmaxf(am, __shfl_xor(am, 8, 64));
                     const float sc = group_scale<act_fmt<WF>()>(am);
                     int q[8];
                     quant8<act_fmt<WF>()>(v, sc, q);
@@ -464,11 +473,12 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         // descriptors over this wavefront's rows: rows past the matrix read 0
         const __amdgpu_buffer_rsrc_t qr =
             uniform_rsrc(a.qs + (size_t)min(wrow0, o - 1) * row_bytes, (int)(rows_here * row_bytes));
-        // scales per row: one per block, or one per block pair (kQ8S64)
-        constexpr int kBlocksPerScale = WF == kQ8S64 ? 2 : 1;
+        // scales per row: one per block, or one per group of 2 or 4 blocks
+        constexpr int kBlocksPerScale = blocks_per_group<WF>();
         const int nsc = nb / kBlocksPerScale;
-        const void* scale_rows = WF == kQ8S || WF == kQ8S64 ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nsc)
-                                                            : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
+        constexpr bool kF32Scales = WF == kQ8S || WF == kQ8S64 || WF == kQ8S128;
+        const void* scale_rows = kF32Scales ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nsc)
+                                            : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
         const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(scale_rows, rows_here * nsc * kScaleBytes);
         const int qv = (int)(r * row_bytes) + j * kBlockBytes;
         const int dv_off = (r * nsc + j / kBlocksPerScale) * kScaleBytes;
@@ -484,7 +494,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         SW dv[LA];
         auto issue = [&](int k) {
             load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
-            if constexpr (WF == kQ8S || WF == kQ8S64)
+            if constexpr (kF32Scales)
                 dv[k % LA] = __builtin_bit_cast(
                     float, __builtin_amdgcn_raw_buffer_load_b32(dr, dv_off, k * (LPR / kBlocksPerScale) * kScaleBytes,
                                                                 kPolStream));
@@ -512,15 +522,17 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             const int bb = b < nb ? b : nb - 1;
             int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
             float ws;
-            if constexpr (WF == kQ8S || WF == kQ8S64) ws = dv[k % LA];
+            if constexpr (kF32Scales) ws = dv[k % LA];
             else ws = f16_to_f32(dv[k % LA]);
-            if constexpr (WF == kQ8S64) {
+            if constexpr (kBlocksPerScale > 1) {
                 // the group's exact int32 dot: this block's plus the next
-                // lane's (row_shl:1; read on the even lanes, which own the
-                // groups), then its one term ((float)isum * w_scale) * x_scale
+                // lanes' (row_shl:1, then row_shl:2 for 4 blocks; the first
+                // lane of each group owns it), then its one term
+                // ((float)isum * w_scale) * x_scale
                 isum += __builtin_amdgcn_update_dpp(0, isum, 0x101, 0xF, 0xF, true);
-                const float term = fmul(fmul((float)isum, ws), xsl[bb >> 1]);
-                acc = chain_slot_dpp2<LPR>(acc, term, k * LPR, nb);
+                if constexpr (kBlocksPerScale == 4) isum += __builtin_amdgcn_update_dpp(0, isum, 0x102, 0xF, 0xF, true);
+                const float term = fmul(fmul((float)isum, ws), xsl[bb / kBlocksPerScale]);
+                acc = chain_slot_dppg<LPR, kBlocksPerScale>(acc, term, k * LPR, nb);
             } else {
                 const float term = fmul(fmul((float)isum, ws), xsl[bb]);
                 acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
@@ -682,7 +694,7 @@ static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t s
     case kEpiResid: return launch_plan<WF, kEpiResid, false>(a, p, batch, st);
     case kEpiSwiglu: return launch_plan<WF, kEpiSwiglu, false>(a, p, batch, st);
     case kEpiResidQ:
-        if constexpr (WF == kQ8S64) return launch_plan<WF, kEpiResidQ, false>(a, p, batch, st);
+        if constexpr (WF == kQ8S64 || WF == kQ8S128) return launch_plan<WF, kEpiResidQ, false>(a, p, batch, st);
         return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
@@ -691,8 +703,9 @@ static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t s
 hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipStream_t s) {
     if ((epi == kEpiQkvRope || epi == kEpiSwiglu) && (args.n % 32 || args.n > 4096)) return hipErrorInvalidValue;
     if (epi == kEpiResidQ && (args.n > 8192 || !args.xf)) return hipErrorInvalidValue;
-    // kQ8S64 activations are quantized in 64-groups by the kernel's own prologue
-    if (wfmt == kQ8S64 && (args.n % 64 || args.nb != args.n / 32 || epi == kEpiResid || epi == kEpiStore))
+    // kQ8S64 / kQ8S128 activations are quantized in 64 / 128-groups by the kernel's own prologue
+    if ((wfmt == kQ8S64 || wfmt == kQ8S128) &&
+        (args.n % (wfmt == kQ8S64 ? 64 : 128) || args.nb != args.n / 32 || epi == kEpiResid || epi == kEpiStore))
         return hipErrorInvalidValue;
     if (args.n % 32 || args.n > 16384 || args.o <= 0) return hipErrorInvalidValue;
     GemvArgs a = args;
@@ -701,6 +714,7 @@ hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipSt
     if (wfmt == kQ4) return launch_wf<kQ4>(a, epi, batch, s);
     if (wfmt == kQ8S) return launch_wf<kQ8S>(a, epi, batch, s);
     if (wfmt == kQ8S64) return launch_wf<kQ8S64>(a, epi, batch, s);
+    if (wfmt == kQ8S128) return launch_wf<kQ8S128>(a, epi, batch, s);
     return hipErrorInvalidValue;
 }
 

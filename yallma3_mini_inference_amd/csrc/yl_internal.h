@@ -36,10 +36,11 @@ enum Fmt : int { kQ8 = 0, kQ4 = 1, kF16 = 2 };   // WeightFormat, weight_type.rs
 // (QMat::sf: lm.rs and safetensors Q8 with group size 32); activations and
 // results as for kQ8.
 constexpr int kQ8S = 3;
-// The same with one f32 scale per group of 64 elements (two 32-blocks):
-// activations are quantized in 64-groups, and a group's two block dots are
-// added as integers before its one f32 term.
+// The same with one f32 scale per group of 64 (two 32-blocks) or 128 (four)
+// elements: activations are quantized in those groups, and a group's block
+// dots are added as integers before its one f32 term.
 constexpr int kQ8S64 = 4;
+constexpr int kQ8S128 = 5;
 // F16 gate/up matrices interleave blocks of this many gate rows with the
 // same up rows (the SwiGLU tiles of the F16 GEMV: 32 + 32 rows); the gate
 // and up row counts are multiples of 32.
@@ -114,7 +115,7 @@ enum Epi : int {
 struct GemvArgs {
     // weights and activations
     const uint8_t* qs; const uint16_t* d; int n, o, nb;
-    const float* sf;                           // kQ8S: f32 block scales [o][nb]; kQ8S64: [o][nb / 2] (d unused)
+    const float* sf;                           // kQ8S / kQ8S64 / kQ8S128: f32 scales [o][nb], [o][nb / 2], [o][nb / 4] (d unused)
     const float* xf;                           // kEpiResidQ: f32 input rows [batch][n]
     const int8_t* xq; const float* xs;        // [batch][n], [batch][nb] (staged prologue)
     // kEpiQkvRope / kEpiSwiglu prologue: RMSNorm + quantize of x [batch][n]

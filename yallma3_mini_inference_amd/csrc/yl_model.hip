@@ -323,7 +323,7 @@ struct yl_model {
     int gs = 32;
     int hf_rope = 0;            // 1: util::rope pairs (j, j + head/2); 0: rope_gguf pairs (2j, 2j + 1)
     int pair_rows = 16;         // q8g: gate/up rows per interleaved block of w13 (16, or 32 with q8_gemv)
-    bool q8_gemv = false;       // q8g with group size 32 or 64: one-token steps on the GGUF path's GEMVs (kQ8S, kQ8S64)
+    bool q8_gemv = false;       // q8g with group size 32, 64 or 128: one-token steps on the GGUF path's GEMVs
     uint32_t bos = 128000, eos = 128009;
     std::string name = "TransformerLlamaGguf";
     std::vector<std::string> vocab_str;
@@ -707,12 +707,12 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
     m->f16 = h.f16;
     m->q8g = !h.f16;
     m->gs = h.gs;
-    // group size 32 or 64 (rows up to the GEMV's limits): one-token steps run
-    // the 32-block GEMV (kQ8S / kQ8S64), whose SwiGLU tiles are 32 gate + 32
-    // up rows
+    // group size 32, 64 or 128 (rows up to the GEMV's limits): one-token
+    // steps run the 32-block GEMV (kQ8S / kQ8S64 / kQ8S128), whose SwiGLU
+    // tiles are 32 gate + 32 up rows
     m->q8_gemv = m->q8g && m->dim <= 4096 &&
                  ((m->gs == 32 && m->att <= 16384 && m->hidden <= 16384) ||
-                  (m->gs == 64 && m->att <= 8192 && m->hidden <= 8192));
+                  ((m->gs == 64 || m->gs == 128) && m->att <= 8192 && m->hidden <= 8192));
     m->pair_rows = m->q8_gemv ? 32 : 16;
     if (m->n_kv <= 0 || m->n_heads % m->n_kv || (m->hd != 32 && m->hd != 64 && m->hd != 128) || m->dim % 32 ||
         m->hidden % 32 || m->att % 32 || m->kv % 32 || m->ctx <= 0 || m->dim > 8192 ||
@@ -862,10 +862,13 @@ bool session_grow(yl_session* s, int batch) {
     return true;
 }
 
-// The GEMV weight format of a matrix: its own, or kQ8S / kQ8S64 for Q8 rows
-// with f32 scales (which reach the GEMV with group size 32 or 64 only:
-// yl_model::q8_gemv).
-static int gemv_fmt(const QMat& w) { return w.sf ? (w.gs == 64 ? kQ8S64 : kQ8S) : w.fmt; }
+// The GEMV weight format of a matrix: its own, or kQ8S / kQ8S64 / kQ8S128
+// for Q8 rows with f32 scales (which reach the GEMV with group size 32, 64
+// or 128 only: yl_model::q8_gemv).
+static int gemv_fmt(const QMat& w) {
+    if (!w.sf) return w.fmt;
+    return w.gs == 128 ? kQ8S128 : (w.gs == 64 ? kQ8S64 : kQ8S);
+}
 
 uint64_t gemv_bytes(const QMat& w, int out_elems, int batch) {
     return (uint64_t)w.bytes() + (uint64_t)batch * ((uint64_t)w.n + (uint64_t)w.nb * 4 + (uint64_t)out_elems * 4);
@@ -947,10 +950,10 @@ hipError_t enqueue_op(const yl_model* m, yl_session* s, int cls, int l, int batc
     const Layer& L = m->layers[l];
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
-    // f32-scaled Q8 with 64-groups: attention and SwiGLU hand over f32 rows,
-    // which the Wo and down GEMVs quantize (a 64-group spans two of the
-    // producers' 32-wide workgroups)
-    const bool f32_act = m->q8g && m->gs == 64;
+    // f32-scaled Q8 with 64- or 128-groups: attention and SwiGLU hand over
+    // f32 rows, which the Wo and down GEMVs quantize (such a group spans
+    // several of the producers' 32-wide workgroups)
+    const bool f32_act = m->q8g && m->gs > 32;
     if (batch >= kGemmMinTokens && cls != kOpAttn) {
         hipError_t e = enqueue_op_gemm(m, s, cls, l, batch, tok, kc, vc, bytes, prologue);
         if (e != hipErrorNotSupported) return e;
