@@ -20,6 +20,10 @@
 // vectors) stream into LDS by LDS DMA, 4 stages deep, so no register holds
 // data in flight.  Q4_0 weights keep the reference nibble order and are
 // unpacked in registers to int8 in k order (values 0..15, no offset).
+// Q8 with f32 scales (lm.rs, safetensors): per block (kQ8S), or per group
+// of 2 or 4 blocks (kQ8S64, kQ8S128), whose block MFMAs accumulate into one
+// int32 tile -- the group's exact dot -- before its one f32 term; the
+// activations are quantized in the same groups.
 #include <hip/hip_runtime.h>
 
 #include "yl_blocks.h"
@@ -37,13 +41,22 @@ constexpr int kGmTN = 128;      // weight rows per workgroup
 constexpr int kGmBK = 2;        // blocks per stage
 constexpr int kGmStages = 4;    // stages in flight
 
+// 32-blocks per scale group
+template <int WF>
+constexpr int gm_bpg() { return WF == kQ8S64 ? 2 : (WF == kQ8S128 ? 4 : 1); }
+
 template <int WF>
 struct GmStage {
-    static constexpr int kRowB = WF == kQ8 ? 32 : 16;         // weight bytes per row and block
+    static constexpr bool kF32 = WF == kQ8S || WF == kQ8S64 || WF == kQ8S128;
+    static constexpr int kRowB = WF == kQ4 ? 16 : 32;         // weight bytes per row and block
     static constexpr int A = kGmBK * kGmTM * 32;              // [blk][token][32] int8
     static constexpr int B = kGmBK * kGmTN * kRowB;           // [blk][row][32 | 16]
-    static constexpr int XS = kGmBK * kGmTM * 4;              // [blk][token] f32
-    static constexpr int WS = kGmTN * 4;                      // [row][2] f16 (the stage's 2 blocks)
+    // activation scales: [blk][token] f32, or one per token for a stage
+    // inside one group
+    static constexpr int XS = gm_bpg<WF>() > 1 ? kGmTM * 4 : kGmBK * kGmTM * 4;
+    // weight scales: [row][2] f16 (Q8_0 / Q4_0), [row][2] f32 (kQ8S), or one
+    // f32 per row (the stage's group)
+    static constexpr int WS = WF == kQ8S ? kGmTN * 8 : kGmTN * 4;
     static constexpr int bytes = A + B + XS + WS;
     // LDS DMA instructions per wavefront and stage (16-byte lanes move 1 KiB,
     // 4-byte lanes 256 B); every wavefront issues the same number
@@ -51,11 +64,17 @@ struct GmStage {
     static constexpr int dmaB = B / 1024 / 4;
     static constexpr int dma = dmaA + dmaB + 1 + 1;
     static_assert(A % 4096 == 0 && B % 4096 == 0, "16-byte DMA split over 4 wavefronts");
-    static_assert(XS == 4 * 256 && WS == 2 * 256, "scale DMA shapes");
+    static_assert((XS == 4 * 256 || XS == 2 * 256) && (WS == 2 * 256 || WS == 4 * 256), "scale DMA shapes");
 };
 
 size_t gemm_lds_bytes(int wfmt) {
-    return (size_t)kGmStages * (wfmt == kQ8 ? GmStage<kQ8>::bytes : GmStage<kQ4>::bytes);
+    switch (wfmt) {
+    case kQ8: return (size_t)kGmStages * GmStage<kQ8>::bytes;
+    case kQ4: return (size_t)kGmStages * GmStage<kQ4>::bytes;
+    case kQ8S: return (size_t)kGmStages * GmStage<kQ8S>::bytes;
+    case kQ8S64: return (size_t)kGmStages * GmStage<kQ8S64>::bytes;
+    default: return (size_t)kGmStages * GmStage<kQ8S128>::bytes;
+    }
 }
 
 template <int D>
@@ -117,7 +136,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                         // K/V rows accumulate into the cache (forward.rs:166-169)
                         const int att = a.att_dim, kv = a.kv_dim;
                         if (c >= att && c < att + kv) {
-                            const int cc = c - att;
+                            const int cc = qk_column(c - att, a.head_size, a.hf_rows);
                             if (cc < (kv / 4) * 4) v = a.k_cache[(size_t)cc * a.kv_ld + pos + t];
                         } else if (c >= att + kv) {
                             const int cc = c - att - kv;
@@ -147,7 +166,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int k = 0; k < S::dmaB; k++) {
             const int j = wave * S::dmaB + k;
             const uint8_t* src;
-            if constexpr (WF == kQ8) {
+            if constexpr (WF != kQ4) {
                 const int blk = j / 4, row = min(c0 + 32 * (j % 4) + (lane >> 1), a.o - 1);
                 src = a.qs + (size_t)row * a.n + (size_t)(b0 + blk) * 32 + 16 * (lane & 1);
             } else {
@@ -156,15 +175,34 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             }
             __builtin_amdgcn_global_load_lds(src, buf + S::A + j * 1024, 16, 0, 0);
         }
-        // activation scales: wavefront w -> block w/2, tokens 64*(w%2) + lane
-        {
+        constexpr int G = gm_bpg<WF>();
+        if constexpr (G == 1) {
+            // activation scales: wavefront w -> block w/2, tokens 64*(w%2) + lane
             const int tok = min(t0 + 64 * (wave & 1) + lane, M - 1);
             __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * a.nb + b0 + (wave >> 1),
                                              buf + S::A + S::B + wave * 256, 4, 0, 0);
+        } else {
+            // the group's scale per token: wavefront w -> tokens 64*(w%2) + lane
+            // (wavefronts 2 and 3 repeat 0 and 1)
+            const int tok = min(t0 + 64 * (wave & 1) + lane, M - 1);
+            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * (a.nb / G) + b0 / G,
+                                             buf + S::A + S::B + (wave & 1) * 256, 4, 0, 0);
         }
-        // weight scales: rows 64*(w%2) + lane, the stage's two f16 as one dword
-        // (wavefronts 2 and 3 repeat 0 and 1)
-        {
+        if constexpr (WF == kQ8S) {
+            // f32 block scales [row][2]: wavefront w -> rows 32w .. +31, lane i
+            // -> row i/2, block i%2
+            const int row = min(c0 + 32 * wave + (lane >> 1), a.o - 1);
+            __builtin_amdgcn_global_load_lds(a.sf + (size_t)row * a.nb + b0 + (lane & 1),
+                                             buf + S::A + S::B + S::XS + wave * 256, 4, 0, 0);
+        } else if constexpr (G > 1) {
+            // the group's f32 scale per row: rows 64*(w%2) + lane (wavefronts 2
+            // and 3 repeat 0 and 1)
+            const int row = min(c0 + 64 * (wave & 1) + lane, a.o - 1);
+            __builtin_amdgcn_global_load_lds(a.sf + (size_t)row * (a.nb / G) + b0 / G,
+                                             buf + S::A + S::B + S::XS + (wave & 1) * 256, 4, 0, 0);
+        } else {
+            // weight scales: rows 64*(w%2) + lane, the stage's two f16 as one dword
+            // (wavefronts 2 and 3 repeat 0 and 1)
             const int row = min(c0 + 64 * (wave & 1) + lane, a.o - 1);
             __builtin_amdgcn_global_load_lds(a.d + (size_t)row * a.nb + b0, buf + S::A + S::B + S::XS + (wave & 1) * 256,
                                              4, 0, 0);
@@ -179,6 +217,10 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int s = 0; s < kGmStages - 1; s++)
         if (s < nst) issue(gsm + s * S::bytes, s);
 
+    // group dots of the f32-scaled formats with 2 or 4 blocks per group,
+    // accumulated over the group's blocks (exact int32)
+    constexpr int G = gm_bpg<WF>();
+    v16i gd[2][2] = {};
     for (int s = 0; s < nst; s++) {
         gm_wait<S::dma>(min(kGmStages - 2, nst - 1 - s));
         __syncthreads();   // every wavefront's DMA of stage s landed; stage s-1's buffer is free
@@ -197,15 +239,50 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 av[tm] = *reinterpret_cast<const v4i*>(Ab + (64 * wm + 32 * tm + li) * 32 + 16 * lh);
 #pragma unroll
             for (int tn = 0; tn < 2; tn++) {
-                if constexpr (WF == kQ8) {
+                if constexpr (WF != kQ4) {
                     bv[tn] = *reinterpret_cast<const v4i*>(Bb + (64 * wn + 32 * tn + li) * 32 + 16 * lh);
                 } else {
                     bv[tn] = q4_unpack16(*reinterpret_cast<const uint2*>(Bb + (64 * wn + 32 * tn + li) * 16 + 8 * lh));
                 }
             }
+            if constexpr (G > 1) {
+                // this block's dots join the group's (the first block of a
+                // group starts from zero); the term follows the group's last
+                const bool first = ((s * kGmBK + blk) % G) == 0;
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                    for (int tn = 0; tn < 2; tn++) {
+                        const v16i zero = {};
+                        gd[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[tm], bv[tn], first ? zero : gd[tm][tn],
+                                                                           0, 0, 0);
+                    }
+                if ((s * kGmBK + blk) % G != G - 1) continue;
+                __builtin_amdgcn_sched_barrier(0);
+                const float* wsf = reinterpret_cast<const float*>(wsl);
+                float wsc[2];
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) wsc[tn] = wsf[64 * wn + 32 * tn + li];
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                    for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) {
+                            const float xs = xsl[64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh];
+                            const float term = fmul(fmul((float)gd[tm][tn][i], wsc[tn]), xs);
+                            acc[tm][tn][i] = fadd(acc[tm][tn][i], term);
+                        }
+                continue;
+            }
             float wsc[2];
 #pragma unroll
-            for (int tn = 0; tn < 2; tn++) wsc[tn] = f16_to_f32(wsl[(64 * wn + 32 * tn + li) * 2 + blk]);
+            for (int tn = 0; tn < 2; tn++) {
+                if constexpr (WF == kQ8S)
+                    wsc[tn] = reinterpret_cast<const float*>(wsl)[(64 * wn + 32 * tn + li) * 2 + blk];
+                else
+                    wsc[tn] = f16_to_f32(wsl[(64 * wn + 32 * tn + li) * 2 + blk]);
+            }
             vf4 xv[2][4];
 #pragma unroll
             for (int tm = 0; tm < 2; tm++)
@@ -250,6 +327,10 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 const float g = acc[tm][0][i], u = acc[tm][1][i];
                 const float den = fadd(1.0f, expf_rn(-g));
                 const float h = fmul(g / den, u);
+                if (!a.hq) {   // f32 h only (quantized afterwards in the model's groups)
+                    if (tok_ok && grp_ok) a.h_f32[(size_t)t * a.hidden + (size_t)grp * kGroup + li] = h;
+                    continue;
+                }
                 float am = group_max(fabsf(h), 32);
                 am = fmaxf(am, 0.0f);
                 const float sc = a.h_fmt == kQ4 ? group_scale<kQ4>(am) : group_scale<kQ8>(am);
@@ -274,8 +355,9 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                             if (c >= att + kv) {
                                 a.v_cache[(size_t)(pos + t) * kv + (c - att - kv)] = v;
                             } else {
-                                const int col = c < att ? c : c - att;
-                                const int pair = (col % hd) >> 1;
+                                const int scol = c < att ? c : c - att;   // stored row within q or k
+                                const int col = qk_column(scol, hd, a.hf_rows);
+                                const int pair = (scol % hd) >> 1;
                                 const float cs = a.rope_cos[(size_t)(pos + t) * (hd >> 1) + pair];
                                 const float sn = a.rope_sin[(size_t)(pos + t) * (hd >> 1) + pair];
                                 const float v0 = (li & 1) ? other : v, v1 = (li & 1) ? v : other;
@@ -316,7 +398,10 @@ static hipError_t launch_gemm_k(const GemvArgs& a, int M, hipStream_t st) {
 }
 
 bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M) {
-    if (M < 1 || a.n % 32 || a.nb != a.n / 32 || a.nb % kGmBK || (wfmt != kQ8 && wfmt != kQ4)) return false;
+    if (M < 1 || a.n % 32 || a.nb != a.n / 32 || a.nb % kGmBK) return false;
+    if (wfmt != kQ8 && wfmt != kQ4 && wfmt != kQ8S && wfmt != kQ8S64 && wfmt != kQ8S128) return false;
+    if ((wfmt == kQ8S64 && a.nb % 2) || (wfmt == kQ8S128 && a.nb % 4)) return false;
+    if (epi == kEpiSwiglu && !a.hq && !a.h_f32) return false;
     if (epi == kEpiSwiglu && (a.o % 64 || a.hidden * 2 != a.o)) return false;
     if (epi == kEpiQkvRope && (a.head_size % 2 || a.att_dim % 32)) return false;
     return true;
@@ -333,6 +418,9 @@ hipError_t launch_gemm(const GemvArgs& a, int wfmt, int epi, int M, hipStream_t 
     default: return hipErrorInvalidValue;                                      \
     }
     if (wfmt == kQ8) { YL_GEMM_EPI(kQ8) }
+    if (wfmt == kQ8S) { YL_GEMM_EPI(kQ8S) }
+    if (wfmt == kQ8S64) { YL_GEMM_EPI(kQ8S64) }
+    if (wfmt == kQ8S128) { YL_GEMM_EPI(kQ8S128) }
     YL_GEMM_EPI(kQ4)
 #undef YL_GEMM_EPI
 }

@@ -1125,6 +1125,57 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
 // Prompts: the rows are normalized and quantized once by their own kernels
 // first.  `bytes`: int8 weights + f32 scales, the activations read, the
 // outputs written.
+// The projections of op `cls` of layer l of an f32-scaled Q8 model over
+// `batch` tokens on the int8 MFMA GEMM (group sizes 32, 64, 128: the GEMM's
+// kQ8S / kQ8S64 / kQ8S128): every input row normalized (QKV, gate/up) and
+// quantized in groups of gs by its own kernels first; SwiGLU hands over f32
+// h.  hipErrorNotSupported when a shape needs the tile kernel instead.
+static hipError_t enqueue_op_gemm_q8g(const yl_model* m, yl_session* s, int cls, int l, int batch,
+                                      const uint32_t* tok, float* kc, float* vc, uint64_t* bytes) {
+    hipStream_t st = s->stream;
+    const Layer& L = m->layers[l];
+    const int gs = m->gs;
+    GemvArgs a{};
+    const QMat* w = nullptr;
+    int epi = 0, n = 0;
+    const float* in = nullptr;        // the f32 rows quantized for the GEMM
+    const float* norm_w = nullptr;    // RMSNorm of the residual stream first
+    switch (cls) {
+    case kOpQkv:
+        w = &L.qkv; epi = kEpiQkvRope; n = m->dim; norm_w = L.rms_att;
+        a.q_out = s->sq; a.k_cache = kc; a.v_cache = vc;
+        a.att_dim = m->att; a.kv_dim = m->kv; a.head_size = m->hd; a.kv_ld = m->kv_ld;
+        a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.state = s->st; a.hf_rows = m->hf_rope;
+        break;
+    case kOpWo:
+        w = &L.wo; epi = kEpiResid; n = m->att; in = s->attf; a.x = s->x;
+        break;
+    case kOpW13:
+        w = &L.w13; epi = kEpiSwiglu; n = m->dim; norm_w = L.rms_ffn;
+        a.hq = nullptr; a.hs = nullptr; a.h_f32 = s->hf; a.hidden = m->hidden;
+        break;
+    case kOpW2:
+        w = &L.w2; epi = kEpiResid; n = m->hidden; in = s->hf; a.x = s->x;
+        break;
+    default:
+        return hipErrorNotSupported;
+    }
+    a.qs = w->qs; a.sf = w->sf; a.n = w->n; a.o = w->o; a.nb = w->nb;
+    a.xq = s->gq; a.xs = s->gsc;
+    const int wf = gemv_fmt(*w);
+    if (!gemm_supported(a, wf, epi, batch)) return hipErrorNotSupported;
+    hipError_t e = hipSuccess;
+    if (norm_w) {
+        if (cls == kOpQkv && l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
+        if (e == hipSuccess) e = launch_rmsnorm(-1, s->x, norm_w, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
+        in = s->xn;
+    }
+    if (e == hipSuccess) e = launch_quantize_gs(in, s->gq, s->gsc, gs, (size_t)batch * n, st);
+    if (e != hipSuccess) return e;
+    if (bytes) *bytes = gemv_bytes(*w, w->o, batch);
+    return launch_gemm(a, wf, epi, batch, st);
+}
+
 hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int batch, const uint32_t* tok,
                           int advance, uint64_t* bytes) {
     hipStream_t st = s->stream;
@@ -1139,6 +1190,10 @@ hipError_t enqueue_op_q8g(const yl_model* m, yl_session* s, int cls, int l, int 
     const Layer& L = m->layers[l];
     float* kc = s->kc + (size_t)l * lay_kv;
     float* vc = s->vc + (size_t)l * lay_kv;
+    if (m->q8_gemv && batch >= kGemmMinTokens && cls != kOpAttn) {
+        const hipError_t e = enqueue_op_gemm_q8g(m, s, cls, l, batch, tok, kc, vc, bytes);
+        if (e != hipErrorNotSupported) return e;
+    }
     const bool one = batch == 1;
     auto args = [&](const QMat& w, int epi) {
         Q8gArgs a;
