@@ -13,9 +13,9 @@
 //   each, fed from LDS by three product wavefronts (below).  The prologue
 //   can apply RMSNorm (util.rs:389-426) to the input row, and the epilogue
 //   add the residual or form SwiGLU from gate/up row pairs;
-//   batches: a workgroup takes 64 rows x 4 tokens, one wavefront per token,
-//   each lane multiplying and adding its own (token, row) chain, the weight
-//   tile shared through LDS.
+//   batches: a workgroup takes 64 rows x 64 tokens, each lane running 16
+//   token chains of its row, the weight and activation tiles shared through
+//   LDS.
 #include <hip/hip_runtime.h>
 
 #include "yl_blocks.h"
@@ -24,9 +24,6 @@
 
 namespace yl {
 
-constexpr int kF16Rows = 64;     // output rows per workgroup
-constexpr int kF16Cols = 64;     // columns per tile
-constexpr int kF16Tok = 4;       // tokens per workgroup (batched kernel)
 
 __device__ __forceinline__ float h2f(uint32_t bits16) { return f16_to_f32((uint16_t)bits16); }
 
@@ -312,61 +309,100 @@ __global__ void k_swiglu_pairs(const float* __restrict__ raw, int hidden, float*
 }
 
 // --------------------------------------------------------------- batches
-// 256 threads: wave t takes token blockIdx.y * 4 + t over the workgroup's
-// 64 rows.  LDS: the weight tile transposed to [8 chunks][64 rows][8
-// halves], double-buffered, and the 4 tokens' activation tiles.
+// A workgroup owns 64 rows x 64 tokens: lane r of wavefront w runs the
+// chains of row r for the 16 tokens 16w .. 16w+15, one accumulator each, so
+// every weight tile is read once per 64 tokens.  Per K tile of 32 columns
+// the weights ([64 rows][32 halves], row stride 80 bytes) and the
+// activations ([32 columns][64 tokens] f32, read as broadcast vf4 of 4
+// tokens) sit in LDS, double-buffered; the next tile's global loads are in
+// registers while the current tile is added.  Each chain adds its products
+// x[t][k] * w[r][k] in column order (matmul_f32's serial sum).
+constexpr int kFbRows = 64;          // rows per workgroup (lane = row)
+constexpr int kFbTok = 64;           // tokens per workgroup (16 per wavefront)
+constexpr int kFbKT = 32;            // columns per tile
+constexpr int kFbWStride = 40;       // halves per weight row in LDS (32 + 8: 16-byte aligned, spread banks)
+constexpr int kFbXStride = kFbTok + 4;   // floats per activation column in LDS
+
 template <int EPI>
 __global__ __launch_bounds__(256) void k_matmul_f16_batch(const uint16_t* __restrict__ w, int n, int o,
                                                           const float* __restrict__ x, int batch,
                                                           float* __restrict__ out, int out_ld) {
-    __shared__ __align__(16) uint4 wt[2][8 * kF16Rows];
-    __shared__ __align__(16) float xt[2][kF16Tok * kF16Cols];
+    __shared__ __align__(16) uint16_t wt[2][kFbRows * kFbWStride];
+    __shared__ __align__(16) float xt[2][kFbKT * kFbXStride];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int row0 = blockIdx.x * kF16Rows;
-    const int tok = blockIdx.y * kF16Tok + wave;
-    const int ntile = (n + kF16Cols - 1) / kF16Cols;
-    // loader thread t: chunk c = t % 8 of rows t / 8 and t / 8 + 32; x: float4 t % 16 of token t / 16
-    const int lc = tid & 7, lr = tid >> 3;
-    uint4 wreg[2];
-    vf4 xreg;
+    const int row0 = blockIdx.x * kFbRows, tok0 = blockIdx.y * kFbTok;
+    const int ntile = (n + kFbKT - 1) / kFbKT;
+    // loader thread i: weight chunk (row i / 4, halves 8 (i % 4) .. +8); two
+    // activation float4 (token i / 4 ... see below)
+    const int wr_row = tid >> 2, wr_c = (tid & 3) * 8;
+    uint4 wreg;
+    vf4 xreg[2];
     auto load = [&](int t) {
-        const int k = t * kF16Cols + lc * 8;
-        const int kk = k < n ? k : n - 8;
+        const int k0 = t * kFbKT;
+        const int r = min(row0 + wr_row, o - 1);
+        wreg = *reinterpret_cast<const uint4*>(w + (size_t)r * n + min(k0 + wr_c, n - 8));
+        // activations: 64 tokens x 32 columns = 512 float4; thread i takes
+        // float4 i and i + 256: token (j / 8), columns 4 (j % 8) .. +3
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int r = min(row0 + lr + 32 * h, o - 1);
-            wreg[h] = *reinterpret_cast<const uint4*>(w + (size_t)r * n + kk);
+            const int j = tid + 256 * h;
+            const int tk = min(tok0 + (j >> 3), batch - 1);
+            xreg[h] = *reinterpret_cast<const vf4*>(x + (size_t)tk * n + min(k0 + 4 * (j & 7), n - 4));
         }
-        const int xtok = blockIdx.y * kF16Tok + (tid >> 4), xk = t * kF16Cols + (tid & 15) * 4;
-        xreg = vf4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (tid < 64 && xtok < batch && xk < n) xreg = *reinterpret_cast<const vf4*>(x + (size_t)xtok * n + xk);
     };
     auto store = [&](int b) {
+        *reinterpret_cast<uint4*>(&wt[b][wr_row * kFbWStride + wr_c]) = wreg;
 #pragma unroll
-        for (int h = 0; h < 2; h++) wt[b][lc * kF16Rows + lr + 32 * h] = wreg[h];
-        if (tid < 64) *reinterpret_cast<vf4*>(&xt[b][(tid >> 4) * kF16Cols + (tid & 15) * 4]) = xreg;
+        for (int h = 0; h < 2; h++) {
+            const int j = tid + 256 * h;
+            const int tk = j >> 3, c = 4 * (j & 7);
+            xt[b][(c + 0) * kFbXStride + tk] = xreg[h].x;
+            xt[b][(c + 1) * kFbXStride + tk] = xreg[h].y;
+            xt[b][(c + 2) * kFbXStride + tk] = xreg[h].z;
+            xt[b][(c + 3) * kFbXStride + tk] = xreg[h].w;
+        }
     };
     load(0);
     store(0);
     __syncthreads();
-    float acc = 0.0f;
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
     for (int t = 0; t < ntile; t++) {
         const int b = t & 1;
         if (t + 1 < ntile) load(t + 1);
-        const int kn = min(kF16Cols, n - t * kF16Cols);
-        for (int c = 0; c < kn / 8; c++) {
-            float wf[8];
-            widen8(wt[b][c * kF16Rows + lane], wf);
-            const float* xk = &xt[b][wave * kF16Cols + c * 8];
+        const int kn = min(kFbKT, n - t * kFbKT);   // 32, or 32 (n % 32 == 0)
+        const uint16_t* wrow = &wt[b][lane * kFbWStride];
+        const float* xc = &xt[b][16 * wave];
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc = fadd(acc, fmul(xk[j], wf[j]));
+        for (int c8 = 0; c8 < kFbKT / 8; c8++) {
+            if (8 * c8 >= kn) break;
+            float wf[8];
+            widen8(*reinterpret_cast<const uint4*>(wrow + 8 * c8), wf);
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                const float* xk = xc + (8 * c8 + kk) * kFbXStride;
+                const vf4 x0 = *reinterpret_cast<const vf4*>(xk), x1 = *reinterpret_cast<const vf4*>(xk + 4),
+                          x2 = *reinterpret_cast<const vf4*>(xk + 8), x3 = *reinterpret_cast<const vf4*>(xk + 12);
+                const float xs[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                      x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i] = fadd(acc[i], fmul(xs[i], wf[kk]));
+            }
         }
         if (t + 1 < ntile) store(b ^ 1);
         __syncthreads();
     }
-    if (tok < batch && row0 + lane < o) {
-        float* dst = out + (size_t)tok * out_ld + row0 + lane;
-        *dst = EPI == 0 ? acc : fadd(*dst, acc);
+    const int row = row0 + lane;
+    if (row < o) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int tk = tok0 + 16 * wave + i;
+            if (tk < batch) {
+                float* dst = out + (size_t)tk * out_ld + row;
+                *dst = EPI == 0 ? acc[i] : fadd(*dst, acc[i]);
+            }
+        }
     }
 }
 
@@ -412,9 +448,9 @@ hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, in
                              int epi, hipStream_t s) {
     if (n % 32 || n <= 0 || o <= 0 || batch <= 0 || epi < 0 || epi > 1) return hipErrorInvalidValue;
     if (batch == 1) return launch_f16_gemv(w, n, o, x, nullptr, 0.0f, epi, out, s);
-    const int rb = (o + kF16Rows - 1) / kF16Rows;
+    const int rb = (o + kFbRows - 1) / kFbRows;
     auto k = epi == 0 ? k_matmul_f16_batch<0> : k_matmul_f16_batch<1>;
-    hipLaunchKernelGGL(k, dim3(rb, (batch + kF16Tok - 1) / kF16Tok), dim3(256), 0, s, w, n, o, x, batch, out, out_ld);
+    hipLaunchKernelGGL(k, dim3(rb, (batch + kFbTok - 1) / kFbTok), dim3(256), 0, s, w, n, o, x, batch, out, out_ld);
     return hipGetLastError();
 }
 
