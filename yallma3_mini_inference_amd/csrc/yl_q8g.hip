@@ -307,6 +307,36 @@ __global__ __launch_bounds__(kQ8gThreads) void k_matmul_q8g(
 }
 
 // quantization::quantize (quantization.rs:29-52) over `groups` groups of gs.
+// Quantization in groups of gs = 8 * 2^LG (32 .. 512): 8 consecutive
+// elements per lane (coalesced 16-byte loads), the group's absmax over its
+// 2^LG lanes by xor shuffles, then quant8 (the same integers as quant_one).
+template <int LG>
+__global__ void k_quantize_gs_v(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s,
+                                size_t n8) {
+    constexpr int LPG = 1 << LG;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // 8-element slice
+    const bool live = i < n8;   // a group's lanes are all live or all past the end
+    vf4 a = vf4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    if (live) {
+        a = reinterpret_cast<const vf4*>(x)[2 * i];
+        b = reinterpret_cast<const vf4*>(x)[2 * i + 1];
+    }
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(v[k]));
+#pragma unroll
+    for (int off = 1; off < LPG; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float sc = group_scale<kQ8>(am);
+    int qv[8];
+    quant8<kQ8>(v, sc, qv);
+    if (live) {
+        *reinterpret_cast<uint2*>(q + 8 * i) = make_uint2(pack4(qv[0], qv[1], qv[2], qv[3]), pack4(qv[4], qv[5], qv[6], qv[7]));
+        if ((i & (LPG - 1)) == 0) s[i >> LG] = sc;
+    }
+}
+
+// Any other group size: one thread per group.
 __global__ void k_quantize_gs(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s, int gs,
                               size_t groups) {
     const size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -411,6 +441,16 @@ hipError_t launch_quantize_gs(const float* x, int8_t* q, float* sc, int gs, size
     if (gs <= 0 || n % gs) return hipErrorInvalidValue;
     const size_t groups = n / gs;
     if (!groups) return hipSuccess;
+    const size_t n8 = n / 8;
+    const dim3 g8((unsigned)((n8 + 255) / 256));
+    switch (gs) {
+    case 32: hipLaunchKernelGGL(k_quantize_gs_v<2>, g8, dim3(256), 0, s, x, q, sc, n8); return hipGetLastError();
+    case 64: hipLaunchKernelGGL(k_quantize_gs_v<3>, g8, dim3(256), 0, s, x, q, sc, n8); return hipGetLastError();
+    case 128: hipLaunchKernelGGL(k_quantize_gs_v<4>, g8, dim3(256), 0, s, x, q, sc, n8); return hipGetLastError();
+    case 256: hipLaunchKernelGGL(k_quantize_gs_v<5>, g8, dim3(256), 0, s, x, q, sc, n8); return hipGetLastError();
+    case 512: hipLaunchKernelGGL(k_quantize_gs_v<6>, g8, dim3(256), 0, s, x, q, sc, n8); return hipGetLastError();
+    default: break;
+    }
     hipLaunchKernelGGL(k_quantize_gs, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, q, sc, gs, groups);
     return hipGetLastError();
 }
