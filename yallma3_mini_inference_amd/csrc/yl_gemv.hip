@@ -605,8 +605,8 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
 // ------------------------------------------------------------ dispatch ----
 
 // Lanes per row and slots per lane for a row of nb blocks: 8 lanes per row
-// (8 rows per wavefront) up to 64 blocks, then 16 lanes (4 rows) with 8, 16
-// or 32 slots.  A row's lanes stay inside one 16-lane DPP row, where the
+// (8 rows per wavefront) up to 32 blocks, 16 lanes (4 rows) with 4 slots up
+// to 64, then 16 lanes with 8, 16 or 32 slots.  A row's lanes stay inside one 16-lane DPP row, where the
 // row sums gather the terms.  The gate/up matmul needs 64 rows per
 // workgroup (8 weight wavefronts of 8 rows), so it keeps 8 lanes per row and
 // takes 16 slots up to 128 blocks.
@@ -620,6 +620,17 @@ static bool plan_gemv(int o, int nb, int epi, GemvPlan* p) {
         p->lpr = 8;
         p->ppl = nb <= 8 ? 1 : nb <= 16 ? 2 : nb <= 32 ? 4 : nb <= 64 ? 8 : 16;
         p->nww = 8;
+        return true;
+    }
+    if (nb > 32 && nb <= 64) {
+        // 16 lanes per row, all 4 slots of a row in flight at once, and as
+        // many weight wavefronts (4 rows each, not only powers of two) as
+        // keep the grid within one round of 256 workgroups: more independent
+        // load streams per CU for the small projections
+        p->lpr = 16;
+        p->ppl = 4;
+        p->nww = 1;
+        while (p->nww < kMaxWeightWaves && (o + 4 * p->nww - 1) / (4 * p->nww) > 256) p->nww++;
         return true;
     }
     if (nb <= 64) {
@@ -672,6 +683,7 @@ static hipError_t launch_plan(const GemvArgs& a, const GemvPlan& p, int batch, h
     if constexpr (EPI != kEpiSwiglu) {
         if (p.lpr == 16) {
             switch (p.ppl) {
+            case 4: return launch_k<WF, EPI, EMB, 16, 4>(a, p.nww, batch, st);
             case 8: return launch_k<WF, EPI, EMB, 16, 8>(a, p.nww, batch, st);
             case 16: return launch_k<WF, EPI, EMB, 16, 16>(a, p.nww, batch, st);
             case 32: return launch_k<WF, EPI, EMB, 16, 32>(a, p.nww, batch, st);

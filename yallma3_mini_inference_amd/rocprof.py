@@ -34,8 +34,8 @@ import sys
 # template signatures of the decode GEMV kernels at the Llama-3.2-1B shape
 # (weight format, epilogue, embedding prologue, lanes per row, slots)
 CLASS_KERNELS = {
-    "qkv": "k_gemv<0, 1, false, 8, 8>",
-    "wo": "k_gemv<0, 2, false, 8, 8>",
+    "qkv": "k_gemv<0, 1, false, 16, 4>",
+    "wo": "k_gemv<0, 2, false, 16, 4>",
     "w13": "k_gemv<0, 3, false, 8, 8>",
     "w2": "k_gemv<0, 2, false, 16, 16>",
 }
