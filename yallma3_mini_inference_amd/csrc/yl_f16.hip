@@ -174,7 +174,9 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
                 for (int k = 1; k < PW; k++) r = min(r, c[k]);
                 if (r > t) return r;
             }
-            if (fault && lane == 0) __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            // (every lane stores the same word: no divergent branch in the
+            // chain's control flow, which stays in scalar registers)
+            if (fault) __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             return ntile;
         };
         // the chain's adds go first when a product wavefront shares the SIMD
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
         const int myrow = lane < R ? lane : R - 1;
         float acc = 0.0f;
         vf4 ra[16], rb[16];
-        int ready = refresh(0);
+        int ready = __builtin_amdgcn_readfirstlane(refresh(0));
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         fg_read_row<R>(ra, P, 0, myrow);
         // two tiles per trip: ra holds tile t, rb is read with tile t + 1
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
         // previous tile's adds
         for (int t = 0; t < ntile; t += 2) {
             const int t1 = t + 1 < ntile ? t + 1 : t;
-            if (t1 >= ready) ready = refresh(t1);
+            if (t1 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t1));
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             fg_read_row<R>(rb, P, t1 % SL, myrow);
             __builtin_amdgcn_sched_barrier(0);
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
                 break;
             }
             const int t2 = t + 2 < ntile ? t + 2 : t + 1;
-            if (t2 >= ready) ready = refresh(t2);
+            if (t2 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t2));
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             fg_read_row<R>(ra, P, t2 % SL, myrow);
             __builtin_amdgcn_sched_barrier(0);
