@@ -111,12 +111,14 @@ __device__ __forceinline__ float fg_add_row(float acc, const vf4 (&v)[16], int k
 
 // PRO 1: x <- RMSNorm(x) * norm_w first.  EPI 0: out[r] = sum; EPI 1: out[r]
 // += sum (the residual add); EPI 2 (R = 64): out[32 * blockIdx.x + c] =
-// silu(g) * u of rows (c, c + 32) of the workgroup (forward.rs:220-237).
+// silu(g) * u of rows (c, c + 32) of the workgroup (forward.rs:220-237);
+// EPI 3: the QKV step (F16Qkv): pairs of adjacent rows rotated, q stored, k
+// and v assigned into the caches (forward.rs:149-179 with the F16Kernel).
 template <int PRO, int EPI, int R>
 __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __restrict__ w, int n, int o,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ norm_w, float eps,
-                                                            float* __restrict__ out, unsigned* fault) {
+                                                            float* __restrict__ out, unsigned* fault, F16Qkv qa) {
     using Sh = FgShape<R>;
     constexpr int PW = Sh::PW, CPL = Sh::CPL, D = Sh::D, SF = Sh::slot_floats, SL = Sh::slots;
     static_assert(EPI != 2 || R == 2 * kFgPairRows, "SwiGLU tiles are 64 rows");
@@ -215,7 +217,30 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
         }
         const int row = row0 + lane;
-        if constexpr (EPI == 2) {
+        if constexpr (EPI == 3) {
+            // rope_gguf (util.rs:653-718) on rows (2i, 2i+1), or util::rope's
+            // pair (j, j + head/2) stored there (qk_column); the partner row
+            // is the neighbouring lane (R is even, rows start even)
+            const float other = dpp_mov<0xB1>(acc);   // quad_perm [1,0,3,2]: lane ^ 1
+            if (lane < R && row < o) {
+                const int pos = qa.st->pos;
+                const int att = qa.att, kv = qa.kv, hd = qa.hd;
+                if (row >= att + kv) {
+                    qa.v_cache[(size_t)pos * kv + (row - att - kv)] = acc;
+                } else {
+                    const int scol = row < att ? row : row - att;
+                    const int col = qk_column(scol, hd, qa.hf);
+                    const int pair = (scol % hd) >> 1;
+                    const float c = qa.rope_cos[(size_t)pos * (hd >> 1) + pair];
+                    const float sn = qa.rope_sin[(size_t)pos * (hd >> 1) + pair];
+                    const bool odd = row & 1;
+                    const float v0 = odd ? other : acc, v1 = odd ? acc : other;
+                    const float r = odd ? fadd(fmul(v0, sn), fmul(v1, c)) : fmul(v0, c) - fmul(v1, sn);
+                    if (row < att) qa.q_out[col] = r;
+                    else qa.k_cache[(size_t)col * qa.kv_ld + pos] = r;
+                }
+            }
+        } else if constexpr (EPI == 2) {
             const float u = __shfl_down(acc, kFgPairRows, 64);
             if (lane < kFgPairRows) {
                 const float den = fadd(1.0f, expf_rn(-acc));
@@ -427,10 +452,14 @@ __global__ void k_qkv_f16(const float* __restrict__ raw, const float* __restrict
         const bool isq = i < nq;
         const int p = isq ? i : i - nq;            // pair index within q or k
         const int head = p / half, j = p % half;
-        const int e0 = head * hd + (hf_pairs ? j : 2 * j), e1 = e0 + (hf_pairs ? half : 1);
+        // hf_pairs 0: pairs (2j, 2j+1); 1: (j, j + half); 2: util::rope's pair
+        // (j, j + half) whose rows are stored at (2j, 2j+1) (qk_column): read
+        // there, written to columns (j, j + half)
+        const int e0 = head * hd + (hf_pairs == 0 ? 2 * j : j), e1 = e0 + (hf_pairs == 0 ? 1 : half);
+        const int s0 = hf_pairs == 2 ? head * hd + 2 * j : e0, s1 = hf_pairs == 2 ? s0 + 1 : e1;
         const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
         const float* src = isq ? r : r + att;
-        const float v0 = src[e0], v1 = src[e1];
+        const float v0 = src[s0], v1 = src[s1];
         const float a = fmul(v0, c) - fmul(v1, s);
         const float b = fadd(fmul(v0, s), fmul(v1, c));
         if (isq) {
@@ -458,7 +487,7 @@ hipError_t launch_matmul_f16(const uint16_t* w, int n, int o, const float* x, in
 
 template <int PRO, int EPI, int R>
 static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps,
-                            float* out, hipStream_t s) {
+                            float* out, hipStream_t s, const F16Qkv& qa = F16Qkv{}) {
     const size_t lds = fg_lds_floats(n, PRO, R) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto k = k_f16_gemv<PRO, EPI, R>;
@@ -470,7 +499,7 @@ static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, con
         raised = true;
     }
     hipLaunchKernelGGL(k, dim3((o + R - 1) / R), dim3(FgShape<R>::threads), lds, s, w, n, o, x, norm_w, eps, out,
-                       wait_fault_word(false));
+                       wait_fault_word(false), qa);
     return hipGetLastError();
 }
 
@@ -479,17 +508,21 @@ static hipError_t launch_fg(const uint16_t* w, int n, int o, const float* x, con
 // with the first and halve both)
 template <int PRO, int EPI>
 static hipError_t launch_fg_rows(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps,
-                                 float* out, hipStream_t s) {
-    if (o <= 256 * 8) return launch_fg<PRO, EPI, 8>(w, n, o, x, norm_w, eps, out, s);
-    if (o <= 256 * 16) return launch_fg<PRO, EPI, 16>(w, n, o, x, norm_w, eps, out, s);
-    if (o <= 256 * 32) return launch_fg<PRO, EPI, 32>(w, n, o, x, norm_w, eps, out, s);
-    return launch_fg<PRO, EPI, 64>(w, n, o, x, norm_w, eps, out, s);
+                                 float* out, hipStream_t s, const F16Qkv& qa = F16Qkv{}) {
+    if (o <= 256 * 8) return launch_fg<PRO, EPI, 8>(w, n, o, x, norm_w, eps, out, s, qa);
+    if (o <= 256 * 16) return launch_fg<PRO, EPI, 16>(w, n, o, x, norm_w, eps, out, s, qa);
+    if (o <= 256 * 32) return launch_fg<PRO, EPI, 32>(w, n, o, x, norm_w, eps, out, s, qa);
+    return launch_fg<PRO, EPI, 64>(w, n, o, x, norm_w, eps, out, s, qa);
 }
 
 hipError_t launch_f16_gemv(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps, int epi,
-                           float* out, hipStream_t s) {
-    if (n % 32 || n <= 0 || o <= 0 || epi < 0 || epi > 2 || (epi == 2 && o % (2 * kFgPairRows)))
+                           float* out, hipStream_t s, const F16Qkv* qkv) {
+    if (n % 32 || n <= 0 || o <= 0 || epi < 0 || epi > 3 || (epi == 2 && o % (2 * kFgPairRows)))
         return hipErrorInvalidValue;
+    if (epi == 3) {
+        if (!qkv || !norm_w || qkv->hd % 2 || qkv->att % qkv->hd || o != qkv->att + 2 * qkv->kv) return hipErrorInvalidValue;
+        return launch_fg_rows<1, 3>(w, n, o, x, norm_w, eps, out, s, *qkv);
+    }
     if (epi == 2) {
         if (norm_w) return launch_fg<1, 2, 64>(w, n, o, x, norm_w, eps, out, s);
         return launch_fg<0, 2, 64>(w, n, o, x, norm_w, eps, out, s);

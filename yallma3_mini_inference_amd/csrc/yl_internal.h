@@ -235,8 +235,19 @@ hipError_t launch_rope_cache(const float* cos_t, const float* sin_t, const StepS
 // One token through f16 weights with the chain fed from LDS (o % 16 == 0):
 // norm_w non-null applies RMSNorm to x first; epi 0 store, 1 add, 2 SwiGLU
 // of the 8-row gate/up pairs of each 16-row block -> out[o / 2].
+// The F16 one-token QKV epilogue (epi 3): rows [q | k | v] rotated in
+// pairs of adjacent rows (rope_gguf pairs, or util::rope pairs stored in pair
+// order when hf: qk_column), q to q_out, k and v assigned into the caches at
+// position st->pos (keys transposed [kv][kv_ld]).
+struct F16Qkv {
+    float* q_out = nullptr; float* k_cache = nullptr; float* v_cache = nullptr;
+    const float* rope_cos = nullptr; const float* rope_sin = nullptr;   // [ctx][head/2]
+    const StepState* st = nullptr;
+    int att = 0, kv = 0, hd = 0, kv_ld = 0, hf = 0;
+};
 hipError_t launch_f16_gemv(const uint16_t* w, int n, int o, const float* x, const float* norm_w, float eps, int epi,
-                           float* out, hipStream_t s);
+                           float* out, hipStream_t s,
+                           const F16Qkv* qkv = nullptr);
 // raw [batch][2 * hidden] in that pair layout -> h [batch][hidden]
 hipError_t launch_swiglu_pairs(const float* raw, int hidden, int batch, float* h, hipStream_t s);
 hipError_t launch_qkv_f16(const float* raw, const float* cos_t, const float* sin_t, const StepState* st, int batch,

@@ -740,10 +740,16 @@ yl_model* model_from_host(HostModel& h, yl_status* st) {
         if (!L.rms_att || !L.rms_ffn) { set_error(err); return nullptr; }
         bool ok;
         if (m->f16) {
+            // q, k and v rows in one matrix, q and k in util::rope's pair
+            // order as below (the QKV GEMV rotates adjacent rows)
             HostQMat qkv;
             qkv.fmt = kF16; qkv.n = H[0].n; qkv.o = H[0].o + H[1].o + H[2].o;
             for (int k = 0; k < 3; k++)
-                qkv.qs.insert(qkv.qs.end(), (const uint8_t*)H[k].h.data(), (const uint8_t*)H[k].h.data() + H[k].h.size() * 2);
+                for (size_t p = 0; p < H[k].o; p++) {
+                    const size_t r = k < 2 ? (size_t)qk_column((int)p, m->hd, 1) : p;
+                    const uint8_t* src = (const uint8_t*)(H[k].h.data() + r * H[k].n);
+                    qkv.qs.insert(qkv.qs.end(), src, src + H[k].n * 2);
+                }
             HostQMat w13;
             f16_pair_rows(H[4].h.data(), H[6].h.data(), H[4].o, H[4].n, &w13);
             ok = upload_qmat(qkv, &L.qkv, &err) && upload_hostmat(H[3], &L.wo, &err) && upload_qmat(w13, &L.w13, &err) &&
@@ -1075,10 +1081,15 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
         const int qkv_n = m->att + 2 * m->kv;
         if (bytes) *bytes = (uint64_t)qkv_n * m->dim * 2 + B * ((uint64_t)m->dim * 4 + (uint64_t)qkv_n * 4);
         if (l == 0) e = launch_embed(m->emb, tok, batch, s->x, st);
-        if (one) {   // RMSNorm inside the GEMV
+        if (one) {   // RMSNorm, RoPE and the cache writes inside the GEMV
+            F16Qkv qa;
+            qa.q_out = s->sq; qa.k_cache = kc; qa.v_cache = vc;
+            qa.rope_cos = m->rope_cos; qa.rope_sin = m->rope_sin; qa.st = s->st;
+            qa.att = m->att; qa.kv = m->kv; qa.hd = m->hd; qa.kv_ld = m->kv_ld; qa.hf = m->hf_rope;
             if (e == hipSuccess)
-                e = launch_f16_gemv((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->x, L.rms_att, m->eps, 0, s->qkv_raw,
-                                    st);
+                e = launch_f16_gemv((const uint16_t*)L.qkv.qs, m->dim, qkv_n, s->x, L.rms_att, m->eps, 3, nullptr,
+                                    st, &qa);
+            return e;
         } else {
             if (e == hipSuccess)
                 e = launch_rmsnorm(-1, s->x, L.rms_att, m->dim, m->eps, batch, s->xn, nullptr, nullptr, st);
@@ -1087,7 +1098,7 @@ hipError_t enqueue_op_f16(const yl_model* m, yl_session* s, int cls, int l, int 
         }
         if (e == hipSuccess)
             e = launch_qkv_f16(s->qkv_raw, m->rope_cos, m->rope_sin, s->st, batch, s->sq, kc, vc, m->att, m->kv, m->hd,
-                               m->kv_ld, m->hf_rope, st);
+                               m->kv_ld, m->hf_rope ? 2 : 0, st);
         return e;
     }
     case kOpAttn:
