@@ -87,25 +87,37 @@ __host__ __device__ inline size_t fg_lds_floats(int n, int pro, int R) {
 
 __device__ __forceinline__ float f16_prod(uint32_t bits16, float x) { return fmul(h2f(bits16), x); }
 
-// 16 product reads (one tile row: 64 floats) of row `row` from slot `s`
+// half h of a tile row of products (32 floats, 8 reads) of row `row` from
+// slot `s`
 template <int R>
-__device__ __forceinline__ void fg_read_row(vf4 (&v)[16], const float* P, int s, int row) {
-    const vf4* r = reinterpret_cast<const vf4*>(P + s * FgShape<R>::slot_floats + row * kFgStride);
+__device__ __forceinline__ void fg_read_half(vf4 (&v)[16], const float* P, int s, int row, int h) {
+    const vf4* r = reinterpret_cast<const vf4*>(P + s * FgShape<R>::slot_floats + row * kFgStride) + 8 * h;
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = r[i];
+    for (int i = 0; i < 8; i++) v[8 * h + i] = r[i];
 }
-// the serial adds of one tile row (kn = 64 or 32 columns)
-__device__ __forceinline__ float fg_add_row(float acc, const vf4 (&v)[16], int kn) {
+// the serial adds of half h of a tile row
+__device__ __forceinline__ float fg_add_half(float acc, const vf4 (&v)[16], int h) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 8 * h; i < 8 * h + 8; i++) {
         acc = fadd(acc, v[i].x); acc = fadd(acc, v[i].y); acc = fadd(acc, v[i].z); acc = fadd(acc, v[i].w);
     }
-    if (kn > 32) {
-#pragma unroll
-        for (int i = 8; i < 16; i++) {
-            acc = fadd(acc, v[i].x); acc = fadd(acc, v[i].y); acc = fadd(acc, v[i].z); acc = fadd(acc, v[i].w);
-        }
-    }
+    return acc;
+}
+// The adds of tile row `cur` (kn = 64 or 32 columns) with the reads of the
+// next tile's row into `nxt` issued half by half ahead of them: at most 8
+// reads are new when an add waits, so the 4-bit LDS wait count (15) never
+// makes an add wait for a read of the next tile.
+template <int R>
+__device__ __forceinline__ float fg_add_tile(float acc, const vf4 (&cur)[16], vf4 (&nxt)[16], const float* P, int s,
+                                             int row, int kn) {
+    fg_read_half<R>(nxt, P, s, row, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    acc = fg_add_half(acc, cur, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    fg_read_half<R>(nxt, P, s, row, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kn > 32) acc = fg_add_half(acc, cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
     return acc;
 }
 
@@ -189,18 +201,15 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
         vf4 ra[16], rb[16];
         int ready = __builtin_amdgcn_readfirstlane(refresh(0));
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        fg_read_row<R>(ra, P, 0, myrow);
+        fg_read_half<R>(ra, P, 0, myrow, 0);
+        fg_read_half<R>(ra, P, 0, myrow, 1);
         // two tiles per trip: ra holds tile t, rb is read with tile t + 1
-        // (or tile t again past the end: every read is unconditional), and
-        // the scheduling barriers keep each tile's reads ahead of the
-        // previous tile's adds
+        // (or tile t again past the end: every read is unconditional)
         for (int t = 0; t < ntile; t += 2) {
             const int t1 = t + 1 < ntile ? t + 1 : t;
             if (t1 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t1));
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            fg_read_row<R>(rb, P, t1 % SL, myrow);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = fg_add_row(acc, ra, min(kFgKT, n - t * kFgKT));
+            acc = fg_add_tile<R>(acc, ra, rb, P, t1 % SL, myrow, min(kFgKT, n - t * kFgKT));
             if (t + 1 >= ntile) {
                 lds_arrive_nowait(ctr + 4);
                 break;
@@ -208,12 +217,11 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
             const int t2 = t + 2 < ntile ? t + 2 : t + 1;
             if (t2 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t2));
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            fg_read_row<R>(ra, P, t2 % SL, myrow);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = fg_add_row(acc, rb, min(kFgKT, n - (t + 1) * kFgKT));
+            acc = fg_add_tile<R>(acc, rb, ra, P, t2 % SL, myrow, min(kFgKT, n - (t + 1) * kFgKT));
             // tiles t and t + 1 consumed (one count per two tiles)
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (lane == 0) __hip_atomic_fetch_add(ctr + 4, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            // (a store: the chain wavefront is the counter's one writer)
+            if (lane == 0) __hip_atomic_store(ctr + 4, t + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
         }
         const int row = row0 + lane;
