@@ -203,26 +203,32 @@ __global__ __launch_bounds__(kFgThreadsMax) void k_f16_gemv(const uint16_t* __re
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         fg_read_half<R>(ra, P, 0, myrow, 0);
         fg_read_half<R>(ra, P, 0, myrow, 1);
-        // two tiles per trip: ra holds tile t, rb is read with tile t + 1
-        // (or tile t again past the end: every read is unconditional)
-        for (int t = 0; t < ntile; t += 2) {
-            const int t1 = t + 1 < ntile ? t + 1 : t;
-            if (t1 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t1));
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            acc = fg_add_tile<R>(acc, ra, rb, P, t1 % SL, myrow, min(kFgKT, n - t * kFgKT));
-            if (t + 1 >= ntile) {
-                lds_arrive_nowait(ctr + 4);
-                break;
+        // two tiles per pair: ra holds tile t, rb is read with tile t + 1.
+        // Eight tiles per trip, so every slot index is a constant and the
+        // reads address LDS by immediate offsets from one register; a read
+        // past the last tile reads a stale slot whose adds never run.
+        static_assert(8 % SL == 0, "slots per trip");
+        for (int t0 = 0; t0 < ntile; t0 += 8) {
+#pragma unroll
+            for (int k = 0; k < 8; k += 2) {
+                const int t = t0 + k;
+                if (t >= ntile) break;
+                if (t + 1 < ntile && t + 1 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t + 1));
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                acc = fg_add_tile<R>(acc, ra, rb, P, (k + 1) % SL, myrow, min(kFgKT, n - t * kFgKT));
+                if (t + 1 >= ntile) {
+                    lds_arrive_nowait(ctr + 4);
+                    break;
+                }
+                if (t + 2 < ntile && t + 2 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t + 2));
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                acc = fg_add_tile<R>(acc, rb, ra, P, (k + 2) % SL, myrow, min(kFgKT, n - (t + 1) * kFgKT));
+                // tiles t and t + 1 consumed (one count per two tiles; a
+                // store: the chain wavefront is the counter's one writer)
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (lane == 0) __hip_atomic_store(ctr + 4, t + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
             }
-            const int t2 = t + 2 < ntile ? t + 2 : t + 1;
-            if (t2 >= ready) ready = __builtin_amdgcn_readfirstlane(refresh(t2));
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            acc = fg_add_tile<R>(acc, rb, ra, P, t2 % SL, myrow, min(kFgKT, n - (t + 1) * kFgKT));
-            // tiles t and t + 1 consumed (one count per two tiles)
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            // (a store: the chain wavefront is the counter's one writer)
-            if (lane == 0) __hip_atomic_store(ctr + 4, t + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
         }
         const int row = row0 + lane;
         if constexpr (EPI == 3) {
