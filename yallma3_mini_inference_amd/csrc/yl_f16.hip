@@ -69,7 +69,7 @@ template <int R>
 struct FgShape {
     static constexpr int PW = R == 64 ? 3 : (R == 8 ? 1 : 2);
     static constexpr int CPL = (8 * R + 64 * PW - 1) / (64 * PW);
-    static constexpr int D = R == 8 ? 24 : (R == 16 ? 16 : 8);
+    static constexpr int D = R == 8 ? 12 : (R == 16 ? 8 : (R == 32 ? 8 : 4));
     static constexpr int threads = 64 * (1 + PW);
     static constexpr int slot_floats = R * kFgStride;
     static constexpr int slots = R == 64 ? 4 : 8;   // tiles in the LDS ring
