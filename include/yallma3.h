@@ -399,6 +399,12 @@ typedef struct {
     int32_t embd_format;   /* yl_format of token_embd (Q8_0 or Q4_0) */
     int32_t file_type;     /* general.file_type written (1, 2 or 7) */
     uint64_t seed;
+    /* llama.rope.scaling.{factor, ext_factor, attn_factor,
+     * original_context_length}: written when rope_scaling is nonzero */
+    int32_t rope_scaling;
+    float rope_scaling_factor, rope_ext_factor, rope_attn_factor;
+    uint32_t rope_original_ctx;
+    float attention_scale;  /* llama.attention.scale: written when nonzero */
 } yl_synth_config;
 
 /* Writes a deterministic GGUF v3 llama model: every weight ~N(0, weight_std)

@@ -238,14 +238,11 @@ void yo_rmsnorm(float *o, const float *x, const float *weight, size_t size, floa
     for (size_t i = 0; i < n_simd * 8; i++) o[i] = weight[i] * (ss * x[i]);
 }
 
-/* util.rs:720-724 */
+/* util.rs:720-724.  Rust's f32 max/min return the other operand when one
+ * is NaN, which is C's fmaxf/fminf. */
 static float rope_yarn_ramp(float low, float high, float i0) {
-    float d = high - low;
-    if (d < 0.001f) d = 0.001f;
-    float y = (i0 * 0.5f - low) / d;
-    if (y < 0.0f) y = 0.0f;
-    if (y > 1.0f) y = 1.0f;
-    return 1.0f - y;
+    const float y = (i0 * 0.5f - low) / fmaxf(high - low, 0.001f);
+    return 1.0f - fminf(1.0f, fmaxf(y, 0.0f));
 }
 
 /* The per-pair (cos, sin) of util.rs:653-718 at position `pos`. */
@@ -257,8 +254,7 @@ void yo_rope_cos_sin(const yo_rope_params *p, uint32_t pos, float *cos_out, floa
     const float n_ctx_orig = (float)p->original_ctx_len;
     float corr_start = fmaf(logf(n_ctx_orig / (beta_fast * two_pi)), (float)p->head_size, 0.0f) /
                        (2.0f * logf(p->rope_theta));
-    corr_start = floorf(corr_start);
-    if (corr_start < 0.0f) corr_start = 0.0f;
+    corr_start = fmaxf(floorf(corr_start), 0.0f);
     float corr_end = fmaf(logf(n_ctx_orig / (beta_slow * two_pi)), (float)p->head_size, 0.0f) /
                      (2.0f * logf(p->rope_theta));
     float corr_dims_1 = fminf(corr_start, corr_end) + fminf(corr_end, (float)n_pairs) - fmaxf(corr_start, 0.0f);

@@ -177,13 +177,24 @@ def write(path: str, meta: list, tensors: list, alignment: int = 32) -> None:
 
 
 def llama_meta(dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx, file_type=7, rope_theta=10000.0,
-               eps=1e-5):
-    return [("general.architecture", _STR, "llama"), ("general.file_type", _U32, file_type),
+               eps=1e-5, rope_scaling=None, attention_scale=None):
+    """rope_scaling: (factor, ext_factor, attn_factor, original_context_length)
+    written as the llama.rope.scaling.* keys; attention_scale as
+    llama.attention.scale."""
+    meta = [("general.architecture", _STR, "llama"), ("general.file_type", _U32, file_type),
             ("llama.embedding_length", _U32, dim), ("llama.feed_forward_length", _U32, hidden),
             ("llama.block_count", _U32, n_layers), ("llama.attention.head_count", _U32, n_heads),
             ("llama.attention.head_count_kv", _U32, n_kv_heads), ("llama.context_length", _U32, ctx),
             ("llama.rope.freq_base", _F32, rope_theta), ("llama.attention.layer_norm_rms_epsilon", _F32, eps),
             ("tokenizer.ggml.tokens", _ARR, (_STR, [f"<t{i}>" for i in range(vocab)]))]
+    if rope_scaling is not None:
+        f, e, a, n = rope_scaling
+        meta += [("llama.rope.scaling.factor", _F32, f), ("llama.rope.scaling.ext_factor", _F32, e),
+                 ("llama.rope.scaling.attn_factor", _F32, a),
+                 ("llama.rope.scaling.original_context_length", _U32, n)]
+    if attention_scale is not None:
+        meta.append(("llama.attention.scale", _F32, attention_scale))
+    return meta
 
 
 # ------------------------------------------------- float64 forward (forward.rs)
@@ -215,13 +226,10 @@ def _rmsnorm(x, w, eps):
     return w * (x / np.sqrt(np.mean(x * x) + eps))
 
 
-def _rope_pairs(v, pos, head_size, theta_base, neox=False):
-    """rope_gguf with the defaults (util.rs:653-718): consecutive pairs
-    (2k, 2k+1), angle pos * base^(-2k/head_size) for pair k.  neox=True pairs
+def _rope_pairs(v, c, s, head_size, neox=False):
+    """rope_gguf's rotation (util.rs:653-718) with pair k's (cos, sin):
+    consecutive pairs (2k, 2k+1) of every head.  neox=True pairs
     (k, k + head_size/2) instead (the HF layout, a negative control)."""
-    k = np.arange(head_size // 2, dtype=np.float64)
-    ang = pos * theta_base ** (-2.0 * k / head_size)
-    c, s = np.cos(ang), np.sin(ang)
     if neox:
         out = v.copy().reshape(-1, 2, head_size // 2)
         a, b = out[:, 0].copy(), out[:, 1].copy()
@@ -235,7 +243,48 @@ def _rope_pairs(v, pos, head_size, theta_base, neox=False):
     return out.reshape(-1)
 
 
-VARIANTS = ("reference", "q4_ggml_order", "rope_neox", "gate_up_swapped", "norms_swapped", "no_attn_scale")
+YARN_VARIANTS = ("yarn_interp_in_mix", "yarn_no_floor", "yarn_no_attn_factor", "yarn_ramp_reversed")
+
+
+def yarn_cos_sin(pos, head_size, base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, n_ctx_orig=4096,
+                 variant="reference"):
+    """rope_gguf's per-pair (cos, sin) (util.rs:653-724) in float64, from the
+    closed form of the angle: pair k's base angle is pos * base^(-2k/head_size)
+    (the reference's `theta *= theta_scale` recurrence, unrounded).  With
+    freq_scale = 1/factor, YaRN's ramp between the correction dims
+    low = max(floor(head_size * ln(n_ctx_orig / (2 pi * 32)) / (2 ln base)), 0)
+    and high = min(low, c) + min(c, head_size/2) - low, where
+    c = head_size * ln(n_ctx_orig / (2 pi)) / (2 ln base), gives
+    ramp(k) = 1 - clamp((k - low) / max(high - low, 0.001), 0, 1) and the angle
+    t = freq_scale*theta*(1 - ramp*ext) + theta*ramp*ext; both are scaled by
+    attn_factor.  A `variant` from YARN_VARIANTS plants one mistake: the mix
+    with freq_scale*theta in place of theta, corr_start without floor, no
+    attn_factor, or the ramp reversed."""
+    n_pairs = head_size // 2
+    k = np.arange(n_pairs, dtype=np.float64)
+    theta = pos * float(base) ** (-2.0 * k / head_size)
+    ln_b2 = 2.0 * np.log(float(base))
+    cs = head_size * np.log(n_ctx_orig / (2.0 * np.pi * 32.0)) / ln_b2
+    low = max(cs if variant == "yarn_no_floor" else np.floor(cs), 0.0)
+    ce = head_size * np.log(n_ctx_orig / (2.0 * np.pi)) / ln_b2
+    high = min(low, ce) + min(ce, float(n_pairs)) - max(low, 0.0)
+    interp = freq_scale * theta
+    t = interp
+    if ext_factor != 0.0:
+        ramp = 1.0 - np.clip((k - low) / max(high - low, 0.001), 0.0, 1.0)
+        if variant == "yarn_ramp_reversed":
+            ramp = 1.0 - ramp
+        mix = ramp * ext_factor
+        t = interp * (1.0 - mix) + (interp if variant == "yarn_interp_in_mix" else theta) * mix
+    a = 1.0 if variant == "yarn_no_attn_factor" else attn_factor
+    return a * np.cos(t), a * np.sin(t)
+
+
+# mistakes visible on any model, and those that need the YaRN keys and
+# llama.attention.scale to be present
+BASE_VARIANTS = ("q4_ggml_order", "rope_neox", "gate_up_swapped", "norms_swapped", "no_attn_scale")
+SCALING_VARIANTS = YARN_VARIANTS + ("attention_scale_ignored",)
+VARIANTS = ("reference",) + BASE_VARIANTS + SCALING_VARIANTS
 
 
 class Float64Model:
@@ -257,6 +306,13 @@ class Float64Model:
         self.kv_dim = self.n_kv * self.hd
         self.eps = float(m["llama.attention.layer_norm_rms_epsilon"])
         self.theta = float(m.get("llama.rope.freq_base", 10000.0))
+        # YaRN keys and the attention scale (transformer_llama_gguf.rs:242-249)
+        raw = float(m.get("llama.rope.scaling.factor", 1.0))
+        self.freq_scale = 1.0 / raw if raw != 0.0 else 1.0
+        self.ext_factor = float(m.get("llama.rope.scaling.ext_factor", 0.0))
+        self.attn_factor = float(m.get("llama.rope.scaling.attn_factor", 1.0))
+        self.n_ctx_orig = int(m.get("llama.rope.scaling.original_context_length", m["llama.context_length"]))
+        self.attention_scale = float(m.get("llama.attention.scale", 0.0))
         self.vocab = len(m["tokenizer.ggml.tokens"])
         order = "ggml" if variant == "q4_ggml_order" else "reference"
         if g.tensor_type("token_embd.weight") in (T_Q8_0, T_Q4_0):
@@ -296,7 +352,9 @@ class Float64Model:
             k = self._mm(l, "attn_k", xn, self.kv_dim, self.dim)
             v = self._mm(l, "attn_v", xn, self.kv_dim, self.dim)
             neox = self.variant == "rope_neox"
-            q, k = _rope_pairs(q, pos, self.hd, self.theta, neox), _rope_pairs(k, pos, self.hd, self.theta, neox)
+            c, sn = yarn_cos_sin(pos, self.hd, self.theta, self.freq_scale, self.ext_factor, self.attn_factor,
+                                 self.n_ctx_orig, self.variant)
+            q, k = _rope_pairs(q, c, sn, self.hd, neox), _rope_pairs(k, c, sn, self.hd, neox)
             newk[l, 0], newv[l, 0] = k, v
             K = np.concatenate([self.k[l], k[None]], 0)
             V = np.concatenate([self.v[l], v[None]], 0)
@@ -306,7 +364,9 @@ class Float64Model:
                 kvh = h // r
                 sl = slice(kvh * self.hd, (kvh + 1) * self.hd)
                 s = K[:, sl] @ q[h * self.hd:(h + 1) * self.hd]
-                if self.variant != "no_attn_scale":
+                if self.attention_scale != 0.0 and self.variant != "attention_scale_ignored":
+                    s = s * self.attention_scale   # llama.attention.scale (forward.rs:142-146)
+                elif self.variant != "no_attn_scale":
                     s = s / np.sqrt(self.hd)
                 p = np.exp(s - s.max())
                 p /= p.sum()
@@ -343,7 +403,8 @@ def _rand_q4(rng, rows, cols, std):
 
 def random_llama(path, dim=64, hidden=128, n_layers=2, n_heads=2, n_kv_heads=1, vocab=96, ctx=64,
                  attn_fmt=T_Q8_0, ffn_fmt=T_Q8_0, embd_fmt=T_Q8_0, seed=0, rope_theta=10000.0,
-                 nan_embedding_rows=(), nan_output_norm=False, emb_std=0.5, w_std=0.05):
+                 nan_embedding_rows=(), nan_output_norm=False, emb_std=0.5, w_std=0.05, rope_scaling=None,
+                 attention_scale=None):
     """A random llama GGUF whose norm weights differ per tensor (so a swapped
     norm changes the result), with optional NaN block scales in chosen rows
     of the token embedding or a NaN final-norm weight."""
@@ -380,7 +441,8 @@ def random_llama(path, dim=64, hidden=128, n_layers=2, n_heads=2, n_kv_heads=1, 
                     qt(p + "ffn_up.weight", hidden, dim, ffn_fmt)]
     ft = 2 if attn_fmt == ffn_fmt == T_Q4_0 else 7
     write(path, llama_meta(dim, hidden, n_layers, n_heads, n_kv_heads, vocab, ctx, file_type=ft,
-                           rope_theta=rope_theta), tensors)
+                           rope_theta=rope_theta, rope_scaling=rope_scaling, attention_scale=attention_scale),
+          tensors)
     return path
 
 

@@ -1,6 +1,7 @@
 """Writes tests/golden/forward_golden.npz: the oracle's end-to-end results on
-seeded random llama GGUFs built by tests/gguf_np.py (Q8_0, Q4_0, and Q8_0
-attention beside a Q4_0 FFN).  Per model: a prompt's last-token logits, 12
+seeded random llama GGUFs built by tests/gguf_np.py (Q8_0, Q4_0, Q8_0
+attention beside a Q4_0 FFN, and Q8_0 with YaRN RoPE scaling and an explicit
+attention scale).  Per model: a prompt's last-token logits, 12
 greedy token ids after it, and the logits of the last greedy step.
 
     python tests/golden/make_golden.py      (rewrites the fixture)
@@ -26,14 +27,18 @@ MODELS = {
     "q8": (G.T_Q8_0, G.T_Q8_0, G.T_Q8_0, 21, 9),
     "q4": (G.T_Q4_0, G.T_Q4_0, G.T_Q4_0, 22, 17),
     "mixed": (G.T_Q8_0, G.T_Q4_0, G.T_Q8_0, 23, 70),
+    "yarn": (G.T_Q8_0, G.T_Q8_0, G.T_Q8_0, 24, 40),
 }
+# GGUF keys beyond the shape: YaRN RoPE scaling (factor 4 from an original
+# context of 2048, ext_factor 1, attn_factor 1.2) and llama.attention.scale
+EXTRA = {"yarn": dict(rope_scaling=(4.0, 1.0, 1.2, 2048), attention_scale=0.15)}
 
 
 def model_path(name, directory):
     a, f, e, seed, _ = MODELS[name]
     return G.random_llama(os.path.join(directory, f"golden_{name}.gguf"), dim=128, hidden=256, n_layers=2,
                           n_heads=4, n_kv_heads=2, vocab=300, ctx=128, attn_fmt=a, ffn_fmt=f, embd_fmt=e,
-                          seed=seed, rope_theta=500000.0, emb_std=0.05, w_std=0.2)
+                          seed=seed, rope_theta=500000.0, emb_std=0.05, w_std=0.2, **EXTRA.get(name, {}))
 
 
 def prompt(name):

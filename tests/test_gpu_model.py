@@ -23,7 +23,9 @@ def _models(gpu, oracle, model_dir, name):
 
 @pytest.mark.parametrize("name,prompt_len,steps", [("tiny", 20, 24), ("tiny_q4", 17, 16), ("tiny_mixed", 33, 20),
                                                     ("tiny_pad", 9, 12), ("tiny", 100, 6), ("tiny_q4", 130, 4),
-                                                    ("tiny_mixed", 200, 4)])
+                                                    ("tiny_mixed", 200, 4), ("tiny_yarn", 40, 12),
+                                                    ("tiny_yarn", 100, 6), ("tiny_yarn_q4", 70, 8),
+                                                    ("tiny_yarn_q4", 23, 10)])
 def test_prefill_then_greedy_decode(gpu, oracle, model_dir, name, prompt_len, steps):
     g, o, _ = _models(gpu, oracle, model_dir, name)
     rng = np.random.default_rng(prompt_len)
@@ -44,7 +46,7 @@ def test_prefill_then_greedy_decode(gpu, oracle, model_dir, name, prompt_len, st
     assert_bits(gs.value_cache()[:, :pos], os_.value_cache()[:, :pos], "V cache")
 
 
-@pytest.mark.parametrize("name", ["tiny", "tiny_mixed"])
+@pytest.mark.parametrize("name", ["tiny", "tiny_mixed", "tiny_yarn"])
 def test_generate_greedy_matches_oracle_tokens(gpu, oracle, model_dir, name):
     g, o, _ = _models(gpu, oracle, model_dir, name)
     prompt = (np.arange(12, dtype=np.uint32) * 37) % o.vocab
@@ -136,3 +138,31 @@ def test_long_context_decode(gpu, oracle, model_dir):
         tok = oracle.argmax(o.forward_x([tok], 2100 + i, os_))
         ref.append(tok)
     assert list(toks_g) == ref
+
+
+@pytest.mark.parametrize("name,start", [("tiny_yarn", 3000), ("tiny_yarn_q4", 4000)])
+def test_yarn_decode_at_high_positions(gpu, oracle, model_dir, name, start):
+    # YaRN RoPE scaling and llama.attention.scale (util.rs:653-724,
+    # forward.rs:142-146) where the angles are large: a random KV cache below
+    # `start` shared by both sides, then single-token steps and a greedy run
+    g, o, _ = _models(gpu, oracle, model_dir, name)
+    rng = np.random.default_rng(start)
+    L, kvd = o.n_layers, o.n_kv_heads * o.head_size
+    kc = rng.standard_normal((L, start, kvd), dtype=np.float32)
+    vc = rng.standard_normal((L, start, kvd), dtype=np.float32)
+    gs, os_ = g.create_session(), o.create_session()
+    gs.upload_kv(kc, vc)
+    os_.key_cache()[:, :start] = kc
+    os_.value_cache()[:, :start] = vc
+    tok, pos = 7, start
+    for step in range(4):
+        lg, lo = g.forward_x([tok], pos, gs), o.forward_x([tok], pos, os_)
+        assert_bits(lg, lo, f"step {step} logits")
+        tok = oracle.argmax(lo)
+        pos += 1
+    ref = []
+    for i in range(8):
+        ref.append(oracle.argmax(o.forward_x([tok if not ref else ref[-1]], pos + i, os_)))
+    toks = g.generate_greedy(gs, tok, pos, 8)
+    assert list(toks) == ref
+    assert_bits(gs.key_cache()[:, :pos + 8], os_.key_cache()[:, :pos + 8], "K cache")

@@ -228,6 +228,27 @@ def test_rope(gpu, oracle, hd, nh, nkv, theta, pos, batch):
         assert_bits(gk[t], rk)
 
 
+@pytest.mark.parametrize("hd,nh,nkv,theta,fs,ext,attn,orig,pos,batch", [
+    (64, 32, 8, 500000.0, 0.25, 1.0, 1.1, 1024, 0, 1), (64, 4, 2, 10000.0, 0.25, 1.0, 1.1, 1024, 3001, 3),
+    (64, 9, 3, 500000.0, 0.125, 0.5, 0.9, 2048, 777, 2), (128, 32, 8, 500000.0, 1 / 32, 1.0, 1.0, 8192, 8300, 2),
+    (32, 8, 4, 500000.0, 0.25, 1.0, 1.2, 2048, 40, 5), (128, 8, 2, 10000.0, 0.5, 0.5, 1.05, 4096, 20000, 1)])
+def test_rope_yarn(gpu, oracle, hd, nh, nkv, theta, fs, ext, attn, orig, pos, batch):
+    # rope_gguf's YaRN branch (util.rs:653-724): the library's angle table and
+    # rotation against the oracle's, bit for bit
+    from yallma3_mini_inference_amd import ops
+    from yallma3_mini_inference_amd._lib import RopeParams
+    rng = np.random.default_rng(pos + hd)
+    q = rng.normal(0, 1, (batch, nh * hd)).astype(np.float32)
+    k = rng.normal(0, 1, (batch, nkv * hd)).astype(np.float32)
+    gq, gk = ops.rope_gguf(RopeParams(hd, nh, nkv, theta, fs, ext, attn, orig), q, k, pos, batch)
+    op = oracle.rope_params(hd, nh, nkv, theta, fs, ext, attn, orig)
+    for t in range(batch):
+        rq, rk = q[t].copy(), k[t].copy()
+        oracle.rope_gguf(op, rq, rk, pos + t)
+        assert_bits(gq[t], rq)
+        assert_bits(gk[t], rk)
+
+
 @pytest.mark.parametrize("batch,start,nh,nkv,hd", [(1, 0, 4, 2, 64), (1, 700, 32, 8, 64), (7, 13, 9, 3, 64),
                                                    (4, 250, 8, 2, 128), (1, 8447, 4, 1, 128), (1, 4999, 8, 4, 64), (1, 6000, 16, 2, 128), (1, 8191, 32, 8, 128),
                                                    (1, 3000, 9, 3, 64), (1, 2100, 2, 2, 32), (1, 5119, 8, 8, 64),

@@ -63,7 +63,9 @@ class SynthConfig(C.Structure):
                 ("n_kv_heads", C.c_uint32), ("vocab", C.c_uint32), ("ctx_len", C.c_uint32),
                 ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("weight_std", C.c_float),
                 ("attn_format", C.c_int32), ("ffn_format", C.c_int32), ("embd_format", C.c_int32),
-                ("file_type", C.c_int32), ("seed", C.c_uint64)]
+                ("file_type", C.c_int32), ("seed", C.c_uint64), ("rope_scaling", C.c_int32),
+                ("rope_scaling_factor", C.c_float), ("rope_ext_factor", C.c_float), ("rope_attn_factor", C.c_float),
+                ("rope_original_ctx", C.c_uint32), ("attention_scale", C.c_float)]
 
 
 class SynthTokenizer(C.Structure):

@@ -264,8 +264,7 @@ static void rope_table(const yl_rope_params& p, uint32_t pos_begin, uint32_t cou
     const float n_ctx_orig = (float)p.original_ctx_len;
     float corr_start = fmaf(logf(n_ctx_orig / (beta_fast * two_pi)), (float)p.head_size, 0.0f) /
                        (2.0f * logf(p.rope_theta));
-    corr_start = floorf(corr_start);
-    if (corr_start < 0.0f) corr_start = 0.0f;
+    corr_start = fmaxf(floorf(corr_start), 0.0f);   // Rust's f32::max: NaN gives the other operand
     const float corr_end = fmaf(logf(n_ctx_orig / (beta_slow * two_pi)), (float)p.head_size, 0.0f) /
                            (2.0f * logf(p.rope_theta));
     const float corr_dims_1 =
@@ -276,11 +275,9 @@ static void rope_table(const yl_rope_params& p, uint32_t pos_begin, uint32_t cou
             const float theta_interp = p.freq_scale * theta / 1.0f;
             float t = theta_interp;
             if (p.ext_factor != 0.0f) {
-                float dd = corr_dims_1 - corr_start;
-                if (dd < 0.001f) dd = 0.001f;
-                float y = ((float)(k * 2) * 0.5f - corr_start) / dd;
-                y = y < 0.0f ? 0.0f : (y > 1.0f ? 1.0f : y);
-                const float ramp_mix = (1.0f - y) * p.ext_factor;
+                // rope_yarn_ramp(corr_start, corr_dims_1, 2k) (util.rs:720-724)
+                const float y = ((float)(k * 2) * 0.5f - corr_start) / fmaxf(corr_dims_1 - corr_start, 0.001f);
+                const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(y, 0.0f))) * p.ext_factor;
                 t = theta_interp * (1.0f - ramp_mix) + theta / 1.0f * ramp_mix;
             }
             cos_t[(size_t)r * n_pairs + k] = cosf(t) * p.attn_factor;

@@ -268,9 +268,10 @@ static yl_status write_gguf(const char* path, const yl_synth_config* c, const yl
     Writer w;
     w.f = fopen(path, "wb");
     if (!w.f) { yl::set_error(std::string("cannot create ") + path); return YL_ERR_IO; }
-    const uint32_t n_kv = 15 + (tk ? (tk->n_merges ? 1 : 0) + (tk->pre ? 1 : 0) + (tk->chat_template ? 1 : 0) +
-                                         (tk->add_bos_token >= 0 ? 1 : 0) + (tk->add_space_prefix >= 0 ? 1 : 0)
-                                    : 0);
+    const uint32_t n_kv = 15 + (c->rope_scaling ? 4 : 0) + (c->attention_scale != 0.0f ? 1 : 0) +
+                          (tk ? (tk->n_merges ? 1 : 0) + (tk->pre ? 1 : 0) + (tk->chat_template ? 1 : 0) +
+                                    (tk->add_bos_token >= 0 ? 1 : 0) + (tk->add_space_prefix >= 0 ? 1 : 0)
+                              : 0);
     w.u32(0x46554747u);
     w.u32(3);
     w.u64(ts.size());
@@ -287,6 +288,14 @@ static yl_status write_gguf(const char* path, const yl_synth_config* c, const yl
     w.kv_u32("llama.attention.head_count_kv", c->n_kv_heads);
     w.kv_f32("llama.attention.layer_norm_rms_epsilon", c->rms_eps);
     w.kv_f32("llama.rope.freq_base", c->rope_theta);
+    if (c->rope_scaling) {
+        // the YaRN keys rope_gguf reads (transformer_llama_gguf.rs:242-248)
+        w.kv_f32("llama.rope.scaling.factor", c->rope_scaling_factor);
+        w.kv_f32("llama.rope.scaling.ext_factor", c->rope_ext_factor);
+        w.kv_f32("llama.rope.scaling.attn_factor", c->rope_attn_factor);
+        w.kv_u32("llama.rope.scaling.original_context_length", c->rope_original_ctx);
+    }
+    if (c->attention_scale != 0.0f) w.kv_f32("llama.attention.scale", c->attention_scale);
     w.kv_u32("tokenizer.ggml.bos_token_id", tk ? tk->bos : 1);
     w.kv_u32("tokenizer.ggml.eos_token_id", tk ? tk->eos : 2);
     w.str("tokenizer.ggml.tokens");

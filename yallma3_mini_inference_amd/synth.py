@@ -36,11 +36,17 @@ class ModelConfig:
     embd_format: int = Q8
     file_type: int = 7
     seed: int = 0
+    # llama.rope.scaling.{factor, ext_factor, attn_factor, original_context_length}
+    # (written when not None) and llama.attention.scale (written when nonzero)
+    rope_scaling: tuple | None = None
+    attention_scale: float = 0.0
 
     def to_c(self) -> SynthConfig:
+        sc = self.rope_scaling or (0.0, 0.0, 0.0, 0)
         return SynthConfig(self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.vocab,
                            self.ctx_len, self.rope_theta, self.rms_eps, self.weight_std, int(self.attn_format),
-                           int(self.ffn_format), int(self.embd_format), self.file_type, self.seed)
+                           int(self.ffn_format), int(self.embd_format), self.file_type, self.seed,
+                           1 if self.rope_scaling else 0, sc[0], sc[1], sc[2], int(sc[3]), self.attention_scale)
 
 
 CONFIGS = {
@@ -79,6 +85,15 @@ CONFIGS = {
     "llama32_1b": ModelConfig(2048, 8192, 16, 32, 8, 128256, 4096, rope_theta=500000.0),
     "llama32_1b_q4": ModelConfig(2048, 8192, 16, 32, 8, 128256, 4096, rope_theta=500000.0, attn_format=Q4,
                                  ffn_format=Q4, file_type=2),
+    # YaRN RoPE scaling (factor 4 from an original context of 1024, ext_factor 1,
+    # attn_factor 1.1: pairs 0-5 keep the unscaled angle, pairs past 17.7 take
+    # the interpolated one, the ramp mixes those between) and an explicit
+    # attention scale of 0.11 instead of 1/sqrt(64)
+    "tiny_yarn": ModelConfig(256, 512, 2, 4, 2, 512, 4096, seed=31, rope_scaling=(4.0, 1.0, 1.1, 1024),
+                             attention_scale=0.11),
+    # the same scaling with ext_factor 0.5 (a half-weight ramp) on a Q4_0 model
+    "tiny_yarn_q4": ModelConfig(256, 512, 2, 4, 2, 512, 4096, rope_theta=500000.0, attn_format=Q4, ffn_format=Q4,
+                                file_type=2, seed=32, rope_scaling=(8.0, 0.5, 0.9, 2048), attention_scale=0.2),
     # Llama-3-8B shape, Q4_0 FFN beside Q8_0 attention, context for 8192 + 256 tokens
     "llama3_8b_mixed": ModelConfig(4096, 14336, 32, 32, 8, 128256, 8448, rope_theta=500000.0, ffn_format=Q4),
 }
