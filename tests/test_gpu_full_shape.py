@@ -130,3 +130,41 @@ def test_llama3_8b_mixed_decode_at_8k(gpu, oracle, model_dir):
         ref.append(tok)
     assert list(g.generate_greedy(gs2, 128000, P, 3)) == ref
     print(f"max relative logit difference {worst:.3g}")
+
+
+@pytest.mark.timeout(600)
+def test_llama3_8b_layer_shape_prefill_chunk_at_7680(gpu, oracle, model_dir):
+    """The Llama-3-8B configuration's prefill leg at its own layer shape: a
+    256-token prompt chunk at positions 7680..7935 over a random KV cache
+    below 7680 (the same on both sides), then two decode steps.  The chunk's
+    projections run on the int8-MFMA GEMM at K = 4096 and, for the Q4_0 down
+    projection, K = 14336 (448 blocks per row); its attention runs the tiled
+    prompt kernels at head size 128 over 7,936 positions; the logits cover
+    the 128,256-row table.  The model has two layers of the 8B shape (dim
+    4096, FFN 14336 Q4_0, attention Q8_0, 32/8 heads): every launch is the
+    32-layer model's, which repeats them, and the oracle finishes two layers
+    of this chunk in test time (forward.rs:120-280)."""
+    g, o = _models(oracle, model_dir, "llama3_8b_mixed_2l")
+    P, B = 7680, 256
+    rng = np.random.default_rng(7680)
+    k = rng.standard_normal((o.n_layers, P, o.kv_dim), dtype=np.float32)
+    v = rng.standard_normal((o.n_layers, P, o.kv_dim), dtype=np.float32)
+    gs, os_ = g.create_session(), o.create_session()
+    os_.key_cache()[:, :P] = k
+    os_.value_cache()[:, :P] = v
+    gs.upload_kv(k, v)
+    del k, v
+    prompt = rng.integers(0, o.vocab, B).astype(np.uint32)
+    lo = o.forward_x(prompt, P, os_)
+    worst = assert_logits(g.forward_x(prompt, P, gs), lo, f"{B}-token chunk at {P}")
+    kc, vc = gs.key_cache(), gs.value_cache()
+    ok, ov = os_.key_cache(), os_.value_cache()
+    for l in range(o.n_layers):
+        assert np.array_equal(kc[l, P:P + B].view(np.uint32), ok[l, P:P + B].view(np.uint32)), f"K layer {l}"
+        assert np.array_equal(vc[l, P:P + B].view(np.uint32), ov[l, P:P + B].view(np.uint32)), f"V layer {l}"
+    tok = oracle.argmax(lo)
+    for pos in range(P + B, P + B + 2):
+        lo = o.forward_x([tok], pos, os_)
+        worst = max(worst, assert_logits(g.forward_x([tok], pos, gs), lo, f"decode at {pos}"))
+        tok = oracle.argmax(lo)
+    print(f"max relative logit difference {worst:.3g}")

@@ -148,7 +148,8 @@ def test_matmul_q4_parity(gpu, oracle, batch, n, o):
 
 
 @pytest.mark.parametrize("fmt,batch,n,o", [(0, 16, 2048, 256), (0, 130, 576, 190), (0, 257, 8192, 128),
-                                           (1, 64, 2048, 384), (1, 200, 1536, 96)])
+                                           (1, 64, 2048, 384), (1, 200, 1536, 96), (1, 256, 14336, 512),
+                                           (0, 96, 14336, 136)])
 def test_matmul_mfma_parity(gpu, oracle, fmt, batch, n, o):
     # batches of >= 16 rows run the int8-MFMA GEMM: partial token and row
     # tiles, the `+=` columns and the `=` tail columns, both formats

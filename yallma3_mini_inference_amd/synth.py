@@ -96,6 +96,10 @@ CONFIGS = {
                                 file_type=2, seed=32, rope_scaling=(8.0, 0.5, 0.9, 2048), attention_scale=0.2),
     # Llama-3-8B shape, Q4_0 FFN beside Q8_0 attention, context for 8192 + 256 tokens
     "llama3_8b_mixed": ModelConfig(4096, 14336, 32, 32, 8, 128256, 8448, rope_theta=500000.0, ffn_format=Q4),
+    # two layers of that shape (same vocabulary): a prompt chunk's kernels at
+    # the 8B layer shape, within the oracle's test time
+    "llama3_8b_mixed_2l": ModelConfig(4096, 14336, 2, 32, 8, 128256, 8448, rope_theta=500000.0, ffn_format=Q4,
+                                      seed=41),
 }
 
 
