@@ -25,7 +25,12 @@ Also reported (same JSON line):
                 copy kernel) from profiles/pmc_traffic_llama32_1b_decode.json
                 when that file covers this kernel, else null.
   gemv_all      all four GEMV classes together: weight bytes per token / GEMV
-                time per token (the 60%-of-8-TB/s target's figure).
+                time per token from the per-class replays.
+  in_step       the decode step as its graph launches it, replayed whole and
+                without each class's launches (yl_profile_step): a class's
+                cost inside the step, kernel boundaries included, is the
+                difference; gemv_all over those costs (the 60%-of-8-TB/s
+                target's figure inside the step).
   cpu_baseline  the oracle (C restatement of the reference's Rayon CPU path,
                 OpenMP) decoding a bounded sample of the same workload on this
                 host's cores; `variants` times the same sample at the
@@ -391,6 +396,9 @@ def main():
     ap.add_argument("--cpu-variants", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the oracle at the reference's default thread count and as an SSE2-only build")
     ap.add_argument("--cpu-variant-child", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--stream-table", action="store_true",
+                    help="also print a markdown table: each GEMV class's graph replay against a plain stream of "
+                         "its own weight bytes with the same grid (GGUF configs)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
@@ -480,12 +488,32 @@ def main():
         if nb:
             kern[cls]["gbs"] = round(nb / (us * 1e-6) / 1e9, 1)
         log(f"{cls}: {us:.2f} us/launch x {n}/step" + (f", {nb / 1e6:.2f} MB -> {nb / (us * 1e3):.0f} GB/s" if nb else ""))
+    if args.stream_table and args.config not in FILE_CONFIGS:
+        print("| class | bytes per launch | GEMV us (replay) | plain stream us | GEMV TB/s | stream TB/s | "
+              "GEMV / stream |", file=sys.stderr)
+        print("|---|---|---|---|---|---|---|", file=sys.stderr)
+        for cls in ("qkv", "wo", "w13", "w2"):
+            sus, sb = model.profile_stream(sess, cls, reps=20)
+            gus = kern[cls]["us"]
+            print(f"| {cls} | {sb:,} | {gus:.2f} | {sus:.2f} | {sb / gus / 1e6:.2f} | {sb / sus / 1e6:.2f} | "
+                  f"{gus / sus:.2f} |", file=sys.stderr, flush=True)
+    # the step as its graph launches it, whole and without each class
+    step_us = model.profile_step(sess, nxt, ppos, None, reps=20)
+    marg = {}
+    for cls in ("qkv", "attention", "wo", "w13", "w2", "logits"):
+        marg[cls] = round(step_us - model.profile_step(sess, nxt, ppos, cls, reps=20), 2)
+    log(f"step replay {step_us:.1f} us; cost of each class inside it: " +
+        ", ".join(f"{c} {v:.1f}" for c, v in marg.items()))
     gemv = ("qkv", "wo", "w13", "w2")
     gemv_us = sum(kern[c]["us"] * kern[c]["launches_per_step"] for c in gemv)
     gemv_bytes = sum(kern[c]["bytes"] * kern[c]["launches_per_step"] for c in gemv)
     gemv_gbs = gemv_bytes / (gemv_us * 1e-6) / 1e9
     log(f"GEMVs: {gemv_us:.1f} us/token for {gemv_bytes / 1e6:.1f} MB -> {gemv_gbs:.0f} GB/s "
         f"({gemv_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+    gemv_in = sum(marg[c] for c in gemv)
+    gemv_in_gbs = gemv_bytes / (gemv_in * 1e-6) / 1e9 if gemv_in > 0 else 0.0
+    log(f"GEMVs inside the step: {gemv_in:.1f} us/token -> {gemv_in_gbs:.0f} GB/s "
+        f"({gemv_in_gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
     dom = max(gemv, key=lambda c: kern[c]["us"] * kern[c]["launches_per_step"])
     dom_gbs = kern[dom]["bytes"] / (kern[dom]["us"] * 1e-6) / 1e9
     traffic = None
@@ -525,7 +553,14 @@ def main():
             "avg_launch_us": kern[dom]["us"], "bytes_per_launch": kern[dom]["bytes"],
         },
         "gemv_all": {"us_per_token": round(gemv_us, 2), "bytes_per_token": gemv_bytes,
-                     "achieved_gbs": round(gemv_gbs, 1), "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+                     "achieved_gbs": round(gemv_gbs, 1), "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                     "from": "per-class graph replays"},
+        "in_step": {"step_replay_us": round(step_us, 2), "class_cost_us_per_step": marg,
+                    "gemv_all": {"us_per_token": round(gemv_in, 2), "bytes_per_token": gemv_bytes,
+                                 "achieved_gbs": round(gemv_in_gbs, 1),
+                                 "frac": round(gemv_in_gbs / HBM_PEAK_GBS, 4)},
+                    "how": "decode step graph replayed whole and without each class's launches; a class's "
+                           "cost = difference (its kernels and the boundaries they bring)"},
         "kernels": kern,
         "prefill_ms": round(prefill_s * 1e3, 2),
         "tokens_head": [int(t) for t in toks[:8]],

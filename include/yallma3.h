@@ -319,6 +319,28 @@ yl_status yl_profile_kernel(const yl_model *m, yl_session *s, uint32_t token, ui
                             uint32_t batch, int32_t kernel_class, uint32_t reps, double *us_per_launch,
                             uint64_t *bytes_per_launch, uint32_t *launches);
 
+/* Timing of one decode step at start_pos as its graph launches it (every
+ * layer's five kernels, then the logits kernel, which here leaves the
+ * position unchanged), without the launches of kernel_class (the classes of
+ * yl_profile_kernel; -1: none): the graph is replayed `reps` times between
+ * two HIP events on the session's stream.  A class's cost inside the step,
+ * with the kernel boundaries it brings, is the full step's time minus the
+ * time without it.  No counterpart in the reference: a measurement hook for
+ * benchmarks.  Leaves the session's state modified, as yl_profile_kernel. */
+yl_status yl_profile_step(const yl_model *m, yl_session *s, uint32_t token, uint32_t start_pos,
+                          int32_t kernel_class, uint32_t reps, double *us_per_step);
+
+/* Timing of a plain stream of one GEMV class's weights (kernel_class 0, 2,
+ * 3 or 4 of yl_profile_kernel; GGUF Q8_0/Q4_0 models): per layer, one
+ * launch of as many workgroups of the same size as that class's one-token
+ * GEMV, each reading its slice of the layer's quantized values and scales
+ * with 16-byte non-temporal loads; the layers' launches in one graph,
+ * replayed `reps` times.  Returns us per launch and the bytes one launch
+ * reads: the floor a GEMV of this shape can reach with kernels per layer.
+ * No counterpart in the reference: a measurement hook for benchmarks. */
+yl_status yl_profile_stream(const yl_model *m, yl_session *s, int32_t kernel_class, uint32_t reps,
+                            double *us_per_launch, uint64_t *bytes_per_launch);
+
 /* Elementwise probe of the device arithmetic the path relies on (device
  * pointers, n floats): exp, sqrt(|x|), 1/x and f16 widening of (i & 0xffff). */
 yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt_out,

@@ -27,7 +27,7 @@ EXPORTS = [
     "yl_model_free", "yl_model_name", "yl_model_shape", "yl_vocab_size", "yl_max_ctx_len", "yl_bos_token",
     "yl_eos_token", "yl_model_weight_bytes", "yl_model_embedding_bytes", "yl_get_embeddings",
     "yl_create_session", "yl_session_free", "yl_session_reset", "yl_session_set_attention", "yl_session_pos", "yl_session_set_pos",
-    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_math_selftest", "yl_serial_sum_selftest", "yl_wait_fault_selftest",
+    "yl_session_kv", "yl_forward_x", "yl_generate_greedy", "yl_profile_kernel", "yl_profile_step", "yl_profile_stream", "yl_math_selftest", "yl_serial_sum_selftest", "yl_wait_fault_selftest",
     "yl_write_synthetic_gguf", "yl_synthetic_normal", "yl_write_synthetic_gguf_tok", "yl_infer_set_max_tokens",
     "yl_infer_reset", "yl_tokenizer_load", "yl_tokenizer_free", "yl_model_tokenizer", "yl_tokenizer_vocab_size",
     "yl_tokenize", "yl_detokenize", "yl_chat_template", "yl_chat_prompt", "yl_pretokenize", "yl_sampler_new",
@@ -134,6 +134,8 @@ def lib():
         "yl_session_kv": (st, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz)]),
         "yl_forward_x": (st, [vp, vp, sz, u32, vp, vp, vp]),
         "yl_generate_greedy": (st, [vp, vp, u32, u32, u32, vp]),
+        "yl_profile_step": (st, [vp, vp, u32, u32, st, u32, C.POINTER(C.c_double)]),
+        "yl_profile_stream": (st, [vp, vp, st, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
         "yl_profile_kernel": (st, [vp, vp, u32, u32, u32, st, u32, C.POINTER(C.c_double), C.POINTER(u64),
                                    C.POINTER(u32)]),
         "yl_math_selftest": (st, [vp, sz, vp, vp, vp, vp]),

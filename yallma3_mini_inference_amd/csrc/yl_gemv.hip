@@ -732,4 +732,14 @@ hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipSt
 
 size_t gemv_bytes_per_row_block(int wfmt) { return wfmt == kQ8 ? 34 : 18; }
 
+bool gemv_launch_shape(int o, int nb, int epi, int* grid, int* threads) {
+    GemvPlan p{};
+    if (!plan_gemv(o, nb, epi, &p)) return false;
+    const int na = epi == kEpiQkvRope || epi == kEpiSwiglu || epi == kEpiResidQ ? kNormWaves : 1;
+    const int R = (64 / p.lpr) * p.nww;
+    *grid = (o + R - 1) / R;
+    *threads = 64 * (p.nww + na);
+    return true;
+}
+
 }  // namespace yl

@@ -2117,6 +2117,110 @@ yl_status yl_profile_kernel(const yl_model* m, yl_session* s, uint32_t token, ui
     return YL_OK;
 }
 
+
+yl_status yl_profile_step(const yl_model* m, yl_session* s, uint32_t token, uint32_t start_pos, int32_t skip_class,
+                          uint32_t reps, double* us_per_step) {
+    if (!m || !s || s->m != m || skip_class < -1 || skip_class > kOpLogits || reps == 0 || !us_per_step) {
+        set_error("profile_step: bad arguments");
+        return YL_ERR_ARG;
+    }
+    if ((uint64_t)start_pos + 1 > (uint64_t)m->ctx) { set_error("profile_step: position beyond ctx_len"); return YL_ERR_RANGE; }
+    if (!decode_in_range(m, s, (uint64_t)start_pos + 1, "profile_step")) return YL_ERR_RANGE;
+    s->dec_seq = decode_bucket(m, (uint64_t)start_pos + 1);
+    s->prof_seq = (uint64_t)start_pos + 1;
+    yl_status rs = put_state(s, (int32_t)start_pos, token);
+    if (rs != YL_OK) return rs;
+    // one decode step as its graph launches it, without the skipped class's
+    // launches (the logits kernel leaves the position where it is)
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "profile_step capture");
+    hipError_t ec = hipSuccess;
+    for (int l = 0; l < m->n_layers && ec == hipSuccess; l++)
+        for (int c = kOpQkv; c <= kOpW2 && ec == hipSuccess; c++)
+            if (c != skip_class) ec = enqueue_class(m, s, c, l, 1, &s->st->token, 0, nullptr);
+    if (ec == hipSuccess && skip_class != kOpLogits) ec = enqueue_class(m, s, kOpLogits, 0, 1, &s->st->token, 0, nullptr);
+    e = hipStreamEndCapture(s->stream, &g);
+    if (ec != hipSuccess || e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return hip_fail(ec != hipSuccess ? ec : e, "profile_step capture");
+    }
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "profile_step instantiate");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    for (int w = 0; w < 2 && e == hipSuccess; w++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, s->stream);
+    for (uint32_t r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, s->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    hipGraphExecDestroy(ge);
+    if (e != hipSuccess) return hip_fail(e, "profile_step");
+    if (check_wait_fault("profile_step") != YL_OK) return YL_ERR_HIP;
+    *us_per_step = (double)ms * 1000.0 / (double)reps;
+    return YL_OK;
+}
+
+yl_status yl_profile_stream(const yl_model* m, yl_session* s, int32_t kernel_class, uint32_t reps,
+                            double* us_per_launch, uint64_t* bytes_per_launch) {
+    if (!m || !s || s->m != m || reps == 0 || !us_per_launch ||
+        (kernel_class != kOpQkv && kernel_class != kOpWo && kernel_class != kOpW13 && kernel_class != kOpW2)) {
+        set_error("profile_stream: bad arguments");
+        return YL_ERR_ARG;
+    }
+    if (m->f16 || m->q8g) { set_error("profile_stream: GGUF Q8_0/Q4_0 weights only"); return YL_ERR_UNSUPPORTED; }
+    const int epi = kernel_class == kOpQkv ? kEpiQkvRope : kernel_class == kOpW13 ? kEpiSwiglu : kEpiResid;
+    // the class's weight bytes of every layer, streamed by as many
+    // workgroups of the same size as its one-token GEMV launches
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    uint64_t nbytes = 0;
+    hipError_t e = hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "profile_stream capture");
+    hipError_t ec = hipSuccess;
+    for (int l = 0; l < m->n_layers && ec == hipSuccess; l++) {
+        const Layer& L = m->layers[l];
+        const QMat& w = kernel_class == kOpQkv ? L.qkv : kernel_class == kOpWo ? L.wo : kernel_class == kOpW13 ? L.w13 : L.w2;
+        int grid = 0, threads = 0;
+        if (!gemv_launch_shape(w.o, w.nb, epi, &grid, &threads)) { ec = hipErrorInvalidValue; break; }
+        const size_t qb = (size_t)w.o * (w.fmt == kQ4 ? w.n / 2 : w.n), db = (size_t)w.o * w.nb * 2;
+        nbytes = qb + db;
+        ec = launch_stream(w.qs, qb, w.d, db, grid, threads, reinterpret_cast<unsigned*>(s->logits), s->stream);
+    }
+    e = hipStreamEndCapture(s->stream, &g);
+    if (ec != hipSuccess || e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return hip_fail(ec != hipSuccess ? ec : e, "profile_stream capture");
+    }
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "profile_stream instantiate");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    for (int w = 0; w < 2 && e == hipSuccess; w++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, s->stream);
+    for (uint32_t r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, s->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, s->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    hipGraphExecDestroy(ge);
+    if (e != hipSuccess) return hip_fail(e, "profile_stream");
+    *us_per_launch = (double)ms * 1000.0 / ((double)reps * m->n_layers);
+    if (bytes_per_launch) *bytes_per_launch = nbytes;
+    return YL_OK;
+}
+
 // ------------------------------------------------ tokenizer and sampler
 
 namespace {

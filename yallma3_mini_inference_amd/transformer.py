@@ -182,6 +182,25 @@ class Transformer:
                                       C.byref(nbytes), C.byref(n)))
         return us.value, nbytes.value, n.value
 
+    def profile_step(self, session: InferenceSession, token: int, start_pos: int, skip_class: str | None = None,
+                     reps: int = 20):
+        """Time (us) of one decode step at start_pos as its graph launches it,
+        without the launches of skip_class (None: the whole step), from
+        `reps` replays between two HIP events.  Modifies the session's state
+        at that position (reset it afterwards)."""
+        us = C.c_double()
+        cls = -1 if skip_class is None else self.PROFILE_CLASSES[skip_class]
+        check(lib().yl_profile_step(self._h, session._h, int(token), int(start_pos), cls, int(reps), C.byref(us)))
+        return us.value
+
+    def profile_stream(self, session: InferenceSession, kernel_class: str, reps: int = 20):
+        """Plain stream of one GEMV class's weights with that GEMV's grid, per
+        layer, replayed as a graph: (us per launch, bytes per launch)."""
+        us, nbytes = C.c_double(), C.c_uint64()
+        check(lib().yl_profile_stream(self._h, session._h, self.PROFILE_CLASSES[kernel_class], int(reps),
+                                      C.byref(us), C.byref(nbytes)))
+        return us.value, nbytes.value
+
     def create_session(self) -> InferenceSession:
         return InferenceSession(self)
 
