@@ -71,9 +71,11 @@ typedef struct yl_model yl_model;
 typedef struct yl_session yl_session;
 
 /* ------------------------------------------------ product ABI (unchanged) */
-/* lib.rs:135-152: loads a model (".gguf") into the process-wide current
- * transformer, replacing the previous one.  false on NULL, unknown
- * extension or any load error. */
+/* lib.rs:135-152: loads a model into the process-wide current transformer,
+ * replacing the previous one; the loader is chosen by the path's extension
+ * as load_transformer does (lib.rs:107-133): ".gguf", ".lmrs" or
+ * ".safetensors".  false on NULL, a path that is not UTF-8 (the reference
+ * maps it to ""), no or another extension, or any load error. */
 bool load_transformer_ffi(const char *model_path);
 /* README.md:81-92 (documented by the reference, which leaves it
  * unimplemented): one chat turn with the current model, as the reference's

@@ -40,6 +40,23 @@ def test_reference_ffi_signatures(yl):
     yl.lib().free_string(None)   # NULL-safe
 
 
+# lib.rs:107-152: the loader is picked by Path::extension of the path, and a
+# path that is not UTF-8 is taken as "" (no extension).  Refused paths fail
+# before any device or file access; accepted ones fail later (no file here).
+@pytest.mark.parametrize("path,accepted", [
+    ("m.gguf", True), ("/a/b.c/m.lmrs", True), ("x.tar.safetensors", True),
+    ("m.gguf/", True), ("m.gguf/.", True), ("m.gguf//", True),
+    ("m.GGUF", False), (".gguf", False), ("/a/.gguf", False), ("m.gguf/..", False),
+    ("gguf", False), ("m.", False), ("/a.gguf/m", False), ("", False), ("/", False),
+    (b"\xff/m.gguf", False), (b"m\xc3.gguf", False),
+])
+def test_loader_extension_rule(yl, path, accepted):
+    from yallma3_mini_inference_amd import transformer
+    assert transformer.load_transformer_ffi(path) is False
+    refused = "Unsupported model extension" in transformer.last_error()
+    assert refused is not accepted, transformer.last_error()
+
+
 def test_synthetic_normal_statistics(yl):
     import ctypes as C
     out = np.zeros(200000, np.float32)

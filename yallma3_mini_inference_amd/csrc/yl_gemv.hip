@@ -110,14 +110,26 @@ __device__ __forceinline__ uint4 buf_u4(__amdgpu_buffer_rsrc_t r, int voff, int 
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kPolStream));
 }
 
-template <int WF>
+// The 16-byte pieces of a lane's slot: for 32-byte blocks, at voff and
+// voff + HB.  The weight wavefronts use HB = 16 * LPR: the LPR lanes of a
+// row then read 16 * LPR contiguous bytes per instruction (whole cache
+// lines), each lane one half of two blocks (see half_dot).
+template <int WF, int HB>
 __device__ __forceinline__ void load_block(WBlock<WF>& w, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
     if constexpr (WF != kQ4) {
         w.a = buf_u4(r, voff, soff);
-        w.b = buf_u4(r, voff + 16, soff);
+        w.b = buf_u4(r, voff + HB, soff);
     } else {
         w.a = buf_u4(r, voff, soff);
     }
+}
+
+// Exact int32 dot of one 16-byte half block with its 16 activations.
+__device__ __forceinline__ int half_dot(uint4 w, const int32_t* xw) {
+    int a = __builtin_amdgcn_sdot4((int)w.x, xw[0], 0, false);
+    a = __builtin_amdgcn_sdot4((int)w.y, xw[1], a, false);
+    a = __builtin_amdgcn_sdot4((int)w.z, xw[2], a, false);
+    return __builtin_amdgcn_sdot4((int)w.w, xw[3], a, false);
 }
 
 // Exact int32 dot of one block (|sum| < 2^24, integer adds in any order):
@@ -210,53 +222,67 @@ __device__ __forceinline__ float add_from_lane_plus(float acc, float v) {
     else return fadd(acc, dpp_zero<0x100 + I, 0xF>(v));   // row_shl:I
 }
 
+// The lane (of a row's LPR) that holds the term of the slot's block I: lane
+// I, or with split halves (SPLIT) lane 2I for the slot's first LPR/2 blocks
+// and lane 2(I - LPR/2) + 1 for the others.
+template <int LPR, bool SPLIT, int I>
+constexpr int term_lane() {
+    return !SPLIT ? I : (I < LPR / 2 ? 2 * I : 2 * (I - LPR / 2) + 1);
+}
+
 // Chain step of one slot (LPR <= 16): the row's first lane adds the slot's
-// terms of its row in block order, reading lane j's term by row_shl:j.
-template <int LPR, int I = 0>
+// terms of its row in block order, reading block I's term by
+// row_shl:term_lane(I).
+template <int LPR, bool SPLIT, int I = 0>
 __device__ __forceinline__ float chain_slot_full(float acc, float term) {
-    if constexpr (I < LPR) return chain_slot_full<LPR, I + 1>(add_from_lane_plus<I>(acc, term), term);
+    if constexpr (I < LPR)
+        return chain_slot_full<LPR, SPLIT, I + 1>(add_from_lane_plus<term_lane<LPR, SPLIT, I>()>(acc, term), term);
     else return acc;
 }
 // The same for the row's last, partial slot: `valid` (< LPR) terms.
-template <int LPR, int I = 0>
+template <int LPR, bool SPLIT, int I = 0>
 __device__ __forceinline__ float chain_slot_part(float acc, float term, int valid) {
     if constexpr (I < LPR) {
         if (I >= valid) return acc;
-        return chain_slot_part<LPR, I + 1>(add_from_lane_plus<I>(acc, term), term, valid);
+        return chain_slot_part<LPR, SPLIT, I + 1>(add_from_lane_plus<term_lane<LPR, SPLIT, I>()>(acc, term), term,
+                                                  valid);
     } else {
         return acc;
     }
 }
-template <int LPR>
+template <int LPR, bool SPLIT>
 __device__ __forceinline__ float chain_slot_dpp(float acc, float term, int first_block, int nb) {
     const int valid = nb - first_block;   // uniform
-    if (valid >= LPR) return chain_slot_full<LPR>(acc, term);
+    if (valid >= LPR) return chain_slot_full<LPR, SPLIT>(acc, term);
     if (valid <= 0) return acc;
-    return chain_slot_part<LPR>(acc, term, valid);
+    return chain_slot_part<LPR, SPLIT>(acc, term, valid);
 }
-// The same for groups of G blocks: a group's term sits on the first lane of
-// its blocks, so the chain reads lanes 0, G, 2G, ... (`valid` counts blocks;
-// nb is a multiple of G).
-template <int LPR, int G, int I = 0>
+// The same for groups of G blocks: a group's term sits on the lane of its
+// first block, so the chain reads the lanes of blocks 0, G, 2G, ...
+// (`valid` counts blocks; nb is a multiple of G).
+template <int LPR, bool SPLIT, int G, int I = 0>
 __device__ __forceinline__ float chain_slot_fullg(float acc, float term) {
-    if constexpr (I < LPR) return chain_slot_fullg<LPR, G, I + G>(add_from_lane_plus<I>(acc, term), term);
+    if constexpr (I < LPR)
+        return chain_slot_fullg<LPR, SPLIT, G, I + G>(add_from_lane_plus<term_lane<LPR, SPLIT, I>()>(acc, term),
+                                                      term);
     else return acc;
 }
-template <int LPR, int G, int I = 0>
+template <int LPR, bool SPLIT, int G, int I = 0>
 __device__ __forceinline__ float chain_slot_partg(float acc, float term, int valid) {
     if constexpr (I < LPR) {
         if (I >= valid) return acc;
-        return chain_slot_partg<LPR, G, I + G>(add_from_lane_plus<I>(acc, term), term, valid);
+        return chain_slot_partg<LPR, SPLIT, G, I + G>(add_from_lane_plus<term_lane<LPR, SPLIT, I>()>(acc, term),
+                                                      term, valid);
     } else {
         return acc;
     }
 }
-template <int LPR, int G>
+template <int LPR, bool SPLIT, int G>
 __device__ __forceinline__ float chain_slot_dppg(float acc, float term, int first_block, int nb) {
     const int valid = nb - first_block;   // uniform
-    if (valid >= LPR) return chain_slot_fullg<LPR, G>(acc, term);
+    if (valid >= LPR) return chain_slot_fullg<LPR, SPLIT, G>(acc, term);
     if (valid <= 0) return acc;
-    return chain_slot_partg<LPR, G>(acc, term, valid);
+    return chain_slot_partg<LPR, SPLIT, G>(acc, term, valid);
 }
 
 // Few wavefronts per SIMD: registers go to loads in flight rather than to
@@ -480,8 +506,16 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         const void* scale_rows = kF32Scales ? (const void*)(a.sf + (size_t)min(wrow0, o - 1) * nsc)
                                             : (const void*)(a.d + (size_t)min(wrow0, o - 1) * nb);
         const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(scale_rows, rows_here * nsc * kScaleBytes);
-        const int qv = (int)(r * row_bytes) + j * kBlockBytes;
-        const int dv_off = (r * nsc + j / kBlocksPerScale) * kScaleBytes;
+        // 32-byte blocks are read in split halves: in a slot's 32*LPR bytes of
+        // a row, lane j reads the 16 bytes at 16j (half j%2 of block j/2) and
+        // those at 16(LPR + j) (the same half of block LPR/2 + j/2), so each
+        // load instruction covers whole lines.  The pair of lanes (2m, 2m+1)
+        // then holds blocks m and LPR/2 + m whole; lane 2m takes the term of
+        // block m, lane 2m+1 that of block LPR/2 + m (term_lane).
+        constexpr bool kSplit = WF != kQ4;
+        const int jb = kSplit ? ((j & 1) ? LPR / 2 + (j >> 1) : (j >> 1)) : j;   // the block of this lane's term
+        const int qv = (int)(r * row_bytes) + (kSplit ? j * 16 : j * kBlockBytes);
+        const int dv_off = (r * nsc + jb / kBlocksPerScale) * kScaleBytes;
         // Slot by slot (loads complete in issue order, so slot k's wait
         // leaves the later slots in flight; the scheduling barriers keep the
         // compiler from regrouping them).  LA slots go out first, then slot
@@ -493,7 +527,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         WBlock<WF> wv[LA];
         SW dv[LA];
         auto issue = [&](int k) {
-            load_block<WF>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
+            load_block<WF, 16 * LPR>(wv[k % LA], qr, qv, k * LPR * kBlockBytes);
             if constexpr (kF32Scales)
                 dv[k % LA] = __builtin_bit_cast(
                     float, __builtin_amdgcn_raw_buffer_load_b32(dr, dv_off, k * (LPR / kBlocksPerScale) * kScaleBytes,
@@ -517,25 +551,41 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         float acc = initl[min(w * RW + my_r, R - 1)];
 #pragma unroll
         for (int k = 0; k < PPL; k++) {
-            // exact block dot -> f32 term
-            const int b = k * LPR + j;
+            // exact block dot -> f32 term (lanes past nb compute a term the
+            // chain never reads)
+            const int b = k * LPR + jb;
             const int bb = b < nb ? b : nb - 1;
-            int isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
+            int isum;
+            if constexpr (kSplit) {
+                const int h = (j & 1) * 16;
+                const int b0 = min(k * LPR + (j >> 1), nb - 1), b1 = min(k * LPR + LPR / 2 + (j >> 1), nb - 1);
+                int s0 = half_dot(wv[k % LA].a, reinterpret_cast<const int32_t*>(xl + b0 * 32 + h));
+                int s1 = half_dot(wv[k % LA].b, reinterpret_cast<const int32_t*>(xl + b1 * 32 + h));
+                // whole-block dots from the pair's two halves (quad_perm [1,0,3,2])
+                s0 += __builtin_amdgcn_update_dpp(0, s0, 0xB1, 0xF, 0xF, false);
+                s1 += __builtin_amdgcn_update_dpp(0, s1, 0xB1, 0xF, 0xF, false);
+                isum = (j & 1) ? s1 : s0;
+            } else {
+                isum = block_dot<WF>(wv[k % LA], reinterpret_cast<const int32_t*>(xl + bb * 32));
+            }
             float ws;
             if constexpr (kF32Scales) ws = dv[k % LA];
             else ws = f16_to_f32(dv[k % LA]);
             if constexpr (kBlocksPerScale > 1) {
                 // the group's exact int32 dot: this block's plus the next
-                // lanes' (row_shl:1, then row_shl:2 for 4 blocks; the first
-                // lane of each group owns it), then its one term
+                // blocks' (their lanes are 1 apart, or 2 with split halves:
+                // row_shl, then twice that for 4 blocks; the lane of the
+                // group's first block owns it), then its one term
                 // ((float)isum * w_scale) * x_scale
-                isum += __builtin_amdgcn_update_dpp(0, isum, 0x101, 0xF, 0xF, true);
-                if constexpr (kBlocksPerScale == 4) isum += __builtin_amdgcn_update_dpp(0, isum, 0x102, 0xF, 0xF, true);
+                constexpr int kMate = kSplit ? 2 : 1;
+                isum += __builtin_amdgcn_update_dpp(0, isum, 0x100 + kMate, 0xF, 0xF, true);
+                if constexpr (kBlocksPerScale == 4)
+                    isum += __builtin_amdgcn_update_dpp(0, isum, 0x100 + 2 * kMate, 0xF, 0xF, true);
                 const float term = fmul(fmul((float)isum, ws), xsl[bb / kBlocksPerScale]);
-                acc = chain_slot_dppg<LPR, kBlocksPerScale>(acc, term, k * LPR, nb);
+                acc = chain_slot_dppg<LPR, kSplit, kBlocksPerScale>(acc, term, k * LPR, nb);
             } else {
                 const float term = fmul(fmul((float)isum, ws), xsl[bb]);
-                acc = chain_slot_dpp<LPR>(acc, term, k * LPR, nb);
+                acc = chain_slot_dpp<LPR, kSplit>(acc, term, k * LPR, nb);
             }
             if (k + LA < PPL) issue(k + LA);
         }

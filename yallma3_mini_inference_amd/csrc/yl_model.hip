@@ -1845,6 +1845,29 @@ yl_status yl_serial_sum_selftest(const float* v, const uint32_t* offsets, size_t
 
 // ---------------------------------------------------------------- model
 
+// The extension of a path as Rust's Path::extension gives it (lib.rs:112):
+// the file name is the last component (trailing separators and "."
+// components ignored; none for "/" or a ".." component), and the extension
+// is what follows its last '.', unless it has no '.' or only a leading one.
+// `has` is false when there is none.
+static std::string path_extension(const std::string& path, bool* has) {
+    *has = false;
+    std::string p = path;
+    for (;;) {
+        while (p.size() > 1 && p.back() == '/') p.pop_back();
+        if (p.size() >= 2 && p.compare(p.size() - 2, 2, "/.") == 0) { p.resize(p.size() - 2); continue; }
+        break;
+    }
+    if (p.empty() || p == "/" || p == ".") return "";
+    const size_t slash = p.rfind('/');
+    const std::string name = slash == std::string::npos ? p : p.substr(slash + 1);
+    if (name.empty() || name == "..") return "";
+    const size_t dot = name.rfind('.');
+    if (dot == std::string::npos || dot == 0) return "";
+    *has = true;
+    return name.substr(dot + 1);
+}
+
 yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) {
     if (!path) { set_error("null path"); return nullptr; }
     int ndev = 0;
@@ -1852,9 +1875,9 @@ yl_model* yl_load(const char* path, uint32_t max_ctx_len, int32_t fmt_override) 
     yl_status st;
     // lib.rs:107-133: the loader by file extension
     const std::string p(path);
-    const size_t dot = p.rfind('.');
-    const std::string ext = dot == std::string::npos ? "" : p.substr(dot + 1);
-    if (ext == "safetensors" || ext == "lmrs") {
+    bool has_ext = false;
+    const std::string ext = path_extension(p, &has_ext);
+    if (has_ext && (ext == "safetensors" || ext == "lmrs")) {
         HostModel h;
         std::string err;
         const bool ok = ext == "lmrs" ? load_lmrs(p, max_ctx_len, fmt_override, &h, &err)
@@ -2310,10 +2333,12 @@ static void chat_close() {
 
 bool load_transformer_ffi(const char* model_path) {
     if (!model_path) return false;
-    const std::string p(model_path);
-    const size_t dot = p.rfind('.');
-    const std::string ext = dot == std::string::npos ? "" : p.substr(dot + 1);
-    if (ext != "gguf" && ext != "lmrs" && ext != "safetensors") {
+    // lib.rs:141-142: a path that is not UTF-8 becomes "", which has no
+    // extension and so is refused
+    const std::string p = valid_utf8(model_path) ? std::string(model_path) : std::string();
+    bool has_ext = false;
+    const std::string ext = path_extension(p, &has_ext);
+    if (!has_ext || (ext != "gguf" && ext != "lmrs" && ext != "safetensors")) {
         set_error("Unsupported model extension for path: " + p);
         return false;
     }
