@@ -11,9 +11,10 @@
 // block order with the reference's two roundings.  The f32 work (convert,
 // two products, one sum per output and block) is the bound, not the MFMA.
 //
-// Tile: a 256-thread workgroup owns 128 tokens x 128 weight rows; wavefront
-// w covers tokens 64*(w&1) .. +63 and rows 64*(w>>1) .. +63 as 2x2 MFMA
-// tiles.  MFMA lane layout (gfx950): operand lane l holds row l%32 (token
+// Tile: a 256-thread workgroup owns TM tokens x 128 weight rows (TM = 128,
+// or 64 when the 128-token tiles would not give every CU two workgroups);
+// wavefront w covers tokens (TM/2)*(w&1) .. +TM/2-1 and rows 64*(w>>1) ..
+// +63 as (TM/64)x2 MFMA tiles.  MFMA lane layout (gfx950): operand lane l holds row l%32 (token
 // for A, weight row for B) and k = 16*(l/32) .. +15 of the block; result
 // register i of lane l is (token (i%4) + 8*(i/4) + 4*(l/32), row l%32).
 // Stages of 2 blocks (activations 8 KiB, weights 8/4 KiB, both scale
@@ -36,7 +37,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kGmThreads = 256;
-constexpr int kGmTM = 128;      // tokens per workgroup
 constexpr int kGmTN = 128;      // weight rows per workgroup
 constexpr int kGmBK = 2;        // blocks per stage
 constexpr int kGmStages = 4;    // stages in flight
@@ -45,15 +45,15 @@ constexpr int kGmStages = 4;    // stages in flight
 template <int WF>
 constexpr int gm_bpg() { return WF == kQ8S64 ? 2 : (WF == kQ8S128 ? 4 : 1); }
 
-template <int WF>
+template <int WF, int TM>
 struct GmStage {
     static constexpr bool kF32 = WF == kQ8S || WF == kQ8S64 || WF == kQ8S128;
     static constexpr int kRowB = WF == kQ4 ? 16 : 32;         // weight bytes per row and block
-    static constexpr int A = kGmBK * kGmTM * 32;              // [blk][token][32] int8
+    static constexpr int A = kGmBK * TM * 32;                 // [blk][token][32] int8
     static constexpr int B = kGmBK * kGmTN * kRowB;           // [blk][row][32 | 16]
     // activation scales: [blk][token] f32, or one per token for a stage
     // inside one group
-    static constexpr int XS = gm_bpg<WF>() > 1 ? kGmTM * 4 : kGmBK * kGmTM * 4;
+    static constexpr int XS = gm_bpg<WF>() > 1 ? TM * 4 : kGmBK * TM * 4;
     // weight scales: [row][2] f16 (Q8_0 / Q4_0), [row][2] f32 (kQ8S), or one
     // f32 per row (the stage's group)
     static constexpr int WS = WF == kQ8S ? kGmTN * 8 : kGmTN * 4;
@@ -64,18 +64,20 @@ struct GmStage {
     static constexpr int dmaB = B / 1024 / 4;
     static constexpr int dma = dmaA + dmaB + 1 + 1;
     static_assert(A % 4096 == 0 && B % 4096 == 0, "16-byte DMA split over 4 wavefronts");
-    static_assert((XS == 4 * 256 || XS == 2 * 256) && (WS == 2 * 256 || WS == 4 * 256), "scale DMA shapes");
+    static_assert(XS % 256 == 0 && XS <= 4 * 256 && (WS == 2 * 256 || WS == 4 * 256), "scale DMA shapes");
 };
 
-size_t gemm_lds_bytes(int wfmt) {
+template <int TM>
+static size_t gemm_lds_bytes_tm(int wfmt) {
     switch (wfmt) {
-    case kQ8: return (size_t)kGmStages * GmStage<kQ8>::bytes;
-    case kQ4: return (size_t)kGmStages * GmStage<kQ4>::bytes;
-    case kQ8S: return (size_t)kGmStages * GmStage<kQ8S>::bytes;
-    case kQ8S64: return (size_t)kGmStages * GmStage<kQ8S64>::bytes;
-    default: return (size_t)kGmStages * GmStage<kQ8S128>::bytes;
+    case kQ8: return (size_t)kGmStages * GmStage<kQ8, TM>::bytes;
+    case kQ4: return (size_t)kGmStages * GmStage<kQ4, TM>::bytes;
+    case kQ8S: return (size_t)kGmStages * GmStage<kQ8S, TM>::bytes;
+    case kQ8S64: return (size_t)kGmStages * GmStage<kQ8S64, TM>::bytes;
+    default: return (size_t)kGmStages * GmStage<kQ8S128, TM>::bytes;
     }
 }
+size_t gemm_lds_bytes(int wfmt, int tm) { return tm == 64 ? gemm_lds_bytes_tm<64>(wfmt) : gemm_lds_bytes_tm<128>(wfmt); }
 
 template <int D>
 __device__ __forceinline__ void gm_wait(int later) {
@@ -102,32 +104,34 @@ __device__ __forceinline__ v4i q4_unpack16(uint2 p) {
     return r;
 }
 
-template <int WF, int EPI>
+template <int WF, int EPI, int TM>
 __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemvArgs a, int M) {
     // (device pass only: the host pass has no gfx950 MFMA builtins and
     // needs just the launch stub)
 #if defined(__HIP_DEVICE_COMPILE__)
-    using S = GmStage<WF>;
+    using S = GmStage<WF, TM>;
+    constexpr int TMW = TM / 64;   // 32-token MFMA tiles per wavefront
+    constexpr int WT = TM / 2;     // tokens per wavefront
     extern __shared__ __align__(16) unsigned char gsm[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 31, lh = lane >> 5;
     const int wm = wave & 1, wn = wave >> 1;
-    const int c0 = blockIdx.x * kGmTN, t0 = blockIdx.y * kGmTM;
+    const int c0 = blockIdx.x * kGmTN, t0 = blockIdx.y * TM;
     const int nst = a.nb / kGmBK;
 
-    // accumulators: acc[tm][tn][i] = (token t0 + 64wm + 32tm + (i%4) + 8(i/4) + 4lh,
+    // accumulators: acc[tm][tn][i] = (token t0 + WT*wm + 32tm + (i%4) + 8(i/4) + 4lh,
     //                                 row c0 + 64wn + 32tn + li)
-    float acc[2][2][16];
+    float acc[TMW][2][16];
     int pos = 0;
     if constexpr (EPI == kEpiQkvRope) pos = a.state->pos;
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++)
+    for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
         for (int tn = 0; tn < 2; tn++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 float v = 0.0f;
-                const int t = t0 + 64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
+                const int t = t0 + WT * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
                 const int c = c0 + 64 * wn + 32 * tn + li;
                 if (t < M && c < a.o) {
                     if constexpr (EPI == kEpiStore) {
@@ -151,12 +155,12 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     // row indices past the matrix re-read the last valid one (results unused).
     auto issue = [&](unsigned char* buf, int s) {
         const int b0 = s * kGmBK;
-        // activations: instruction j covers block j/4, tokens 32*(j%4) .. +31;
-        // lane i -> token i/2, half i%2
+        // activations: instruction j covers block j/(TM/32), tokens
+        // 32*(j%(TM/32)) .. +31; lane i -> token i/2, half i%2
 #pragma unroll
         for (int k = 0; k < S::dmaA; k++) {
             const int j = wave * S::dmaA + k;
-            const int blk = j / 4, tok = min(t0 + 32 * (j % 4) + (lane >> 1), M - 1);
+            const int blk = j / (TM / 32), tok = min(t0 + 32 * (j % (TM / 32)) + (lane >> 1), M - 1);
             const int8_t* src = a.xq + (size_t)tok * a.n + (size_t)(b0 + blk) * 32 + 16 * (lane & 1);
             __builtin_amdgcn_global_load_lds(src, buf + j * 1024, 16, 0, 0);
         }
@@ -176,17 +180,20 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             __builtin_amdgcn_global_load_lds(src, buf + S::A + j * 1024, 16, 0, 0);
         }
         constexpr int G = gm_bpg<WF>();
+        // activation scales in 256-byte pieces of 64 tokens, piece p by
+        // wavefront p (the others repeat the first ones: identical bytes)
+        constexpr int XP = S::XS / 256, TP = TM / 64;   // pieces; pieces per block
+        const int p = wave % XP;
         if constexpr (G == 1) {
-            // activation scales: wavefront w -> block w/2, tokens 64*(w%2) + lane
-            const int tok = min(t0 + 64 * (wave & 1) + lane, M - 1);
-            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * a.nb + b0 + (wave >> 1),
-                                             buf + S::A + S::B + wave * 256, 4, 0, 0);
+            // piece p: block p/TP, tokens 64*(p%TP) + lane
+            const int tok = min(t0 + 64 * (p % TP) + lane, M - 1);
+            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * a.nb + b0 + p / TP, buf + S::A + S::B + p * 256, 4,
+                                             0, 0);
         } else {
-            // the group's scale per token: wavefront w -> tokens 64*(w%2) + lane
-            // (wavefronts 2 and 3 repeat 0 and 1)
-            const int tok = min(t0 + 64 * (wave & 1) + lane, M - 1);
-            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * (a.nb / G) + b0 / G,
-                                             buf + S::A + S::B + (wave & 1) * 256, 4, 0, 0);
+            // the group's scale per token: piece p -> tokens 64p + lane
+            const int tok = min(t0 + 64 * p + lane, M - 1);
+            __builtin_amdgcn_global_load_lds(a.xs + (size_t)tok * (a.nb / G) + b0 / G, buf + S::A + S::B + p * 256, 4,
+                                             0, 0);
         }
         if constexpr (WF == kQ8S) {
             // f32 block scales [row][2]: wavefront w -> rows 32w .. +31, lane i
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     // group dots of the f32-scaled formats with 2 or 4 blocks per group,
     // accumulated over the group's blocks (exact int32)
     constexpr int G = gm_bpg<WF>();
-    v16i gd[2][2] = {};
+    v16i gd[TMW][2] = {};
     for (int s = 0; s < nst; s++) {
         gm_wait<S::dma>(min(kGmStages - 2, nst - 1 - s));
         __syncthreads();   // every wavefront's DMA of stage s landed; stage s-1's buffer is free
@@ -231,12 +238,12 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const uint16_t* wsl = reinterpret_cast<const uint16_t*>(buf + S::A + S::B + S::XS);
 #pragma unroll
         for (int blk = 0; blk < kGmBK; blk++) {
-            const unsigned char* Ab = buf + blk * (kGmTM * 32);
+            const unsigned char* Ab = buf + blk * (TM * 32);
             const unsigned char* Bb = buf + S::A + blk * (kGmTN * S::kRowB);
-            v4i av[2], bv[2];
+            v4i av[TMW], bv[2];
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
-                av[tm] = *reinterpret_cast<const v4i*>(Ab + (64 * wm + 32 * tm + li) * 32 + 16 * lh);
+            for (int tm = 0; tm < TMW; tm++)
+                av[tm] = *reinterpret_cast<const v4i*>(Ab + (WT * wm + 32 * tm + li) * 32 + 16 * lh);
 #pragma unroll
             for (int tn = 0; tn < 2; tn++) {
                 if constexpr (WF != kQ4) {
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 // group starts from zero); the term follows the group's last
                 const bool first = ((s * kGmBK + blk) % G) == 0;
 #pragma unroll
-                for (int tm = 0; tm < 2; tm++)
+                for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
                     for (int tn = 0; tn < 2; tn++) {
                         const v16i zero = {};
@@ -264,12 +271,12 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
                 for (int tn = 0; tn < 2; tn++) wsc[tn] = wsf[64 * wn + 32 * tn + li];
 #pragma unroll
-                for (int tm = 0; tm < 2; tm++)
+                for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
                     for (int tn = 0; tn < 2; tn++)
 #pragma unroll
                         for (int i = 0; i < 16; i++) {
-                            const float xs = xsl[64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh];
+                            const float xs = xsl[WT * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh];
                             const float term = fmul(fmul((float)gd[tm][tn][i], wsc[tn]), xs);
                             acc[tm][tn][i] = fadd(acc[tm][tn][i], term);
                         }
@@ -283,17 +290,17 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 else
                     wsc[tn] = f16_to_f32(wsl[(64 * wn + 32 * tn + li) * 2 + blk]);
             }
-            vf4 xv[2][4];
+            vf4 xv[TMW][4];
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
                 for (int g = 0; g < 4; g++)
-                    xv[tm][g] = *reinterpret_cast<const vf4*>(xsl + blk * kGmTM + 64 * wm + 32 * tm + 8 * g + 4 * lh);
+                    xv[tm][g] = *reinterpret_cast<const vf4*>(xsl + blk * TM + WT * wm + 32 * tm + 8 * g + 4 * lh);
             // the four tiles' dots first (in separate registers), so the f32
             // work of one tile does not wait on the next tile's MFMA
-            v16i dots[2][2];
+            v16i dots[TMW][2];
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
                 for (int tn = 0; tn < 2; tn++) {
                     const v16i zero = {};
@@ -301,7 +308,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++)
+            for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
                 for (int tn = 0; tn < 2; tn++)
 #pragma unroll
@@ -314,10 +321,10 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 
     // epilogues
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++) {
+    for (int tm = 0; tm < TMW; tm++) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int t = t0 + 64 * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
+            const int t = t0 + WT * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
             const bool tok_ok = t < M;
             if constexpr (EPI == kEpiSwiglu) {
                 // SwiGLU (forward.rs:220-237) over the 64-row group [32 gate |
@@ -382,19 +389,35 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 #endif
 }
 
-template <int WF, int EPI>
-static hipError_t launch_gemm_k(const GemvArgs& a, int M, hipStream_t st) {
-    const size_t smem = gemm_lds_bytes(WF);
+template <int WF, int EPI, int TM>
+static hipError_t launch_gemm_tm(const GemvArgs& a, int M, hipStream_t st) {
+    const size_t smem = gemm_lds_bytes_tm<TM>(WF);
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm<WF, EPI>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm<WF, EPI, TM>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const dim3 grid((a.o + kGmTN - 1) / kGmTN, (M + kGmTM - 1) / kGmTM);
-    hipLaunchKernelGGL((k_gemm<WF, EPI>), grid, dim3(kGmThreads), smem, st, a, M);
+    const dim3 grid((a.o + kGmTN - 1) / kGmTN, (M + TM - 1) / TM);
+    hipLaunchKernelGGL((k_gemm<WF, EPI, TM>), grid, dim3(kGmThreads), smem, st, a, M);
     return hipGetLastError();
+}
+
+// 64-token tiles when 128-token tiles would give each CU at most one
+// workgroup (the f32 rescale is VALU-bound: a second workgroup per CU keeps
+// the matrix pipe and the VALU of one SIMD busy from different wavefronts).
+// Measured at 2048 tokens: Wo 82.5 -> 62.8 us and down 267 -> 203 us with 64
+// (256 -> 512 workgroups), but QKV 108 -> 131 us (384 -> 768), so 1.5
+// workgroups per CU keep 128.
+int gemm_tile_tokens(int o, int M) {
+    const long wg128 = (long)((o + kGmTN - 1) / kGmTN) * ((M + 127) / 128);
+    return wg128 <= 256 ? 64 : 128;
+}
+
+template <int WF, int EPI>
+static hipError_t launch_gemm_k(const GemvArgs& a, int M, hipStream_t st) {
+    return gemm_tile_tokens(a.o, M) == 64 ? launch_gemm_tm<WF, EPI, 64>(a, M, st) : launch_gemm_tm<WF, EPI, 128>(a, M, st);
 }
 
 bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M) {

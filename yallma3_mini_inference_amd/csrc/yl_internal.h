@@ -156,7 +156,7 @@ hipError_t launch_quantize(int fmt, int8_t* q, float* scale, const float* x, siz
 // many-token matmul on int8 MFMA (same epilogues and results as the GEMV;
 // activations always pre-quantized in xq/xs, M = tokens)
 bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M);
-size_t gemm_lds_bytes(int wfmt);
+size_t gemm_lds_bytes(int wfmt, int tm);
 hipError_t launch_gemm(const GemvArgs& a, int wfmt, int epi, int M, hipStream_t s);
 // out[c * out_ld + r] = in[r][c] for an in[rows][cols] f32 matrix
 hipError_t launch_transpose(const float* in, float* out, int rows, int cols, int out_ld, hipStream_t s);
