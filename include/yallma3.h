@@ -353,7 +353,9 @@ yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt
  * v[b-1] in f32 for a = offsets[c], b = offsets[c+1], values >= 0 (device
  * pointers; offsets holds cases + 1 entries).  segment 0 sums each case in
  * one pass; segment k > 0 in consecutive pieces of k values, each piece
- * continuing from the previous piece's sum (the long-context path). */
+ * continuing from the previous piece's sum (the long-context path);
+ * segment 0xFFFFFFFF by the segmented sum of the decode attention (four
+ * wavefronts, candidate starts per segment; cases up to 37,000 values). */
 yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, uint32_t segment,
                                  float *out);
 

@@ -317,12 +317,21 @@ def test_serial_sum_exact(gpu):
         for i in range(0, len(spots), 2):
             w[spots[i]] = spots[i + 1]
         segs.append(w)
+    # rows whose one-at-a-time sum drifts far from the exact sum: after a
+    # first value of 1, every value is 3/4 of the sum's ulp (each add rounds
+    # up by 1/4 ulp), so the segmented sum's candidate starts miss and it
+    # continues one value at a time
+    for n in (600, 3000):
+        w = np.full(n, np.float32(0.75 * 2.0 ** -23), np.float32)
+        w[0] = 1.0
+        segs.append(w)
     ref = np.array([sequential(v) for v in segs], np.float32)
     nan = np.isnan(ref)
     # whole rows, and rows summed in pieces that continue from the previous
     # piece's sum (the softmax of contexts longer than LDS holds): pieces of
-    # 700 (partial super-rows), 37 (inside the one-at-a-time prologue), 8192
-    for piece in (0, 700, 37, 8192):
+    # 700 (partial super-rows), 37 (inside the one-at-a-time prologue), 8192;
+    # -1: the decode attention's segmented sum (candidate starts per segment)
+    for piece in (0, 700, 37, 8192, -1):
         got = ops.serial_sum_selftest(segs, piece)
         assert np.array_equal(np.isnan(got), nan), piece
         assert_bits(got[~nan], ref[~nan])

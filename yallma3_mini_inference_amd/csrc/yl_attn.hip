@@ -61,10 +61,16 @@ constexpr int kVTileFloats = kVTileRows * kDecDims;
 constexpr int kMaxVTiles = 4;                  // V tiles in flight
 constexpr int kDecLdsBudget = 156 * 1024;      // LDS bytes one workgroup may use
 constexpr int kBufFlags = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
-// softmax sums over more positions than this take one wavefront's row
-// streaming; shorter ones one lane (the restarts at binade changes cost more
-// than the rows save)
+// the long-context softmax kernel sums rows longer than this with one
+// wavefront (wave_serial_sum), shorter ones with one lane
 constexpr int kWaveSumSeq = 2560;
+// wavefronts that run the softmax denominator of contexts up to
+// kAttnSplitSeq (seg_serial_sum: 2 segments of the row each)
+constexpr int kSumWaves = 4;
+// seg_serial_sum's LDS scratch (floats): segment ends, bases, then the
+// float64 segment sums
+constexpr int kSumScratch = 2 * kSumWaves * 64 + 2 * kSumWaves + 2 * (2 * kSumWaves);
+static_assert(kDecThreads / 64 == 2 * kSumWaves, "one sum segment per wavefront's exponentials");
 
 // pt row stride: positions up to max_seq rounded to 64 (the serial sum
 // reads zero padding to that length), + 4 floats to spread banks
@@ -72,9 +78,10 @@ __host__ __device__ inline int attn_pt_stride(int max_seq) { return ((max_seq + 
 // contexts longer than this take the scores kernel + the decode kernel
 constexpr int kAttnSplitSeq = 4096;
 // + for contexts up to kAttnSplitSeq, the exponentials in position order for
-// the serial sum (max_seq rounded up to 64); longer ones sum from pt
+// the serial sum (max_seq rounded up to 64) and the sum's scratch; longer
+// ones sum from pt
 __host__ __device__ inline size_t attn_fixed_lds_floats(int max_seq) {
-    const size_t el = max_seq <= kAttnSplitSeq ? (size_t)((max_seq + 63) & ~63) : 0;
+    const size_t el = max_seq <= kAttnSplitSeq ? (size_t)((max_seq + 63) & ~63) + kSumScratch : 0;
     return 8 * (size_t)attn_pt_stride(max_seq) + 8 * kDecDims + kDecDims + 16 + el;
 }
 // V tile buffers that fit beside the fixed part (0: fewer than 2 fit)
@@ -126,6 +133,35 @@ __device__ __forceinline__ void wait_v_tiles(int later) {
     }
 }
 
+// e = exp(score - max) into pt and in position order into el for
+// contexts up to kAttnSplitSeq: wavefront w takes positions [w L, w L + L)
+// (L = seg_sum_len(seq, 8), 8 L = seq rounded up to 64), which is segment w
+// of the serial sum, and stores their float64 sum in segsum[w]
+template <int NV>
+__device__ __forceinline__ void exp_segment(float* pt, float* el, int PCS, int L, int seq, float mx,
+                                            double* segsum) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float ev[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int t2 = w * L + min(lane + 64 * i, L - 1);
+        ev[i] = pt[(t2 & 7) * PCS + (t2 >> 3)];
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int t2 = w * L + lane + 64 * i;
+        const float e = t2 < seq ? expf_rn(ev[i] - mx) : 0.0f;
+        if (lane + 64 * i < L) {
+            pt[(t2 & 7) * PCS + (t2 >> 3)] = e;
+            el[t2] = e;
+            acc += (double)e;
+        }
+    }
+    acc = wave_sum_f64(acc);
+    if (lane == 0) segsum[w] = acc;
+}
+
 // e = exp(score - max) into pt and, with EL, in position order into el
 template <int NV, bool EL>
 __device__ __forceinline__ void exp_row(float* pt, float* el, int PCS, int b0, int seq, int pad, float mx) {
@@ -144,54 +180,6 @@ __device__ __forceinline__ void exp_row(float* pt, float* el, int PCS, int b0, i
             if constexpr (EL) el[t2] = e;
         }
     }
-}
-
-// s_waitcnt lgkmcnt(N) tied to the 8 registers of one block of the serial
-// sum (see lgkm_wait_tie)
-template <int N>
-__device__ __forceinline__ void lgkm_wait_tie8(vf4 (&r)[8]) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt field");
-    asm volatile("s_waitcnt lgkmcnt(%8)"
-                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
-                 : "n"(N)
-                 : "memory");
-}
-// The reads of one block (32 consecutive floats at LDS offset a), untracked
-__device__ __forceinline__ void sum_block_reads(vf4 (&r)[8], unsigned a) {
-    r[0] = lds_read_b128<0>(a);
-    r[1] = lds_read_b128<16>(a);
-    r[2] = lds_read_b128<32>(a);
-    r[3] = lds_read_b128<48>(a);
-    r[4] = lds_read_b128<64>(a);
-    r[5] = lds_read_b128<80>(a);
-    r[6] = lds_read_b128<96>(a);
-    r[7] = lds_read_b128<112>(a);
-}
-__device__ __forceinline__ float sum_block_adds(float sum, const vf4 (&r)[8]) {
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) sum = fadd(sum, r[k][c]);
-    return sum;
-}
-// ((0 + e[0]) + e[1]) + ... over nblk blocks of 32 (nblk even; one lane):
-// the next block's reads are in flight while the current one is added.
-__device__ __forceinline__ float lds_serial_sum_blocks(const float* e, int nblk) {
-    const unsigned a0 = lds_addr(e);
-    vf4 ra[8], rb[8];
-    float sum = 0.0f;
-    sum_block_reads(ra, a0);
-    for (int b = 0; b < nblk; b += 2) {
-        sum_block_reads(rb, a0 + 128u * (unsigned)(b + 1));
-        lgkm_wait_tie8<8>(ra);
-        sum = sum_block_adds(sum, ra);
-        // (past the last block: a re-read of block 0, never used)
-        sum_block_reads(ra, a0 + (b + 2 < nblk ? 128u * (unsigned)(b + 2) : 0u));
-        lgkm_wait_tie8<8>(rb);
-        sum = sum_block_adds(sum, rb);
-    }
-    lgkm_wait_tie8<0>(ra);
-    return sum;
 }
 
 constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decode kernel)
@@ -290,7 +278,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     const float* __restrict__ sq, const float* __restrict__ kc, const float* __restrict__ vc,
     const StepState* __restrict__ st, int n_heads, int n_kv_heads, float attn_scale, int max_seq, int kv_ld,
     int n_vt, int8_t* __restrict__ aq, float* __restrict__ as, float* __restrict__ att_f32,
-    const float* __restrict__ sc, int sc_ld) {
+    const float* __restrict__ sc, int sc_ld, unsigned* __restrict__ fault) {
     extern __shared__ __align__(16) float lds[];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -311,6 +299,9 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     float* outl = part + kDecChains;
     float* red = outl + kDecDims;
     float* el = red + 16;   // exponentials in position order (!LONG)
+    float* sx = el + ((max_seq + 63) & ~63);   // the serial sum's scratch (!LONG)
+    int* sum_ctr = reinterpret_cast<int*>(red + 12);
+    if (tid == 0) *sum_ctr = 0;   // (seen after the score rounds' barriers)
     const float* __restrict__ qh = sq + (size_t)h * HD;
     const int col0 = kvh * HD + ds * kDecDims;
     // keys of this kv head through a buffer descriptor: a per-lane 32-bit
@@ -445,15 +436,24 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
     for (int w = 1; w < kDecThreads / 64; w++) mx = fmaxf(mx, red[w]);
     const int pad = (seq + 63) & ~63;
-    {
+    double* segsum = reinterpret_cast<double*>(sx + 2 * kSumWaves * 65);
+    if constexpr (LONG) {
         // up to 8 independent exponentials per thread and round (the
         // polynomial is a chain of dependent double-precision steps)
         const int nv = (pad + kDecThreads - 1) / kDecThreads;
-        if (nv <= 1) exp_row<1, !LONG>(pt, el, PCS, 0, seq, pad, mx);
-        else if (nv == 2) exp_row<2, !LONG>(pt, el, PCS, 0, seq, pad, mx);
-        else if (nv <= 4) exp_row<4, !LONG>(pt, el, PCS, 0, seq, pad, mx);
+        if (nv <= 1) exp_row<1, false>(pt, el, PCS, 0, seq, pad, mx);
+        else if (nv == 2) exp_row<2, false>(pt, el, PCS, 0, seq, pad, mx);
+        else if (nv <= 4) exp_row<4, false>(pt, el, PCS, 0, seq, pad, mx);
         else
-            for (int b0 = 0; b0 < pad; b0 += 8 * kDecThreads) exp_row<8, !LONG>(pt, el, PCS, b0, seq, pad, mx);
+            for (int b0 = 0; b0 < pad; b0 += 8 * kDecThreads) exp_row<8, false>(pt, el, PCS, b0, seq, pad, mx);
+    } else {
+        // wavefront w: segment w of the serial sum (L <= 512 positions)
+        const int L = seg_sum_len(seq, 2 * kSumWaves);
+        const int nv = (L + 63) / 64;
+        if (nv <= 1) exp_segment<1>(pt, el, PCS, L, seq, mx, segsum);
+        else if (nv == 2) exp_segment<2>(pt, el, PCS, L, seq, mx, segsum);
+        else if (nv <= 4) exp_segment<4>(pt, el, PCS, L, seq, mx, segsum);
+        else exp_segment<8>(pt, el, PCS, L, seq, mx, segsum);
     }
     lds_barrier();
     // the first V tiles start now, issued by the DMA wavefronts while
@@ -461,20 +461,16 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     if (dma_wave)
         for (int t = 0; t < n_tiles && t < n_vt; t++)
             v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
-    const bool wave_sum = LONG || seq > kWaveSumSeq;
     if (LONG && tid < 64) {
         // one wavefront, from the transposed row
         const float sum = wave_serial_sum_at([pt, PCS](int i) { return pt[(i & 7) * PCS + (i >> 3)]; }, seq);
         if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
-    } else if (!LONG && wave_sum && tid < 64) {
-        // one wavefront, rows of 64 positions (see wave_serial_sum)
-        const float sum = wave_serial_sum(el, seq);
+    } else if (!LONG && tid < 64 * kSumWaves) {
+        // the exponentials in position order (zero-padded to 64) by the
+        // wavefronts without V DMA
+        static_assert(kSumWaves <= kDmaWave0, "the sum's wavefronts issue no DMA");
+        const float sum = seg_serial_sum<kSumWaves>(el, seq, segsum, sx, sum_ctr, 0, fault);
         if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
-    } else if (!wave_sum && tid == 0) {
-        // the exponentials in position order, blocks of 32 (pad / 32 is even;
-        // the zero padding adds nothing)
-        const float sum = lds_serial_sum_blocks(el, pad / 32);
-        red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     lds_barrier();
     const float inv = red[8];
@@ -980,7 +976,7 @@ static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const f
         e = opt_in_lds(&k_attn_decode<QF, HD, true>, smem);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((k_attn_decode<QF, HD, true>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
-                           n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, sc, sc_ld);
+                           n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, sc, sc_ld, nullptr);
         return hipGetLastError();
     }
     const int n_vt = attn_v_tiles(max_seq);
@@ -989,7 +985,7 @@ static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const f
     const hipError_t e = opt_in_lds(&k_attn_decode<QF, HD, false>, smem);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((k_attn_decode<QF, HD, false>), grid, dim3(kDecThreads), smem, s, sq, kc, vc, st, n_heads,
-                       n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, nullptr, 0);
+                       n_kv_heads, scale, max_seq, kv_ld, n_vt, aq, as, att_f32, nullptr, 0, wait_fault_word(false));
     return hipGetLastError();
 }
 

@@ -428,4 +428,232 @@ __device__ __forceinline__ int lds_wait_count(int* ctr, int target, unsigned* fa
     return c;
 }
 
+// ---------------------------------------------------------------------------
+// The serial f32 sum ((0 + v[0]) + v[1]) + ... + v[n-1] (the softmax
+// denominator, forward.rs:356-361), bit-identical to the one-at-a-time loop,
+// by wavefronts 0..NW-1 of a workgroup in about n / (2 NW) dependent adds
+// instead of n.
+//
+// The row is cut into NS = 2 NW segments of L values (L = 8 * ceil(n / 8NS)).
+// Segment i starts from the serial sum of the values before it, known only
+// once those are added; so every lane of the wavefront that owns segment i
+// runs the serial recurrence over the segment from its own candidate start:
+// 64 consecutive f32 values around the float64 sum of the values before the
+// segment (the one-at-a-time sum drifts from the exact sum by its rounding
+// errors, a random walk of a few ulps at these lengths; candidate 32 is the
+// exact sum rounded).  A lane whose start equals the true start bit for bit
+// computes the true end.  Wavefront 0 then walks the segments in order:
+// segment 0 starts at +0 (candidate 0), and each segment's true end selects
+// the next segment's lane.  A true start outside its segment's candidates
+// continues one value at a time from there, so the result is the serial sum
+// for any input (a NaN or infinity included); only the speed depends on the
+// data.  Each wavefront owns segments 2w and 2w+1, two independent chains per
+// lane, fed from registers (see the chain below).
+//
+// v: LDS, holding +0 from n up to 64 * ceil(n / 64) (adding +0 leaves every
+// start >= +0 unchanged) and readable for 8 values more.  segsum: LDS, the float64 sum of each segment (in
+// any order: they only place the candidates).  sx: LDS scratch of NS * 64
+// floats + NS ints, 16-byte aligned.  ctr: an LDS counter that reads `ctr0`
+// on entry; it reads ctr0 + NW once every wavefront has arrived.  Every lane
+// of wavefronts 0..NW-1 calls this with the same arguments; the sum is
+// returned to wavefront 0 (the others return 0).
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = (int)b, hi = (int)(b >> 32);
+    const int rl = __builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xF, 0xF, false);
+    const int rh = __builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)rh << 32) | (unsigned)rl));
+}
+__device__ __forceinline__ double lane_value_f64(double v, int lane) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_readlane((int)b, lane), hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+// Sum over the 64 lanes in some order (every lane active; the result, the
+// same on every lane, only serves as an estimate).
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    x += dpp_mov_f64<0xB1>(x);    // quad_perm [1,0,3,2]
+    x += dpp_mov_f64<0x4E>(x);    // quad_perm [2,3,0,1]
+    x += dpp_mov_f64<0x141>(x);   // row_half_mirror
+    x += dpp_mov_f64<0x140>(x);   // row_mirror: every lane holds its row's total
+    return (lane_value_f64(x, 0) + lane_value_f64(x, 16)) + (lane_value_f64(x, 32) + lane_value_f64(x, 48));
+}
+// 4 bytes at LDS offset a, untracked by the compiler's waits: the caller
+// waits with lgkm_wait_tie4f before any use
+__device__ __forceinline__ float lds_read_b32_at(unsigned a) {
+    float r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a) : "memory");
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tie4f(float& a, float& b, float& c, float& d) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+// Lane K of each 16-lane row, read by every lane of its row (DPP
+// row_newbcast; the add that uses it takes it as its DPP operand).
+template <int K>
+__device__ __forceinline__ float row_bcast_lane(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + K, 0xF, 0xF,
+                                                                 false));
+}
+// s0 += lanes 0..N-1 of v0's row one at a time, and s1 likewise from v1
+// (two independent chains interleaved)
+template <int N, int K = 0>
+__device__ __forceinline__ void dpp_row_adds(float& s0, float v0, float& s1, float v1) {
+    if constexpr (K < N) {
+        s0 = fadd(s0, row_bcast_lane<K>(v0));
+        s1 = fadd(s1, row_bcast_lane<K>(v1));
+        dpp_row_adds<N, K + 1>(s0, v0, s1, v1);
+    }
+}
+// Registers per chain that hold a short segment whole (16 values each).
+constexpr int kSegShortRegs = 8;
+// The chains over registers 0..L/16 of r0 and r1 (L a multiple of 8, at
+// most 16 * kSegShortRegs), unrolled so that every register is named at
+// compile time
+template <int R = 0>
+__device__ __forceinline__ void seg_chain_regs(float& s0, const float (&r0)[kSegShortRegs], float& s1,
+                                               const float (&r1)[kSegShortRegs], int L) {
+    if constexpr (R < kSegShortRegs) {
+        if (16 * R + 16 <= L) {
+            dpp_row_adds<16>(s0, r0[R], s1, r1[R]);
+            seg_chain_regs<R + 1>(s0, r0, s1, r1, L);
+        } else if (16 * R < L) {
+            dpp_row_adds<8>(s0, r0[R], s1, r1[R]);
+        }
+    }
+}
+// Segment length of seg_serial_sum with NS segments: 8 * ceil(n / 8NS).
+__host__ __device__ inline int seg_sum_len(int n, int NS) { return 8 * ((n + 8 * NS - 1) / (8 * NS)); }
+// float64 sums of the NS = 2 NW segments of v (segsum, LDS), for callers
+// that do not form them while writing v: wavefront w sums segments 2w and
+// 2w+1.  Every lane of wavefronts 0..NW-1; a barrier must follow.
+template <int NW>
+__device__ void seg_sums_f64(const float* v, int n, double* segsum) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int L = seg_sum_len(n, 2 * NW);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int i = 2 * w + h;
+        double acc = 0.0;
+        for (int k = i * L + lane; k < (i + 1) * L; k += 64) acc += k < n ? (double)v[k] : 0.0;
+        acc = wave_sum_f64(acc);
+        if (lane == 0) segsum[i] = acc;
+    }
+}
+template <int NW>
+__device__ __forceinline__ float seg_serial_sum(const float* v, int n, const double* segsum, float* sx, int* ctr, int ctr0,
+                                unsigned* fault) {
+    constexpr int NS = 2 * NW;
+    static_assert(NS <= 8, "one ds_read_b128 pair per lane holds the segment ends");
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int L = seg_sum_len(n, NS);
+    const int i0 = 2 * w, i1 = 2 * w + 1;
+    // float64 sum of the values before segment i0 (any order: an estimate)
+    double sg[NS];
+#pragma unroll
+    for (int i = 0; i < NS; i++) sg[i] = segsum[i];   // (all loads issued together)
+    double before = 0.0, own = 0.0;
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) {
+        before += i < i0 ? sg[i] : 0.0;
+        own += i == i0 ? sg[i] : 0.0;
+    }
+    const double before1 = before + own;
+    // candidate starts: 64 consecutive finite f32 bit patterns from `base`
+    auto base_of = [](double est) {
+        const int b = __float_as_int((float)est) - 32;
+        return b < 0 ? 0 : (b > 0x7f7fffbf ? 0x7f7fffbf : b);
+    };
+    const int base0 = i0 == 0 ? 0 : base_of(before);
+    const int base1 = base_of(before1);
+    float s0 = __int_as_float(base0 + lane), s1 = __int_as_float(base1 + lane);
+    // Each step of a chain is one add whose operand comes by DPP
+    // row_newbcast from a register holding 16 of the segment's values in
+    // every 16-lane row (lane l: value 16 r + l % 16), so no memory access
+    // sits inside the chain (measured on gfx950: 8.5 cycles per dependent
+    // add, 14 per step of two interleaved chains from registers, 23 with LDS
+    // broadcast reads of the values in the loop).  Values from n on are +0
+    // in v; positions past L belong to the next segment and are never added.
+    const float* p0 = v + i0 * L + (lane & 15);
+    const float* p1 = v + i1 * L + (lane & 15);
+    const unsigned a0 = lds_addr(p0), a1 = lds_addr(p1);
+    if (L <= 16 * kSegShortRegs) {
+        // Short segments (contexts up to 1024): every register is read
+        // first, then the chains run straight through (an LDS read in flight
+        // slows DPP adds down).  The reads are unconditional, so they all go
+        // out before the first wait; registers past the segment re-read its
+        // last one and are never added.
+        float r0[kSegShortRegs], r1[kSegShortRegs];
+        const int rlast = (L - 1) / 16;
+#pragma unroll
+        for (int r = 0; r < kSegShortRegs; r++) {
+            r0[r] = p0[16 * (r < rlast ? r : rlast)];
+            r1[r] = p1[16 * (r < rlast ? r : rlast)];
+        }
+        seg_chain_regs(s0, r0, s1, r1, L);
+    } else {
+        // Longer segments: a loop over blocks of 16 values, the next block's
+        // register read while the current one is added (the half block after
+        // the last whole one reads the next segment's values in lanes 8-15,
+        // never added; past the end a re-read of this block).  The reads are
+        // untracked by the compiler, which would otherwise place them after
+        // the adds and wait at the loop's top, and so is the first one (a
+        // tracked read before the loop makes it wait for every LDS read at
+        // the top of the loop).
+        const int nfull = L / 16;   // whole blocks; L % 16 is 0 or 8
+        float c0 = lds_read_b32_at(a0), c1 = lds_read_b32_at(a1);
+        lgkm_wait_tie4f<0>(c0, c1, s0, s1);
+        for (int b = 0; b < nfull; b++) {
+            const unsigned o = 64u * (unsigned)(16 * (b + 1) < L ? b + 1 : b);
+            float n0 = lds_read_b32_at(a0 + o), n1 = lds_read_b32_at(a1 + o);
+            __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of the adds
+            dpp_row_adds<16>(s0, c0, s1, c1);
+            lgkm_wait_tie4f<0>(n0, n1, s0, s1);  // after the adds (tied to their results)
+            c0 = n0;
+            c1 = n1;
+        }
+        if (L % 16) dpp_row_adds<8>(s0, c0, s1, c1);
+    }
+    // lane l's ends at sx[8 l + i]; the bases after them
+    int* sbase = reinterpret_cast<int*>(sx + 8 * 64);
+    sx[8 * lane + i0] = s0;
+    sx[8 * lane + i1] = s1;
+    if (lane == 0) {
+        sbase[i0] = base0;
+        sbase[i1] = base1;
+    }
+    lds_arrive(ctr);
+    if (w != 0) return 0.0f;
+    lds_wait_count(ctr, ctr0 + NW, fault);
+    const vf4 e03 = *reinterpret_cast<const vf4*>(sx + 8 * lane);
+    const vf4 e47 = *reinterpret_cast<const vf4*>(sx + 8 * lane + 4);
+    const int myb = sbase[lane & (NS - 1)];
+    const vf4 ends[2] = {e03, e47};
+    // The walk is straight-line scalar code (the sum's bits in a scalar
+    // register, selects, no branches): segment i's true start picks lane idx
+    // of its ends; `from` is the first segment whose start is not among its
+    // candidates (NS if none).
+    int Sb = __builtin_amdgcn_readlane(__float_as_int(e03.x), 0);
+    int from = NS;
+#pragma unroll
+    for (int i = 1; i < NS; i++) {
+        const int idx = Sb - __builtin_amdgcn_readlane(myb, i);
+        const bool live = i * L < n, hit = (unsigned)idx < 64u;
+        const int next = __builtin_amdgcn_readlane(__float_as_int(ends[i / 4][i % 4]), idx & 63);
+        const bool take = from == NS && live && hit;
+        from = from == NS && live && !hit ? i : from;
+        Sb = take ? next : Sb;
+    }
+    float S = __int_as_float(Sb);
+    if (from < NS) {
+        // the true start of segment `from` is not among its candidates:
+        // one value at a time from there
+        for (int k = from * L; k < n; k++) S = fadd(S, v[k]);
+    }
+    return S;
+}
+
 }  // namespace yl

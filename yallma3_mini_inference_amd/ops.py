@@ -94,12 +94,13 @@ def math_selftest(x: np.ndarray):
 def serial_sum_selftest(segments, piece: int = 0):
     """Device serial f32 sums ((0 + v0) + v1) + ... of each nonnegative segment
     (piece > 0: summed in consecutive pieces of that many values, each piece
-    continuing from the previous one's sum)."""
+    continuing from the previous one's sum; piece -1: by the decode
+    attention's segmented sum over four wavefronts)."""
     segs = [np.ascontiguousarray(s, np.float32).ravel() for s in segments]
     offs = np.zeros(len(segs) + 1, np.uint32)
     offs[1:] = np.cumsum([s.size for s in segs])
     v = np.concatenate(segs) if segs else np.zeros(1, np.float32)
     dv, do = DeviceBuffer.from_numpy(v if v.size else np.zeros(1, np.float32)), DeviceBuffer.from_numpy(offs)
     out = DeviceBuffer.zeros(max(1, len(segs)), np.float32)
-    check(lib().yl_serial_sum_selftest(dv.ptr, do.ptr, len(segs), int(piece), out.ptr))
+    check(lib().yl_serial_sum_selftest(dv.ptr, do.ptr, len(segs), int(piece) & 0xFFFFFFFF, out.ptr))
     return out.numpy()[: len(segs)]
