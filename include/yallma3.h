@@ -355,7 +355,9 @@ yl_status yl_math_selftest(const float *x, size_t n, float *exp_out, float *sqrt
  * one pass; segment k > 0 in consecutive pieces of k values, each piece
  * continuing from the previous piece's sum (the long-context path);
  * segment 0xFFFFFFFF by the segmented sum of the decode attention (four
- * wavefronts, candidate starts per segment; cases up to 37,000 values). */
+ * wavefronts, candidate starts per segment; cases up to 37,000 values);
+ * segment 0xFFFFFFFE by the wide segmented sum of the long-context softmax
+ * (eight wavefronts, 128 candidate starts per segment). */
 yl_status yl_serial_sum_selftest(const float *v, const uint32_t *offsets, size_t cases, uint32_t segment,
                                  float *out);
 

@@ -330,8 +330,9 @@ def test_serial_sum_exact(gpu):
     # whole rows, and rows summed in pieces that continue from the previous
     # piece's sum (the softmax of contexts longer than LDS holds): pieces of
     # 700 (partial super-rows), 37 (inside the one-at-a-time prologue), 8192;
-    # -1: the decode attention's segmented sum (candidate starts per segment)
-    for piece in (0, 700, 37, 8192, -1):
+    # -1: the decode attention's segmented sum (candidate starts per segment);
+    # -2: the long-context softmax's wide segmented sum
+    for piece in (0, 700, 37, 8192, -1, -2):
         got = ops.serial_sum_selftest(segs, piece)
         assert np.array_equal(np.isnan(got), nan), piece
         assert_bits(got[~nan], ref[~nan])

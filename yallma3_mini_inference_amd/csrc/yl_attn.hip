@@ -61,9 +61,6 @@ constexpr int kVTileFloats = kVTileRows * kDecDims;
 constexpr int kMaxVTiles = 4;                  // V tiles in flight
 constexpr int kDecLdsBudget = 156 * 1024;      // LDS bytes one workgroup may use
 constexpr int kBufFlags = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
-// the long-context softmax kernel sums rows longer than this with one
-// wavefront (wave_serial_sum), shorter ones with one lane
-constexpr int kWaveSumSeq = 2560;
 // wavefronts that run the softmax denominator of contexts up to
 // kAttnSplitSeq (seg_serial_sum: 2 segments of the row each)
 constexpr int kSumWaves = 4;
@@ -561,14 +558,23 @@ constexpr int kPvSlots = 8;     // slots in flight
 
 // Waits until at most n of this wavefront's vector memory operations are
 // in flight (n < 64; the immediate must be a constant).
-// Softmax of one head: max from -1e10, e = exp(score - max) into LDS, the
-// serial sum (one lane up to kWaveSumSeq positions, one wavefront beyond),
-// p = e * (1 / sum) written transposed for the P.V kernel.
+// Softmax of one head: max from -1e10, e = exp(score - max) into LDS (+0
+// from seq to the next multiple of 64), the serial sum by the segmented sum
+// of all 8 wavefronts (seg_serial_sum_wide), p = e * (1 / sum) written
+// transposed for the P.V kernel.  LDS: el (attn_softmax_el_floats) | the
+// sum's scratch.
+__host__ __device__ inline int attn_softmax_el_floats(int sc_ld) { return ((sc_ld + 63) & ~63) + 64; }
+constexpr int kSoftSumScratch = 16 * 64 + 8 + 2 * 8 + 4;   // ends, bases, float64 segment sums, counter
 __global__ __launch_bounds__(kDecThreads) void k_attn_softmax(const StepState* __restrict__ st, int sc_ld,
-                                                              int n_heads, float* __restrict__ scratch) {
+                                                              int n_heads, float* __restrict__ scratch,
+                                                              unsigned* __restrict__ fault) {
     extern __shared__ __align__(16) float el[];
     __shared__ float red[16];
     const int h = blockIdx.x, tid = threadIdx.x;
+    float* sx = el + attn_softmax_el_floats(sc_ld);
+    double* segsum = reinterpret_cast<double*>(sx + 16 * 64 + 8);
+    int* sum_ctr = reinterpret_cast<int*>(segsum + 8);
+    if (tid == 0) *sum_ctr = 0;   // (seen after the first barrier)
     const int seq = st->pos + 1, n_quads = (seq + 3) / 4;
     const float* __restrict__ sh = scratch + (size_t)h * sc_ld;
     float* __restrict__ pt = scratch + (size_t)n_heads * sc_ld + (size_t)h * sc_ld;   // [8][pcs] of this head
@@ -595,16 +601,13 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_softmax(const StepState* _
             const int p = 4 * (tid + i * kDecThreads) + pp;
             if (p < seq) el[p] = expf_rn(s4[i][pp] - mx);
         }
+    for (int p = seq + tid; p < ((seq + 63) & ~63); p += kDecThreads) el[p] = 0.0f;
     __syncthreads();
-    if (seq > kWaveSumSeq) {
-        if (tid < 64) {
-            const float sum = wave_serial_sum(el, seq);
-            if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
-        }
-    } else if (tid == 0) {
-        float sum = 0.0f;
-        for (int i = 0; i < seq; i++) sum = fadd(sum, el[i]);
-        red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    seg_sums_f64_wide<kDecThreads / 64>(el, seq, segsum);
+    __syncthreads();
+    {
+        const float sum = seg_serial_sum_wide<kDecThreads / 64>(el, seq, segsum, sx, sum_ctr, 0, fault);
+        if (tid == 0) red[8] = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
     const float inv = red[8];
@@ -619,7 +622,8 @@ __global__ __launch_bounds__(kDecThreads) void k_attn_softmax(const StepState* _
 // then p = e * (1 / sum) transposed as above.
 constexpr int kSoftSeg = 6144;
 __global__ __launch_bounds__(kDecThreads) void k_attn_softmax_long(const StepState* __restrict__ st, int sc_ld,
-                                                                   int n_heads, float* __restrict__ scratch) {
+                                                                   int n_heads, float* __restrict__ scratch,
+                                                                   unsigned* __restrict__ fault) {
     extern __shared__ __align__(16) float seg[];   // [2][kSoftSeg]
     __shared__ float red[16];
     const int h = blockIdx.x, tid = threadIdx.x;
@@ -955,14 +959,16 @@ static hipError_t launch_attn_decode_k(const float* sq, const float* kc, const f
             // softmax, P.V by lane j, output
             // (rows up to 16384 positions are held in LDS whole)
             const bool long_row = max_seq > kLongQuads * 4 * kDecThreads;
-            const size_t smem_e = long_row ? 2 * (size_t)kSoftSeg * sizeof(float) : (size_t)sc_ld * sizeof(float);
+            const size_t smem_e = long_row ? 2 * (size_t)kSoftSeg * sizeof(float)
+                                           : ((size_t)attn_softmax_el_floats(sc_ld) + kSoftSumScratch) * sizeof(float);
             const size_t smem_r = (size_t)kPvSlots * (kPvRows + r) * 64 * sizeof(float);
             auto pv = r == 2 ? &k_attn_pv_j<HD, 2> : r == 4 ? &k_attn_pv_j<HD, 4> : &k_attn_pv_j<HD, 8>;
             auto softmax = long_row ? &k_attn_softmax_long : &k_attn_softmax;
             e = opt_in_lds(softmax, smem_e);
             if (e == hipSuccess) e = opt_in_lds(pv, smem_r);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL(softmax, dim3(n_heads), dim3(kDecThreads), smem_e, s, st, sc_ld, n_heads, sc);
+            hipLaunchKernelGGL(softmax, dim3(n_heads), dim3(kDecThreads), smem_e, s, st, sc_ld, n_heads, sc,
+                               wait_fault_word(false));
             hipLaunchKernelGGL(pv, dim3(n_kv_heads * (HD / 64), 8), dim3(64 * r), smem_r, s, vc, st, n_heads,
                                n_kv_heads, sc_ld, sc);
             hipLaunchKernelGGL((k_attn_pv_out<QF, HD>), dim3(n_heads), dim3(HD), 0, s, vc, st, n_heads, n_kv_heads,

@@ -479,18 +479,6 @@ __device__ __forceinline__ double wave_sum_f64(double x) {
     x += dpp_mov_f64<0x140>(x);   // row_mirror: every lane holds its row's total
     return (lane_value_f64(x, 0) + lane_value_f64(x, 16)) + (lane_value_f64(x, 32) + lane_value_f64(x, 48));
 }
-// 4 bytes at LDS offset a, untracked by the compiler's waits: the caller
-// waits with lgkm_wait_tie4f before any use
-__device__ __forceinline__ float lds_read_b32_at(unsigned a) {
-    float r;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a) : "memory");
-    return r;
-}
-template <int N>
-__device__ __forceinline__ void lgkm_wait_tie4f(float& a, float& b, float& c, float& d) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt field");
-    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
-}
 // Lane K of each 16-lane row, read by every lane of its row (DPP
 // row_newbcast; the add that uses it takes it as its DPP operand).
 template <int K>
@@ -579,7 +567,6 @@ __device__ __forceinline__ float seg_serial_sum(const float* v, int n, const dou
     // in v; positions past L belong to the next segment and are never added.
     const float* p0 = v + i0 * L + (lane & 15);
     const float* p1 = v + i1 * L + (lane & 15);
-    const unsigned a0 = lds_addr(p0), a1 = lds_addr(p1);
     if (L <= 16 * kSegShortRegs) {
         // Short segments (contexts up to 1024): every register is read
         // first, then the chains run straight through (an LDS read in flight
@@ -595,27 +582,20 @@ __device__ __forceinline__ float seg_serial_sum(const float* v, int n, const dou
         }
         seg_chain_regs(s0, r0, s1, r1, L);
     } else {
-        // Longer segments: a loop over blocks of 16 values, the next block's
-        // register read while the current one is added (the half block after
-        // the last whole one reads the next segment's values in lanes 8-15,
-        // never added; past the end a re-read of this block).  The reads are
-        // untracked by the compiler, which would otherwise place them after
-        // the adds and wait at the loop's top, and so is the first one (a
-        // tracked read before the loop makes it wait for every LDS read at
-        // the top of the loop).
-        const int nfull = L / 16;   // whole blocks; L % 16 is 0 or 8
-        float c0 = lds_read_b32_at(a0), c1 = lds_read_b32_at(a1);
-        lgkm_wait_tie4f<0>(c0, c1, s0, s1);
-        for (int b = 0; b < nfull; b++) {
-            const unsigned o = 64u * (unsigned)(16 * (b + 1) < L ? b + 1 : b);
-            float n0 = lds_read_b32_at(a0 + o), n1 = lds_read_b32_at(a1 + o);
-            __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of the adds
-            dpp_row_adds<16>(s0, c0, s1, c1);
-            lgkm_wait_tie4f<0>(n0, n1, s0, s1);  // after the adds (tied to their results)
-            c0 = n0;
-            c1 = n1;
+        // Longer segments: chunks of 16 * kSegShortRegs values, each read
+        // into registers whole before its adds (no LDS read in flight while
+        // the chains run)
+        for (int c0 = 0; c0 < L; c0 += 16 * kSegShortRegs) {
+            const int len = L - c0 < 16 * kSegShortRegs ? L - c0 : 16 * kSegShortRegs;
+            float r0[kSegShortRegs], r1[kSegShortRegs];
+            const int rlast = (len - 1) / 16;
+#pragma unroll
+            for (int r = 0; r < kSegShortRegs; r++) {
+                r0[r] = p0[c0 + 16 * (r < rlast ? r : rlast)];
+                r1[r] = p1[c0 + 16 * (r < rlast ? r : rlast)];
+            }
+            seg_chain_regs(s0, r0, s1, r1, len);
         }
-        if (L % 16) dpp_row_adds<8>(s0, c0, s1, c1);
     }
     // lane l's ends at sx[8 l + i]; the bases after them
     int* sbase = reinterpret_cast<int*>(sx + 8 * 64);
@@ -651,6 +631,92 @@ __device__ __forceinline__ float seg_serial_sum(const float* v, int n, const dou
     if (from < NS) {
         // the true start of segment `from` is not among its candidates:
         // one value at a time from there
+        for (int k = from * L; k < n; k++) S = fadd(S, v[k]);
+    }
+    return S;
+}
+
+// seg_serial_sum for long rows: wavefront w sums segment w (NS = NW
+// segments of L = 8 * ceil(n / 8NW) values) from 128 candidate starts, two
+// chains per lane (base + lane and base + 64 + lane, base 64 below the float64
+// estimate), since the one-at-a-time sum drifts further from the exact sum
+// over thousands of values (a few tens of ulps at 8192).  Both chains read
+// the same values, one register per 16.  Same contract as seg_serial_sum,
+// with sx holding NW * 128 floats + NW ints and segsum one float64 sum per
+// segment (seg_sums_f64_wide).
+template <int NW>
+__device__ void seg_sums_f64_wide(const float* v, int n, double* segsum) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int L = seg_sum_len(n, NW);
+    double acc = 0.0;
+    for (int k = w * L + lane; k < (w + 1) * L; k += 64) acc += k < n ? (double)v[k] : 0.0;
+    acc = wave_sum_f64(acc);
+    if (lane == 0) segsum[w] = acc;
+}
+template <int NW>
+__device__ __forceinline__ float seg_serial_sum_wide(const float* v, int n, const double* segsum, float* sx, int* ctr,
+                                                     int ctr0, unsigned* fault) {
+    static_assert(NW <= 8, "two ds_read_b128 per lane and chain hold the segment ends");
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int L = seg_sum_len(n, NW);
+    double sg[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) sg[i] = segsum[i];
+    double before = 0.0;
+#pragma unroll
+    for (int i = 0; i < NW - 1; i++) before += i < w ? sg[i] : 0.0;
+    int base = __float_as_int((float)before) - 64;
+    base = base < 0 ? 0 : (base > 0x7f7fff7f ? 0x7f7fff7f : base);
+    if (w == 0) base = 0;
+    float s0 = __int_as_float(base + lane), s1 = __int_as_float(base + 64 + lane);
+    const float* p = v + w * L + (lane & 15);
+    if (L <= 16 * kSegShortRegs) {
+        float r[kSegShortRegs];
+        const int rlast = (L - 1) / 16;
+#pragma unroll
+        for (int k = 0; k < kSegShortRegs; k++) r[k] = p[16 * (k < rlast ? k : rlast)];
+        seg_chain_regs(s0, r, s1, r, L);
+    } else {
+        // chunks of 16 * kSegShortRegs values read into registers whole
+        // before their adds (see seg_serial_sum)
+        for (int c0 = 0; c0 < L; c0 += 16 * kSegShortRegs) {
+            const int len = L - c0 < 16 * kSegShortRegs ? L - c0 : 16 * kSegShortRegs;
+            float r[kSegShortRegs];
+            const int rlast = (len - 1) / 16;
+#pragma unroll
+            for (int k = 0; k < kSegShortRegs; k++) r[k] = p[c0 + 16 * (k < rlast ? k : rlast)];
+            seg_chain_regs(s0, r, s1, r, len);
+        }
+    }
+    // lane l's ends at sx[16 l + 2 i + h] (segment i, chain h); bases after
+    int* sbase = reinterpret_cast<int*>(sx + 16 * 64);
+    sx[16 * lane + 2 * w] = s0;
+    sx[16 * lane + 2 * w + 1] = s1;
+    if (lane == 0) sbase[w] = base;
+    lds_arrive(ctr);
+    if (w != 0) return 0.0f;
+    lds_wait_count(ctr, ctr0 + NW, fault);
+    vf4 e[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) e[k] = *reinterpret_cast<const vf4*>(sx + 16 * lane + 4 * k);
+    const int myb = sbase[lane & (NW - 1)];
+    // the walk in scalar registers (see seg_serial_sum); candidate idx of
+    // segment i is chain idx / 64 of lane idx % 64
+    int Sb = __builtin_amdgcn_readlane(__float_as_int(e[0].x), 0);
+    int from = NW;
+#pragma unroll
+    for (int i = 1; i < NW; i++) {
+        const int idx = Sb - __builtin_amdgcn_readlane(myb, i);
+        const bool live = i * L < n, hit = (unsigned)idx < 128u;
+        const int n0 = __builtin_amdgcn_readlane(__float_as_int(e[(2 * i) / 4][(2 * i) % 4]), idx & 63);
+        const int n1 = __builtin_amdgcn_readlane(__float_as_int(e[(2 * i + 1) / 4][(2 * i + 1) % 4]), idx & 63);
+        const int next = idx >= 64 ? n1 : n0;
+        const bool take = from == NW && live && hit;
+        from = from == NW && live && !hit ? i : from;
+        Sb = take ? next : Sb;
+    }
+    float S = __int_as_float(Sb);
+    if (from < NW) {
         for (int k = from * L; k < n; k++) S = fadd(S, v[k]);
     }
     return S;

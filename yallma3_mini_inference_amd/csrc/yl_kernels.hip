@@ -205,6 +205,29 @@ __global__ __launch_bounds__(64 * kSegSumWaves) void k_seg_sum_selftest(const fl
     if (threadIdx.x == 0) out[c] = s;
 }
 
+// seg_serial_sum_wide (the long-context softmax denominator) over one case
+// per workgroup of 8 wavefronts, the values staged as the softmax kernel
+// stages them (+0 up to the next multiple of 64).
+constexpr int kSegSumWideWaves = 8;
+__global__ __launch_bounds__(64 * kSegSumWideWaves) void k_seg_sum_wide_selftest(const float* __restrict__ v,
+                                                                                 const uint32_t* __restrict__ offs,
+                                                                                 float* out, unsigned* fault) {
+    extern __shared__ __align__(16) float lds[];
+    const int c = blockIdx.x;
+    const uint32_t a = offs[c], b = offs[c + 1];
+    const int n = (int)(b - a), pad = (n + 63) & ~63;
+    float* sx = lds + pad + 64;
+    double* segsum = reinterpret_cast<double*>(sx + 16 * 64 + 8);
+    int* ctr = reinterpret_cast<int*>(segsum + kSegSumWideWaves);
+    for (int i = threadIdx.x; i < pad + 64; i += blockDim.x) lds[i] = i < n ? v[a + i] : 0.0f;
+    if (threadIdx.x == 0) *ctr = 0;
+    __syncthreads();
+    seg_sums_f64_wide<kSegSumWideWaves>(lds, n, segsum);
+    __syncthreads();
+    const float s = seg_serial_sum_wide<kSegSumWideWaves>(lds, n, segsum, sx, ctr, 0, fault);
+    if (threadIdx.x == 0) out[c] = s;
+}
+
 // The step state of an op call: its first position (and token).
 __global__ void k_set_state(StepState* st, int32_t pos, uint32_t token) {
     if (threadIdx.x == 0) {
@@ -336,6 +359,22 @@ hipError_t launch_raise_fault(unsigned* fault, hipStream_t s) {
 hipError_t launch_serial_sum_selftest(const float* v, const uint32_t* offs, int cases, int seg, float* out,
                                       hipStream_t s) {
     if (cases <= 0) return hipSuccess;
+    if (seg == -2) {
+        // the wide segmented sum: LDS for the longest case
+        std::vector<uint32_t> h((size_t)cases + 1);
+        hipError_t e = hipMemcpy(h.data(), offs, h.size() * sizeof(uint32_t), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return e;
+        uint32_t mx = 0;
+        for (int c = 0; c < cases; c++) mx = std::max(mx, h[c + 1] - h[c]);
+        const size_t smem = ((((size_t)mx + 63) & ~(size_t)63) + 64 + 16 * 64 + 8 + 2 * kSegSumWideWaves + 4) * 4;
+        if (smem > 150 * 1024) return hipErrorInvalidValue;
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_seg_sum_wide_selftest),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_seg_sum_wide_selftest, dim3(cases), dim3(64 * kSegSumWideWaves), smem, s, v, offs, out,
+                           wait_fault_word(false));
+        return hipGetLastError();
+    }
     if (seg < 0) {
         // the segmented sum: LDS for the longest case
         std::vector<uint32_t> h((size_t)cases + 1);

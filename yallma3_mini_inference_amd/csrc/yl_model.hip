@@ -1837,10 +1837,10 @@ yl_status yl_math_selftest(const float* x, size_t n, float* exp_out, float* sqrt
 yl_status yl_serial_sum_selftest(const float* v, const uint32_t* offsets, size_t cases, uint32_t segment,
                                  float* out) {
     if ((!v || !offsets || !out) && cases) return YL_ERR_ARG;
-    if (segment > (1u << 30) && segment != 0xFFFFFFFFu) return YL_ERR_ARG;
+    if (segment > (1u << 30) && segment < 0xFFFFFFFEu) return YL_ERR_ARG;
     wait_fault_word(true);
-    hipError_t e = launch_serial_sum_selftest(v, offsets, (int)cases, segment == 0xFFFFFFFFu ? -1 : (int)segment,
-                                              out, nullptr);
+    const int seg = segment == 0xFFFFFFFFu ? -1 : (segment == 0xFFFFFFFEu ? -2 : (int)segment);
+    hipError_t e = launch_serial_sum_selftest(v, offsets, (int)cases, seg, out, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess && check_wait_fault("serial sum self-test") != YL_OK) return YL_ERR_HIP;
     return e == hipSuccess ? YL_OK : hip_fail(e, "serial sum self-test");

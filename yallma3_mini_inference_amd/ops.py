@@ -95,7 +95,8 @@ def serial_sum_selftest(segments, piece: int = 0):
     """Device serial f32 sums ((0 + v0) + v1) + ... of each nonnegative segment
     (piece > 0: summed in consecutive pieces of that many values, each piece
     continuing from the previous one's sum; piece -1: by the decode
-    attention's segmented sum over four wavefronts)."""
+    attention's segmented sum over four wavefronts; piece -2: by the
+    long-context softmax's wide segmented sum over eight wavefronts)."""
     segs = [np.ascontiguousarray(s, np.float32).ravel() for s in segments]
     offs = np.zeros(len(segs) + 1, np.uint32)
     offs[1:] = np.cumsum([s.size for s in segs])
