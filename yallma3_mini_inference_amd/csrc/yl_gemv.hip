@@ -522,8 +522,10 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
         // k + LA right after slot k is consumed, into the registers slot k
         // used: under full HBM load a load waits for queue space, and a
         // wavefront that issued everything up front would start its first
-        // slot only when most data had arrived.
-        constexpr int LA = PPL <= 4 ? PPL : (PPL / 2 < 8 ? PPL / 2 : 8);
+        // slot only when most data had arrived.  Measured on the 1B shapes:
+        // 4 slots ahead for 8-slot rows (2, 3 and 6 are slower), 6 for
+        // 16-slot rows (down matmul 6.5 -> 6.3 us; 4 and 8 are slower).
+        constexpr int LA = PPL <= 4 ? PPL : PPL == 16 ? 6 : (PPL / 2 < 8 ? PPL / 2 : 8);
         WBlock<WF> wv[LA];
         SW dv[LA];
         auto issue = [&](int k) {
