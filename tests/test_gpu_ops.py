@@ -268,6 +268,25 @@ def test_attention(gpu, oracle, batch, start, nh, nkv, hd):
     assert_bits(out, ref)
 
 
+# One-token contexts around the register P.V chains' bounds: 1 to 7 registers
+# of 16 chunks (8 positions each), partial registers, a seq % 8 tail or none,
+# 112 chunks (the most held in registers) and the LDS-tile chains past it.
+@pytest.mark.parametrize("seq,nh,nkv,hd", [(s, 8, 2, 64) for s in (8, 9, 16, 17, 127, 128, 129, 255, 256, 257, 383,
+                                                                    600, 768, 769, 775, 776, 895, 896, 897, 903, 904,
+                                                                    905, 1024)]
+                         + [(300, 4, 1, 128), (896, 4, 1, 128), (904, 4, 1, 128), (200, 2, 2, 32), (897, 2, 2, 32)])
+def test_attention_decode_chain_lengths(gpu, oracle, seq, nh, nkv, hd):
+    from yallma3_mini_inference_amd import ops
+    rng = np.random.default_rng(seq * 7 + hd)
+    q = rng.normal(0, 1, nh * hd).astype(np.float32)
+    kc = rng.normal(0, 1, seq * nkv * hd).astype(np.float32)
+    vc = rng.normal(0, 1, seq * nkv * hd).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    out = ops.attention(q, kc, vc, 1, seq - 1, nh, nkv, hd, scale)
+    ref = oracle.fused_attention(q, kc, vc, seq, 1, nh, nkv, hd, seq - 1, nkv * hd, scale)
+    assert_bits(out, ref)
+
+
 def test_prompt_attention_nonfinite_v(gpu, oracle):
     # an infinity in V past some rows' causal bound: the reference still adds
     # p * v there (p = 0), so those rows turn NaN; the tiled kernel must not

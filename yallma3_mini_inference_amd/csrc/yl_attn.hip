@@ -42,9 +42,13 @@ __device__ void quantize_head_output(const float* outl, int hd, int8_t* aq, floa
 //      lane brings a key dimension of 4 positions, and the dimensions are
 //      consumed in groups of 8 (the reference's lane partials) with the next
 //      group's loads in flight; q is read as uniform (scalar) values;
-//   2. max, exp, and the serial sum (one lane, LDS reads kept in flight);
-//   3. the P.V chains of its 32 dimensions, reading V from LDS tiles of 256
-//      positions that LDS DMA (16 bytes per lane) fills up to 4 tiles ahead;
+//   2. max, exp, and the serial sum (segmented over wavefronts 0-3);
+//   3. the P.V chains of its 32 dimensions over V tiles of 256 positions
+//      that LDS DMA (16 bytes per lane) fills: up to 112 chunks (903
+//      positions) with every tile resident, the DMA wavefronts copy their V
+//      values into registers during the sum and run the chains with p from
+//      registers; longer contexts refill the tiles up to 4 ahead and the
+//      chains read V and p from LDS;
 //   4. the 8-lane reduction + tail, and the quantized group.
 // Only 16-byte loads per lane keep the CU's memory pipeline at full width
 // (a 4-byte load per lane moves a quarter of the bytes per address cycle).
@@ -185,6 +189,45 @@ constexpr int kScoreLoads = 32;   // 16-byte key loads in flight per lane (decod
 // j computes partial j (key dimensions 8s + j, s in order) of NC chunks of
 // 256 positions starting at r0 (4 positions per lane), every key load of
 // the round issued before the first product; partials go to
+// P.V from registers, for contexts of at most kPvRegChunks chunks whose V
+// tiles all fit in LDS at once.  The DMA wavefronts hold the chains: while
+// the others sum the softmax denominator they copy their V values
+// v[8c + j][d] into registers (c in order, +0 past the last chunk), and once
+// 1 / sum is known lane i of each 16-lane row (one lane partial j per row)
+// holds p[8(16r + i) + j] = e * (1 / sum) in register r (+0 past the last
+// chunk).  Each product p * v takes its p by DPP row broadcast, and the
+// chain adds the products in c order with no LDS read inside it (each
+// product rounded on its own, as in the reference).  The padded steps add
+// +0 * +0 = +0, which
+// leaves every sum unchanged: a chain that starts at +0 never holds -0
+// (round-to-nearest gives +0 for an exact cancellation).
+constexpr int kPvRegChunks = 112;   // 7 registers of 16 chunks (8 spill to scratch)
+constexpr int kPvRegs = kPvRegChunks / 16;
+// v[k] = p_k * v[k] for the 16 chunks of one register (p_k by DPP row
+// broadcast from lane k of the row): the products go first, independent of
+// the chain, so the chain is plain dependent adds (9.5 cycles per step
+// measured, against 13 with each product between two adds)
+template <int K = 0>
+__device__ __forceinline__ void pv_dpp_products(float p, float (&v)[16]) {
+    if constexpr (K < 16) {
+        v[K] = fmul(row_bcast_lane<K>(p), v[K]);
+        pv_dpp_products<K + 1>(p, v);
+    }
+}
+// The chain over NR registers of products (one straight block, so the
+// products of later registers are scheduled among the adds)
+template <int NR>
+__device__ __forceinline__ float pv_chain_regs(const float (&pr)[kPvRegs], float (&vr)[kPvRegs][16]) {
+#pragma unroll
+    for (int r = 0; r < NR; r++) pv_dpp_products(pr[r], vr[r]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = fadd(acc, vr[r][i]);
+    return acc;
+}
+
 // part[j][RP].  Quads past the row re-read its last quad (never used).
 template <int HD, int NC>
 __device__ __forceinline__ void score_loads(__amdgpu_buffer_rsrc_t krs, int r0, int n_quads, int lane, int wave,
@@ -298,7 +341,11 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     float* el = red + 16;   // exponentials in position order (!LONG)
     float* sx = el + ((max_seq + 63) & ~63);   // the serial sum's scratch (!LONG)
     int* sum_ctr = reinterpret_cast<int*>(red + 12);
-    if (tid == 0) *sum_ctr = 0;   // (seen after the score rounds' barriers)
+    int* dma_ctr = reinterpret_cast<int*>(red + 13);   // DMA wavefronts whose V tiles landed
+    if (tid == 0) {   // (seen after the score rounds' barriers)
+        *sum_ctr = 0;
+        *dma_ctr = 0;
+    }
     const float* __restrict__ qh = sq + (size_t)h * HD;
     const int col0 = kvh * HD + ds * kDecDims;
     // keys of this kv head through a buffer descriptor: a per-lane 32-bit
@@ -455,9 +502,40 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     lds_barrier();
     // the first V tiles start now, issued by the DMA wavefronts while
     // wavefront 0 sums
+    const bool regpv = !LONG && n_chunks <= kPvRegChunks && n_tiles <= n_vt;   // (uniform)
     if (dma_wave)
         for (int t = 0; t < n_tiles && t < n_vt; t++)
             v_tile_dma(vt + t * kVTileFloats, vc, kv_dim, col0, t * kVTileRows, seq);
+    // with regpv the DMA wavefronts hold the P.V chains: chain (j, d) of
+    // thread rt = tid - 64 kDmaWave0, j = rt / 32, d = rt % 32
+    const int rt = tid - 64 * kDmaWave0;
+    const int rj = (rt >> 5) & 7, rd = rt & 31;
+    float vr[kPvRegs][16];
+    if (regpv && dma_wave) {
+        // once every DMA wavefront's tiles have landed: V values into
+        // registers while the denominator is summed
+        wait_v_tiles(0);
+        lds_arrive(dma_ctr);
+        lds_wait_count(dma_ctr, kDmaWaves, fault);
+        // (a chunk c of a live 16-group lies in tile c / 32 < n_tiles:
+        // 16 ceil(n / 16) <= 32 ceil(n / 32); rows past seq repeat row
+        // seq - 1, and the partial group's padding is set to +0)
+        const float* vb = vt + rj * kDecDims + rd;
+#pragma unroll
+        for (int r = 0; r < kPvRegs; r++)
+            if (16 * r < n_chunks) {   // (uniform)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    constexpr int kRowFloats = 8 * kDecDims;   // one chunk: 8 rows
+                    const int c = 16 * r + i;
+                    vr[r][i] = vb[(c / 32) * kVTileFloats + (c % 32) * kRowFloats];
+                }
+                if (16 * r + 16 > n_chunks) {   // (uniform)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) vr[r][i] = 16 * r + i < n_chunks ? vr[r][i] : 0.0f;
+                }
+            }
+    }
     if (LONG && tid < 64) {
         // one wavefront, from the transposed row
         const float sum = wave_serial_sum_at([pt, PCS](int i) { return pt[(i & 7) * PCS + (i >> 3)]; }, seq);
@@ -471,55 +549,86 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     }
     lds_barrier();
     const float inv = red[8];
-    for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
-        float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
-        *e = fmul(*e, inv);
-    }
 
     // 3. P.V chains (forward.rs:372-395): lane j adds p*v over c in order.
-    // Chain (j, d) of thread tid < kDecChains: j = tid / 32, d = tid % 32.
-    const int cj = (tid >> 5) & 7, cd = tid & 31;
-    float acc = 0.0f;
-    for (int t = 0; t < n_tiles; t++) {
-        // this wavefront's DMA into tile t; the later tiles already issued
-        // may stay in flight
-        if (dma_wave) wait_v_tiles(min(n_vt - 1, n_tiles - 1 - t));
-        lds_barrier();    // the DMA of tile t (and, for t = 0, the p row)
-        const float* tile = vt + (t % n_vt) * kVTileFloats;
-        if (tid < kDecChains) {
-            const int c0 = t * (kVTileRows / 8);
-            const int steps = min(kVTileRows / 8, n_chunks - c0);
-            const float* pj = pt + cj * PCS + c0;
-            float vv[kVTileRows / 8];
+    if (regpv) {
+        if (dma_wave) {
+            // p = e * (1 / sum) of this row's 16 chunks per register
+            const float* pj = pt + rj * PCS;
+            // (every read issued before the first is used: clamped
+            // indexes, no branch)
+            const int last = n_chunks - 1, i16 = tid & 15;
+            float pr[kPvRegs];
 #pragma unroll
-            for (int i = 0; i < kVTileRows / 8; i++) vv[i] = tile[(8 * i + cj) * kDecDims + cd];
-            if (steps == kVTileRows / 8) {
-                // a whole tile: no per-step bound
+            for (int r = 0; r < kPvRegs; r++) {
+                const int c = 16 * r + i16;
+                const float e = pj[max(min(c, last), 0)];
+                pr[r] = c <= last ? fmul(e, inv) : 0.0f;
+            }
+            float acc = 0.0f;
+            static_assert(kPvRegs == 7, "one case per register count");
+            switch ((n_chunks + 15) / 16) {
+            case 1: acc = pv_chain_regs<1>(pr, vr); break;
+            case 2: acc = pv_chain_regs<2>(pr, vr); break;
+            case 3: acc = pv_chain_regs<3>(pr, vr); break;
+            case 4: acc = pv_chain_regs<4>(pr, vr); break;
+            case 5: acc = pv_chain_regs<5>(pr, vr); break;
+            case 6: acc = pv_chain_regs<6>(pr, vr); break;
+            case 7: acc = pv_chain_regs<7>(pr, vr); break;
+            default: break;   // no whole chunk
+            }
+            part[rj * kDecDims + rd] = acc;
+        }
+    } else {
+        for (int t2 = tid; t2 < seq; t2 += kDecThreads) {
+            float* e = pt + (t2 & 7) * PCS + (t2 >> 3);
+            *e = fmul(*e, inv);
+        }
+        // Chain (j, d) of thread tid < kDecChains: j = tid / 32, d = tid % 32,
+        // V from LDS tiles refilled by the DMA wavefronts.
+        const int cj = (tid >> 5) & 7, cd = tid & 31;
+        float acc = 0.0f;
+        for (int t = 0; t < n_tiles; t++) {
+            // this wavefront's DMA into tile t; the later tiles already issued
+            // may stay in flight
+            if (dma_wave) wait_v_tiles(min(n_vt - 1, n_tiles - 1 - t));
+            lds_barrier();    // the DMA of tile t (and, for t = 0, the p row)
+            const float* tile = vt + (t % n_vt) * kVTileFloats;
+            if (tid < kDecChains) {
+                const int c0 = t * (kVTileRows / 8);
+                const int steps = min(kVTileRows / 8, n_chunks - c0);
+                const float* pj = pt + cj * PCS + c0;
+                float vv[kVTileRows / 8];
 #pragma unroll
-                for (int i = 0; i < kVTileRows / 8; i += 4) {
-                    const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
-                    acc = fadd(acc, fmul(p4.x, vv[i + 0]));
-                    acc = fadd(acc, fmul(p4.y, vv[i + 1]));
-                    acc = fadd(acc, fmul(p4.z, vv[i + 2]));
-                    acc = fadd(acc, fmul(p4.w, vv[i + 3]));
-                }
-            } else {
+                for (int i = 0; i < kVTileRows / 8; i++) vv[i] = tile[(8 * i + cj) * kDecDims + cd];
+                if (steps == kVTileRows / 8) {
+                    // a whole tile: no per-step bound
 #pragma unroll
-                for (int i = 0; i < kVTileRows / 8; i += 4) {
-                    const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
-                    if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vv[i + 0]));
-                    if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vv[i + 1]));
-                    if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vv[i + 2]));
-                    if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                    for (int i = 0; i < kVTileRows / 8; i += 4) {
+                        const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
+                        acc = fadd(acc, fmul(p4.x, vv[i + 0]));
+                        acc = fadd(acc, fmul(p4.y, vv[i + 1]));
+                        acc = fadd(acc, fmul(p4.z, vv[i + 2]));
+                        acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kVTileRows / 8; i += 4) {
+                        const vf4 p4 = *reinterpret_cast<const vf4*>(pj + i);
+                        if (i + 0 < steps) acc = fadd(acc, fmul(p4.x, vv[i + 0]));
+                        if (i + 1 < steps) acc = fadd(acc, fmul(p4.y, vv[i + 1]));
+                        if (i + 2 < steps) acc = fadd(acc, fmul(p4.z, vv[i + 2]));
+                        if (i + 3 < steps) acc = fadd(acc, fmul(p4.w, vv[i + 3]));
+                    }
                 }
             }
+            if (t + n_vt < n_tiles) {
+                lds_barrier();    // tile t consumed before it is refilled
+                if (dma_wave) v_tile_dma(vt + (t % n_vt) * kVTileFloats, vc, kv_dim, col0, (t + n_vt) * kVTileRows, seq);
+            }
         }
-        if (t + n_vt < n_tiles) {
-            lds_barrier();    // tile t consumed before it is refilled
-            if (dma_wave) v_tile_dma(vt + (t % n_vt) * kVTileFloats, vc, kv_dim, col0, (t + n_vt) * kVTileRows, seq);
-        }
+        if (tid < kDecChains) part[cj * kDecDims + cd] = acc;
     }
-    if (tid < kDecChains) part[cj * kDecDims + cd] = acc;
     __syncthreads();
 
     // 4. out[d] = reduce_add(8 lane chains) + the seq % 8 tail in order,
@@ -531,7 +640,11 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         float out = reduce_add8(lj);
 #pragma unroll
         for (int i = 0; i < 7; i++)
-            if (n_chunks * 8 + i < seq) out = fadd(out, fmul(pt[i * PCS + n_chunks], vtail[i]));
+            if (n_chunks * 8 + i < seq) {
+                // (p normalized in place only on the tile path)
+                const float pe = pt[i * PCS + n_chunks];
+                out = fadd(out, fmul(regpv ? fmul(pe, inv) : pe, vtail[i]));
+            }
         const size_t col = (size_t)h * HD + (size_t)ds * kDecDims + tid;
         if (att_f32) att_f32[col] = out;
         if constexpr (QF >= 0) {
