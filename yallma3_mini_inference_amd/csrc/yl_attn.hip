@@ -637,20 +637,24 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
         float lj[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) lj[j] = part[j * kDecDims + tid];
+        // the tail's p values, all read before the first is used (pt rows
+        // have PCS > n_chunks entries; p is normalized in place only on the
+        // tile path)
+        float pe[7];
+#pragma unroll
+        for (int i = 0; i < 7; i++) pe[i] = pt[i * PCS + n_chunks];
         float out = reduce_add8(lj);
 #pragma unroll
-        for (int i = 0; i < 7; i++)
-            if (n_chunks * 8 + i < seq) {
-                // (p normalized in place only on the tile path)
-                const float pe = pt[i * PCS + n_chunks];
-                out = fadd(out, fmul(regpv ? fmul(pe, inv) : pe, vtail[i]));
-            }
+        for (int i = 0; i < 7; i++) {
+            const float sum = fadd(out, fmul(regpv ? fmul(pe[i], inv) : pe[i], vtail[i]));
+            out = n_chunks * 8 + i < seq ? sum : out;
+        }
         const size_t col = (size_t)h * HD + (size_t)ds * kDecDims + tid;
         if (att_f32) att_f32[col] = out;
         if constexpr (QF >= 0) {
-            float am = fabsf(out);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+            // (fmaxf keeps the larger non-NaN operand, so the order of the
+            // 32-lane reduction does not matter)
+            float am = group_max(fabsf(out), 32);
             am = fmaxf(am, 0.0f);
             const float s = group_scale<QF>(am);
             aq[col] = (int8_t)quant_one<QF>(out, s);

@@ -143,10 +143,18 @@ __device__ __forceinline__ float group_max(float v, int P) {
     return v;
 }
 
+// Maximum over the 64 lanes of a wavefront (every lane active), returned to
+// every lane: the 16-lane row maxima by DPP, then the four rows' by
+// readlane, with no LDS round trip.  fmaxf keeps the larger non-NaN operand,
+// so the order of the reduction does not change the result.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = group_max(v, 16);
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // DPP move with out-of-row (or masked-off) lanes reading 0.
