@@ -27,8 +27,9 @@
 //    (v_dot4_i32_i8) becomes the f32 term ((float)isum * w_scale) * x_scale,
 //    and the row's first lane adds the slot's terms of its row in block
 //    order onto the row's accumulator, reading lane j's term through DPP
-//    (row_shl:j) -- the reference's `xout += term` sequence, so every output
-//    is bit-identical to matmul_q8_slices.  The sums advance while later
+//    (row_shl:j), or by readlane when a row spans the wavefront -- the
+//    reference's `xout += term` sequence, so every output is bit-identical
+//    to matmul_q8_slices.  The sums advance while later
 //    slots are in flight; the loads of slot k + LA go out after slot k.
 // 4. Epilogues: residual add (WO, W2), RoPE + K/V cache (QKV), SwiGLU +
 //    quantize of h (gate/up; the only cross-wavefront step, after one
@@ -285,12 +286,50 @@ __device__ __forceinline__ float chain_slot_dppg(float acc, float term, int firs
     return chain_slot_partg<LPR, SPLIT, G>(acc, term, valid);
 }
 
+// Chain step of one slot when a row spans the whole wavefront (LPR = 64):
+// each term in block order by readlane, added in every lane (the row's sum
+// is the same in all 64).  valid (uniform) terms of a partial slot.
+__device__ __forceinline__ float lane_term(float term, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term), l));
+}
+// (the scheduler issues each term's readlane two adds ahead of its use)
+template <bool SPLIT, int B, int I = 0>
+__device__ __forceinline__ void wave_terms16_at(float (&v)[16], float term) {
+    if constexpr (I < 16) {
+        v[I] = lane_term(term, term_lane<64, SPLIT, B + I>());
+        wave_terms16_at<SPLIT, B, I + 1>(v, term);
+    }
+}
+template <bool SPLIT, int G = 0>
+__device__ __forceinline__ float chain_wave_full(float acc, float term) {
+    if constexpr (G < 4) {
+        float v[16];
+        wave_terms16_at<SPLIT, 16 * G>(v, term);
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = fadd(acc, v[i]);
+        return chain_wave_full<SPLIT, G + 1>(acc, term);
+    } else {
+        return acc;
+    }
+}
+template <bool SPLIT>
+__device__ __forceinline__ float chain_slot_wave(float acc, float term, int first_block, int nb) {
+    const int valid = nb - first_block;   // uniform
+    if (valid >= 64) return chain_wave_full<SPLIT>(acc, term);
+    for (int i = 0; i < valid; i++) acc = fadd(acc, lane_term(term, SPLIT ? (i < 32 ? 2 * i : 2 * (i - 32) + 1) : i));
+    return acc;
+}
+
 // Few wavefronts per SIMD: registers go to loads in flight rather than to
 // occupancy.
 template <int WF, int EPI, bool EMB, int LPR, int PPL>
 __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu(1, 3))) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    static_assert(LPR == 8 || LPR == 16, "a row's lanes share one 16-lane DPP row");
+    // a row's lanes share one 16-lane DPP row, or a row spans the wavefront
+    // (one scale per block, the residual and plain-store epilogues)
+    static_assert(LPR == 8 || LPR == 16 ||
+                      (LPR == 64 && blocks_per_group<WF>() == 1 && (EPI == kEpiResid || EPI == kEpiStore)),
+                  "lanes per row");
     constexpr int RW = 64 / LPR;          // rows per weight wavefront
     constexpr bool kNorm = EPI == kEpiQkvRope || EPI == kEpiSwiglu;
     constexpr bool kQPro = EPI == kEpiResidQ;   // an f32 input row, quantized here (no RMSNorm)
@@ -587,7 +626,8 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
                 acc = chain_slot_dppg<LPR, kSplit, kBlocksPerScale>(acc, term, k * LPR, nb);
             } else {
                 const float term = fmul(fmul((float)isum, ws), xsl[bb]);
-                acc = chain_slot_dpp<LPR, kSplit>(acc, term, k * LPR, nb);
+                if constexpr (LPR == 64) acc = chain_slot_wave<kSplit>(acc, term, k * LPR, nb);
+                else acc = chain_slot_dpp<LPR, kSplit>(acc, term, k * LPR, nb);
             }
             if (k + LA < PPL) issue(k + LA);
         }
@@ -661,12 +701,22 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
 // to 64, then 16 lanes with 8, 16 or 32 slots.  A row's lanes stay inside one 16-lane DPP row, where the
 // row sums gather the terms.  The gate/up matmul needs 64 rows per
 // workgroup (8 weight wavefronts of 8 rows), so it keeps 8 lanes per row and
-// takes 16 slots up to 128 blocks.
+// takes 16 slots up to 128 blocks.  Residual and plain-store matmuls of 128
+// to 512 blocks and at most 4096 rows, in formats with one scale per block,
+// give each row a whole wavefront (64 lanes, 2, 4 or 8 slots, 8 rows per
+// workgroup): with few rows (the down projection's 2048) that keeps 8
+// weight wavefronts per CU streaming instead of 2.
 struct GemvPlan {
     int lpr, ppl, nww;
 };
-static bool plan_gemv(int o, int nb, int epi, GemvPlan* p) {
+static bool plan_gemv(int o, int nb, int epi, bool wave_rows, GemvPlan* p) {
     if (nb <= 0) return false;
+    if (wave_rows && (epi == kEpiResid || epi == kEpiStore) && nb >= 128 && nb <= 512 && o <= 4096) {
+        p->lpr = 64;
+        p->ppl = nb <= 128 ? 2 : nb <= 256 ? 4 : 8;
+        p->nww = kMaxWeightWaves;
+        return true;
+    }
     if (epi == kEpiSwiglu) {
         if (o % 64 || nb > 128) return false;
         p->lpr = 8;
@@ -732,6 +782,16 @@ static hipError_t launch_plan(const GemvArgs& a, const GemvPlan& p, int batch, h
         default: return hipErrorInvalidValue;
         }
     }
+    if constexpr (blocks_per_group<WF>() == 1 && (EPI == kEpiResid || EPI == kEpiStore)) {
+        if (p.lpr == 64) {
+            switch (p.ppl) {
+            case 2: return launch_k<WF, EPI, EMB, 64, 2>(a, p.nww, batch, st);
+            case 4: return launch_k<WF, EPI, EMB, 64, 4>(a, p.nww, batch, st);
+            case 8: return launch_k<WF, EPI, EMB, 64, 8>(a, p.nww, batch, st);
+            default: return hipErrorInvalidValue;
+            }
+        }
+    }
     if constexpr (EPI != kEpiSwiglu) {
         if (p.lpr == 16) {
             switch (p.ppl) {
@@ -749,7 +809,7 @@ static hipError_t launch_plan(const GemvArgs& a, const GemvPlan& p, int batch, h
 template <int WF>
 static hipError_t launch_wf(const GemvArgs& a, int epi, int batch, hipStream_t st) {
     GemvPlan p{};
-    if (!plan_gemv(a.o, a.nb, epi, &p)) return hipErrorInvalidValue;
+    if (!plan_gemv(a.o, a.nb, epi, blocks_per_group<WF>() == 1, &p)) return hipErrorInvalidValue;
     switch (epi) {
     case kEpiStore: return launch_plan<WF, kEpiStore, false>(a, p, batch, st);
     case kEpiQkvRope:
@@ -784,9 +844,9 @@ hipError_t launch_gemv(const GemvArgs& args, int wfmt, int epi, int batch, hipSt
 
 size_t gemv_bytes_per_row_block(int wfmt) { return wfmt == kQ8 ? 34 : 18; }
 
-bool gemv_launch_shape(int o, int nb, int epi, int* grid, int* threads) {
+bool gemv_launch_shape(int o, int nb, int epi, int wfmt, int* grid, int* threads) {
     GemvPlan p{};
-    if (!plan_gemv(o, nb, epi, &p)) return false;
+    if (!plan_gemv(o, nb, epi, wfmt == kQ8 || wfmt == kQ4 || wfmt == kQ8S, &p)) return false;
     const int na = epi == kEpiQkvRope || epi == kEpiSwiglu || epi == kEpiResidQ ? kNormWaves : 1;
     const int R = (64 / p.lpr) * p.nww;
     *grid = (o + R - 1) / R;

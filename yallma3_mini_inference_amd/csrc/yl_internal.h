@@ -146,8 +146,9 @@ unsigned* wait_fault_word(bool allocate);
 // kernel launchers; all return the hipError_t of the launch
 hipError_t launch_set_state(StepState* st, int32_t pos, uint32_t token, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs& a, int wfmt, int epi, int batch, hipStream_t s);
-// the one-token GEMV's grid and workgroup size for o rows of nb blocks
-bool gemv_launch_shape(int o, int nb, int epi, int* grid, int* threads);
+// the one-token GEMV's grid and workgroup size for o rows of nb blocks in
+// weight format wfmt
+bool gemv_launch_shape(int o, int nb, int epi, int wfmt, int* grid, int* threads);
 // a plain stream of abytes at a then bbytes at b (multiples of 16) by `grid`
 // workgroups of `threads` (measurement only; sink is never written in practice)
 hipError_t launch_stream(const void* a, size_t abytes, const void* b, size_t bbytes, int grid, int threads,

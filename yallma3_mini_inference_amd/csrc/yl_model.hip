@@ -2215,7 +2215,7 @@ yl_status yl_profile_stream(const yl_model* m, yl_session* s, int32_t kernel_cla
         const Layer& L = m->layers[l];
         const QMat& w = kernel_class == kOpQkv ? L.qkv : kernel_class == kOpWo ? L.wo : kernel_class == kOpW13 ? L.w13 : L.w2;
         int grid = 0, threads = 0;
-        if (!gemv_launch_shape(w.o, w.nb, epi, &grid, &threads)) { ec = hipErrorInvalidValue; break; }
+        if (!gemv_launch_shape(w.o, w.nb, epi, w.fmt, &grid, &threads)) { ec = hipErrorInvalidValue; break; }
         const size_t qb = (size_t)w.o * (w.fmt == kQ4 ? w.n / 2 : w.n), db = (size_t)w.o * w.nb * 2;
         nbytes = qb + db;
         ec = launch_stream(w.qs, qb, w.d, db, grid, threads, reinterpret_cast<unsigned*>(s->logits), s->stream);
