@@ -347,9 +347,7 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
     int8_t* xl = reinterpret_cast<int8_t*>(smem + L.act);
     float* xsl = reinterpret_cast<float*>(smem + L.scales);
     int* ctr_sq = reinterpret_cast<int*>(smem + L.sync);       // squares written
-    int* ctr_ss = ctr_sq + 1;                                    // ss published
     int* ctr_row = ctr_sq + 2;                                   // activation row ready
-    float* ssl = reinterpret_cast<float*>(ctr_sq + 3);
     float* initl = reinterpret_cast<float*>(smem + L.init);
     float* outl = reinterpret_cast<float*>(smem + L.outs);
 
@@ -430,46 +428,45 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
             }
             // initial values of the rows' sums: the K/V `+=` columns start
             // from the cache (forward.rs:166-169, weight_type.rs:190-201),
-            // published with the activation row (ctr_row) while the chain runs
-            if (wave == NA - 1) {
+            // and (QKV) the epilogue's position and the RoPE angles of the
+            // rows (util.rs:653-718; the table row of the position), loaded
+            // by the last activation wavefront into registers before the
+            // chain and staged after it (lane i: row i, R <= 64), published
+            // with the activation row (ctr_row)
+            static_assert(64 / LPR * kMaxWeightWaves <= 64, "one lane per row of the workgroup");
+            float ini = 0.0f, rcos = 0.0f, rsin = 0.0f;
+            if (wave == NA - 1 && lane < R) {
                 if constexpr (EPI == kEpiQkvRope) {
-                    // the epilogue's position and the RoPE angles of the rows
-                    // (util.rs:653-718; the table row of the position)
                     const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
+                    const int row = min(row0 + lane, o - 1);
+                    const int col = row < att ? row : (row < att + kv ? row - att : row - att - kv);
+                    const int pair = (col % hd) >> 1;
+                    rcos = a.rope_cos[(size_t)pos * (hd >> 1) + pair];
+                    rsin = a.rope_sin[(size_t)pos * (hd >> 1) + pair];
+                    const bool is_k = row >= att && row < att + kv, is_v = row >= att + kv;
+                    const int c = is_v ? row - att - kv : (is_k ? qk_column(row - att, a.head_size, a.hf_rows) : 0);
+                    if ((is_k || is_v) && c < (kv / 4) * 4)
+                        ini = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
+                }
+            }
+            // the serial sum of squares -> ss: every activation wavefront
+            // runs the 8 chains itself (lanes 0-7), so none waits for
+            // another's result
+            float ss = 1.0f;
+            if constexpr (kNorm) {
+                lds_wait_count(ctr_sq, NA, a.fault);
+                ss = rowq_chain(dim, a.eps, sq);
+            }
+            if (wave == NA - 1) {
+                if (lane < R) initl[lane] = ini;
+                if constexpr (EPI == kEpiQkvRope) {
                     float* ropel = reinterpret_cast<float*>(smem + L.rope);
-                    for (int i = lane; i < R; i += 64) {
-                        const int row = min(row0 + i, o - 1);
-                        const int col = row < att ? row : (row < att + kv ? row - att : row - att - kv);
-                        const int pair = (col % hd) >> 1;
-                        ropel[2 * i] = a.rope_cos[(size_t)pos * (hd >> 1) + pair];
-                        ropel[2 * i + 1] = a.rope_sin[(size_t)pos * (hd >> 1) + pair];
+                    if (lane < R) {
+                        ropel[2 * lane] = rcos;
+                        ropel[2 * lane + 1] = rsin;
                     }
                     if (lane == 0) reinterpret_cast<int*>(ropel)[2 * R] = pos;
                 }
-                for (int i = lane; i < R; i += 64) {
-                    float v = 0.0f;
-                    if constexpr (EPI == kEpiQkvRope) {
-                        const int row = min(row0 + i, o - 1);
-                        const int att = a.att_dim, kv = a.kv_dim;
-                        const bool is_k = row >= att && row < att + kv, is_v = row >= att + kv;
-                        const int c = is_v ? row - att - kv : (is_k ? qk_column(row - att, a.head_size, a.hf_rows) : 0);
-                        if ((is_k || is_v) && c < (kv / 4) * 4)
-                            v = is_v ? a.v_cache[(size_t)pos * kv + c] : a.k_cache[(size_t)c * a.kv_ld + pos];
-                    }
-                    initl[i] = v;
-                }
-            }
-            // the serial sum of squares (wavefront 0, lanes 0-7) -> ss
-            float ss = 1.0f;
-            if constexpr (kNorm) {
-                if (wave == 0) {
-                    lds_wait_count(ctr_sq, NA, a.fault);
-                    const float s0 = rowq_chain(dim, a.eps, sq);
-                    if (lane == 0) *ssl = s0;
-                    lds_arrive(ctr_ss);
-                }
-                lds_wait_count(ctr_ss, 1, a.fault);
-                ss = *ssl;
             }
             // o = w * (ss * x) and the GSZ-group quantization of the
             // member's slices (the 4 lanes of a quad hold one 32-group, 8
