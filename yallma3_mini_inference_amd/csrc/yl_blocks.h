@@ -580,6 +580,10 @@ __device__ __forceinline__ float seg_serial_sum(const float* v, int n, const dou
             r0[r] = p0[16 * (r < rlast ? r : rlast)];
             r1[r] = p1[16 * (r < rlast ? r : rlast)];
         }
+        // (used here, so the compiler keeps every read ahead of the chains
+        // instead of sinking each into the block of adds that needs it)
+#pragma unroll
+        for (int r = 0; r < kSegShortRegs; r++) asm volatile("" ::"v"(r0[r]), "v"(r1[r]));
         seg_chain_regs(s0, r0, s1, r1, L);
     } else {
         // Longer segments: chunks of 16 * kSegShortRegs values, each read
@@ -594,6 +598,8 @@ __device__ __forceinline__ float seg_serial_sum(const float* v, int n, const dou
                 r0[r] = p0[c0 + 16 * (r < rlast ? r : rlast)];
                 r1[r] = p1[c0 + 16 * (r < rlast ? r : rlast)];
             }
+#pragma unroll
+            for (int r = 0; r < kSegShortRegs; r++) asm volatile("" ::"v"(r0[r]), "v"(r1[r]));
             seg_chain_regs(s0, r0, s1, r1, len);
         }
     }
@@ -675,6 +681,8 @@ __device__ __forceinline__ float seg_serial_sum_wide(const float* v, int n, cons
         const int rlast = (L - 1) / 16;
 #pragma unroll
         for (int k = 0; k < kSegShortRegs; k++) r[k] = p[16 * (k < rlast ? k : rlast)];
+#pragma unroll
+        for (int k = 0; k < kSegShortRegs; k++) asm volatile("" ::"v"(r[k]));   // (see seg_serial_sum)
         seg_chain_regs(s0, r, s1, r, L);
     } else {
         // chunks of 16 * kSegShortRegs values read into registers whole
@@ -685,6 +693,8 @@ __device__ __forceinline__ float seg_serial_sum_wide(const float* v, int n, cons
             const int rlast = (len - 1) / 16;
 #pragma unroll
             for (int k = 0; k < kSegShortRegs; k++) r[k] = p[c0 + 16 * (k < rlast ? k : rlast)];
+#pragma unroll
+            for (int k = 0; k < kSegShortRegs; k++) asm volatile("" ::"v"(r[k]));
             seg_chain_regs(s0, r, s1, r, len);
         }
     }
