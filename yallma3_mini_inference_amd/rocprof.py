@@ -57,7 +57,7 @@ CLASS_KERNELS = {
     "qkv": "k_gemv<0, 1, false, 16, 4>",
     "wo": "k_gemv<0, 2, false, 16, 4>",
     "w13": "k_gemv<0, 3, false, 8, 8>",
-    "w2": "k_gemv<0, 2, false, 16, 16>",
+    "w2": "k_gemv<0, 2, false, 64, 4>",
     "attention": "k_attn_decode<0, 64, false>",
 }
 # algorithmic bytes per launch at the Llama-3.2-1B shape, as bench.py counts
