@@ -119,12 +119,13 @@ def _gguf_q8_blocks(wf):
     return out.ravel(), q.ravel(), d.astype(np.float16).astype(np.float32)
 
 
-# 128-512 blocks per row and at most 4096 rows take one wavefront per row:
-# whole slots, a partial slot (160 blocks), 512 blocks, 4096 rows, and 4097
-# rows on the 16-lane rows
+# 128-512 blocks per row, at most 2048 rows and 2048 x 256 row-blocks take
+# one wavefront per row: whole slots, a partial slot (160 blocks), 512
+# blocks, both bounds met exactly (2048 x 256, 1024 x 512), and one past each
+# on the 16-lane rows
 @pytest.mark.parametrize("batch,n,o", [(1, 2048, 2048), (1, 8192, 1024), (3, 576, 190), (2, 4096, 37),
-                                       (1, 14336, 128), (1, 5120, 77), (2, 16384, 64), (1, 8192, 4096),
-                                       (1, 8192, 4097)])
+                                       (1, 14336, 128), (1, 5120, 77), (2, 16384, 64), (1, 8192, 2048),
+                                       (1, 8192, 2049), (1, 16384, 1024), (1, 16384, 1025)])
 def test_matmul_q8_parity(gpu, oracle, batch, n, o):
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul
     rng = np.random.default_rng(n + o)

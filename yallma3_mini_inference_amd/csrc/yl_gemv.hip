@@ -699,16 +699,21 @@ __global__ __launch_bounds__(kGemvMaxThreads) __attribute__((amdgpu_waves_per_eu
 // row sums gather the terms.  The gate/up matmul needs 64 rows per
 // workgroup (8 weight wavefronts of 8 rows), so it keeps 8 lanes per row and
 // takes 16 slots up to 128 blocks.  Residual and plain-store matmuls of 128
-// to 512 blocks and at most 4096 rows, in formats with one scale per block,
-// give each row a whole wavefront (64 lanes, 2, 4 or 8 slots, 8 rows per
-// workgroup): with few rows (the down projection's 2048) that keeps 8
-// weight wavefronts per CU streaming instead of 2.
+// to 512 blocks, at most 2048 rows and at most 2048 x 256 row-blocks, in
+// formats with one scale per block, give each row a whole wavefront (64
+// lanes, 2, 4 or 8 slots, 8 rows per workgroup): with few rows (the 1B down
+// projection's 2048) that keeps 8 weight wavefronts per CU streaming
+// instead of 2.  Its chain advances one row per instruction (a DPP chain
+// advances four), so beyond those bounds the chain's VALU work outgrows the
+// stream (Llama-3-8B's down projection, 4096 x 448 blocks: 13.8 us against
+// 10.1 on 16-lane rows).
 struct GemvPlan {
     int lpr, ppl, nww;
 };
 static bool plan_gemv(int o, int nb, int epi, bool wave_rows, GemvPlan* p) {
     if (nb <= 0) return false;
-    if (wave_rows && (epi == kEpiResid || epi == kEpiStore) && nb >= 128 && nb <= 512 && o <= 4096) {
+    if (wave_rows && (epi == kEpiResid || epi == kEpiStore) && nb >= 128 && nb <= 512 && o <= 2048 &&
+        o * nb <= 2048 * 256) {
         p->lpr = 64;
         p->ppl = nb <= 128 ? 2 : nb <= 256 ? 4 : 8;
         p->nww = kMaxWeightWaves;
