@@ -176,6 +176,56 @@ def test_matmul_mfma_parity(gpu, oracle, fmt, batch, n, o):
     assert_bits(out, ref)
 
 
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("negz", [False, True])
+@pytest.mark.parametrize("batch,n,o", [(96, 512, 384), (2048, 256, 2304)])
+def test_matmul_mfma_special_scales(gpu, oracle, fmt, negz, batch, n, o):
+    # The GEMM folds the int32-to-f32 convert into an FMA on a biased dot for
+    # f16 scales.  That form differs from the reference's only in the sign of
+    # a zero term, which the sum can show only from a -0 start, and on
+    # non-finite scales; both must take the reference's form.  Rows 0..127:
+    # zero, -0, negative, smallest-subnormal and largest f16 scales; token 10
+    # has all-zero activations (every term of its outputs is a signed zero),
+    # token 11 two zero blocks.  Initial values are +0 there (the biased form
+    # stays exact) or -0 (negz: the workgroup must fall back).  Rows 128..255
+    # hold inf, -inf and NaN scales.  (96, 512, 384) runs 64-token tiles,
+    # (2048, 256, 2304) 128-token tiles.
+    from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, matmul
+    rng = np.random.default_rng(5 + fmt + 2 * negz + n)
+    nb = n // 32
+    if fmt == 0:
+        wq = rng.integers(-128, 128, o * n).astype(np.int8)
+    else:
+        wq = rng.integers(0, 16, o * n).astype(np.int8)
+    ws = rng.normal(0, 0.003, (o, nb)).astype(np.float16).astype(np.float32)
+    ws[3, :] = 0.0
+    ws[4, :] = -0.0
+    ws[5, 2] = 0.0
+    ws[6, :] = -np.abs(ws[6, :])
+    ws[7, 0] = np.float32(2.0 ** -24)
+    ws[8, 1] = np.float32(65504.0)
+    ws[9, :] = -np.float32(2.0 ** -24)
+    ws[130, 3] = np.inf
+    ws[131, 5] = -np.inf
+    ws[132, 1] = np.nan
+    w = QuantizedWeight.upload(WeightFormat.Q8_0 if fmt == 0 else WeightFormat.Q4_0, wq, ws.ravel(), o, n)
+    x = rng.normal(0, 1, (batch, n)).astype(np.float32)
+    x[10, :] = 0.0
+    x[11, :64] = 0.0
+    xq, xs = oracle.quantize(fmt, x.ravel())
+    init = rng.normal(0, 1, (batch, o)).astype(np.float32)
+    init[10, :128] = -0.0 if negz else 0.0
+    init[11, :16] = -0.0 if negz else 0.0
+    out = matmul(init.ravel().copy(), xq, xs, w, n, o, fmt=WeightFormat(fmt))
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = oracle.matmul_q8_slices(init.ravel().copy(), xq, xs, wq, ws.ravel(), n, o)
+    nan = np.isnan(ref)
+    assert nan.any() and np.array_equal(np.isnan(out), nan)
+    assert_bits(np.where(nan, 0, out), np.where(nan, 0, ref))
+    zero_rows = ref.reshape(batch, o)[10, :128]
+    assert (np.signbit(zero_rows).any() if negz else True) and np.all(zero_rows == 0)
+
+
 def test_matmul_format_mismatch_raises(gpu):
     from yallma3_mini_inference_amd import QuantizedWeight, WeightFormat, YlError, matmul
     w = QuantizedWeight.upload(WeightFormat.Q8_0, np.ones(64, np.int8), np.ones(2, np.float32), 2, 32)

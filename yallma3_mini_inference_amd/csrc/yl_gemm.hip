@@ -8,8 +8,11 @@
 // exact int32 dot of one 32-element block.  v_mfma_i32_32x32x32_i8 has
 // K = 32: one instruction yields exactly the 32x32 block dots of one block,
 // and each lane then folds its 16 dots into its 16 f32 accumulators in
-// block order with the reference's two roundings.  The f32 work (convert,
-// two products, one sum per output and block) is the bound, not the MFMA.
+// block order with the reference's two roundings.  The f32 work per output
+// and block is the bound, not the MFMA: with f16 scales (Q8_0, Q4_0) one
+// fused multiply-add on a biased dot (the convert folded away; see `bias`
+// in k_gemm), one product and one sum; with f32 scales a convert, two
+// products and one sum.
 //
 // Tile: a 256-thread workgroup owns TM tokens x 128 weight rows (TM = 128,
 // or 64 when the 128-token tiles would not give every CU two workgroups);
@@ -124,6 +127,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     float acc[TMW][2][16];
     int pos = 0;
     if constexpr (EPI == kEpiQkvRope) pos = a.state->pos;
+    auto init_acc = [&]() {
 #pragma unroll
     for (int tm = 0; tm < TMW; tm++)
 #pragma unroll
@@ -150,6 +154,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
                 acc[tm][tn][i] = v;
             }
+    };
 
     // DMA of stage s (blocks 2s, 2s+1) into LDS buffer `buf`.  Token and
     // row indices past the matrix re-read the last valid one (results unused).
@@ -216,6 +221,49 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         }
     };
 
+    // f16 block scales (Q8_0, Q4_0): every block dot starts from the int32
+    // bits of the float 3*2^22 instead of 0, so the MFMA's result reads as the
+    // float f = 3*2^22 + isum, exactly (|isum| <= 32*128*128 < 2^22).  Then
+    //     fma(f, ws, -3*2^22*ws) = round(isum * ws),
+    // one rounding of the exact product (3*2^22*ws is exact for an f16 ws):
+    // the convert drops out of the per-output work (3 VALU operations
+    // instead of 4).  The value equals (float)isum * ws, except that an exact
+    // cancellation gives +0 where isum = 0 or ws = 0 gives the product's
+    // signed zero.  A zero term's sign changes the sum only while the
+    // accumulator is -0, and an accumulator that does not start at -0 never
+    // becomes -0 (+0 + -0 = +0, and x + -x = +0).  A non-finite scale makes
+    // inf - inf.  So the fused pass is exact unless a -0 initial value or a
+    // non-finite scale is present; the lanes that see one flag it, and the
+    // workgroup then reloads its initial values (only the epilogue writes
+    // them) and runs the reference's form.  The bias tuple is opaque to the
+    // compiler, so it stays in registers rather than being rematerialized
+    // before each MFMA.
+    constexpr bool kBias = WF == kQ8 || WF == kQ4;
+    constexpr float kBiasF = 12582912.0f;   // 3 * 2^22, bits 0x4B400000
+    __shared__ int redo;
+    v16i bias = {};
+    if constexpr (kBias) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) bias[i] = 0x4B400000;
+        asm volatile("" : "+v"(bias));
+        if (threadIdx.x == 0) redo = 0;   // ordered before any flag by the first stage's barrier
+    }
+
+    // group dots of the f32-scaled formats with 2 or 4 blocks per group,
+    // accumulated over the group's blocks (exact int32)
+    constexpr int G = gm_bpg<WF>();
+    // the K loop: FUSED.value selects the biased form above
+    auto run = [&](auto FUSED) -> bool {
+    constexpr bool kFused = decltype(FUSED)::value;
+    bool flag = false;   // this lane saw a -0 initial value or a non-finite scale
+    if constexpr (kFused) {
+#pragma unroll
+        for (int tm = 0; tm < TMW; tm++)
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) flag = flag || __float_as_uint(acc[tm][tn][i]) == 0x80000000u;
+    }
     // the initial values have landed before any DMA is issued, so the
     // stage waits below count DMA instructions only
     wait_vm_all();
@@ -224,9 +272,6 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int s = 0; s < kGmStages - 1; s++)
         if (s < nst) issue(gsm + s * S::bytes, s);
 
-    // group dots of the f32-scaled formats with 2 or 4 blocks per group,
-    // accumulated over the group's blocks (exact int32)
-    constexpr int G = gm_bpg<WF>();
     v16i gd[TMW][2] = {};
     for (int s = 0; s < nst; s++) {
         gm_wait<S::dma>(min(kGmStages - 2, nst - 1 - s));
@@ -296,6 +341,34 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
                 for (int g = 0; g < 4; g++)
                     xv[tm][g] = *reinterpret_cast<const vf4*>(xsl + blk * TM + WT * wm + 32 * tm + 8 * g + 4 * lh);
+            if constexpr (kFused) {
+                // two tiles in flight: tile k+1's MFMA runs while tile k is
+                // folded (the bias leaves no registers for all four)
+                flag = flag || !(fabsf(wsc[0]) < INFINITY) || !(fabsf(wsc[1]) < INFINITY);
+                const float cb[2] = {fmul(-kBiasF, wsc[0]), fmul(-kBiasF, wsc[1])};
+                // f32 scales in registers: otherwise the compiler folds the f16
+                // convert into each FMA (v_fma_mix_f32)
+                asm volatile("" : "+v"(wsc[0]), "+v"(wsc[1]));
+                constexpr int NT = TMW * 2;
+                v16i d[2];
+                d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[0], bv[0], bias, 0, 0, 0);
+#pragma unroll
+                for (int k = 0; k < NT; k++) {
+                    if (k + 1 < NT)
+                        d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[(k + 1) >> 1], bv[(k + 1) & 1],
+                                                                               bias, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int tm = k >> 1, tn = k & 1;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const float f = __int_as_float(d[k & 1][i]);
+                        const float term = fmul(__builtin_fmaf(f, wsc[tn], cb[tn]), xv[tm][i >> 2][i & 3]);
+                        acc[tm][tn][i] = fadd(acc[tm][tn][i], term);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                continue;
+            }
             // the four tiles' dots first (in separate registers), so the f32
             // work of one tile does not wait on the next tile's MFMA
             v16i dots[TMW][2];
@@ -317,6 +390,20 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                         acc[tm][tn][i] = fadd(acc[tm][tn][i], term);
                     }
         }
+    }
+    return flag;
+    };
+
+    init_acc();
+    if constexpr (kBias) {
+        if (run(std::true_type{})) redo = 1;
+        __syncthreads();   // every flag is in; every wavefront is done with the LDS stages
+        if (redo) {
+            init_acc();
+            run(std::false_type{});
+        }
+    } else {
+        run(std::false_type{});
     }
 
     // epilogues
