@@ -45,32 +45,47 @@ __device__ __forceinline__ float reduce_add8(const float l[8]) {
 // correctly rounded expf except with probability ~1e-9 per input; it stands
 // in for f32::exp in the softmax (forward.rs:358) and wide::f32x8::exp in
 // SwiGLU (forward.rs:230).
-__device__ __forceinline__ float expf_rn(float xf) {
+// Its binary64 constants (the polynomial's 1/2 and 1s are inline operands).
+// f64 operations take no 64-bit literal, so an immediate constant is moved
+// into a register pair at each use (two moves per Horner step ahead of a
+// v_fmac_f64).  A kernel that evaluates many exponentials takes the
+// constants into registers once (expf_k_regs) and passes them to
+// expf_rn(x, k), whose steps are then register-operand FMAs: the same
+// operations on the same values, so the same results.
+struct ExpfK {
+    double log2e, ln2_hi, ln2_lo;
+    double c[11];   // Horner coefficients of degrees 13 .. 3
+};
+__device__ __forceinline__ constexpr ExpfK expf_k_imm() {
+    return ExpfK{0x1.71547652b82fep+0, 0x1.62e42fee00000p-1, 0x1.a39ef35793c76p-33,
+                 {0x1.6124613a86d09p-33, 0x1.1eed8eff8d898p-29, 0x1.ae64567f544e4p-26, 0x1.27e4fb7789f5cp-22,
+                  0x1.71de3a556c734p-19, 0x1.a01a01a01a01ap-16, 0x1.a01a01a01a01ap-13, 0x1.6c16c16c16c17p-10,
+                  0x1.1111111111111p-7, 0x1.5555555555555p-5, 0x1.5555555555555p-3}};
+}
+// the constants in registers, opaque to the compiler (so not re-materialized)
+__device__ __forceinline__ ExpfK expf_k_regs() {
+    ExpfK k = expf_k_imm();
+    asm volatile("" : "+v"(k.log2e), "+v"(k.ln2_hi), "+v"(k.ln2_lo));
+#pragma unroll
+    for (int i = 0; i < 11; i++) asm volatile("" : "+v"(k.c[i]));
+    return k;
+}
+__device__ __forceinline__ float expf_rn(float xf, const ExpfK& k) {
     if (xf != xf) return xf;
     if (xf > 88.8f) return __builtin_inff();
     if (xf < -104.0f) return 0.0f;
     const double x = (double)xf;
-    const double log2e = 0x1.71547652b82fep+0;
-    const double ln2_hi = 0x1.62e42fee00000p-1;
-    const double ln2_lo = 0x1.a39ef35793c76p-33;
-    const double kd = __builtin_rint(x * log2e);
-    const double r = (x - kd * ln2_hi) - kd * ln2_lo;
-    double p = 0x1.6124613a86d09p-33;
-    p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
-    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
-    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
-    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
-    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
-    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
-    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
-    p = __builtin_fma(p, r, 0x1.1111111111111p-7);
-    p = __builtin_fma(p, r, 0x1.5555555555555p-5);
-    p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+    const double kd = __builtin_rint(x * k.log2e);
+    const double r = (x - kd * k.ln2_hi) - kd * k.ln2_lo;
+    double p = k.c[0];
+#pragma unroll
+    for (int i = 1; i < 11; i++) p = __builtin_fma(p, r, k.c[i]);
     p = __builtin_fma(p, r, 0x1.0000000000000p-1);
     p = __builtin_fma(p, r, 1.0);
     p = __builtin_fma(p, r, 1.0);
     return (float)__builtin_amdgcn_ldexp(p, (int)kd);
 }
+__device__ __forceinline__ float expf_rn(float xf) { return expf_rn(xf, expf_k_imm()); }
 
 // Rust `(v).round() as i8`: half away from zero, saturating, NaN -> 0
 // (written with selects only, no branches).

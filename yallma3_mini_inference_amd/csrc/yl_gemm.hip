@@ -406,7 +406,9 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         run(std::false_type{});
     }
 
-    // epilogues
+    // epilogues (SwiGLU: TMW * 16 exponentials per lane, with expf's
+    // constants in registers)
+    [[maybe_unused]] const ExpfK ek = EPI == kEpiSwiglu ? expf_k_regs() : expf_k_imm();
 #pragma unroll
     for (int tm = 0; tm < TMW; tm++) {
 #pragma unroll
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 const int grp = (c0 + 64 * wn) / 64;
                 const bool grp_ok = c0 + 64 * wn < a.o;
                 const float g = acc[tm][0][i], u = acc[tm][1][i];
-                const float den = fadd(1.0f, expf_rn(-g));
+                const float den = fadd(1.0f, expf_rn(-g, ek));
                 const float h = fmul(g / den, u);
                 if (!a.hq) {   // f32 h only (quantized afterwards in the model's groups)
                     if (tok_ok && grp_ok) a.h_f32[(size_t)t * a.hidden + (size_t)grp * kGroup + li] = h;

@@ -113,12 +113,12 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
     __syncthreads();
     const int ty = tid >> 4, tx = tid & 15;
     float A[4][4], Bh[4][4], l[4][4];
-    // lane partial j of the 4 x 4 pairs
+    // lane partial j of the 4 x 4 pairs.  The reference's lane sums start
+    // from 0.0; these start from the first product, which differs only in
+    // a zero's sign (0 + -0 = +0).  A score is only ever used as
+    // exp(score - max) (and in the max), where +-0 - m = -m for m != 0 and
+    // exp(+-0) = 1, so no result depends on that sign.
     auto partial = [&](int j) {
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) l[a][b] = 0.0f;
 #pragma unroll
         for (int s = 0; s < HD / 8; s++) {
             const vf4 qv = *reinterpret_cast<const vf4*>(qT + (8 * s + j) * kPTS + 4 * ty);
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
 #pragma unroll
             for (int a = 0; a < 4; a++)
 #pragma unroll
-                for (int b = 0; b < 4; b++) l[a][b] = fadd(l[a][b], fmul(qv[a], kv[b]));
+                for (int b = 0; b < 4; b++) l[a][b] = s == 0 ? fmul(qv[a], kv[b]) : fadd(l[a][b], fmul(qv[a], kv[b]));
         }
     };
     // reduce_add8: A = ((l0 + l1) + l2) + l3, Bh = ((l4 + l5) + l6) + l7.
@@ -222,6 +222,7 @@ __global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__
     // 4 positions x 4 consecutive rows per thread, as 16-byte accesses:
     // position pp = tid / 16 + 16k, rows 4 * (tid % 16) + 0..3
     const int r4 = 4 * (tid & 15);
+    const ExpfK ek = expf_k_regs();   // 16 exponentials per thread
     vf4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__
         const int p = p0 + (tid >> 4) + 16 * k, t = row0 + r4;
         vf4 e;
 #pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = expf_rn(v[k][i] - mxl[r4 + i]);
+        for (int i = 0; i < 4; i++) e[i] = expf_rn(v[k][i] - mxl[r4 + i], ek);
         float* dst = S.sc + ((size_t)h * seq_ld + p) * Bp + t;
         // live: p < seq, row < batch and p <= pos0 + row (rising with the row)
         if (p < seq && t + 3 < batch && p <= pos0 + t) {
