@@ -265,24 +265,25 @@ __global__ __launch_bounds__(256) void k_pattn_sum(const StepState* __restrict__
     const int wlast = min(pos0 + min((int)(blockIdx.x * 256 + (tid & ~63) + 63), batch - 1), seq - 1);
     const float* col = S.sc + (size_t)h * seq_ld * Bp + tc;
     float sum = 0.0f;
-    // a ring of two 8-position groups: the next group's loads are in flight
-    // while the current one is added
-    float ea[8], eb[8];
+    // a ring of kG 8-position groups: the next kG - 1 groups' loads are in
+    // flight while one group is added (the walk is bound by load latency)
+    constexpr int kG = 4;
+    float e[kG][8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) ea[i] = col[(size_t)min(i, wlast) * Bp];
-    for (int t2 = 0; t2 <= wlast; t2 += 16) {
+    for (int g = 0; g < kG - 1; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) eb[i] = col[(size_t)min(t2 + 8 + i, wlast) * Bp];
-        __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 8; i++) e[g][i] = col[(size_t)min(8 * g + i, wlast) * Bp];
+    for (int t2 = 0; t2 <= wlast; t2 += 8 * kG) {
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (t2 + i <= t1 && t2 + i <= wlast) sum = fadd(sum, ea[i]);
+        for (int g = 0; g < kG; g++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) ea[i] = col[(size_t)min(t2 + 16 + i, wlast) * Bp];
-        __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < 8; i++)
+                e[(g + kG - 1) % kG][i] = col[(size_t)min(t2 + 8 * (g + kG - 1) + i, wlast) * Bp];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (t2 + 8 + i <= t1 && t2 + 8 + i <= wlast) sum = fadd(sum, eb[i]);
+            for (int i = 0; i < 8; i++)
+                if (t2 + 8 * g + i <= t1 && t2 + 8 * g + i <= wlast) sum = fadd(sum, e[g][i]);
+        }
     }
     if (t >= batch) return;
     // masked positions t1+1 .. seq-1 add exp(-1e10 - max) each
@@ -313,7 +314,10 @@ __global__ __launch_bounds__(HD * 4) void k_pattn_pv(const float* __restrict__ v
     __shared__ __align__(16) float vT[kPT * VS];     // [position][dim]
     __shared__ float invl[kPT], pml[kPT];
     __shared__ int full_sh;
-    const int rt = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    // a row tile's work grows with its causal bound: the grid runs heads
+    // fastest and row tiles from the last, so the longest workgroups are
+    // dispatched first and the short ones fill the slots they leave
+    const int h = blockIdx.x, rt = gridDim.y - 1 - blockIdx.y, tid = threadIdx.x;
     const int pos0 = st->pos, seq = pos0 + batch;
     if (seq > seq_ld) return;
     const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
@@ -475,7 +479,7 @@ static hipError_t launch_pattn_hd(const float* sq, const float* kc, const float*
     hipLaunchKernelGGL(k_pattn_exp, tiles, dim3(256), 0, s, st, batch, seq_ld, n_heads, scratch);
     hipLaunchKernelGGL(k_pattn_sum, dim3((pattn_rows_ld(batch) + 255) / 256, n_heads), dim3(256), 0, s, st, batch,
                        seq_ld, n_heads, scratch);
-    hipLaunchKernelGGL((k_pattn_pv<QF, HD>), dim3(pattn_tiles(batch), n_heads), dim3(HD * 4), 0, s, vc, st, batch,
+    hipLaunchKernelGGL((k_pattn_pv<QF, HD>), dim3(n_heads, pattn_tiles(batch)), dim3(HD * 4), 0, s, vc, st, batch,
                        seq_ld, n_heads, n_kv_heads, scratch, aq, as, att_f32);
     return hipGetLastError();
 }
