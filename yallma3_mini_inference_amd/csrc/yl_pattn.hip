@@ -1,6 +1,6 @@
 // yl_pattn.hip -- attention of prompt batches (forward.rs:299-400), tiled.
 //
-// A prompt of B >= 64 tokens attends in four kernels that share every K, V
+// A prompt of B >= 64 tokens attends in three kernels that share every K, V
 // and score tile among 64 query rows.  The arithmetic is the reference's,
 // operation by operation:
 //   score[t][t2] = reduce_add8(8 lane partials over head_size) * scale,
@@ -14,10 +14,11 @@
 // 1. k_pattn_scores: workgroup (position tile, row tile, head) computes the
 //    64 x 64 scores with 4 x 4 register tiles, one lane partial j at a time
 //    (folded in reduce_add8's order), and the tile's row maxima.
-// 2. k_pattn_exp: the same tiles, e = exp(score - max) in place.
-// 3. k_pattn_sum: one lane per row walks the row in position order (the
-//    serial denominator), then inv = 1 / sum and the masked p.
-// 4. k_pattn_pv: workgroup (row tile, head) chains p * v for its 64 rows and
+// 2. k_pattn_expsum: workgroup (head, row tile): e = exp(score - max) in
+//    place, chunk by chunk, while one wavefront adds each chunk to its rows'
+//    serial denominators in position order; then inv = 1 / sum and the
+//    masked p.
+// 3. k_pattn_pv: workgroup (head, row tile) chains p * v for its 64 rows and
 //    every dimension (4 rows x 4 dimensions x 8 lane chains per thread),
 //    then the 32-group quantization of the output projection's input.
 // Scores live in a scratch [head][position][row] (rows contiguous, so a
@@ -183,23 +184,33 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// 2. e = exp(score - max) in place over the causal entries of a tile; the
-//    row max folds the tile maxima from -1e10 (the position-0 tile stores it)
+// 2. exponentials and serial denominators, workgroup (head, row tile).  The
+//    row max folds the tile maxima from -1e10.  Then, chunk by chunk of 64
+//    positions up to the tile's causal bound, every thread computes 4
+//    positions x 4 rows of e = exp(score - max), written back in place (for
+//    P.V) and into an LDS tile, and wavefront 0 (lane r: row r) adds the
+//    chunk's causal e to its rows' sums in position order while the other
+//    wavefronts go on to the next chunk (two LDS tiles alternate; the next
+//    chunk's scores are loaded while the current one is computed).  Last,
+//    the masked positions' exp(-1e10 - max), inv = 1 / sum and the masked p.
+//    Row tiles run longest first (heads fastest), as in P.V.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__ st, int batch, int seq_ld,
-                                                   int n_heads, float* __restrict__ scratch) {
+__global__ __launch_bounds__(256) void k_pattn_expsum(const StepState* __restrict__ st, int batch, int seq_ld,
+                                                      int n_heads, float* __restrict__ scratch) {
     __shared__ float mxl[kPT];
-    const int pt = blockIdx.x, rt = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    __shared__ __align__(16) float eT[2][kPT * kPTS];   // [position][row]
+    const int h = blockIdx.x, rt = gridDim.y - 1 - blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int pos0 = st->pos, seq = pos0 + batch;
-    const int row0 = rt * kPT, p0 = pt * kPT;
-    if (seq > seq_ld || p0 >= seq || p0 > pos0 + row0 + kPT - 1) return;
+    if (seq > seq_ld) return;
     const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
     const int Bp = pattn_rows_ld(batch), ntl = pattn_tiles(seq_ld);
+    const int row0 = rt * kPT;
     {
         // row r = tid % 64 folds tile maxima q = tid / 64 + 4k (loads issued
         // 8 at a time), then the 4 partial maxima meet in LDS
         __shared__ float mxp[4][kPT];
-        const int r = tid & 63, part = tid >> 6, t = row0 + r;
+        const int r = lane, part = wave, t = row0 + r;
         const int last = min(pos0 + t, seq - 1) / kPT;
         const float* tmr = S.tm + (size_t)h * ntl * Bp + t;
         float mx = -1e10f;
@@ -215,79 +226,71 @@ __global__ __launch_bounds__(256) void k_pattn_exp(const StepState* __restrict__
         if (tid < kPT) {
             mx = fmaxf(fmaxf(mxp[0][tid], mxp[1][tid]), fmaxf(mxp[2][tid], mxp[3][tid]));
             mxl[tid] = mx;
-            if (pt == 0) S.mx[(size_t)h * Bp + row0 + tid] = mx;
+            S.mx[(size_t)h * Bp + row0 + tid] = mx;
         }
+        __syncthreads();
     }
-    __syncthreads();
+    const int bound = min(seq, pos0 + row0 + kPT);   // positions < bound: every row's causal part
+    const int nq = (bound + kPT - 1) / kPT;
+    const ExpfK ek = expf_k_regs();   // 16 exponentials per thread and chunk
     // 4 positions x 4 consecutive rows per thread, as 16-byte accesses:
-    // position pp = tid / 16 + 16k, rows 4 * (tid % 16) + 0..3
-    const int r4 = 4 * (tid & 15);
-    const ExpfK ek = expf_k_regs();   // 16 exponentials per thread
+    // position pp = tid / 16 + 16k of the chunk, rows 4 * (tid % 16) + 0..3
+    const int r4 = 4 * (tid & 15), tr = row0 + r4;
+    float mr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) mr[i] = mxl[r4 + i];
+    float* sch = S.sc + (size_t)h * seq_ld * Bp + row0 + r4;
     vf4 v[4];
+    auto load = [&](int q0) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int p = min(p0 + (tid >> 4) + 16 * k, seq - 1);
-        v[k] = *reinterpret_cast<const vf4*>(S.sc + ((size_t)h * seq_ld + p) * Bp + row0 + r4);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int p = p0 + (tid >> 4) + 16 * k, t = row0 + r4;
-        vf4 e;
-#pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = expf_rn(v[k][i] - mxl[r4 + i], ek);
-        float* dst = S.sc + ((size_t)h * seq_ld + p) * Bp + t;
-        // live: p < seq, row < batch and p <= pos0 + row (rising with the row)
-        if (p < seq && t + 3 < batch && p <= pos0 + t) {
-            *reinterpret_cast<vf4*>(dst) = e;
-        } else if (p < seq) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (t + i < batch && p <= pos0 + t + i) dst[i] = e[i];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// 3. serial denominators, one lane per row, positions in order; 8 loads in
-//    flight per lane (the adds stay in order)
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pattn_sum(const StepState* __restrict__ st, int batch, int seq_ld,
-                                                   int n_heads, float* __restrict__ scratch) {
-    const int h = blockIdx.y, tid = threadIdx.x;
-    const int t = blockIdx.x * 256 + tid;
-    const int pos0 = st->pos, seq = pos0 + batch;
-    if (seq > seq_ld) return;
-    const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
-    const int Bp = pattn_rows_ld(batch);
-    const int tc = min(t, Bp - 1);
-    const int t1 = pos0 + t;
-    // the wavefront walks to the last causal position of its last row
-    const int wlast = min(pos0 + min((int)(blockIdx.x * 256 + (tid & ~63) + 63), batch - 1), seq - 1);
-    const float* col = S.sc + (size_t)h * seq_ld * Bp + tc;
+        for (int k = 0; k < 4; k++)
+            v[k] = *reinterpret_cast<const vf4*>(sch + (size_t)min(q0 + (tid >> 4) + 16 * k, seq - 1) * Bp);
+    };
+    const int t1 = pos0 + row0 + lane;   // wavefront 0: lane's row's last causal position
     float sum = 0.0f;
-    // a ring of kG 8-position groups: the next kG - 1 groups' loads are in
-    // flight while one group is added (the walk is bound by load latency)
-    constexpr int kG = 4;
-    float e[kG][8];
+    load(0);
+    for (int c = 0; c < nq; c++) {
+        const int q0 = c * kPT;
+        float* et = eT[c & 1];
+        vf4 e[4];
 #pragma unroll
-    for (int g = 0; g < kG - 1; g++)
+        for (int k = 0; k < 4; k++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) e[g][i] = col[(size_t)min(8 * g + i, wlast) * Bp];
-    for (int t2 = 0; t2 <= wlast; t2 += 8 * kG) {
+            for (int i = 0; i < 4; i++) e[k][i] = expf_rn(v[k][i] - mr[i], ek);
+        if (c + 1 < nq) load(q0 + kPT);
 #pragma unroll
-        for (int g = 0; g < kG; g++) {
+        for (int k = 0; k < 4; k++) {
+            const int pp = (tid >> 4) + 16 * k, p = q0 + pp;
+            *reinterpret_cast<vf4*>(et + pp * kPTS + r4) = e[k];
+            float* dst = sch + (size_t)p * Bp;
+            // live: p < seq, row < batch and p <= pos0 + row (rising with the row)
+            if (p < seq && tr + 3 < batch && p <= pos0 + tr) {
+                *reinterpret_cast<vf4*>(dst) = e[k];
+            } else if (p < seq) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                e[(g + kG - 1) % kG][i] = col[(size_t)min(t2 + 8 * (g + kG - 1) + i, wlast) * Bp];
-            __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < 4; i++)
+                    if (tr + i < batch && p <= pos0 + tr + i) dst[i] = e[k][i];
+            }
+        }
+        __syncthreads();   // the chunk's tile is complete; eT[c & 1] is next written after the next barrier
+        if (wave == 0) {
+            // the row's causal e of this chunk in position order, read 16 at a time
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                if (t2 + 8 * g + i <= t1 && t2 + 8 * g + i <= wlast) sum = fadd(sum, e[g][i]);
+            for (int g = 0; g < kPT; g += 16) {
+                float ev[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) ev[i] = et[(g + i) * kPTS + lane];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (q0 + g + i <= t1) sum = fadd(sum, ev[i]);
+            }
         }
     }
+    if (wave != 0) return;
+    const int t = row0 + lane;
     if (t >= batch) return;
     // masked positions t1+1 .. seq-1 add exp(-1e10 - max) each
-    const float em = t1 < seq - 1 ? expf_rn(-1e10f - S.mx[(size_t)h * Bp + t]) : 0.0f;
+    const float em = t1 < seq - 1 ? expf_rn(-1e10f - mxl[lane], ek) : 0.0f;
     if (em != 0.0f)
         for (int i = t1 + 1; i < seq; i++) sum = fadd(sum, em);
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(256) void k_pattn_sum(const StepState* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// 4. P.V chains and the output.  Thread (ty, tx): rows 4ty..+3, dimensions
+// 3. P.V chains and the output.  Thread (ty, tx): rows 4ty..+3, dimensions
 //    4tx..+3, 8 lane chains each (acc[row][dim][j] += p * v over t2 = 8c + j,
 //    c in order).  Positions run to the tile's causal bound (the last row's
 //    t1) unless a row's masked p is nonzero or the V rows past the bound hold
@@ -476,9 +479,8 @@ static hipError_t launch_pattn_hd(const float* sq, const float* kc, const float*
     const dim3 tiles(pattn_tiles(seq_ld), pattn_tiles(batch), n_heads);
     hipLaunchKernelGGL((k_pattn_scores<HD>), tiles, dim3(256), 0, s, sq, kc, st, batch, seq_ld, kv_ld, n_heads,
                        n_kv_heads, scale, scratch);
-    hipLaunchKernelGGL(k_pattn_exp, tiles, dim3(256), 0, s, st, batch, seq_ld, n_heads, scratch);
-    hipLaunchKernelGGL(k_pattn_sum, dim3((pattn_rows_ld(batch) + 255) / 256, n_heads), dim3(256), 0, s, st, batch,
-                       seq_ld, n_heads, scratch);
+    hipLaunchKernelGGL(k_pattn_expsum, dim3(n_heads, pattn_tiles(batch)), dim3(256), 0, s, st, batch, seq_ld, n_heads,
+                       scratch);
     hipLaunchKernelGGL((k_pattn_pv<QF, HD>), dim3(n_heads, pattn_tiles(batch)), dim3(HD * 4), 0, s, vc, st, batch,
                        seq_ld, n_heads, n_kv_heads, scratch, aq, as, att_f32);
     return hipGetLastError();
