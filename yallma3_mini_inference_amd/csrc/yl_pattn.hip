@@ -65,11 +65,19 @@ bool prompt_attn_applies(int batch, int seq_len, int head_size) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. scores and tile row maxima.  Thread (ty, tx) of 16 x 16: rows 4ty..+3,
-//    positions 4tx..+3 of the tile.  Lane partial j (dimensions 8s + j, s in
-//    order) of all 16 scores, then folded: a = ((l0 + l1) + l2) + l3,
-//    b = ((l4 + l5) + l6) + l7, score = (a + b) * scale.
+// 1. scores and tile row maxima.  Workgroup (head, row tile, segment): the
+//    segment's position tiles (at most kScSeg of the row tile's causal ones)
+//    in order, the Q tile loaded once, the next K tile's loads in flight
+//    while the current one is computed.  Thread (ty, tx) of 16 x 16: rows
+//    4ty..+3, positions 4tx..+3 of the tile.  Lane partial j (dimensions
+//    8s + j, s in order) of all 16 scores, then folded:
+//    a = ((l0 + l1) + l2) + l3, b = ((l4 + l5) + l6) + l7,
+//    score = (a + b) * scale.  Grid (x only): heads fastest, then segments,
+//    then row tiles from the last (the longest).
 // ---------------------------------------------------------------------------
+constexpr int kScSeg = 8;   // position tiles per workgroup at most
+__host__ __device__ inline int pattn_score_segs(int seq_ld) { return (pattn_tiles(seq_ld) + kScSeg - 1) / kScSeg; }
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ sq, const float* __restrict__ kc,
                                                       const StepState* __restrict__ st, int batch, int seq_ld,
@@ -77,39 +85,60 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
                                                       float* __restrict__ scratch) {
     __shared__ __align__(16) float qT[HD * kPTS];   // [dim][row]
     __shared__ __align__(16) float kT[HD * kPTS];   // [dim][position]
-    const int pt = blockIdx.x, rt = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    const int nseg = pattn_score_segs(seq_ld);
+    const int tid = threadIdx.x, h = (int)(blockIdx.x % n_heads), ys = (int)(blockIdx.x / n_heads);
+    const int rt = pattn_tiles(batch) - 1 - ys / nseg, seg = ys % nseg;
     const int pos0 = st->pos, seq = pos0 + batch;
-    const int row0 = rt * kPT, p0 = pt * kPT;
-    if (seq > seq_ld || p0 >= seq || p0 > pos0 + row0 + kPT - 1) return;   // past the sequence, or all masked
+    const int row0 = rt * kPT;
+    if (seq > seq_ld) return;
+    // position tiles holding a causal position of some row of the tile
+    const int last_pt = min(pos0 + row0 + kPT - 1, seq - 1) / kPT;
+    const int pt0 = seg * kScSeg, pt1 = min(pt0 + kScSeg - 1, last_pt);
+    if (pt0 > pt1) return;
     const PromptScratch S = pattn_carve(scratch, n_heads, seq_ld, batch);
     const int Bp = pattn_rows_ld(batch);
     const int kvh = h / (n_heads / n_kv_heads), att_dim = n_heads * HD;
-    // every load first (q rows as 16-byte pieces, key quads), then the LDS
-    // stores: keys transposed, dimension d of position p at
+    // q rows as 16-byte pieces and key quads: dimension d of position p at
     // kc[(kvh*HD + d) * kv_ld + p]; quads past the row (kv_ld is a multiple
     // of 4) re-read its last quad (positions past seq are never stored)
     constexpr int NV = HD / 16;   // 16-byte pieces per thread, q and keys each
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(kc + (size_t)kvh * HD * kv_ld), (short)0, HD * kv_ld * 4, kBufRawP);
-    vf4 qa[NV], ka[NV];
-    // (q pieces: consecutive lanes take consecutive rows, so the transposed
-    // LDS stores below hit consecutive banks)
+    vf4 ka[NV];
+    auto load_k = [&](int pt) {
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
-        qa[i] = *reinterpret_cast<const vf4*>(sq + (size_t)min(row0 + r, batch - 1) * att_dim + (size_t)h * HD + 4 * d4);
-        const int d = idx / (kPT / 4), q4 = idx % (kPT / 4);
-        const int p = min(p0 + 4 * q4, kv_ld - 4);
-        ka[i] = __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(krs, p * 4, d * kv_ld * 4, 0));
-    }
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i, d = idx / (kPT / 4), q4 = idx % (kPT / 4);
+            const int p = min(pt * kPT + 4 * q4, kv_ld - 4);
+            ka[i] = __builtin_bit_cast(vf4, __builtin_amdgcn_raw_buffer_load_b128(krs, p * 4, d * kv_ld * 4, 0));
+        }
+    };
+    // keys transposed
+    auto store_k = [&]() {
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
-        const bool live = row0 + r < batch;
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i, d = idx / (kPT / 4), q4 = idx % (kPT / 4);
+            *reinterpret_cast<vf4*>(kT + d * kPTS + 4 * q4) = ka[i];
+        }
+    };
+    {
+        // (q pieces: consecutive lanes take consecutive rows, so the
+        // transposed LDS stores below hit consecutive banks)
+        vf4 qa[NV];
 #pragma unroll
-        for (int c = 0; c < 4; c++) qT[(4 * d4 + c) * kPTS + r] = live ? qa[i][c] : 0.0f;
-        const int d = idx / (kPT / 4), q4 = idx % (kPT / 4);
-        *reinterpret_cast<vf4*>(kT + d * kPTS + 4 * q4) = ka[i];
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
+            qa[i] = *reinterpret_cast<const vf4*>(sq + (size_t)min(row0 + r, batch - 1) * att_dim + (size_t)h * HD + 4 * d4);
+        }
+        load_k(pt0);
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int idx = tid + 256 * i, r = idx % kPT, d4 = idx / kPT;
+            const bool live = row0 + r < batch;
+#pragma unroll
+            for (int c = 0; c < 4; c++) qT[(4 * d4 + c) * kPTS + r] = live ? qa[i][c] : 0.0f;
+        }
+        store_k();
     }
     __syncthreads();
     const int ty = tid >> 4, tx = tid & 15;
@@ -130,57 +159,66 @@ __global__ __launch_bounds__(256) void k_pattn_scores(const float* __restrict__ 
                 for (int b = 0; b < 4; b++) l[a][b] = s == 0 ? fmul(qv[a], kv[b]) : fadd(l[a][b], fmul(qv[a], kv[b]));
         }
     };
-    // reduce_add8: A = ((l0 + l1) + l2) + l3, Bh = ((l4 + l5) + l6) + l7.
-    // One partial at a time (unrolled, the compiler would hoist every
-    // partial's LDS reads and run out of registers); each fold is a loop of
-    // its own so that no per-element branch on j remains.
-    partial(0);
-#pragma unroll
-    for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) A[a][b] = l[a][b];
-#pragma unroll 1
-    for (int j = 1; j < 4; j++) {
-        partial(j);
+    for (int pt = pt0; pt <= pt1; pt++) {
+        if (pt < pt1) load_k(pt + 1);   // in flight while this tile is computed
+        const int p0 = pt * kPT;
+        // reduce_add8: A = ((l0 + l1) + l2) + l3, Bh = ((l4 + l5) + l6) + l7.
+        // One partial at a time (unrolled, the compiler would hoist every
+        // partial's LDS reads and run out of registers); each fold is a loop
+        // of its own so that no per-element branch on j remains.
+        partial(0);
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) A[a][b] = fadd(A[a][b], l[a][b]);
-    }
-    partial(4);
-#pragma unroll
-    for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) Bh[a][b] = l[a][b];
+            for (int b = 0; b < 4; b++) A[a][b] = l[a][b];
 #pragma unroll 1
-    for (int j = 5; j < 8; j++) {
-        partial(j);
+        for (int j = 1; j < 4; j++) {
+            partial(j);
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+            for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) Bh[a][b] = fadd(Bh[a][b], l[a][b]);
-    }
-    float rmax[4] = {-1e10f, -1e10f, -1e10f, -1e10f};
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const int p = p0 + 4 * tx + b;
-        float v[4];
-#pragma unroll
-        for (int a = 0; a < 4; a++) {
-            v[a] = fmul(fadd(A[a][b], Bh[a][b]), scale);
-            if (p <= pos0 + row0 + 4 * ty + a) rmax[a] = fmaxf(rmax[a], v[a]);
+                for (int b = 0; b < 4; b++) A[a][b] = fadd(A[a][b], l[a][b]);
         }
-        if (p < seq)
-            *reinterpret_cast<vf4*>(S.sc + ((size_t)h * seq_ld + p) * Bp + row0 + 4 * ty) = vf4{v[0], v[1], v[2], v[3]};
+        partial(4);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) Bh[a][b] = l[a][b];
+#pragma unroll 1
+        for (int j = 5; j < 8; j++) {
+            partial(j);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) Bh[a][b] = fadd(Bh[a][b], l[a][b]);
+        }
+        float rmax[4] = {-1e10f, -1e10f, -1e10f, -1e10f};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int p = p0 + 4 * tx + b;
+            float v[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                v[a] = fmul(fadd(A[a][b], Bh[a][b]), scale);
+                if (p <= pos0 + row0 + 4 * ty + a) rmax[a] = fmaxf(rmax[a], v[a]);
+            }
+            if (p < seq)
+                *reinterpret_cast<vf4*>(S.sc + ((size_t)h * seq_ld + p) * Bp + row0 + 4 * ty) = vf4{v[0], v[1], v[2], v[3]};
+        }
+        // row maxima over the 16 threads of a row group (tx = the low 4 bits)
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) rmax[a] = fmaxf(rmax[a], __shfl_xor(rmax[a], off, 16));
+        if (tx == 0)
+#pragma unroll
+            for (int a = 0; a < 4; a++) S.tm[((size_t)h * pattn_tiles(seq_ld) + pt) * Bp + row0 + 4 * ty + a] = rmax[a];
+        if (pt < pt1) {
+            __syncthreads();   // every wavefront is done with this K tile
+            store_k();
+            __syncthreads();   // the next one is in LDS
+        }
     }
-    // row maxima over the 16 threads of a row group (tx = the low 4 bits)
-#pragma unroll
-    for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) rmax[a] = fmaxf(rmax[a], __shfl_xor(rmax[a], off, 16));
-    if (tx == 0)
-#pragma unroll
-        for (int a = 0; a < 4; a++) S.tm[((size_t)h * pattn_tiles(seq_ld) + pt) * Bp + row0 + 4 * ty + a] = rmax[a];
 }
 
 // ---------------------------------------------------------------------------
@@ -476,7 +514,7 @@ template <int QF, int HD>
 static hipError_t launch_pattn_hd(const float* sq, const float* kc, const float* vc, const StepState* st, int batch,
                                   int seq_ld, int kv_ld, int n_heads, int n_kv_heads, float scale, int8_t* aq,
                                   float* as, float* att_f32, float* scratch, hipStream_t s) {
-    const dim3 tiles(pattn_tiles(seq_ld), pattn_tiles(batch), n_heads);
+    const dim3 tiles((unsigned)n_heads * pattn_tiles(batch) * pattn_score_segs(seq_ld));
     hipLaunchKernelGGL((k_pattn_scores<HD>), tiles, dim3(256), 0, s, sq, kc, st, batch, seq_ld, kv_ld, n_heads,
                        n_kv_heads, scale, scratch);
     hipLaunchKernelGGL(k_pattn_expsum, dim3(n_heads, pattn_tiles(batch)), dim3(256), 0, s, st, batch, seq_ld, n_heads,
