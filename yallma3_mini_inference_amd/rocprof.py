@@ -3,7 +3,7 @@
     python -m yallma3_mini_inference_amd.rocprof trace KERNEL_TRACE.csv > summary.md
         Per kernel (name, grid): dispatch count, mean / median / min duration
         (us).  Decode launches (grid y = 1) and prompt launches (grid y > 1,
-        one row per token) are listed apart, since the bench's per-launch
+        one row per token, and the prompt attention kernels) are listed apart, since the bench's per-launch
         figures are for decode launches only.
 
     python -m yallma3_mini_inference_amd.rocprof instep KERNEL_TRACE.csv N_LAYERS
@@ -81,7 +81,9 @@ def trace(path):
     by = collections.defaultdict(list)
     for r in rows:
         name = r["Kernel_Name"]
-        kind = ("decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in name or "k_attn_scores" in name or "k_attn_pv_j" in name
+        # (the prompt attention kernels run for prompts only, whatever their grid)
+        kind = ("prompt" if "k_pattn_" in name else
+                "decode" if r["Grid_Size_Y"] == "1" or "attn_decode" in name or "k_attn_scores" in name or "k_attn_pv_j" in name
                 else "prompt")
         key = (kind, _short(r["Kernel_Name"]), r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"],
                r["VGPR_Count"], r["LDS_Block_Size"], r["Scratch_Size"])
