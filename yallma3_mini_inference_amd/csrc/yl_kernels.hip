@@ -29,7 +29,20 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
     __shared__ int8_t ql[8192];
     __shared__ float sl[256];
     const int t = blockIdx.x;
-    for (int i = threadIdx.x; i < dim; i += kThreads) store_norm_input(xt, dim, i, x[(size_t)t * dim + i], w[i]);
+    // 8 elements per thread and pass, every load issued before the first
+    // store (a load per iteration would wait out one memory round trip each)
+    for (int i0 = threadIdx.x; i0 < dim; i0 += 8 * kThreads) {
+        float xv[8], wv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = min(i0 + k * kThreads, dim - 1);
+            xv[k] = x[(size_t)t * dim + i];
+            wv[k] = w[i];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + k * kThreads < dim) store_norm_input(xt, dim, i0 + k * kThreads, xv[k], wv[k]);
+    }
     __syncthreads();
     rmsnorm_quant_block<QF, false>(xt, dim, eps, ql, sl, xn ? xn + (size_t)t * dim : nullptr);
     if constexpr (QF >= 0) {
@@ -48,20 +61,28 @@ __global__ __launch_bounds__(kThreads) void k_embed(EmbQ8 e, const uint32_t* __r
     const uint32_t tok = tokens[t];
     const int lane = (int)(tok & 63u);
     const size_t tile = tok >> 6;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-        float v = 0.0f;
-        if (tok < (uint32_t)e.vocab) {
-            const size_t off = emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15);
-            if (e.fmt == 3) {
-                v = fmul((float)e.q[off], e.d32[((size_t)(i / e.gs) * e.tiles + tile) * 64 + lane]);
-            } else if (e.fmt == 1) {
-                v = f16_to_f32(reinterpret_cast<const uint16_t*>(e.q)[off]);
-            } else {
-                const int q = (int)(uint8_t)e.q[off] - 128;
-                v = fmul((float)q, f16_to_f32(e.d[emb_d_idx(e.tiles, tile, i >> 5, lane)]));
+    // 8 elements per thread and pass, computed (loads issued) before any is stored
+    for (int i0 = threadIdx.x; i0 < dim; i0 += 8 * (int)blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = min(i0 + k * (int)blockDim.x, dim - 1);
+            v[k] = 0.0f;
+            if (tok < (uint32_t)e.vocab) {
+                const size_t off = emb_q_off(e.tiles, tile, i >> 4, lane) + (i & 15);
+                if (e.fmt == 3) {
+                    v[k] = fmul((float)e.q[off], e.d32[((size_t)(i / e.gs) * e.tiles + tile) * 64 + lane]);
+                } else if (e.fmt == 1) {
+                    v[k] = f16_to_f32(reinterpret_cast<const uint16_t*>(e.q)[off]);
+                } else {
+                    const int q = (int)(uint8_t)e.q[off] - 128;
+                    v[k] = fmul((float)q, f16_to_f32(e.d[emb_d_idx(e.tiles, tile, i >> 5, lane)]));
+                }
             }
         }
-        x[(size_t)t * dim + i] = v;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + k * (int)blockDim.x < dim) x[(size_t)t * dim + i0 + k * (int)blockDim.x] = v[k];
     }
 }
 
