@@ -86,9 +86,9 @@ __device__ void rmsnorm_quant_block(float* xt, int dim, float eps, int8_t* q_lds
         if (xn && i < dim) xn[i] = v;
         if constexpr (QF >= 0) {
             // groups of 32 never straddle `dim` (dim % 32 == 0 when quantizing)
-            float am = fabsf(v);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+            // (DPP within 16-lane rows, one shuffle across them; the max of
+            // absolute values is order-free)
+            float am = group_max(fabsf(v), 32);
             am = fmaxf(am, 0.0f);
             const float sc = group_scale<QF>(am);
             if (i < dim) {
