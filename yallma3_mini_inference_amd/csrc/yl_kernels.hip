@@ -21,13 +21,14 @@ namespace yl {
 
 constexpr int kThreads = 256;
 
-// RMSNorm (+ quantize) of `batch` rows, one workgroup per row.
+// RMSNorm (+ quantize) of `batch` rows, one workgroup per row.  The
+// quantized row and its scales go straight to global memory (no LDS copy),
+// so a workgroup holds only the transposed row and the norm weights in LDS
+// and a whole 2048-row batch is resident at once.
 template <int QF>
 __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w,
                                                       int dim, float eps, float* xn, int8_t* xq, float* xs) {
     extern __shared__ __align__(16) float xt[];
-    __shared__ int8_t ql[8192];
-    __shared__ float sl[256];
     const int t = blockIdx.x;
     // 8 elements per thread and pass, every load issued before the first
     // store (a load per iteration would wait out one memory round trip each)
@@ -44,11 +45,9 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
             if (i0 + k * kThreads < dim) store_norm_input(xt, dim, i0 + k * kThreads, xv[k], wv[k]);
     }
     __syncthreads();
-    rmsnorm_quant_block<QF, false>(xt, dim, eps, ql, sl, xn ? xn + (size_t)t * dim : nullptr);
-    if constexpr (QF >= 0) {
-        for (int i = threadIdx.x; i < dim; i += kThreads) xq[(size_t)t * dim + i] = ql[i];
-        for (int i = threadIdx.x; i < dim / kGroup; i += kThreads) xs[(size_t)t * (dim / kGroup) + i] = sl[i];
-    }
+    rmsnorm_quant_block<QF, false>(xt, dim, eps, QF >= 0 ? xq + (size_t)t * dim : nullptr,
+                                   QF >= 0 ? xs + (size_t)t * (dim / kGroup) : nullptr,
+                                   xn ? xn + (size_t)t * dim : nullptr);
 }
 
 // Embedding lookup (base_transformer.rs:143-161: out-of-range ids give
