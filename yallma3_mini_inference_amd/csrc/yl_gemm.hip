@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     constexpr int TMW = TM / 64;   // 32-token MFMA tiles per wavefront
     constexpr int WT = TM / 2;     // tokens per wavefront
     extern __shared__ __align__(16) unsigned char gsm[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int wm = wave & 1, wn = wave >> 1;
     const int c0 = blockIdx.x * kGmTN, t0 = blockIdx.y * TM;
@@ -127,6 +127,19 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     float acc[TMW][2][16];
     int pos = 0;
     if constexpr (EPI == kEpiQkvRope) pos = a.state->pos;
+    // QKV rows: each lane's stored column within q or k (RoPE pair order)
+    // and its pair index, for its two 32-row blocks
+    [[maybe_unused]] int kcol[2] = {0, 0}, qkcol[2] = {0, 0}, qpair[2] = {0, 0};
+    if constexpr (EPI == kEpiQkvRope) {
+#pragma unroll
+        for (int tn = 0; tn < 2; tn++) {
+            const int c = c0 + 64 * wn + 32 * tn + li, att = a.att_dim;
+            const int scol = c < att ? c : c - att;   // stored row within q or k
+            kcol[tn] = qk_column(c - att, a.head_size, a.hf_rows);
+            qkcol[tn] = qk_column(scol, a.head_size, a.hf_rows);
+            qpair[tn] = (scol % a.head_size) >> 1;
+        }
+    }
     auto init_acc = [&]() {
 #pragma unroll
     for (int tm = 0; tm < TMW; tm++)
@@ -137,19 +150,21 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 float v = 0.0f;
                 const int t = t0 + WT * wm + 32 * tm + (i & 3) + 8 * (i >> 2) + 4 * lh;
                 const int c = c0 + 64 * wn + 32 * tn + li;
-                if (t < M && c < a.o) {
-                    if constexpr (EPI == kEpiStore) {
-                        if (c < a.accumulate_cols) v = a.out[(size_t)t * a.o + c];
-                    } else if constexpr (EPI == kEpiQkvRope) {
-                        // K/V rows accumulate into the cache (forward.rs:166-169)
-                        const int att = a.att_dim, kv = a.kv_dim;
-                        if (c >= att && c < att + kv) {
-                            const int cc = qk_column(c - att, a.head_size, a.hf_rows);
-                            if (cc < (kv / 4) * 4) v = a.k_cache[(size_t)cc * a.kv_ld + pos + t];
-                        } else if (c >= att + kv) {
-                            const int cc = c - att - kv;
-                            if (cc < (kv / 4) * 4) v = a.v_cache[(size_t)(pos + t) * kv + cc];
-                        }
+                if constexpr (EPI == kEpiStore) {
+                    if (t < M && c < a.o && c < a.accumulate_cols) v = a.out[(size_t)t * a.o + c];
+                } else if constexpr (EPI == kEpiQkvRope) {
+                    // K/V rows accumulate into the cache (forward.rs:166-169);
+                    // q rows start at 0.  A 32-row block is all q, all k or
+                    // all v (att_dim and kv_dim are multiples of 32), so the
+                    // branches are uniform; token t0 stands in for the rows
+                    // past M in the (then unused) loads.
+                    const int cb = c0 + 64 * wn + 32 * tn, att = a.att_dim, kv = a.kv_dim;
+                    if (cb >= att && cb < a.o) {
+                        const int tc = t < M ? t : t0;
+                        const float u = cb < att + kv
+                                            ? a.k_cache[(size_t)kcol[tn] * a.kv_ld + pos + tc]
+                                            : a.v_cache[(size_t)(pos + tc) * kv + (c - att - kv)];
+                        if (t < M) v = u;
                     }
                 }
                 acc[tm][tn][i] = v;
@@ -446,20 +461,21 @@ __global__ __launch_bounds__(kGmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                         // rope_gguf (util.rs:653-718) on q and k pairs (2j, 2j+1):
                         // the pair partner is the neighbouring lane
                         const float other = dpp_mov<0xB1>(v);
-                        if (tok_ok && c < a.o) {
-                            const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
-                            if (c >= att + kv) {
-                                a.v_cache[(size_t)(pos + t) * kv + (c - att - kv)] = v;
-                            } else {
-                                const int scol = c < att ? c : c - att;   // stored row within q or k
-                                const int col = qk_column(scol, hd, a.hf_rows);
-                                const int pair = (scol % hd) >> 1;
-                                const float cs = a.rope_cos[(size_t)(pos + t) * (hd >> 1) + pair];
-                                const float sn = a.rope_sin[(size_t)(pos + t) * (hd >> 1) + pair];
-                                const float v0 = (li & 1) ? other : v, v1 = (li & 1) ? v : other;
-                                const float r = (li & 1) ? fadd(fmul(v0, sn), fmul(v1, cs)) : fmul(v0, cs) - fmul(v1, sn);
-                                if (c < att) a.q_out[(size_t)t * att + col] = r;
-                                else a.k_cache[(size_t)col * a.kv_ld + pos + t] = r;
+                        // (uniform branches on the 32-row block, as in the
+                        // initial values)
+                        const int cb = c0 + 64 * wn + 32 * tn;
+                        const int att = a.att_dim, kv = a.kv_dim, hd = a.head_size;
+                        if (cb >= att + kv) {
+                            if (tok_ok && cb < a.o) a.v_cache[(size_t)(pos + t) * kv + (c - att - kv)] = v;
+                        } else {
+                            const int tc = tok_ok ? t : t0;
+                            const float cs = a.rope_cos[(size_t)(pos + tc) * (hd >> 1) + qpair[tn]];
+                            const float sn = a.rope_sin[(size_t)(pos + tc) * (hd >> 1) + qpair[tn]];
+                            const float v0 = (li & 1) ? other : v, v1 = (li & 1) ? v : other;
+                            const float r = (li & 1) ? fadd(fmul(v0, sn), fmul(v1, cs)) : fmul(v0, cs) - fmul(v1, sn);
+                            if (tok_ok) {
+                                if (cb < att) a.q_out[(size_t)t * att + qkcol[tn]] = r;
+                                else a.k_cache[(size_t)qkcol[tn] * a.kv_ld + pos + t] = r;
                             }
                         }
                     } else if (tok_ok && c < a.o) {
@@ -506,7 +522,13 @@ int gemm_tile_tokens(int o, int M) {
 
 template <int WF, int EPI>
 static hipError_t launch_gemm_k(const GemvArgs& a, int M, hipStream_t st) {
-    return gemm_tile_tokens(a.o, M) == 64 ? launch_gemm_tm<WF, EPI, 64>(a, M, st) : launch_gemm_tm<WF, EPI, 128>(a, M, st);
+    // Q8 with one f32 scale per 4 blocks keeps a group's int32 dots of four
+    // tiles in registers besides the accumulators: at 128 tokens that does
+    // not fit in 256 registers (spills), so it always takes 64-token tiles
+    if constexpr (WF == kQ8S128) return launch_gemm_tm<WF, EPI, 64>(a, M, st);
+    else
+        return gemm_tile_tokens(a.o, M) == 64 ? launch_gemm_tm<WF, EPI, 64>(a, M, st)
+                                              : launch_gemm_tm<WF, EPI, 128>(a, M, st);
 }
 
 bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M) {
@@ -515,7 +537,7 @@ bool gemm_supported(const GemvArgs& a, int wfmt, int epi, int M) {
     if ((wfmt == kQ8S64 && a.nb % 2) || (wfmt == kQ8S128 && a.nb % 4)) return false;
     if (epi == kEpiSwiglu && !a.hq && !a.h_f32) return false;
     if (epi == kEpiSwiglu && (a.o % 64 || a.hidden * 2 != a.o)) return false;
-    if (epi == kEpiQkvRope && (a.head_size % 2 || a.att_dim % 32)) return false;
+    if (epi == kEpiQkvRope && (a.head_size % 2 || a.att_dim % 32 || a.kv_dim % 32)) return false;
     return true;
 }
 
